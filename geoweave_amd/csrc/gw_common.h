@@ -1,0 +1,134 @@
+// Shared host and device helpers for the gfx950 sparse global-attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "geoweave_hip.h"
+
+// ---------------------------------------------------------------------------------------
+// Host side: per-thread error message behind gw_last_error().
+// ---------------------------------------------------------------------------------------
+namespace gw {
+
+// Records a printf-style message for gw_last_error() and returns `code`.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+// Maps a failed HIP call to GW_ERR_HIP with the call site in the message.
+int hip_error(hipError_t err, const char* what);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace gw
+
+#define GW_CHECK_ARG(cond, ...)                                  \
+  do {                                                           \
+    if (!(cond)) return ::gw::set_error(GW_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+#define GW_HIP_LAUNCH_CHECK(what)                                \
+  do {                                                           \
+    hipError_t e__ = hipGetLastError();                          \
+    if (e__ != hipSuccess) return ::gw::hip_error(e__, what);    \
+  } while (0)
+
+// ---------------------------------------------------------------------------------------
+// Device side.
+// ---------------------------------------------------------------------------------------
+namespace gw {
+
+// Element-type tags. Storage is always the 16-bit pattern.
+struct BF16 {};
+struct FP16 {};
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// fp32 dot of two packed pairs accumulated onto c: v_dot2_f32_bf16 / v_dot2_f32_f16.
+// The products of two 16-bit floats are exact in fp32; only the accumulation rounds.
+__device__ __forceinline__ float dot2(BF16, uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+__device__ __forceinline__ float dot2(FP16, uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b),
+                                c, false);
+}
+
+// 8-element dot product of two 16-byte vectors (8 x 16-bit each).
+template <typename E>
+__device__ __forceinline__ float dot8(uint4 a, uint4 b) {
+  float s = dot2(E{}, a.x, b.x, 0.f);
+  s = dot2(E{}, a.y, b.y, s);
+  s = dot2(E{}, a.z, b.z, s);
+  s = dot2(E{}, a.w, b.w, s);
+  return s;
+}
+
+// Unpacks a 32-bit word holding two 16-bit floats (low half first) to fp32.
+__device__ __forceinline__ void unpack2(BF16, uint32_t u, float& lo, float& hi) {
+  lo = __uint_as_float(u << 16);
+  hi = __uint_as_float(u & 0xffff0000u);
+}
+__device__ __forceinline__ void unpack2(FP16, uint32_t u, float& lo, float& hi) {
+  f16x2_t h = __builtin_bit_cast(f16x2_t, u);
+  lo = (float)h.x;
+  hi = (float)h.y;
+}
+
+template <typename E>
+__device__ __forceinline__ void unpack8(uint4 v, float* f) {
+  unpack2(E{}, v.x, f[0], f[1]);
+  unpack2(E{}, v.y, f[2], f[3]);
+  unpack2(E{}, v.z, f[4], f[5]);
+  unpack2(E{}, v.w, f[6], f[7]);
+}
+
+// fp32 -> 16-bit float, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint32_t pack1(BF16, float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ uint32_t pack1(FP16, float f) {
+  _Float16 h = (_Float16)f;
+  return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+template <typename E>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return pack1(E{}, lo) | (pack1(E{}, hi) << 16);
+}
+template <typename E>
+__device__ __forceinline__ uint4 pack8(const float* f) {
+  return make_uint4(pack2<E>(f[0], f[1]), pack2<E>(f[2], f[3]), pack2<E>(f[4], f[5]),
+                    pack2<E>(f[6], f[7]));
+}
+
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float flog2(float x) { return __builtin_amdgcn_logf(x); }
+
+// DPP lane exchange within a 16-lane row (gfx9 encodings).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <- lane 7-i within 8 lanes
+constexpr int kDppMirror = 0x140;     // lane i <- lane 15-i within 16 lanes
+
+// Sum over aligned groups of N consecutive lanes (N in {1,2,4,8,16}); every lane of the
+// group receives the total.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (N >= 2) x += dpp<kDppXor1>(x);
+  if constexpr (N >= 4) x += dpp<kDppXor2>(x);
+  if constexpr (N >= 8) x += dpp<kDppHalfMirror>(x);
+  if constexpr (N >= 16) x += dpp<kDppMirror>(x);
+  return x;
+}
+
+}  // namespace gw

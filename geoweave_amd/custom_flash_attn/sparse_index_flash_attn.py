@@ -1,0 +1,265 @@
+"""Sparse-index flash attention on gfx950: the drop-in for the reference module
+``easyvolcap/utils/custom_flash_attn/sparse_index_flash_attn.py``.
+
+Names, argument meaning and return values follow the reference API (``:3108-3456``):
+
+* ``sparse_index_flash_attn_func(q, k, v, kv_positions, bias=None, causal=False,
+  softmax_scale=None) -> (o, attn_sum)`` with autograd (reference ``:3196-3286``);
+* ``sparse_index_flash_attn_inference_func(..., return_attn=False)`` (``:3138-3163``);
+* the ``[B, H, T, D]`` twins ``sparse_index_flash_attn_bhtd_func`` (``:3289-3370``) and
+  ``sparse_index_flash_attn_inference_bhtd_func`` (``:3166-3193``);
+* ``dense_index_flash_attn_func`` over broadcast dense positions (``:3108-3135``).
+
+q: ``[B, T, H, D]``, k/v: ``[B, S, H, D]`` (bthd), kv_positions: int32 ``[B, T, K]``
+shared by all heads; entries outside ``[0, S)`` are masked. Preconditions are the
+reference's (``:2013-2039``): fp16/bf16 inputs of one dtype, CUDA(HIP) tensors, int32
+positions of shape ``(B, T, K)``; this build supports head dims 64 and 128 (the
+reference: any d <= 128). ``bias`` and ``causal=True`` are rejected, as the reference's
+forward kernel asserts (``:199``, ``:203``).
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from .. import _lib
+
+__all__ = [
+    "sparse_index_flash_attn_func",
+    "sparse_index_flash_attn_inference_func",
+    "sparse_index_flash_attn_bhtd_func",
+    "sparse_index_flash_attn_inference_bhtd_func",
+    "dense_index_flash_attn_func",
+    "SparseIndexFlashAttnFunc",
+    "SparseIndexFlashAttnBhtdFunc",
+]
+
+
+def _bthd_strides(x: torch.Tensor, layout: str):
+    """(stride_b, stride_t, stride_h) of a 4-D tensor in the given logical layout."""
+    if layout == "bthd":
+        return x.stride(0), x.stride(1), x.stride(2)
+    return x.stride(0), x.stride(2), x.stride(1)
+
+
+def _dims(q, k, layout: str):
+    if layout == "bthd":
+        batch, seqlen_q, nheads, d = q.shape
+        seqlen_k = k.shape[1]
+    elif layout == "bhtd":
+        batch, nheads, seqlen_q, d = q.shape
+        seqlen_k = k.shape[2]
+    else:
+        raise ValueError(f"Unsupported q_layout: {layout}")
+    return batch, seqlen_q, seqlen_k, nheads, d
+
+
+def _check_inputs(q, k, v, kv_positions, bias, causal, layout):
+    batch, seqlen_q, seqlen_k, nheads, d = _dims(q, k, layout)
+    if layout == "bthd":
+        exp_kv = (batch, seqlen_k, nheads, d)
+    else:
+        exp_kv = (batch, nheads, seqlen_k, d)
+    if tuple(k.shape) != exp_kv or tuple(v.shape) != exp_kv:
+        raise ValueError(f"k/v shapes {tuple(k.shape)}/{tuple(v.shape)} do not match {exp_kv}")
+    if d > 128:
+        raise ValueError("FlashAttention only support head dimensions up to 128")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("All tensors must have the same type")
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError("Only support fp16 and bf16")
+    if not (q.is_cuda and k.is_cuda and v.is_cuda and kv_positions.is_cuda):
+        raise ValueError("q, k, v and kv_positions must be GPU tensors")
+    if kv_positions.dtype != torch.int32:
+        raise TypeError("kv_positions must be int32")
+    if kv_positions.dim() != 3 or tuple(kv_positions.shape[:2]) != (batch, seqlen_q):
+        raise ValueError(
+            f"kv_positions shape {tuple(kv_positions.shape)} must be (B, T, K) = ({batch}, {seqlen_q}, K)"
+        )
+    if bias is not None:
+        raise NotImplementedError("attention bias is not supported by the sparse forward kernel")
+    if causal:
+        raise NotImplementedError("causal sparse-index attention is not supported")
+    if d not in (64, 128):
+        raise NotImplementedError(f"head dim {d} is not built (supported: 64, 128)")
+    return batch, seqlen_q, seqlen_k, nheads, d
+
+
+def _prep(x: torch.Tensor) -> torch.Tensor:
+    # Last dim contiguous and 16-byte aligned b/t/h strides (reference :3207-3209 makes
+    # the last dim contiguous; the gfx950 kernel also needs 16-byte rows).
+    if x.stride(-1) != 1 or any(s % 8 for s in x.stride()[:-1]) or x.data_ptr() % 16:
+        x = x.contiguous()
+    return x
+
+
+def _flash_attn_forward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    kv_positions: torch.Tensor,
+    bias=None,
+    causal: bool = False,
+    softmax_scale: Optional[float] = None,
+    return_attn: bool = True,
+    q_layout: str = "bthd",
+):
+    """Returns (o, attn_sum | None, lse [B,T,H] fp32, softmax_scale).
+
+    o has q's shape and dtype and is contiguous (reference :2064-2067); attn_sum is fp32
+    ``[B, T, K]`` (reference :2070-2075)."""
+    batch, seqlen_q, seqlen_k, nheads, d = _check_inputs(q, k, v, kv_positions, bias, causal, q_layout)
+    q, k, v = _prep(q), _prep(k), _prep(v)
+    if kv_positions.stride(-1) != 1:
+        kv_positions = kv_positions.contiguous()
+    num_kv = kv_positions.shape[-1]
+    softmax_scale = softmax_scale or 1.0 / math.sqrt(d)
+    o = torch.empty(q.shape, device=q.device, dtype=q.dtype)
+    lse = torch.empty((batch, seqlen_q, nheads), device=q.device, dtype=torch.float32)
+    attn_sum = None
+    ws = None
+    ws_bytes = 0
+    if return_attn:
+        attn_sum = torch.empty((batch, seqlen_q, num_kv), device=q.device, dtype=torch.float32)
+        lib = _lib.load()
+        ws_bytes = int(lib.gw_sparse_attn_fwd_workspace_size(batch, seqlen_q, nheads, num_kv, 1))
+        ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
+    if batch == 0 or seqlen_q == 0 or num_kv == 0:
+        if attn_sum is not None:
+            attn_sum.zero_()
+        o.zero_()
+        lse.fill_(-math.inf)
+        return o, attn_sum, lse, softmax_scale
+    lib = _lib.load()
+    rc = lib.gw_sparse_attn_fwd(
+        _lib.dtype_code(q.dtype),
+        q.data_ptr(), _lib.strides3(*_bthd_strides(q, q_layout)),
+        k.data_ptr(), _lib.strides3(*_bthd_strides(k, q_layout)),
+        v.data_ptr(), _lib.strides3(*_bthd_strides(v, q_layout)),
+        kv_positions.data_ptr(), kv_positions.stride(0), kv_positions.stride(1),
+        o.data_ptr(), _lib.strides3(*_bthd_strides(o, q_layout)),
+        lse.data_ptr(), _lib.ptr(attn_sum),
+        batch, seqlen_q, seqlen_k, nheads, d, num_kv,
+        float(softmax_scale),
+        _lib.ptr(ws), ws_bytes,
+        _lib.stream_handle(q.device),
+    )
+    _lib.check(rc, "gw_sparse_attn_fwd")
+    return o, attn_sum, lse, softmax_scale
+
+
+def _flash_attn_backward(do, q, k, v, kv_positions, o, lse, dattn_sum, softmax_scale, q_layout):
+    from . import _backward
+
+    return _backward.sparse_attn_backward(do, q, k, v, kv_positions, o, lse, dattn_sum, softmax_scale, q_layout)
+
+
+class SparseIndexFlashAttnFunc(torch.autograd.Function):
+    """Autograd wrapper of the bthd kernel (reference ``:3196-3283``)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, kv_positions, bias=None, causal=False, softmax_scale=None):
+        if kv_positions.stride(-1) != 1:
+            kv_positions = kv_positions.contiguous()
+        o, attn_sum, lse, ctx.softmax_scale = _flash_attn_forward(
+            q, k, v, kv_positions, bias=bias, causal=causal, softmax_scale=softmax_scale,
+            return_attn=True, q_layout="bthd",
+        )
+        ctx.save_for_backward(q, k, v, kv_positions, o, lse)
+        return o, attn_sum
+
+    @staticmethod
+    def backward(ctx, do, dattn_sum):
+        q, k, v, kv_positions, o, lse = ctx.saved_tensors
+        dq, dk, dv = _flash_attn_backward(
+            do, q, k, v, kv_positions, o, lse, dattn_sum, ctx.softmax_scale, "bthd"
+        )
+        return dq, dk, dv, None, None, None, None
+
+
+class SparseIndexFlashAttnBhtdFunc(torch.autograd.Function):
+    """Autograd wrapper of the ``[B, H, T, D]`` layout (reference ``:3289-3367``)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, kv_positions, bias=None, causal=False, softmax_scale=None):
+        if kv_positions.stride(-1) != 1:
+            kv_positions = kv_positions.contiguous()
+        o, attn_sum, lse, ctx.softmax_scale = _flash_attn_forward(
+            q, k, v, kv_positions, bias=bias, causal=causal, softmax_scale=softmax_scale,
+            return_attn=True, q_layout="bhtd",
+        )
+        ctx.save_for_backward(q, k, v, kv_positions, o, lse)
+        return o, attn_sum
+
+    @staticmethod
+    def backward(ctx, do, dattn_sum):
+        q, k, v, kv_positions, o, lse = ctx.saved_tensors
+        dq, dk, dv = _flash_attn_backward(
+            do, q, k, v, kv_positions, o, lse, dattn_sum, ctx.softmax_scale, "bhtd"
+        )
+        return dq, dk, dv, None, None, None, None
+
+
+sparse_index_flash_attn_func = SparseIndexFlashAttnFunc.apply
+sparse_index_flash_attn_bhtd_func = SparseIndexFlashAttnBhtdFunc.apply
+
+
+@torch.inference_mode()
+def sparse_index_flash_attn_inference_func(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    kv_positions: torch.Tensor,
+    bias: Optional[torch.Tensor] = None,
+    causal: bool = False,
+    softmax_scale: Optional[float] = None,
+    return_attn: bool = False,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Inference entry that skips attn_sum unless asked (reference ``:3138-3163``)."""
+    o, attn_sum, _, _ = _flash_attn_forward(
+        q, k, v, kv_positions, bias=bias, causal=causal, softmax_scale=softmax_scale,
+        return_attn=return_attn, q_layout="bthd",
+    )
+    return o, attn_sum
+
+
+@torch.inference_mode()
+def sparse_index_flash_attn_inference_bhtd_func(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    kv_positions: torch.Tensor,
+    bias: Optional[torch.Tensor] = None,
+    causal: bool = False,
+    softmax_scale: Optional[float] = None,
+    return_attn: bool = False,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """``[B, H, T, D]`` inference entry (reference ``:3166-3193``)."""
+    o, attn_sum, _, _ = _flash_attn_forward(
+        q, k, v, kv_positions, bias=bias, causal=causal, softmax_scale=softmax_scale,
+        return_attn=return_attn, q_layout="bhtd",
+    )
+    return o, attn_sum
+
+
+def _build_dense_kv_positions(batch: int, seqlen_q: int, seqlen_k: int, device) -> torch.Tensor:
+    """Broadcast dense positions ``[B, Tq, Tk]`` with O(Tk) storage (reference ``:3108-3118``)."""
+    base = torch.arange(seqlen_k, device=device, dtype=torch.int32)
+    return torch.as_strided(base, size=(batch, seqlen_q, seqlen_k), stride=(0, 0, 1))
+
+
+def dense_index_flash_attn_func(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    bias: Optional[torch.Tensor] = None,
+    causal: bool = False,
+    softmax_scale: Optional[float] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Dense attention through the sparse-index kernel (reference ``:3121-3135``)."""
+    batch, seqlen_q, _, _ = q.shape
+    seqlen_k = k.shape[1]
+    kv_positions = _build_dense_kv_positions(batch, seqlen_q, seqlen_k, q.device)
+    return SparseIndexFlashAttnFunc.apply(q, k, v, kv_positions, bias, causal, softmax_scale)

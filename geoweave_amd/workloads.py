@@ -1,0 +1,129 @@
+"""Seeded synthetic inputs for one sparse global-attention layer.
+
+Shapes follow a VGGT/Pi3 global-attention layer: B images-batches, S views of
+P = 1374 tokens (37 x 37 patches at 518 px / patch 14, plus 5 special tokens), N = S * P
+tokens, 16 attention heads of dim 64 (reference ``easyvolcap/official_vggt/models/
+aggregator.py:66-68``), an indexer of 4 heads x 64 (``geoweave/configs/vggt.json:26,33``)
+and top-k 1024 (``vggt.json:40``).
+
+Recipe (all drawn on the CPU with a ``torch.Generator`` so the GPU and CPU sides see the
+same values): x ~ N(0, 1) ``[B, N, 1024]``; indexer q = x Wq, k = x Wk with
+Wq, Wk ~ N(0, 1/1024) ``[1024, 256]`` (about N(0, 1) per element); w = 1 + x Ww with
+Ww ~ N(0, 0.25/1024) ``[1024, 4]`` (the gate's bias-1 init, ``indexer.py:63-68``, with a
+spread that rarely crosses 0); attention q, k, v ~ N(0, 1). Seed = 20261201 + S, plus b
+for batch element b. Values are rounded once to the compute dtype; the oracle upcasts the
+same rounded values.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+TOKENS_PER_VIEW = 1374
+DIM = 1024
+ATTN_HEADS = 16
+HEAD_DIM = 64
+INDEXER_HEADS = 4
+INDEXER_DIM = 64
+TOPK = 1024
+BASE_SEED = 20261201
+
+
+@dataclass
+class LayerInputs:
+    q_idx: torch.Tensor   # [B, N, Hi, Di]
+    k_idx: torch.Tensor   # [B, N, Hi, Di]
+    w_idx: torch.Tensor   # [B, N, Hi]
+    q: torch.Tensor       # [B, N, H, D]
+    k: torch.Tensor       # [B, N, H, D]
+    v: torch.Tensor       # [B, N, H, D]
+    views: int
+    batch: int
+
+    @property
+    def tokens(self) -> int:
+        return int(self.q.shape[1])
+
+
+def _gen(seed: int) -> torch.Generator:
+    g = torch.Generator(device="cpu")
+    g.manual_seed(int(seed))
+    return g
+
+
+def indexer_inputs(
+    views: int,
+    batch: int = 1,
+    dtype: torch.dtype = torch.bfloat16,
+    tokens: Optional[int] = None,
+    seed: Optional[int] = None,
+):
+    """(q, k, w) of the lightning indexer, CPU tensors in ``dtype``."""
+    n = int(tokens) if tokens is not None else views * TOKENS_PER_VIEW
+    base = BASE_SEED + views if seed is None else int(seed)
+    qs, ks, ws = [], [], []
+    for b in range(batch):
+        g = _gen(base + b)
+        wq = torch.randn(DIM, INDEXER_HEADS * INDEXER_DIM, generator=g) / DIM ** 0.5
+        wk = torch.randn(DIM, INDEXER_HEADS * INDEXER_DIM, generator=g) / DIM ** 0.5
+        ww = torch.randn(DIM, INDEXER_HEADS, generator=g) * (0.5 / DIM ** 0.5)
+        x = torch.randn(n, DIM, generator=g)
+        qs.append((x @ wq).view(n, INDEXER_HEADS, INDEXER_DIM))
+        ks.append((x @ wk).view(n, INDEXER_HEADS, INDEXER_DIM))
+        ws.append(1.0 + x @ ww)
+    return (
+        torch.stack(qs).to(dtype).contiguous(),
+        torch.stack(ks).to(dtype).contiguous(),
+        torch.stack(ws).to(dtype).contiguous(),
+    )
+
+
+def attention_inputs(
+    views: int,
+    batch: int = 1,
+    dtype: torch.dtype = torch.bfloat16,
+    tokens: Optional[int] = None,
+    heads: int = ATTN_HEADS,
+    head_dim: int = HEAD_DIM,
+    seed: Optional[int] = None,
+):
+    """(q, k, v) of the attention, ``[B, N, H, D]`` CPU tensors in ``dtype``."""
+    n = int(tokens) if tokens is not None else views * TOKENS_PER_VIEW
+    base = BASE_SEED + views if seed is None else int(seed)
+    out = []
+    for b in range(batch):
+        g = _gen(base + 7919 + b)
+        out.append(torch.randn(3, n, heads, head_dim, generator=g))
+    qkv = torch.stack(out, dim=1).to(dtype)
+    return qkv[0].contiguous(), qkv[1].contiguous(), qkv[2].contiguous()
+
+
+def random_positions(
+    batch: int,
+    tgt_len: int,
+    src_len: int,
+    topk: int,
+    seed: int,
+    invalid_fraction: float = 0.0,
+) -> torch.Tensor:
+    """int32 ``[B, T, K]`` distinct positions per row (random subsets of [0, S)), with an
+    optional ragged tail of -1 entries like the reference test generator
+    (``tests/sparse_index_flash_attn_tests.py:37-44``)."""
+    g = _gen(seed)
+    kk = min(topk, src_len)
+    scores = torch.rand(batch, tgt_len, src_len, generator=g)
+    pos = scores.topk(kk, dim=-1).indices.to(torch.int32)
+    if invalid_fraction > 0:
+        lengths = (kk * (1.0 - invalid_fraction * torch.rand(batch, tgt_len, generator=g))).long().clamp(min=1)
+        ar = torch.arange(kk).view(1, 1, kk)
+        pos = torch.where(ar < lengths.unsqueeze(-1), pos, torch.full_like(pos, -1))
+    return pos.contiguous()
+
+
+def layer_inputs(views: int, batch: int = 1, dtype: torch.dtype = torch.bfloat16,
+                 tokens: Optional[int] = None) -> LayerInputs:
+    qi, ki, wi = indexer_inputs(views, batch, dtype, tokens)
+    q, k, v = attention_inputs(views, batch, dtype, tokens)
+    return LayerInputs(qi, ki, wi, q, k, v, views, batch)

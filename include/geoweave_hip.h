@@ -1,0 +1,86 @@
+/*
+ * geoweave_hip.h - C ABI of the MI355X (gfx950) sparse global-attention hot path.
+ *
+ * One shared library, libgeoweave_hip.so, exports these entry points. Every argument is
+ * a plain pointer, size or scalar; no framework types cross the boundary.
+ *
+ * Conventions (all entry points):
+ *  - Pointers are device pointers unless stated; outputs and workspaces are allocated by
+ *    the caller (the reference allocates them with torch before each launch:
+ *    easyvolcap/utils/custom_flash_attn/sparse_index_flash_attn.py:2061-2080,
+ *    easyvolcap/utils/custom_indexer/sparse_topk_indexer.py:1288-1297).
+ *  - Strides are in elements; the innermost (head-dim) stride must be 1.
+ *  - `stream` is a hipStream_t (NULL = default stream). Work is only enqueued on it; no
+ *    entry point synchronises the host.
+ *  - Return value: GW_OK or an error code; gw_last_error() then gives a message for the
+ *    calling thread. The Python binding turns a non-zero code into RuntimeError, as the
+ *    reference's TORCH_CHECK does (custom_indexer/csrc/topk_exact.cpp:12-35).
+ *  - dtype: GW_DTYPE_BF16 or GW_DTYPE_FP16 for q/k/v/w (the reference accepts only
+ *    fp16/bf16 on its kernel path: sparse_index_flash_attn.py:2036).
+ */
+#ifndef GEOWEAVE_HIP_H
+#define GEOWEAVE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GW_OK 0
+#define GW_ERR_INVALID 1     /* bad shape, stride, pointer or size */
+#define GW_ERR_UNSUPPORTED 2 /* valid request this build does not implement */
+#define GW_ERR_HIP 3         /* a HIP runtime call failed */
+
+#define GW_DTYPE_BF16 0
+#define GW_DTYPE_FP16 1
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* gw_last_error(void);
+
+/* ABI version of this library (major * 100 + minor). */
+int gw_abi_version(void);
+
+/* ------------------------------------------------------------------------------------
+ * Sparse-index attention, forward.
+ *
+ * Replaces _flash_attn_forward + _fwd_kernel + _attn_sum_kernel
+ * (easyvolcap/utils/custom_flash_attn/sparse_index_flash_attn.py:2001-2233, :129-259,
+ * :375-458), i.e. the compute behind sparse_index_flash_attn_func (:3286),
+ * sparse_index_flash_attn_inference_func (:3138-3163) and their bhtd twins
+ * (:3166-3193, :3370).
+ *
+ * For every (b, t, h): over the K candidates j with 0 <= kv_pos[b,t,j] < S,
+ *   p_j = softmax_j(scale * q[b,t,h] . k[b,pos_j,h]),  o[b,t,h] = sum_j p_j v[b,pos_j,h].
+ * Candidates outside [0, S) are masked (sparse_index_flash_attn.py:207-218). A row with
+ * no valid candidate gets o = 0, lse = -inf.
+ *
+ * q/o index (b, t, h, d); k/v index (b, s, h, d); *_strides = {stride_b, stride_t|s,
+ * stride_h}. Both the bthd and the bhtd layouts are expressed through the strides.
+ * kv_pos: int32, element (b,t,j) at b*pos_stride_b + t*pos_stride_t + j.
+ * lse (nullable): fp32 [B, T, H] contiguous, natural-log log-sum-exp of the scaled scores.
+ * attn_sum (nullable): fp32 [B, T, K] contiguous, attn_sum[b,t,j] = sum_h p_j (the
+ *   reference's atomic sum over heads, :375-458; here written once, no atomics).
+ * workspace: gw_sparse_attn_fwd_workspace_size(...) bytes (0 when attn_sum is NULL).
+ * Supported: D in {64, 128}; any H >= 1; K >= 1; dtype bf16/fp16.
+ */
+size_t gw_sparse_attn_fwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K,
+                                         int want_attn_sum);
+int gw_sparse_attn_fwd(int dtype,
+                       const void* q, const int64_t* q_strides,
+                       const void* k, const int64_t* k_strides,
+                       const void* v, const int64_t* v_strides,
+                       const int32_t* kv_pos, int64_t pos_stride_b, int64_t pos_stride_t,
+                       void* o, const int64_t* o_strides,
+                       float* lse, float* attn_sum,
+                       int64_t B, int64_t T, int64_t S, int64_t H, int64_t D, int64_t K,
+                       float softmax_scale,
+                       void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GEOWEAVE_HIP_H */

@@ -1,0 +1,88 @@
+"""CPU checks of the C ABI: the library loads, exports every declared symbol, and rejects
+bad arguments with an error code and message before touching the GPU."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from geoweave_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "geoweave_hip.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gw_\w+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    declared = _declared_functions()
+    assert declared, "no gw_* functions found in the header"
+    assert sorted(_lib.exported_names()) == declared
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.gw_abi_version() == 100
+
+
+def test_one_hip_runtime_in_process():
+    _lib.load()
+    maps = Path("/proc/self/maps").read_text().splitlines()
+    runtimes = {line.split()[-1] for line in maps if "libamdhip64" in line}
+    assert len(runtimes) == 1, runtimes
+
+
+def _attn_call(**over):
+    lib = _lib.load()
+    s = _lib.strides3(1024, 1024, 64)
+    args = dict(dtype=0, q=16, k=16, v=16, pos=16, o=16, lse=None, attn=None,
+                B=1, T=4, S=4, H=16, D=64, K=4, scale=0.125, ws=None, ws_bytes=0)
+    args.update(over)
+    return lib.gw_sparse_attn_fwd(
+        args["dtype"], args["q"], s, args["k"], s, args["v"], s, args["pos"], 16, 4,
+        args["o"], s, args["lse"], args["attn"], args["B"], args["T"], args["S"], args["H"],
+        args["D"], args["K"], args["scale"], args["ws"], args["ws_bytes"], None)
+
+
+def test_attn_fwd_rejects_bad_arguments_without_gpu():
+    lib = _lib.load()
+    assert _attn_call(dtype=7) == 1
+    assert b"dtype" in lib.gw_last_error()
+    assert _attn_call(D=32) == 2  # unsupported head dim
+    assert b"head dim" in lib.gw_last_error()
+    assert _attn_call(q=None) == 1
+    assert _attn_call(q=18) == 1  # misaligned
+    assert b"aligned" in lib.gw_last_error()
+    assert _attn_call(attn=16) == 1  # attn_sum without workspace
+    assert b"workspace" in lib.gw_last_error()
+    assert _attn_call(B=0) == 0  # empty batch is a no-op
+    assert lib.gw_sparse_attn_fwd_workspace_size(1, 10, 16, 8, 1) == 10 * 8 * 16 * 4
+    assert lib.gw_sparse_attn_fwd_workspace_size(1, 10, 16, 8, 0) == 0
+
+
+def test_check_raises_runtime_error_with_message():
+    lib = _lib.load()
+    rc = _attn_call(dtype=9)
+    with pytest.raises(RuntimeError, match="dtype"):
+        _lib.check(rc, "gw_sparse_attn_fwd")
+
+
+def test_python_preconditions_match_reference_errors():
+    from geoweave_amd.custom_flash_attn import sparse_index_flash_attn as m
+
+    q = torch.zeros(1, 4, 2, 64, dtype=torch.float32)
+    pos = torch.zeros(1, 4, 3, dtype=torch.int32)
+    with pytest.raises(TypeError, match="fp16 and bf16"):
+        m._flash_attn_forward(q, q, q, pos)
+    qb = q.bfloat16()
+    with pytest.raises(ValueError, match="head dimensions up to 128"):
+        big = torch.zeros(1, 4, 2, 192, dtype=torch.bfloat16)
+        m._flash_attn_forward(big, big, big, pos)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        m._flash_attn_forward(qb, qb, qb, pos)

@@ -1,0 +1,238 @@
+"""Pins the CPU oracle (oracle/) against fixtures, brute force, closed forms and invariants.
+
+CPU only. Each check is chosen so that a plausible slip in the oracle (a dropped term, a
+wrong sign, a transposed operand, a head/key index mix-up) fails at least one of them.
+"""
+import json
+import math
+from pathlib import Path
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention as oatt
+from oracle import indexer as oidx
+from oracle.topk_check import check_topk_rows
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _t(x, dtype=torch.float32):
+    return torch.tensor(x, dtype=dtype)
+
+
+# ----------------------------------------------------------------------------- indexer
+
+
+@pytest.mark.parametrize("case", json.loads((GOLDEN / "indexer_kat.json").read_text()), ids=lambda c: c["name"])
+def test_indexer_scores_and_topk_match_golden(case):
+    q = _t(case["q"]).unsqueeze(0)
+    k = _t(case["k"]).unsqueeze(0)
+    w = _t(case["w"]).unsqueeze(0)
+    mask = None if case["mask"] is None else _t(case["mask"]).unsqueeze(0)
+    sc = oidx.indexer_scores(q, k, w, mask, case["scale"])
+    torch.testing.assert_close(sc[0], _t(case["scores"]), atol=1e-6, rtol=1e-6)
+    idx, val = oidx.indexer_topk(q, k, w, mask, case["topk"], case["scale"])
+    got = sorted(idx[0].sort(-1).values.tolist())
+    assert [sorted(r) for r in idx[0].tolist()] == case["expected_sets"], got
+    torch.testing.assert_close(val, sc.gather(-1, idx.long()))
+
+
+def test_indexer_scores_closed_form_single_head_unit_gate():
+    # Hi = 1, w = 1  =>  score = relu(scale * q k^T)
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(2, 9, 1, 16, generator=g)
+    k = torch.randn(2, 11, 1, 16, generator=g)
+    w = torch.ones(2, 11, 1)
+    sc = oidx.indexer_scores(q, k, w, None, 0.25)
+    ref = torch.relu(0.25 * torch.einsum("btd,bsd->bts", q[:, :, 0], k[:, :, 0]))
+    torch.testing.assert_close(sc, ref, atol=1e-6, rtol=1e-6)
+
+
+def test_indexer_scores_orthogonal_query_is_zero_and_heads_use_key_gate():
+    q = torch.zeros(1, 1, 2, 4)
+    q[0, 0, 0, 0] = 1.0  # head 0 looks at dim 0; head 1 is zero
+    k = torch.zeros(1, 3, 2, 4)
+    k[0, 0, 0, 1] = 5.0  # orthogonal to q -> 0
+    k[0, 1, 0, 0] = 2.0  # z = 2 on head 0
+    k[0, 2, 1, 0] = 7.0  # only head 1, where q is 0 -> 0
+    w = torch.tensor([[[3.0, 100.0], [-1.5, 100.0], [9.0, 100.0]]])
+    sc = oidx.indexer_scores(q, k, w, None, 1.0)
+    # key 1: w[1, head0] * relu(2) = -3 (the gate is indexed by the KEY token)
+    torch.testing.assert_close(sc[0, 0], torch.tensor([0.0, -3.0, 0.0]))
+
+
+def test_indexer_scores_brute_force_random():
+    g = torch.Generator().manual_seed(1)
+    B, T, S, H, D = 2, 5, 13, 3, 6
+    q = torch.randn(B, T, H, D, generator=g)
+    k = torch.randn(B, S, H, D, generator=g)
+    w = torch.randn(B, S, H, generator=g)
+    mask = torch.randn(B, T, S, generator=g)
+    sc = oidx.indexer_scores(q, k, w, mask, 0.3, key_chunk=4, query_chunk=2)
+    ref = torch.zeros(B, T, S, dtype=torch.float64)
+    for b in range(B):
+        for t in range(T):
+            for s in range(S):
+                acc = 0.0
+                for h in range(H):
+                    z = sum(float(q[b, t, h, d]) * float(k[b, s, h, d]) for d in range(D))
+                    acc += float(w[b, s, h]) * max(0.3 * z, 0.0)
+                ref[b, t, s] = acc + float(mask[b, t, s])
+    torch.testing.assert_close(sc.double(), ref, atol=1e-5, rtol=1e-5)
+
+
+def test_indexer_topk_matches_full_sort():
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn(1, 40, 4, 8, generator=g)
+    k = torch.randn(1, 300, 4, 8, generator=g)
+    w = 1 + 0.2 * torch.randn(1, 300, 4, generator=g)
+    idx, val = oidx.indexer_topk(q, k, w, None, 37, 0.125, query_chunk=7)
+    sc = oidx.indexer_scores(q, k, w, None, 0.125)
+    order = sc.argsort(dim=-1, descending=True)[..., :37]
+    assert torch.equal(idx.long().sort(-1).values, order.sort(-1).values)
+    torch.testing.assert_close(val, sc.gather(-1, idx.long()))
+    sel = oidx.selected_scores(q, k, w, idx, 0.125)
+    torch.testing.assert_close(sel, val, atol=1e-5, rtol=1e-5)
+
+
+def test_indexer_topk_caps_k_at_source_length():
+    q = torch.randn(1, 3, 1, 4)
+    k = torch.randn(1, 5, 1, 4)
+    w = torch.ones(1, 5, 1)
+    idx, _ = oidx.indexer_topk(q, k, w, None, 1024, 0.5)
+    assert idx.shape == (1, 3, 5)
+    assert all(sorted(r) == list(range(5)) for r in idx[0].tolist())
+
+
+def test_indexer_bwd_matches_autograd_of_torch_path():
+    # The reference's torch backend differentiates scores.gather(-1, topk_indices)
+    # (indexer.py:600-603); the explicit kernel formula must agree with it.
+    g = torch.Generator().manual_seed(3)
+    B, T, S, H, D, K = 2, 6, 20, 4, 8, 5
+    q = torch.randn(B, T, H, D, generator=g, requires_grad=True)
+    k = torch.randn(B, S, H, D, generator=g, requires_grad=True)
+    w = torch.randn(B, S, H, generator=g, requires_grad=True)
+    sc = oidx.indexer_scores(q, k, w, None, 0.125)
+    idx = sc.detach().topk(K, dim=-1).indices
+    gsc = torch.randn(B, T, K, generator=g)
+    sc.gather(-1, idx).backward(gsc)
+    dq, dk, dw = oidx.indexer_topk_bwd(q.detach(), k.detach(), w.detach(), idx.int(), gsc, 0.125)
+    torch.testing.assert_close(dq, q.grad, atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(dk, k.grad, atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(dw, w.grad, atol=1e-5, rtol=1e-5)
+
+
+# ----------------------------------------------------------------------------- attention
+
+
+def _fixture():
+    f = json.loads((GOLDEN / "attn_fixture.json").read_text())
+    q = _t(f["q"]).unsqueeze(0)
+    k = _t(f["k"]).unsqueeze(0)
+    v = _t(f["v"]).unsqueeze(0)
+    do = _t(f["do"]).unsqueeze(0)
+    pos = torch.tensor(f["kv_positions"], dtype=torch.int32).unsqueeze(0)
+    dattn = _t(f["dattn"]).unsqueeze(0)
+    return f, q, k, v, do, pos, dattn
+
+
+def test_sparse_attention_matches_golden_bruteforce():
+    f, q, k, v, do, pos, dattn = _fixture()
+    o, asum, lse = oatt.sparse_attention(q, k, v, pos, f["scale"], query_chunk=2)
+    torch.testing.assert_close(o[0], _t(f["o"]), atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(asum[0], _t(f["attn_sum"]), atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(lse[0], _t(f["lse"]), atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("with_dattn", [False, True])
+def test_sparse_attention_bwd_matches_golden_and_autograd(with_dattn):
+    f, q, k, v, do, pos, dattn = _fixture()
+    da = dattn if with_dattn else None
+    o, asum, lse = oatt.sparse_attention(q, k, v, pos, f["scale"])
+    dq, dk, dv = oatt.sparse_attention_bwd(q, k, v, pos, o, lse, do, da, f["scale"], query_chunk=2)
+    aq, ak, av = oatt.sparse_attention_autograd(q, k, v, pos, do, da, f["scale"])
+    torch.testing.assert_close(dq, aq, atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(dk, ak, atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(dv, av, atol=1e-5, rtol=1e-5)
+    if with_dattn:
+        torch.testing.assert_close(dq[0], _t(f["dq"]), atol=1e-5, rtol=1e-5)
+        torch.testing.assert_close(dk[0], _t(f["dk"]), atol=1e-5, rtol=1e-5)
+        torch.testing.assert_close(dv[0], _t(f["dv"]), atol=1e-5, rtol=1e-5)
+
+
+def test_sparse_attention_dense_positions_equal_sdpa():
+    g = torch.Generator().manual_seed(4)
+    B, T, H, D = 2, 17, 3, 8
+    q = torch.randn(B, T, H, D, generator=g)
+    k = torch.randn(B, T, H, D, generator=g)
+    v = torch.randn(B, T, H, D, generator=g)
+    pos = torch.arange(T, dtype=torch.int32).view(1, 1, T).expand(B, T, T).contiguous()
+    o, asum, lse = oatt.sparse_attention(q, k, v, pos, None, query_chunk=5)
+    ref = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)).transpose(1, 2)
+    torch.testing.assert_close(o, ref, atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(asum.sum(-1), torch.full((B, T), float(H)), atol=1e-5, rtol=1e-5)
+    s = torch.einsum("bthd,bshd->bhts", q, k) / math.sqrt(D)
+    torch.testing.assert_close(lse, torch.logsumexp(s, -1).transpose(1, 2), atol=1e-5, rtol=1e-5)
+
+
+def test_sparse_attention_row_permutation_invariance():
+    g = torch.Generator().manual_seed(5)
+    B, T, S, H, D, K = 1, 6, 30, 2, 8, 9
+    q, k, v = (torch.randn(B, n, H, D, generator=g) for n in (T, S, S))
+    pos = torch.stack([torch.randperm(S, generator=g)[:K] for _ in range(T)]).int().unsqueeze(0)
+    perm = torch.randperm(K, generator=g)
+    o1, a1, _ = oatt.sparse_attention(q, k, v, pos)
+    o2, a2, _ = oatt.sparse_attention(q, k, v, pos[..., perm].contiguous())
+    torch.testing.assert_close(o1, o2, atol=1e-6, rtol=1e-6)
+    torch.testing.assert_close(a1[..., perm], a2, atol=1e-6, rtol=1e-6)
+
+
+def test_sparse_attention_invalid_rows_and_bwd_invariants():
+    g = torch.Generator().manual_seed(6)
+    B, T, S, H, D, K = 1, 8, 25, 2, 4, 6
+    q, k, v = (torch.randn(B, n, H, D, generator=g) for n in (T, S, S))
+    pos = torch.stack([torch.randperm(S, generator=g)[:K] for _ in range(T)]).int().unsqueeze(0)
+    bad = pos.clone()
+    bad[0, 1, 3:] = -1
+    bad[0, 2, :] = -1  # no valid candidate at all
+    bad[0, 3, 0] = S   # past the end is masked too
+    o, asum, lse = oatt.sparse_attention(q, k, v, bad)
+    assert torch.all(o[0, 2] == 0) and torch.all(asum[0, 2] == 0) and torch.isinf(lse[0, 2]).all()
+    assert asum[0, 1, 3:].abs().max() == 0 and asum[0, 3, 0] == 0
+    do = torch.randn(B, T, H, D, generator=g)
+    # Exact invariants for all-valid rows and no dattn: sum_s dK = 0, sum_s dV = sum_t dO.
+    o, asum, lse = oatt.sparse_attention(q, k, v, pos)
+    dq, dk, dv = oatt.sparse_attention_bwd(q, k, v, pos, o, lse, do)
+    torch.testing.assert_close(dk.sum(1), torch.zeros(B, H, D), atol=1e-5, rtol=0)
+    torch.testing.assert_close(dv.sum(1), do.sum(1), atol=1e-5, rtol=1e-5)
+
+
+# ----------------------------------------------------------------------------- top-k checker
+
+
+def test_topk_checker_accepts_ties_and_rejects_planted_mistakes():
+    g = torch.Generator().manual_seed(7)
+    rows, S, K = 4, 50, 10
+    sc = torch.randn(rows, S, generator=g)
+    # plant an exact tie at the k-th place of row 0
+    srt = sc[0].sort(descending=True)
+    sc[0, srt.indices[K]] = srt.values[K - 1]
+    ref = sc.topk(K, dim=-1).indices
+    assert check_topk_rows(sc, ref, K).ok
+    swapped = ref.clone()
+    pos_kth = (ref[0] == srt.indices[K - 1]).nonzero()
+    if pos_kth.numel():
+        swapped[0, pos_kth[0, 0]] = srt.indices[K]
+        rep = check_topk_rows(sc, swapped, K)
+        assert rep.ok and rep.rows_tie_swapped >= 1
+    wrong = ref.clone()
+    wrong[1, 0] = sc[1].argmin()
+    assert not check_topk_rows(sc, wrong, K).ok
+    dup = ref.clone()
+    dup[2, 1] = dup[2, 0]
+    assert not check_topk_rows(sc, dup, K).ok
+    oob = ref.clone()
+    oob[3, 0] = -1
+    assert not check_topk_rows(sc, oob, K).ok
