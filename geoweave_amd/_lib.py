@@ -33,6 +33,12 @@ _SIGNATURES = {
         [ctypes.c_int, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64, _i64, _p, _i64p, _p, _p,
          _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p, _sz, _p],
     ),
+    "gw_indexer_topk_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
+    "gw_indexer_topk_fwd": (
+        ctypes.c_int,
+        [ctypes.c_int, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,
+         ctypes.c_int, _p, _p, _p, _sz, _p],
+    ),
 }
 
 _lock = threading.Lock()

@@ -79,6 +79,43 @@ int gw_sparse_attn_fwd(int dtype,
                        void* workspace, size_t workspace_bytes,
                        void* stream);
 
+/* ------------------------------------------------------------------------------------
+ * Lightning-indexer score + exact top-k, forward.
+ *
+ * Replaces SparseTopkIndexerFunc.forward -> _blockwise_topk_scores(_impl)
+ * (easyvolcap/utils/custom_indexer/sparse_topk_indexer.py:2047-2088, :1779-1844,
+ * :1241-1776) and the opt-in CUDA kernels it can call (custom_indexer/csrc/
+ * score_topk_fused_kernel.cu:53-224, topk_exact_kernel.cu:26-149,
+ * merge_two_topk_kernel.cu:25-142), i.e. the compute behind sparse_topk_indexer_func
+ * (:2188-2253).
+ *
+ *   score[b,t,s] = sum_h w[b,s,h] * relu(softmax_scale * q[b,t,h,:] . k[b,s,h,:])
+ *                  (+ mask[b,t,s] when mask != NULL)
+ * out_indices[b,t,:] (int32) = the Kk = min(topk, S) keys with the largest scores, in
+ * unspecified order (the reference uses sorted=False); out_scores (same dtype as q) = their
+ * scores. Exact: the set equals the fp32 top-k except where scores tie within rounding;
+ * ties are broken deterministically. Scores are accumulated in fp32.
+ *
+ * q: [B,T,Hi,Di], k: [B,S,Hi,Di], w: [B,S,Hi], mask: [B,T,S], all contiguous, same dtype.
+ * Supported: Di = 64, Hi in {1,2,4,8}, topk <= 2048, softmax_scale > 0.
+ * workspace: gw_indexer_topk_workspace_size(B, T, S, topk) bytes, 16-byte aligned.
+ * flags: 0 normally. Test hooks that force the exact brute-force path:
+ *   GW_TOPK_FLAG_TAU_PLUS_INF  - no key passes the candidate filter (every query falls
+ *                                back to the brute-force path);
+ *   GW_TOPK_FLAG_TAU_MINUS_INF - every key passes (candidate lists overflow when a key
+ *                                split exceeds its capacity).
+ */
+#define GW_TOPK_FLAG_TAU_PLUS_INF 1
+#define GW_TOPK_FLAG_TAU_MINUS_INF 2
+
+size_t gw_indexer_topk_workspace_size(int64_t B, int64_t T, int64_t S, int64_t topk);
+int gw_indexer_topk_fwd(int dtype, const void* q, const void* k, const void* w, const void* mask,
+                        int64_t B, int64_t T, int64_t S, int64_t Hi, int64_t Di, int64_t topk,
+                        float softmax_scale, int flags,
+                        int32_t* out_indices, void* out_scores,
+                        void* workspace, size_t workspace_bytes,
+                        void* stream);
+
 #ifdef __cplusplus
 }
 #endif
