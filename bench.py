@@ -1,0 +1,265 @@
+#!/usr/bin/env python3
+"""Benchmark of the sparse global-attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--views 32] [--no-cpu-baseline]
+
+One step = one pass of the hot path over one layer of synthetic input, with every input
+already resident in HBM: the fused lightning-indexer score + exact top-k
+(``sparse_topk_indexer_inference_func``), then the sparse-index attention forward over the
+selected positions (``sparse_index_flash_attn_inference_func``, no ``attn_sum``). This is
+the inference path of one VGGT/Pi3 global-attention layer. The workload is BASELINE
+config "Metric row": B = 1, S = 32 views x 1374 tokens (N = 43,968), 16 heads x 64,
+indexer 4 heads x 64, top-k 1024, bf16.
+
+Printed: ONE JSON line. ``value`` = indexer ms + attention-forward ms per layer (lower is
+better), ``roofline`` = the attention forward (the dominant kernel) against the HBM
+roofline on its algorithmic gathered K/V bytes, timed live with HIP events on the stream
+the kernel runs on, ``roofline_indexer`` = the indexer against the bf16 MFMA roofline,
+``cpu_baseline`` = the fp32 CPU oracle (the restatement of the reference's torch backend)
+on a bounded sample of query rows of the same layer, scaled to the full layer.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+if str(REPO) not in sys.path:
+    sys.path.insert(0, str(REPO))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
+METRIC = "sparse global-attn layer fwd ms + indexer top-k ms at S=32 views, k=1024 (1 GPU)"
+
+
+def attn_fwd_algorithmic_bytes(B, T, H, D, K, elt=2):
+    """Gathered K and V rows (K per query, shared by the H heads) + q read + o write +
+    int32 positions: B*T*K*H*D*2*elt + 2*B*T*H*D*elt + 4*B*T*K."""
+    return B * T * K * H * D * 2 * elt + 2 * B * T * H * D * elt + 4 * B * T * K
+
+
+def indexer_algorithmic_flops(B, T, S, Hi, Di):
+    """2 * B * T * S * Hi * Di (the q k^T products over all indexer heads)."""
+    return 2 * B * T * S * Hi * Di
+
+
+def read_traffic_summary(path: Path):
+    """HBM bytes per launch of the attention forward, from the committed rocprofv3 PMC
+    summary (a line ``traffic_bytes_per_launch: <int>``), or None."""
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.strip().startswith("traffic_bytes_per_launch:"):
+            try:
+                return int(float(line.split(":", 1)[1].strip()))
+            except ValueError:
+                return None
+    return None
+
+
+def cpu_baseline(views: int, budget_s: float, rows_per_chunk: int = 128):
+    """Times the fp32 CPU oracle (indexer scores + top-k + sparse attention) on query
+    rows of the same layer until ``budget_s`` seconds have elapsed; scales to all rows."""
+    import torch
+
+    from geoweave_amd import workloads
+    from oracle import attention as oatt
+    from oracle import indexer as oidx
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    qi, ki, wi = workloads.indexer_inputs(views, 1, torch.bfloat16)
+    q, k, v = workloads.attention_inputs(views, 1, torch.bfloat16)
+    qi, ki, wi, q, k, v = (x.float() for x in (qi, ki, wi, q, k, v))
+    n = q.shape[1]
+    g = torch.Generator().manual_seed(0)
+    order = torch.randperm(n, generator=g)
+    done = 0
+    t_idx = t_att = 0.0
+    while done < n and (t_idx + t_att) < budget_s:
+        rows = order[done:done + rows_per_chunk]
+        t0 = time.perf_counter()
+        idx, _ = oidx.indexer_topk(qi[:, rows], ki, wi, None, 1024, 0.125)
+        t1 = time.perf_counter()
+        oatt.sparse_attention(q[:, rows], k, v, idx, 0.125)
+        t2 = time.perf_counter()
+        t_idx += t1 - t0
+        t_att += t2 - t1
+        done += rows.numel()
+    scale = n / done
+    total_ms = (t_idx + t_att) * scale * 1e3
+    return {
+        "value": round(total_ms, 1),
+        "unit": "ms",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"fp32 CPU oracle (indexer scores + torch.topk + gathered sparse attention) on "
+                   f"{done} random query rows of the S={views} layer against all {n} keys, "
+                   f"{t_idx + t_att:.1f} s, scaled x{scale:.1f} to all rows"),
+        "indexer_ms": round(t_idx * scale * 1e3, 1),
+        "attn_fwd_ms": round(t_att * scale * 1e3, 1),
+        "cpu_model": platform.processor() or platform.machine(),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--views", type=int, default=32)
+    ap.add_argument("--topk", type=int, default=1024)
+    ap.add_argument("--cpu-budget-s", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--with-attn-sum", action="store_true",
+                    help="also time the training forward that writes attn_sum")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the sparse global-attention path is benchmarked "
+              "per GPU (queries shard across GPUs with one all-gather of K/V per layer, which "
+              "this build does not launch). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from geoweave_amd import workloads
+    from geoweave_amd.custom_flash_attn.sparse_index_flash_attn import (
+        sparse_index_flash_attn_inference_func,
+    )
+    from geoweave_amd.custom_indexer import sparse_topk_indexer_inference_func
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (MI355X)", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda", 0)
+    props = torch.cuda.get_device_properties(dev)
+
+    views, topk = args.views, args.topk
+    print(f"[bench] generating S={views} inputs", file=sys.stderr, flush=True)
+    lay = workloads.layer_inputs(views, 1, torch.bfloat16)
+    qi, ki, wi = (x.to(dev) for x in (lay.q_idx, lay.k_idx, lay.w_idx))
+    q, k, v = (x.to(dev) for x in (lay.q, lay.k, lay.v))
+    B, T, H, D = q.shape
+    Hi, Di = qi.shape[2], qi.shape[3]
+    empty_mask = qi.new_empty(0)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream(dev)
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record(stream)
+        idx, _ = sparse_topk_indexer_inference_func(qi, ki, wi, empty_mask, topk, 0.125, 256, 0,
+                                                    return_scores=True)
+        if ev is not None:
+            ev[1].record(stream)
+        o, _ = sparse_index_flash_attn_inference_func(q, k, v, idx, softmax_scale=0.125)
+        if ev is not None:
+            ev[2].record(stream)
+        return idx, o
+
+    print("[bench] warmup", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for i in range(args.steps):
+        idx, o = step(evs[i])
+    end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    idx_ms = [e[0].elapsed_time(e[1]) for e in evs]
+    att_ms = [e[1].elapsed_time(e[2]) for e in evs]
+    print(f"[bench] timed {args.steps} steps: {total_ms / args.steps:.3f} ms/step", file=sys.stderr, flush=True)
+
+    Kk = idx.shape[-1]
+    att_bytes = attn_fwd_algorithmic_bytes(B, T, H, D, Kk)
+    idx_flops = indexer_algorithmic_flops(B, T, T, Hi, Di)
+    att_avg = statistics.mean(att_ms)
+    idx_avg = statistics.mean(idx_ms)
+    att_gbs = att_bytes / (att_avg * 1e-3) / 1e9
+    idx_tflops = idx_flops / (idx_avg * 1e-3) / 1e12
+    traffic = read_traffic_summary(REPO / "profiles" / f"sparse_attn_fwd_S{views}_pmc.md")
+
+    extra = {}
+    if args.with_attn_sum:
+        from geoweave_amd.custom_flash_attn.sparse_index_flash_attn import _flash_attn_forward
+
+        for _ in range(2):
+            _flash_attn_forward(q, k, v, idx, softmax_scale=0.125, return_attn=True)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(5):
+            _flash_attn_forward(q, k, v, idx, softmax_scale=0.125, return_attn=True)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        extra["attn_fwd_with_attn_sum_ms"] = round(e0.elapsed_time(e1) / 5, 3)
+
+    result = {
+        "metric": METRIC,
+        "value": round(total_ms / args.steps, 3),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(total_ms / args.steps, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) attention q/k/v; indexer q/k/w from random projections)",
+        "config": {
+            "workload": f"one sparse global-attention layer fwd: indexer score + exact top-{topk} "
+                        f"then sparse-index attention over the selected keys",
+            "batch": B, "views": views, "tokens": T, "heads": H, "head_dim": D,
+            "indexer_heads": Hi, "indexer_dim": Di, "topk": Kk,
+        },
+        "indexer_ms": round(idx_avg, 3),
+        "attn_fwd_ms": round(att_avg, 3),
+        "roofline": {
+            "kernel": "sparse_attn_fwd_kernel",
+            "bound": "hbm",
+            "achieved": round(att_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(att_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes": att_bytes,
+        },
+        "roofline_indexer": {
+            "kernels": "indexer_score_kernel<sample>+select<tau>+score<filter>+select<final>+fallback",
+            "bound": "mfma",
+            "achieved": round(idx_tflops, 2),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(idx_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "algorithmic_flops": idx_flops,
+        },
+        "device": {"name": torch.cuda.get_device_name(dev), "arch": props.gcnArchName,
+                   "cus": props.multi_processor_count},
+        "timing": "HIP events on the launch stream; steady state, caches not flushed",
+    }
+    result.update(extra)
+    if not args.no_cpu_baseline:
+        del lay
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(views, args.cpu_budget_s)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
