@@ -39,6 +39,21 @@ _SIGNATURES = {
         [ctypes.c_int, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,
          ctypes.c_int, _p, _p, _p, _sz, _p],
     ),
+    "gw_kv_csr_size": (_sz, [_i64, _i64, _i64, _i64]),
+    "gw_kv_csr_build": (ctypes.c_int, [_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _sz, _p]),
+    "gw_sparse_attn_bwd_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
+    "gw_sparse_attn_bwd": (
+        ctypes.c_int,
+        [ctypes.c_int, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64, _i64, _p, _i64p, _p, _i64p,
+         _p, _p, _p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64, _i64,
+         ctypes.c_float, _p, _sz, _p, _sz, _p],
+    ),
+    "gw_indexer_topk_bwd_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
+    "gw_indexer_topk_bwd": (
+        ctypes.c_int,
+        [ctypes.c_int, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
+         ctypes.c_float, _p, _sz, _p, _sz, _p],
+    ),
 }
 
 _lock = threading.Lock()

@@ -116,6 +116,88 @@ int gw_indexer_topk_fwd(int dtype, const void* q, const void* k, const void* w, 
                         void* workspace, size_t workspace_bytes,
                         void* stream);
 
+/* ------------------------------------------------------------------------------------
+ * Key-major (CSR) transpose of a [B, T, K] position table, shared by both backward
+ * passes below (the attention's kv_positions and the indexer's topk_indices are the
+ * same table in a DSA layer, so one build serves both).
+ *
+ * Replaces the reference's key grouping of the opt-in grouped backward (device radix
+ * sort + run-length encoding + scan, custom_flash_attn/csrc/sparse_bwd_grouped_kernel.cu:
+ * 232-269, 432-570), and stands in for the fp32 atomics of the default backward
+ * (sparse_index_flash_attn.py:739-740, sparse_topk_indexer.py:1936-1941).
+ *
+ * pos: int32, element (b,t,j) at b*pos_stride_b + t*pos_stride_t + j. Entries outside
+ * [0, S) are skipped. csr: a caller-allocated buffer of gw_kv_csr_size(B,T,S,K) bytes,
+ * 16-byte aligned, opaque; it stays valid until the buffer is reused. The entries of
+ * each key are sorted by (t, j), so results computed from it are bitwise reproducible.
+ * Work runs on `stream`; no host synchronisation.
+ */
+size_t gw_kv_csr_size(int64_t B, int64_t T, int64_t S, int64_t K);
+int gw_kv_csr_build(const int32_t* pos, int64_t pos_stride_b, int64_t pos_stride_t,
+                    int64_t B, int64_t T, int64_t S, int64_t K,
+                    void* csr, size_t csr_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * Sparse-index attention, backward.
+ *
+ * Replaces _sparse_index_flash_attn_backward -> _bwd_preprocess_do_o_dot +
+ * _bwd_sparse_index_kernel (easyvolcap/utils/custom_flash_attn/sparse_index_flash_attn.py:
+ * 2442-2846, :534-576, :579-743) behind SparseIndexFlashAttnFunc.backward (:3240-3283)
+ * and its bhtd twin, and the opt-in grouped CUDA backward
+ * (custom_flash_attn/csrc/sparse_bwd_grouped_kernel.cu:79-603).
+ *
+ * Inputs are the forward's: q/k/v/o (strides as in gw_sparse_attn_fwd), kv_pos, lse
+ * (fp32 [B,T,H] from gw_sparse_attn_fwd), dout (dO, same dtype, strided like q).
+ * dattn_sum (nullable): gradient of attn_sum, [B,T,K] contiguous in the q dtype (the
+ * reference casts it to q.dtype, :3244-3245). Outputs dq (strided like q), dk, dv
+ * (strided like k, v) in the input dtype, accumulated in fp32 with no atomics; every
+ * element of dk/dv is written (keys never selected get 0). csr: built by
+ * gw_kv_csr_build from the same kv_pos, B, T, S, K. workspace:
+ * gw_sparse_attn_bwd_workspace_size(...) bytes, 16-byte aligned.
+ */
+size_t gw_sparse_attn_bwd_workspace_size(int64_t B, int64_t T, int64_t S, int64_t H, int64_t D,
+                                         int64_t K);
+int gw_sparse_attn_bwd(int dtype,
+                       const void* q, const int64_t* q_strides,
+                       const void* k, const int64_t* k_strides,
+                       const void* v, const int64_t* v_strides,
+                       const int32_t* kv_pos, int64_t pos_stride_b, int64_t pos_stride_t,
+                       const void* o, const int64_t* o_strides,
+                       const void* dout, const int64_t* do_strides,
+                       const float* lse, const void* dattn_sum,
+                       void* dq, const int64_t* dq_strides,
+                       void* dk, const int64_t* dk_strides,
+                       void* dv, const int64_t* dv_strides,
+                       int64_t B, int64_t T, int64_t S, int64_t H, int64_t D, int64_t K,
+                       float softmax_scale,
+                       const void* csr, size_t csr_bytes,
+                       void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * Lightning-indexer top-k, backward.
+ *
+ * Replaces SparseTopkIndexerFunc.backward -> _backward_selected_topk_qkw ->
+ * _indexer_topk_bwd_kernel (easyvolcap/utils/custom_indexer/sparse_topk_indexer.py:
+ * 2091-2106, :757-895, :1847-1944). For every selected (t, j), s = topk_indices[b,t,j],
+ * g = grad_scores[b,t,j], per head h: z = scale * q[t,h].k[s,h];
+ * f = g * w[s,h] * [z > 0] * scale; dq[t,h] += f k[s,h]; dk[s,h] += f q[t,h];
+ * dw[s,h] += g relu(z). q/k/w/grad contiguous in one 16-bit dtype; outputs dq, dk, dw
+ * in that dtype, accumulated in fp32 with no atomics; every element is written.
+ * csr: built by gw_kv_csr_build from topk_indices (strides K*T, K). Supported: Di = 64,
+ * Hi in {1,2,4,8}. workspace: gw_indexer_topk_bwd_workspace_size(...) bytes.
+ */
+size_t gw_indexer_topk_bwd_workspace_size(int64_t B, int64_t T, int64_t S, int64_t Hi, int64_t Di,
+                                          int64_t K);
+int gw_indexer_topk_bwd(int dtype, const void* q, const void* k, const void* w,
+                        const int32_t* topk_indices, const void* grad_scores,
+                        void* dq, void* dk, void* dw,
+                        int64_t B, int64_t T, int64_t S, int64_t Hi, int64_t Di, int64_t K,
+                        float softmax_scale,
+                        const void* csr, size_t csr_bytes,
+                        void* workspace, size_t workspace_bytes,
+                        void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -175,3 +175,54 @@ def sparse_attention_autograd(
         loss = loss + (attn_sum * dattn.float()).sum()
     loss.backward()
     return q.grad, k.grad, v.grad
+
+
+def sparse_attention_bwd_keys(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    kv_positions: torch.Tensor,
+    o: torch.Tensor,
+    lse: torch.Tensor,
+    do: torch.Tensor,
+    keys: torch.Tensor,
+    softmax_scale: Optional[float] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(dk, dv) fp32 ``[B, len(keys), H, D]`` of the given key rows only, with no dattn.
+
+    Same formulas as ``sparse_attention_bwd`` (reference ``sparse_index_flash_attn.py:
+    534-743``) restricted to the (t, j) entries whose position is one of ``keys``: with
+    dattn absent, total = delta = sum_d o*dO depends on the query row alone, so a key's
+    gradient needs only the rows that select it. Used to check full-size layers where the
+    whole oracle backward would take minutes.
+    """
+    q = q.float()
+    k = k.float()
+    v = v.float()
+    o = o.float()
+    do = do.float()
+    bsz, tgt_len, n_heads, head_dim = q.shape
+    src_len = k.shape[1]
+    scale = _scale(head_dim, softmax_scale)
+    keys = keys.long()
+    dk = torch.zeros((bsz, keys.numel(), n_heads, head_dim), dtype=torch.float32)
+    dv = torch.zeros_like(dk)
+    num_kv = kv_positions.shape[-1]
+    for b in range(bsz):
+        flat = kv_positions[b].reshape(-1).long()
+        hit = torch.isin(flat, keys).nonzero().squeeze(1)  # entries that select a key
+        t_all, s_all = hit // num_kv, flat[hit]
+        for ki, s in enumerate(keys.tolist()):
+            t_idx = t_all[s_all == s]  # one entry per (t, j) match
+            if t_idx.numel() == 0 or not (0 <= s < src_len):
+                continue
+            qt = q[b, t_idx]  # [n, H, D]
+            dot = do[b, t_idx]
+            delta = (o[b, t_idx] * dot).sum(-1)  # [n, H]
+            sc = (qt * k[b, s]).sum(-1) * scale
+            p = torch.exp(sc - lse[b, t_idx])
+            dp = (v[b, s] * dot).sum(-1)
+            ds = (dp - delta) * p
+            dk[b, ki] = scale * (ds.unsqueeze(-1) * qt).sum(0)
+            dv[b, ki] = (p.unsqueeze(-1) * dot).sum(0)
+    return dk, dv

@@ -155,3 +155,43 @@ def indexer_topk_bwd(
         dw_contrib = g[b].unsqueeze(-1) * torch.relu(z)  # [T, K, H]
         dw[b].index_add_(0, idx[b].reshape(-1), dw_contrib.reshape(-1, n_heads))
     return dq, dk, dw
+
+
+def indexer_topk_bwd_keys(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    w: torch.Tensor,
+    indices: torch.Tensor,
+    grad_scores: torch.Tensor,
+    keys: torch.Tensor,
+    softmax_scale: Optional[float] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(dk, dw) fp32 of the given key rows only: the formulas of ``indexer_topk_bwd``
+    (reference ``sparse_topk_indexer.py:1847-1944``) restricted to the (t, j) entries that
+    select one of ``keys``. Used to check full-size layers."""
+    q = q.float()
+    k = k.float()
+    w = w.float()
+    g = grad_scores.float()
+    bsz, tgt_len, n_heads, head_dim = q.shape
+    scale = _default_scale(head_dim, softmax_scale)
+    keys = keys.long()
+    dk = torch.zeros((bsz, keys.numel(), n_heads, head_dim), dtype=torch.float32)
+    dw = torch.zeros((bsz, keys.numel(), n_heads), dtype=torch.float32)
+    num_topk = indices.shape[-1]
+    for b in range(bsz):
+        flat = indices[b].reshape(-1).long()
+        hit = torch.isin(flat, keys).nonzero().squeeze(1)
+        t_all, j_all, s_all = hit // num_topk, hit % num_topk, flat[hit]
+        for ki, s in enumerate(keys.tolist()):
+            m = s_all == s
+            t_idx, j_idx = t_all[m], j_all[m]
+            if t_idx.numel() == 0:
+                continue
+            qt = q[b, t_idx]  # [n, H, D]
+            gg = g[b, t_idx, j_idx].unsqueeze(-1)  # [n, 1]
+            z = (qt * k[b, s]).sum(-1) * scale  # [n, H]
+            f = gg * w[b, s] * (z > 0).float() * scale
+            dk[b, ki] = (f.unsqueeze(-1) * qt).sum(0)
+            dw[b, ki] = (gg * torch.relu(z)).sum(0)
+    return dk, dw

@@ -236,3 +236,26 @@ def test_topk_checker_accepts_ties_and_rejects_planted_mistakes():
     oob = ref.clone()
     oob[3, 0] = -1
     assert not check_topk_rows(sc, oob, K).ok
+
+
+def test_key_subset_backward_helpers_match_full_backward():
+    # The key-subset helpers (used for full-size GPU checks) must equal the full oracle
+    # backward on the rows they return.
+    g = torch.Generator().manual_seed(8)
+    B, T, S, H, D, K = 2, 40, 30, 3, 8, 7
+    q, do = (torch.randn(B, T, H, D, generator=g) for _ in range(2))
+    k, v = (torch.randn(B, S, H, D, generator=g) for _ in range(2))
+    pos = torch.stack([torch.stack([torch.randperm(S, generator=g)[:K] for _ in range(T)]) for _ in range(B)]).int()
+    pos[0, 3, 2] = pos[0, 3, 1]  # a duplicate entry
+    o, _, lse = oatt.sparse_attention(q, k, v, pos)
+    dq, dk, dv = oatt.sparse_attention_bwd(q, k, v, pos, o, lse, do)
+    keys = torch.tensor([0, 7, pos[0, 3, 1].item(), 29])
+    sk, sv = oatt.sparse_attention_bwd_keys(q, k, v, pos, o, lse, do, keys)
+    torch.testing.assert_close(sk, dk[:, keys], atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(sv, dv[:, keys], atol=1e-5, rtol=1e-5)
+    w = torch.randn(B, S, H, generator=g)
+    gs = torch.randn(B, T, K, generator=g)
+    _, ik, iw = oidx.indexer_topk_bwd(q, k, w, pos, gs, 0.3)
+    hk, hw = oidx.indexer_topk_bwd_keys(q, k, w, pos, gs, keys, 0.3)
+    torch.testing.assert_close(hk, ik[:, keys], atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(hw, iw[:, keys], atol=1e-5, rtol=1e-5)
