@@ -63,6 +63,63 @@ def read_traffic_summary(path: Path):
     return None
 
 
+def train_step_c4(steps: int = 5, warmup: int = 2, views: int = 24, batch: int = 2, topk: int = 1024):
+    """Config C4: one training step of the layer's hot path through autograd, B=2, S=24
+    views (N=32,976), bf16: indexer top-k forward, sparse attention forward with
+    attn_sum, a loss over o, attn_sum and the top-k scores (the KL-loss path's inputs),
+    and the backward of both (CSR build, attention dq/dkv, indexer dq/dkw). Times each
+    phase with HIP events on the launch stream."""
+    import torch
+
+    from geoweave_amd import _csr, workloads
+    from geoweave_amd.custom_flash_attn.sparse_index_flash_attn import sparse_index_flash_attn_func
+    from geoweave_amd.custom_indexer import sparse_topk_indexer_func
+
+    dev = torch.device("cuda", 0)
+    lay = workloads.layer_inputs(views, batch, torch.bfloat16)
+    qi, ki, wi, q, k, v = (x.to(dev).requires_grad_() for x in (lay.q_idx, lay.k_idx, lay.w_idx, lay.q, lay.k, lay.v))
+    g = torch.Generator().manual_seed(views)
+    B, T, H, D = q.shape
+    do = torch.randn(B, T, H, D, generator=g).bfloat16().to(dev)
+    dattn = torch.randn(B, T, topk, generator=g).to(dev)
+    gsc = torch.randn(B, T, topk, generator=g).bfloat16().to(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def one(ev=None):
+        for x in (qi, ki, wi, q, k, v):
+            x.grad = None
+        _csr.clear_cache()
+        if ev:
+            ev[0].record(stream)
+        idx, sc = sparse_topk_indexer_func(qi, ki, wi, None, topk, 0.125, 256, 0)
+        o, attn = sparse_index_flash_attn_func(q, k, v, idx, None, False, 0.125)
+        if ev:
+            ev[1].record(stream)
+        torch.autograd.backward([o, attn, sc], [do, dattn, gsc])
+        if ev:
+            ev[2].record(stream)
+
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    for i in range(steps):
+        one(evs[i])
+    torch.cuda.synchronize()
+    fwd = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+    bwd = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
+    gather = batch * T * topk * H * D * 2 * 2
+    return {
+        "workload": f"C4 training step: B={batch}, S={views} views (N={T}), H={H}, D={D}, top-k {topk}, bf16, "
+                    "indexer + attention forward (attn_sum on) and backward through autograd",
+        "fwd_ms": round(fwd, 3),
+        "bwd_ms": round(bwd, 3),
+        "step_ms": round(fwd + bwd, 3),
+        "attn_gathered_bytes_fwd": gather,
+        "attn_gathered_bytes_bwd": 2 * gather,
+    }
+
+
 def cpu_baseline(views: int, budget_s: float, rows_per_chunk: int = 128):
     """Times the fp32 CPU oracle (indexer scores + top-k + sparse attention) on query
     rows of the same layer until ``budget_s`` seconds have elapsed; scales to all rows."""
@@ -118,6 +175,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--with-attn-sum", action="store_true",
                     help="also time the training forward that writes attn_sum")
+    ap.add_argument("--no-train", action="store_true", help="skip the C4 training-step timing")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -251,6 +309,10 @@ def main() -> int:
         "timing": "HIP events on the launch stream; steady state, caches not flushed",
     }
     result.update(extra)
+    if not args.no_train:
+        del idx, o
+        print("[bench] C4 training step", file=sys.stderr, flush=True)
+        result["train_c4"] = train_step_c4()
     if not args.no_cpu_baseline:
         del lay
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
