@@ -8,7 +8,11 @@ Names, argument meaning and return values follow the reference API (``:3108-3456
 * ``sparse_index_flash_attn_inference_func(..., return_attn=False)`` (``:3138-3163``);
 * the ``[B, H, T, D]`` twins ``sparse_index_flash_attn_bhtd_func`` (``:3289-3370``) and
   ``sparse_index_flash_attn_inference_bhtd_func`` (``:3166-3193``);
-* ``dense_index_flash_attn_func`` over broadcast dense positions (``:3108-3135``).
+* ``dense_index_flash_attn_func`` over broadcast dense positions (``:3108-3135``);
+* ``sparse_index_flash_attn_value_gate_bhtd_func`` is exported as ``None``: the value-gated
+  objective (reference ``:3373-3456``) is off in the presets and not built here. The
+  caller imports all six names in one ``try`` block (``dsa_attention.py:29-45``) and
+  checks this one for ``None`` before use (``:5202``), so it takes its own torch path.
 
 q: ``[B, T, H, D]``, k/v: ``[B, S, H, D]`` (bthd), kv_positions: int32 ``[B, T, K]``
 shared by all heads; entries outside ``[0, S)`` are masked. Preconditions are the
@@ -32,6 +36,7 @@ __all__ = [
     "sparse_index_flash_attn_bhtd_func",
     "sparse_index_flash_attn_inference_bhtd_func",
     "dense_index_flash_attn_func",
+    "sparse_index_flash_attn_value_gate_bhtd_func",
     "SparseIndexFlashAttnFunc",
     "SparseIndexFlashAttnBhtdFunc",
 ]
@@ -263,3 +268,7 @@ def dense_index_flash_attn_func(
     seqlen_k = k.shape[1]
     kv_positions = _build_dense_kv_positions(batch, seqlen_q, seqlen_k, q.device)
     return SparseIndexFlashAttnFunc.apply(q, k, v, kv_positions, bias, causal, softmax_scale)
+
+
+# Not provided (see the module docstring): the caller falls back when it is None.
+sparse_index_flash_attn_value_gate_bhtd_func = None

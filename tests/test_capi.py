@@ -86,3 +86,18 @@ def test_python_preconditions_match_reference_errors():
         m._flash_attn_forward(big, big, big, pos)
     with pytest.raises(ValueError, match="GPU tensors"):
         m._flash_attn_forward(qb, qb, qb, pos)
+
+
+def test_dropin_modules_export_every_name_the_reference_callers_import():
+    # easyvolcap/official_vggt/layers/dsa_attention.py:29-45 imports these six names in one
+    # try block; easyvolcap/official_vggt/layers/indexer.py:10-14 imports these two.
+    from geoweave_amd.custom_flash_attn import sparse_index_flash_attn as m
+    from geoweave_amd import custom_indexer
+
+    for name in ("sparse_index_flash_attn_func", "sparse_index_flash_attn_bhtd_func",
+                 "sparse_index_flash_attn_value_gate_bhtd_func", "dense_index_flash_attn_func",
+                 "sparse_index_flash_attn_inference_func", "sparse_index_flash_attn_inference_bhtd_func"):
+        assert hasattr(m, name), name
+    assert m.sparse_index_flash_attn_value_gate_bhtd_func is None
+    assert callable(custom_indexer.sparse_topk_indexer_func)
+    assert callable(custom_indexer.sparse_topk_indexer_inference_func)
