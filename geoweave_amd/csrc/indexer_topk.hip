@@ -9,25 +9,35 @@
 //
 // Pipeline (all on the caller's stream, no host synchronisation):
 //  K0 score_kernel<SAMPLE>: MFMA scores of every query against Ms strided sample keys.
-//  K0b select_kernel<TAU>:  tau0[t] = the rank-r largest sample score, r chosen so that
-//                           the number of keys scoring >= tau0 is >= topk with very high
-//                           probability and about 1.2-2x topk on average.
-//  K1 score_kernel<FILTER>: MFMA scores against all keys (split into nsplit key ranges for
-//                           load balance); the epilogue keeps (score, key) pairs with
-//                           score >= tau0 in per-(query, split) candidate lists.
-//  K2 select_kernel<FINAL>: exact top-k of the candidates (radix select in LDS). A query
-//                           whose lists overflowed or hold fewer than topk entries is
-//                           queued for K3 instead.
+//  K0b tau_kernel:          one wave per query: a threshold tau whose rank among the
+//                           sample scores lies in [r, r + 8], r chosen so that at least
+//                           topk keys of the whole row score >= tau with very high
+//                           probability (about 1.7 x topk keys on average).
+//  K1 score_kernel<FILTER>: MFMA scores against all keys; the epilogue appends
+//                           (score, key) pairs with score >= tau to candidate sublists.
+//  K2 select_kernel:        one workgroup per query: exact top-k of the candidates
+//                           (register-resident bisection on the order-preserving score
+//                           bits). A query whose sublists overflowed or hold fewer than
+//                           topk entries is queued for K3 instead.
 //  K3 fallback_kernel:      exact brute force for queued queries (scores to scratch, radix
 //                           select) - correct for any input, used rarely.
-// Exactness: if count(score >= tau0) >= topk, every member of the top-k scores >= tau0 and
+// Exactness: if count(score >= tau) >= topk, every member of the top-k scores >= tau and
 // is a candidate, so selecting among the candidates is exact. Ties at the k-th value are
-// broken deterministically (lowest candidate position first).
+// broken deterministically (candidate order: sublist, then position).
 //
 // MFMA layout (v_mfma_f32_32x32x16_{bf16,f16}): C[32 queries x 32 keys]; A = q rows
 // (stationary in VGPRs for the whole key sweep), B = key rows staged through LDS (padded
 // rows, conflict-free 16-byte reads). Lane l owns key column l%32 and query rows
-// 8*(r/4) + 4*(l/32) + r%4 of accumulator element r.
+// 8*(r/4) + 4*(l/32) + r%4 of accumulator element r. Every (query row, key column) cell
+// of the tile therefore belongs to exactly one lane, for every key tile of the sweep, so
+// the candidates of one (query, column) go to a sublist that only that lane appends to:
+// its fill count is a private register and an append is a compare, a clamp, an add and a
+// store, with no cross-lane coordination.
+//
+// Key splits: to fill the chip, the key range is divided over nsplit workgroups per
+// query tile. Split sp takes the 64-key stages sp, sp + nsplit, sp + 2*nsplit, ...; the
+// interleave spreads any locality of a query's favourite keys (e.g. its own view) evenly
+// over the splits, so every sublist receives about (candidates / (32 * nsplit)) entries.
 #include <math.h>
 
 #include "gw_common.h"
@@ -36,13 +46,13 @@
 namespace gw {
 namespace {
 
-constexpr int kQW = 32;          // queries per wave
+constexpr int kQW = 32;            // queries per wave
 constexpr int kWaves = 4;
-constexpr int kBM = kQW * kWaves; // queries per workgroup
-constexpr int kBN = 64;          // keys per LDS stage
-constexpr int kDI = 64;          // indexer head dim
-constexpr int kCapTotal = 4096;  // candidate slots per query (split evenly over splits)
-constexpr int kMaxSplit = 4;
+constexpr int kBM = kQW * kWaves;  // queries per workgroup
+constexpr int kBN = 64;            // keys per LDS stage (and split interleave granule)
+constexpr int kDI = 64;            // indexer head dim
+constexpr int kSubTotal = 8192;    // candidate slots per query over all sublists
+constexpr int kMaxSplit = 8;
 constexpr int kMaxTopk = 2048;
 constexpr int kFallbackBlocks = 256;
 
@@ -64,6 +74,44 @@ __device__ __forceinline__ float to_f32(FP16, uint16_t x) {
   return (float)__builtin_bit_cast(_Float16, x);
 }
 
+// relu on the bit pattern: every negative float (sign bit set) becomes +0, every
+// non-negative one is kept bit for bit. One v_max_i32, where fmaxf(x, 0) costs a NaN
+// canonicalisation plus the max.
+__device__ __forceinline__ float relu_bits(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
+
+// Wave-wide reductions (all 64 lanes active): DPP within each 16-lane row, then the four
+// row results through readlane; the result is wave-uniform.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, true);
+}
+__device__ __forceinline__ uint32_t wave_sum_u(uint32_t x) {
+  x += dpp_u<kDppXor1>(x);
+  x += dpp_u<kDppXor2>(x);
+  x += dpp_u<kDppHalfMirror>(x);
+  x += dpp_u<kDppMirror>(x);
+  return __builtin_amdgcn_readlane(x, 0) + __builtin_amdgcn_readlane(x, 16) +
+         __builtin_amdgcn_readlane(x, 32) + __builtin_amdgcn_readlane(x, 48);
+}
+__device__ __forceinline__ uint32_t wave_min_u(uint32_t x) {
+  x = min(x, dpp_u<kDppXor1>(x));
+  x = min(x, dpp_u<kDppXor2>(x));
+  x = min(x, dpp_u<kDppHalfMirror>(x));
+  x = min(x, dpp_u<kDppMirror>(x));
+  const uint32_t a = min((uint32_t)__builtin_amdgcn_readlane(x, 0), (uint32_t)__builtin_amdgcn_readlane(x, 16));
+  const uint32_t b = min((uint32_t)__builtin_amdgcn_readlane(x, 32), (uint32_t)__builtin_amdgcn_readlane(x, 48));
+  return min(a, b);
+}
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t x) {
+  x = max(x, dpp_u<kDppXor1>(x));
+  x = max(x, dpp_u<kDppXor2>(x));
+  x = max(x, dpp_u<kDppHalfMirror>(x));
+  x = max(x, dpp_u<kDppMirror>(x));
+  const uint32_t a = max((uint32_t)__builtin_amdgcn_readlane(x, 0), (uint32_t)__builtin_amdgcn_readlane(x, 16));
+  const uint32_t b = max((uint32_t)__builtin_amdgcn_readlane(x, 32), (uint32_t)__builtin_amdgcn_readlane(x, 48));
+  return max(a, b);
+}
+
 enum TauMode { kTauArray = 0, kTauPlusInf = 1, kTauMinusInf = 2 };
 
 struct ScoreParams {
@@ -73,12 +121,14 @@ struct ScoreParams {
   const uint16_t* mask;  // [B, T, S] or null
   const float* tau;      // [B*T] or null (-inf)
   float* samp;           // SAMPLE: [B*T, Ms]
-  int2* cand;            // FILTER: [B*T, nsplit, cap]
-  int* counts;           // FILTER: [B*T, nsplit]
+  int2* cand;            // FILTER: [B*T, nsplit*32, cap+1] (slot cap: overflow sink)
+  int* counts;           // FILTER: [B*T, nsplit*32] appends per sublist (may exceed cap)
   int T, S;
-  int nsplit, split_len, cap;
+  int nsplit, cap;
+  int nstages;           // 64-key stages of the sweep
   int Ms;
   int tau_mode;
+  int force_wide;
   float scale;
 };
 
@@ -89,41 +139,46 @@ __device__ __forceinline__ int sweep_key(int i, const ScoreParams& p) {
   return i;
 }
 
+// Key tiles reach LDS through direct global->LDS loads (global_load_lds_dwordx4: lane l
+// of a wave writes 16 bytes at the wave's LDS base + 16*l), so no staging registers are
+// needed. Rows are stored unpadded with the 16-byte chunks of key row kl XOR-swizzled by
+// (kl & 7): the MFMA operand reads (32 consecutive key rows at one logical chunk) then
+// hit 8 distinct 16-byte bank groups per 8 lanes.
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
 template <typename E, int HI, bool SAMPLE, bool HAS_MASK>
-__global__ __launch_bounds__(256) void indexer_score_kernel(const ScoreParams p) {
+__global__ __launch_bounds__(256, (HI <= 4 ? 2 : 1)) void indexer_score_kernel(const ScoreParams p) {
   constexpr int ROW_BYTES = HI * kDI * 2;
-  constexpr int ROW_STRIDE = ROW_BYTES + 16;
-  constexpr int CHUNKS = ROW_BYTES / 16;
-  constexpr int LOADS = (kBN * CHUNKS + 255) / 256;
+  constexpr int CHUNKS = ROW_BYTES / 16;              // 16-byte chunks per key row (>= 8)
+  constexpr int TILE_BYTES = kBN * ROW_BYTES;
+  constexpr int LOADS = TILE_BYTES / (256 * 16);      // direct loads per thread per stage
   constexpr int WVALS = kBN * HI;
   constexpr int WLOADS = (WVALS + 255) / 256;
+  static_assert(LOADS * 256 * 16 == TILE_BYTES, "key tile must split evenly over the threads");
 
-  __shared__ __attribute__((aligned(16))) uint8_t ktile[2][kBN * ROW_STRIDE];
+  __shared__ __attribute__((aligned(16))) uint8_t ktile[2][TILE_BYTES];
   __shared__ float wtile[2][WVALS];
+  __shared__ __attribute__((aligned(16))) float tau_s[kBM];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int b = blockIdx.z;
-  const int split = blockIdx.y;
+  const int split = SAMPLE ? 0 : (int)blockIdx.y;
+  const int nsplit = SAMPLE ? 1 : p.nsplit;
   const int q0 = blockIdx.x * kBM + wave * kQW;
   const int T = p.T, S = p.S;
-
-  int kbeg, kend;  // sweep range
-  if constexpr (SAMPLE) {
-    kbeg = 0;
-    kend = p.Ms;
-  } else {
-    kbeg = split * p.split_len;
-    kend = min(S, kbeg + p.split_len);
-  }
+  const int nkeys = SAMPLE ? p.Ms : S;
+  const int col = lane & 31;
+  const int half = lane >> 5;
 
   // A operands: this lane's query row (lane % 32), k-chunk (lane / 32) of each 16-wide step.
   uint4 a[HI][4];
   {
-    const int row = q0 + (lane & 31);
+    const int row = q0 + col;
     const bool ok = row < T;
-    const uint16_t* qr = p.q + ((int64_t)b * T + (ok ? row : 0)) * (HI * kDI) + (lane >> 5) * 8;
+    const uint16_t* qr = p.q + ((int64_t)b * T + (ok ? row : 0)) * (HI * kDI) + half * 8;
 #pragma unroll
     for (int h = 0; h < HI; ++h)
 #pragma unroll
@@ -131,206 +186,427 @@ __global__ __launch_bounds__(256) void indexer_score_kernel(const ScoreParams p)
         a[h][ks] = ok ? *reinterpret_cast<const uint4*>(qr + h * kDI + ks * 16) : make_uint4(0, 0, 0, 0);
   }
 
-  float tau[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int row = q0 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+  // Per-row thresholds of this wave's 32 rows (rows past T never pass).
+  if (lane < kQW) {
+    const int row = q0 + lane;
     float tv = INFINITY;
     if (row < T) {
       if (p.tau_mode == kTauPlusInf) tv = INFINITY;
       else if (p.tau_mode == kTauMinusInf || p.tau == nullptr) tv = -INFINITY;
       else tv = p.tau[(int64_t)b * T + row];
     }
-    tau[r] = tv;
+    tau_s[wave * kQW + lane] = tv;
+  }
+  uint32_t cnt[16];  // appends so far x 8 (bytes)
+#pragma unroll
+  for (int r = 0; r < 16; ++r) cnt[r] = 0;
+
+  // Sublist addressing (FILTER): element offset from the wave's base =
+  //   (row_in_wave * nsub + col) * SS + slot, row_in_wave = 8*(r/4) + 4*half + r%4.
+  const int nsub = nsplit * 32;
+  const int SS = p.cap + 1;
+  char* wbase = nullptr;       // uniform
+  uint32_t lane_off = 0;       // bytes
+  uint32_t row_step = 0;       // bytes per query row (uniform)
+  const uint32_t cap8 = (uint32_t)p.cap * 8u;
+  if constexpr (!SAMPLE) {
+    wbase = reinterpret_cast<char*>(p.cand + ((int64_t)b * T + q0) * nsub * SS + (int64_t)split * 32 * SS);
+    row_step = (uint32_t)nsub * (uint32_t)SS * 8u;
+    lane_off = (uint32_t)(4 * half) * row_step + (uint32_t)col * (uint32_t)SS * 8u;
   }
 
-  int cnt[32];
+  // Loader geometry: load i of this thread fills LDS bytes [(i*4 + wave)*1024 + 16*lane, +16),
+  // which hold chunk (pc) of key row (kl); the source is logical chunk pc ^ (kl & 7).
+  int ld_kl[LOADS], ld_lc[LOADS];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) cnt[i] = 0;
+  for (int i = 0; i < LOADS; ++i) {
+    const int pos = (i * 4 + wave) * 1024 + 16 * lane;
+    ld_kl[i] = pos / ROW_BYTES;
+    ld_lc[i] = ((pos % ROW_BYTES) / 16) ^ (ld_kl[i] & 7);
+  }
+  // Operand read offsets: key row (nb*32 + col), logical chunk h*8 + 2*ks + half.
+  uint32_t rd_off[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) rd_off[ks] = col * ROW_BYTES + 16 * ((2 * ks + half) ^ (col & 7));
 
-  uint4 kreg[LOADS];
   float wreg[WLOADS];
-
-  auto gload = [&](int kb) {
+  // Keys past the end: K rows are loaded from the last valid key (harmless), and the gate
+  // is NaN (FILTER: the score is NaN and fails every `>= tau`) or 0 (SAMPLE: not stored).
+  auto gload = [&](int kb, int buf) {
+    const int live = min(kBN, nkeys - kb);
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-      const int c = tid + 256 * i;
-      const int kl = c / CHUNKS;
-      const int ch = c % CHUNKS;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (c < kBN * CHUNKS && kb + kl < kend) {
-        const int key = sweep_key<SAMPLE>(kb + kl, p);
-        v = *reinterpret_cast<const uint4*>(p.k + ((int64_t)b * S + key) * (HI * kDI) + ch * 8);
-      }
-      kreg[i] = v;
+      const int kl = min(ld_kl[i], live - 1);
+      const int key = sweep_key<SAMPLE>(kb + kl, p);
+      const uint16_t* src = p.k + ((int64_t)b * S + key) * (HI * kDI) + ld_lc[i] * 8;
+      __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(&ktile[buf][(i * 4 + wave) * 1024]), 16, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < WLOADS; ++i) {
       const int c = tid + 256 * i;
       const int kl = c / HI, h = c % HI;
-      float wv = 0.f;
-      if (c < WVALS && kb + kl < kend) {
+      float wv = SAMPLE ? 0.f : __builtin_nanf("");
+      if (c < WVALS && kl < live) {
         const int key = sweep_key<SAMPLE>(kb + kl, p);
         wv = to_f32(E{}, p.w[((int64_t)b * S + key) * HI + h]) * p.scale;
       }
       wreg[i] = wv;
     }
   };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int c = tid + 256 * i;
-      if (c < kBN * CHUNKS) {
-        const int kl = c / CHUNKS;
-        const int ch = c % CHUNKS;
-        *reinterpret_cast<uint4*>(&ktile[buf][kl * ROW_STRIDE + ch * 16]) = kreg[i];
-      }
-    }
+  auto wstore = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < WLOADS; ++i)
       if (tid + 256 * i < WVALS) wtile[buf][tid + 256 * i] = wreg[i];
   };
 
-  const int64_t row_stride_c = (int64_t)p.nsplit * p.cap;
-  int2* cand_base = nullptr;
-  if constexpr (!SAMPLE) cand_base = p.cand + ((int64_t)b * T + q0) * row_stride_c + (int64_t)split * p.cap;
-
-  if (kbeg < kend) {
-    gload(kbeg);
-    lstore(0);
+  int st = split;
+  if (st < p.nstages) {
+    gload(st * kBN, 0);
+    wstore(0);
   }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct LDS loads have landed
   __syncthreads();
 
   int buf = 0;
-  for (int kb = kbeg; kb < kend; kb += kBN) {
-    const bool more = kb + kBN < kend;
-    if (more) gload(kb + kBN);
+  for (; st < p.nstages; st += nsplit) {
+    const int kb = st * kBN;
+    const bool more = st + nsplit < p.nstages;
+    if (more) gload((st + nsplit) * kBN, buf ^ 1);
 
 #pragma unroll
     for (int nb = 0; nb < kBN / 32; ++nb) {
-      const int kl = nb * 32 + (lane & 31);
-      const uint8_t* brow = &ktile[buf][kl * ROW_STRIDE + (lane >> 5) * 16];
-      f32x16 acc[HI];
+      const int kl = nb * 32 + col;
+      const uint8_t* tile = &ktile[buf][nb * 32 * ROW_BYTES];
+      float s[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = 0.f;
 #pragma unroll
       for (int h = 0; h < HI; ++h) {
-        acc[h] = f32x16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        f32x16 acc = f32x16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          const uint4 bop = *reinterpret_cast<const uint4*>(brow + h * (kDI * 2) + ks * 32);
-          acc[h] = mfma32(E{}, a[h][ks], bop, acc[h]);
+          const uint4 bop = *reinterpret_cast<const uint4*>(tile + rd_off[ks] + h * 128);
+          acc = mfma32(E{}, a[h][ks], bop, acc);
         }
-      }
-      float wv[HI];
+        const float wv = wtile[buf][kl * HI + h];
 #pragma unroll
-      for (int h = 0; h < HI; ++h) wv[h] = wtile[buf][kl * HI + h];
+        for (int r = 0; r < 16; ++r) s[r] = fmaf(wv, relu_bits(acc[r]), s[r]);
+      }
       const int kidx = kb + kl;
-      const bool kvalid = kidx < kend;
+      const bool kvalid = kidx < nkeys;
       const int key = sweep_key<SAMPLE>(kidx, p);
 
+      if constexpr (HAS_MASK) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float s = 0.f;
-#pragma unroll
-        for (int h = 0; h < HI; ++h) s = fmaf(wv[h], fmaxf(acc[h][r], 0.f), s);
-        const int rlo = 8 * (r / 4) + (r % 4);
-        const int rrow = rlo + 4 * (lane >> 5);
-        if constexpr (HAS_MASK) {
-          const int row = q0 + rrow;
-          if (kvalid && row < T) s += to_f32(E{}, p.mask[((int64_t)b * T + row) * S + key]);
+        for (int r = 0; r < 16; ++r) {
+          const int row = q0 + 8 * (r / 4) + 4 * half + (r % 4);
+          if (kvalid && row < T) s[r] += to_f32(E{}, p.mask[((int64_t)b * T + row) * S + key]);
         }
-        if constexpr (SAMPLE) {
-          const int row = q0 + rrow;
-          if (kvalid && row < T) p.samp[((int64_t)b * T + row) * p.Ms + kidx] = s;
-        } else {
-          const bool pass = kvalid && (q0 + rrow < T) && (s >= tau[r]);
-          const uint64_t m = __ballot(pass);
-          if (m) {
-            const uint32_t lo = (uint32_t)m, hi = (uint32_t)(m >> 32);
-            const int plo = __popc(lo), phi = __popc(hi);
-            const int pre = __builtin_amdgcn_mbcnt_hi(hi, __builtin_amdgcn_mbcnt_lo(lo, 0));
-            const int slot = (lane < 32) ? (cnt[rlo] + pre) : (cnt[rlo + 4] + pre - plo);
-            if (pass && slot < p.cap)
-              cand_base[(int64_t)rrow * row_stride_c + slot] = make_int2(__float_as_int(s), key);
-            cnt[rlo] += plo;
-            cnt[rlo + 4] += phi;
+      }
+      if constexpr (SAMPLE) {
+        if (kvalid) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = q0 + 8 * (r / 4) + 4 * half + (r % 4);
+            if (row < T) p.samp[((int64_t)b * T + row) * p.Ms + kidx] = s[r];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 t4 = *reinterpret_cast<const float4*>(&tau_s[wave * kQW + 8 * g + 4 * half]);
+          const float tv[4] = {t4.x, t4.y, t4.z, t4.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int r = 4 * g + j;
+            if (s[r] >= tv[j]) {  // NaN (key past the end) never passes
+              const uint32_t rr = (uint32_t)(8 * g + j);
+              const uint32_t off = lane_off + rr * row_step + min(cnt[r], cap8);
+              *reinterpret_cast<int2*>(wbase + off) = make_int2(__float_as_int(s[r]), key);
+              cnt[r] += 8u;
+            }
           }
         }
       }
     }
 
-    if (more) lstore(buf ^ 1);
+    if (more) wstore(buf ^ 1);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): next stage's direct LDS loads have landed
     __syncthreads();
     buf ^= 1;
   }
 
   if constexpr (!SAMPLE) {
-    int mine = 0;
 #pragma unroll
-    for (int i = 0; i < 32; ++i)
-      if ((lane & 31) == i) mine = cnt[i];
-    const int row = q0 + lane;
-    if (lane < 32 && row < T) p.counts[((int64_t)b * T + row) * p.nsplit + split] = mine;
+    for (int r = 0; r < 16; ++r) {
+      const int row = q0 + 8 * (r / 4) + 4 * half + (r % 4);
+      if (row < T) p.counts[((int64_t)b * T + row) * nsub + split * 32 + col] = (int)(cnt[r] >> 3);
+    }
   }
 }
 
 // ---------------------------------------------------------------------------------------
-// Selection over candidates (FINAL) or over the sample scores (TAU).
+// Threshold from the sample scores: one wave per query row.
 // ---------------------------------------------------------------------------------------
+template <int MPL>
+__global__ __launch_bounds__(256) void indexer_tau_kernel(const float* samp, int Ms, int rank, int slack,
+                                                          float* tau, int64_t rows) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* src = samp + row * Ms;
+  uint32_t kv[MPL];
+  uint32_t lmin = 0xFFFFFFFFu, lmax = 0u;
+#pragma unroll
+  for (int m = 0; m < MPL; ++m) {
+    kv[m] = f2key(src[lane + 64 * m]);
+    lmin = min(lmin, kv[m]);
+    lmax = max(lmax, kv[m]);
+  }
+  // Invariant: count(key >= lo) >= rank and count(key >= hi) < rank.
+  uint64_t lo = wave_min_u(lmin);
+  uint64_t hi = (uint64_t)wave_max_u(lmax) + 1;
+  while (hi - lo > 1) {
+    const uint32_t mid = (uint32_t)(lo + ((hi - lo) >> 1));
+    uint32_t c = 0;
+#pragma unroll
+    for (int m = 0; m < MPL; ++m) c += kv[m] >= mid;
+    c = wave_sum_u(c);
+    if ((int)c < rank) {
+      hi = mid;
+    } else {
+      lo = mid;
+      if ((int)c <= rank + slack) break;
+    }
+  }
+  if (lane == 0) tau[row] = key2f((uint32_t)lo);
+}
+
+// ---------------------------------------------------------------------------------------
+// Exact top-k among the candidates: one wave per query row, candidates in registers.
+//
+// Lane l reads NSEG = max(1, nsub / 64) sublists: l, l + 64, ... (with nsub = 32, lanes
+// l and l + 32 share sublist l % 32, taking its even and odd entries). Each sublist's
+// entries land in a fixed register array of KS = kSelRegs / NSEG slots (expected fill:
+// about 1.7 x topk / nsub, e.g. 14 of 40 at nsub = 128). A row with an overflowed
+// sublist, a register array over KS, or fewer than topk candidates goes to the exact
+// fallback. No barriers: reductions are wave-wide.
+// ---------------------------------------------------------------------------------------
+constexpr int kSelRegs = 80;
+
 struct SelectParams {
-  const float* samp;
-  int Ms, rank;
-  float* tau;
   const int2* cand;
   const int* counts;
-  int nsplit, cap;
+  int nsub, cap;
   int32_t* out_idx;
   uint16_t* out_scores;
   int Kk;
   int* fb_count;
   int* fb_list;
-  int T;
+  int* wide_count;
+  int* wide_list;
+  int64_t rows;
+  int force_wide;  // test hook: every complete row takes the LDS selection
 };
 
-template <typename E, bool FINAL>
-__global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams p) {
-  __shared__ uint32_t keys[kCapTotal];
-  __shared__ int vals[FINAL ? kCapTotal : 1];
-  __shared__ SelectShared sh;
-  __shared__ int offs[kMaxSplit + 1];
-  const int tid = threadIdx.x;
-  const int t = blockIdx.x, b = blockIdx.y;
-  const int64_t row = (int64_t)b * p.T + t;
+// Exclusive prefix over the wave of x; `total` receives the wave sum.
+__device__ __forceinline__ int wave_excl_scan(int x, int& total) {
+  const int lane = threadIdx.x & 63;
+  int incl = x;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o);
+    if (lane >= o) incl += y;
+  }
+  total = __builtin_amdgcn_readlane(incl, 63);
+  return incl - x;
+}
 
-  if constexpr (!FINAL) {
-    const float* src = p.samp + row * p.Ms;
-    for (int i = tid; i < p.Ms; i += kSelThreads) keys[i] = f2key(src[i]);
-    __syncthreads();
-    int take_eq;
-    const uint32_t kth = block_radix_select([&](int i) { return keys[i]; }, p.Ms, p.rank, sh, take_eq);
-    if (tid == 0) p.tau[row] = key2f(kth);
+// Number of set bits of a wave mask below this lane.
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+template <typename E, int NSEG>
+__global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams p) {
+  constexpr int KS = NSEG == 4 ? 24 : kSelRegs / NSEG;  // register slots per sublist
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (row >= p.rows) return;
+  const int SS = p.cap + 1;
+  const int2* src[NSEG];
+  int cnt[NSEG];
+  int stride = 1;
+  bool bad = false;
+  if (p.nsub == 32) {
+    const int sub = lane & 31, part = lane >> 5;
+    const int cc = p.counts[row * 32 + sub];
+    bad = cc > p.cap;
+    const int c = min(cc, p.cap);
+    src[0] = p.cand + (row * 32 + sub) * SS + part;
+    cnt[0] = c > part ? (c - part + 1) / 2 : 0;
+    stride = 2;
+#pragma unroll
+    for (int j = 1; j < NSEG; ++j) {
+      src[j] = src[0];
+      cnt[j] = 0;
+    }
   } else {
-    if (tid == 0) {
-      int total = 0;
-      bool bad = false;
-      for (int sp = 0; sp < p.nsplit; ++sp) {
-        const int c = p.counts[row * p.nsplit + sp];
-        bad |= c > p.cap;
-        offs[sp] = total;
-        total += min(c, p.cap);
+#pragma unroll
+    for (int j = 0; j < NSEG; ++j) {
+      const int sub = lane + 64 * j;
+      const int cc = p.counts[row * p.nsub + sub];
+      bad |= cc > p.cap;
+      cnt[j] = min(cc, p.cap);
+      src[j] = p.cand + (row * p.nsub + sub) * SS;
+    }
+  }
+  int nl = 0, cmax_l = 0;
+#pragma unroll
+  for (int j = 0; j < NSEG; ++j) {
+    nl += cnt[j];
+    cmax_l = max(cmax_l, cnt[j]);
+  }
+  const uint32_t total = wave_sum_u((uint32_t)nl);
+  if (wave_max_u(bad ? 1u : 0u) != 0 || (int)total < p.Kk) {
+    // The candidates may miss part of the top-k: exact brute force.
+    if (lane == 0) p.fb_list[atomicAdd(p.fb_count, 1)] = (int)row;
+    return;
+  }
+  if (p.force_wide || wave_max_u(cmax_l > KS ? 1u : 0u) != 0) {
+    // Complete candidates, more than the registers hold: the LDS selection.
+    if (lane == 0) p.wide_list[atomicAdd(p.wide_count, 1)] = (int)row;
+    return;
+  }
+  const int cmax = (int)wave_max_u((uint32_t)cmax_l);  // register slots in use, uniform
+
+  // Branch-free loads: slots past a sublist's count read its first entry (inside the
+  // buffer) and are replaced by key 0, below the key of every finite score. Chunks of 8
+  // slots past the wave's largest count are skipped with a uniform branch.
+  uint32_t kv[NSEG][KS];
+  uint32_t lmin = 0xFFFFFFFFu, lmax = 0u;
+#pragma unroll
+  for (int m0 = 0; m0 < KS; m0 += 8) {
+#pragma unroll
+    for (int j = 0; j < NSEG; ++j)
+#pragma unroll
+      for (int m = m0; m < min(m0 + 8, KS); ++m) kv[j][m] = 0u;
+    if (m0 < cmax) {
+#pragma unroll
+      for (int j = 0; j < NSEG; ++j) {
+#pragma unroll
+        for (int m = m0; m < min(m0 + 8, KS); ++m) {
+          const bool live = m < cnt[j];
+          const uint32_t key = f2key(__int_as_float(src[j][(live ? m : 0) * stride].x));
+          kv[j][m] = live ? key : 0u;
+        }
       }
-      offs[p.nsplit] = total;
-      if (bad || total < p.Kk) offs[p.nsplit] = -1;
+    }
+  }
+  // Key range of the live slots: empty slots hold 0, which kv - 1 wraps to the maximum.
+#pragma unroll
+  for (int j = 0; j < NSEG; ++j)
+#pragma unroll
+    for (int m = 0; m < KS; ++m) {
+      lmin = min(lmin, kv[j][m] - 1u);
+      lmax = max(lmax, kv[j][m]);
+    }
+  lmin += 1u;
+  // Bisection on the key value: count(key >= lo) >= Kk > count(key >= hi).
+  uint64_t lo = wave_min_u(lmin), hi = (uint64_t)wave_max_u(lmax) + 1;
+  while (hi - lo > 1) {
+    const uint32_t mid = (uint32_t)(lo + ((hi - lo) >> 1));
+    uint32_t cc = 0;
+#pragma unroll
+    for (int m0 = 0; m0 < KS; m0 += 8) {
+      if (m0 < cmax) {
+#pragma unroll
+        for (int j = 0; j < NSEG; ++j)
+#pragma unroll
+          for (int m = m0; m < min(m0 + 8, KS); ++m) cc += kv[j][m] >= mid;
+      }
+    }
+    const int n = (int)wave_sum_u(cc);
+    if (n >= p.Kk) {
+      lo = mid;
+      if (n == p.Kk) break;
+    } else {
+      hi = mid;
+    }
+  }
+  const uint32_t thr = (uint32_t)lo;
+  // Elements > thr are all selected; of those == thr, the first (Kk - count(> thr)) in
+  // candidate order (slot chunk, sublist, slot, lane). Output positions come from wave
+  // ballots, so each write goes to base + (selected lanes below this one).
+  int n_gt = 0;
+#pragma unroll
+  for (int m0 = 0; m0 < KS; m0 += 8) {
+    if (m0 < cmax) {
+#pragma unroll
+      for (int j = 0; j < NSEG; ++j)
+#pragma unroll
+        for (int m = m0; m < min(m0 + 8, KS); ++m) n_gt += __popcll(__ballot(kv[j][m] > thr));
+    }
+  }
+  const int need_eq = p.Kk - n_gt;
+  int32_t* oi = p.out_idx + row * p.Kk;
+  uint16_t* os = p.out_scores + row * p.Kk;
+  int base = 0, eq_run = 0;
+#pragma unroll
+  for (int m0 = 0; m0 < KS; m0 += 8) {
+    if (m0 < cmax) {
+#pragma unroll
+      for (int j = 0; j < NSEG; ++j) {
+#pragma unroll
+        for (int m = m0; m < min(m0 + 8, KS); ++m) {
+          const bool eq = kv[j][m] == thr;
+          const uint64_t eqm = __ballot(eq);
+          const int eq_before = eq_run + lanes_below(eqm);
+          eq_run += __popcll(eqm);
+          const bool sel = kv[j][m] > thr || (eq && eq_before < need_eq);
+          const uint64_t selm = __ballot(sel);
+          const int slot_out = base + lanes_below(selm);
+          base += __popcll(selm);
+          if (sel) {
+            const int2 cdt = src[j][m * stride];
+            oi[slot_out] = cdt.y;
+            os[slot_out] = (uint16_t)pack1(E{}, __int_as_float(cdt.x));
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Exact top-k of rows whose (complete) candidates exceed the register path: all of the
+// row's candidates in LDS, block radix select. Persistent grid over the queue.
+// ---------------------------------------------------------------------------------------
+template <typename E>
+__global__ __launch_bounds__(256) void indexer_select_wide_kernel(const SelectParams p) {
+  __shared__ uint32_t keys[kSubTotal];
+  __shared__ int vals[kSubTotal];
+  __shared__ int offs[kMaxSplit * 32 + 1];
+  __shared__ SelectShared sh;
+  const int tid = threadIdx.x;
+  const int nitems = *((volatile const int*)p.wide_count);
+  const int SS = p.cap + 1;
+  for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+    const int64_t row = p.wide_list[item];
+    if (tid == 0) {
+      int acc = 0;
+      for (int sub = 0; sub < p.nsub; ++sub) {
+        offs[sub] = acc;
+        acc += min(p.counts[row * p.nsub + sub], p.cap);
+      }
+      offs[p.nsub] = acc;
     }
     __syncthreads();
-    const int total = offs[p.nsplit];
-    if (total < 0) {
-      if (tid == 0) p.fb_list[atomicAdd(p.fb_count, 1)] = (int)row;
-      return;
-    }
-    for (int sp = 0; sp < p.nsplit; ++sp) {
-      const int o = offs[sp], n = offs[sp + 1] - o;
-      const int2* src = p.cand + (row * p.nsplit + sp) * p.cap;
-      for (int i = tid; i < n; i += kSelThreads) {
+    const int total = offs[p.nsub];
+    for (int sub = tid; sub < p.nsub; sub += kSelThreads) {
+      const int2* src = p.cand + (row * p.nsub + sub) * SS;
+      const int o = offs[sub], n = offs[sub + 1] - o;
+      for (int i = 0; i < n; ++i) {
         const int2 e = src[i];
         keys[o + i] = f2key(__int_as_float(e.x));
         vals[o + i] = e.y;
@@ -350,6 +626,7 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
                       }
                     },
                     sh);
+    __syncthreads();
   }
 }
 
@@ -379,7 +656,7 @@ __global__ __launch_bounds__(256) void indexer_fallback_kernel(const FallbackPar
   float* sc = p.scratch + (int64_t)blockIdx.x * p.S;
   for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
     const int row = p.fb_list[item];
-    const int b = row / p.T, t = row - b * p.T;
+    const int b = row / p.T;
     const uint32_t* qrow = reinterpret_cast<const uint32_t*>(p.q + (int64_t)row * HI * kDI);
     for (int i = tid; i < HI * kDI / 2; i += kSelThreads) qs[i] = qrow[i];
     __syncthreads();
@@ -399,7 +676,7 @@ __global__ __launch_bounds__(256) void indexer_fallback_kernel(const FallbackPar
           z = dot2(E{}, qv.w, kv.w, z);
         }
         const float wv = to_f32(E{}, p.w[((int64_t)b * p.S + j) * HI + h]) * p.scale;
-        s = fmaf(wv, fmaxf(z, 0.f), s);
+        s = fmaf(wv, relu_bits(z), s);
       }
       if constexpr (HAS_MASK) s += to_f32(E{}, p.mask[(int64_t)row * p.S + j]);
       sc[j] = s;
@@ -424,7 +701,7 @@ __global__ __launch_bounds__(256) void indexer_fallback_kernel(const FallbackPar
 }
 
 __global__ void set_int_kernel(int* ptr, int value) {
-  if (threadIdx.x == 0 && blockIdx.x == 0) *ptr = value;
+  if (threadIdx.x < 2 && blockIdx.x == 0) ptr[threadIdx.x] = value;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -436,55 +713,79 @@ struct Plan {
   int Kk = 0;
   bool sample = false;
   int Ms = 0, rank = 0;
-  int nsplit = 1, split_len = 0, cap = kCapTotal;
+  int nsplit = 1, cap = 0;
   size_t off_tau = 0, off_samp = 0, off_counts = 0, off_cand = 0, off_fb = 0, off_fblist = 0,
-         off_scratch = 0, total = 0;
+         off_widelist = 0, off_scratch = 0, total = 0;
 };
 
-Plan make_plan(int64_t B, int64_t T, int64_t S, int64_t topk) {
+// Workspace layout (independent of the split count, which depends on the device).
+Plan make_layout(int64_t B, int64_t T, int64_t S, int64_t topk) {
   Plan pl;
   pl.Kk = (int)(topk < S ? topk : S);
-  pl.sample = S > kCapTotal;
+  pl.sample = S > kSubTotal / 2;
   if (pl.sample) {
     pl.Ms = (int)(S >= 65536 ? 4096 : 2048);
-    if (pl.Ms > S) pl.Ms = (int)S;
     const double lam = (double)pl.Kk * pl.Ms / (double)S;
     int r = (int)ceil(lam + 4.5 * sqrt(lam) + 2.0);
     pl.rank = r > pl.Ms ? pl.Ms : r;
-    const int64_t qtiles = ((T + kBM - 1) / kBM) * B;
-    int ns = (int)((1024 + qtiles - 1) / qtiles);
-    ns = ns < 1 ? 1 : (ns > kMaxSplit ? kMaxSplit : ns);
-    const int64_t max_by_len = (S + 1023) / 1024;  // keep >= ~1024 keys per split
-    if (ns > max_by_len) ns = (int)max_by_len;
-    int64_t len = (S + ns - 1) / ns;
-    len = (len + kBN - 1) / kBN * kBN;
-    pl.split_len = (int)len;
-    pl.nsplit = (int)((S + len - 1) / len);
-  } else {
-    pl.nsplit = 1;
-    pl.split_len = (int)((S + kBN - 1) / kBN * kBN);
   }
-  pl.cap = kCapTotal / pl.nsplit;
   const size_t rows = (size_t)B * (size_t)T;
   size_t off = 0;
   pl.off_tau = off;      off = align_up(off + rows * 4, 256);
   pl.off_samp = off;     off = align_up(off + (pl.sample ? rows * (size_t)pl.Ms * 4 : 0), 256);
-  pl.off_counts = off;   off = align_up(off + rows * pl.nsplit * 4, 256);
-  pl.off_cand = off;     off = align_up(off + rows * (size_t)pl.nsplit * pl.cap * 8, 256);
+  pl.off_counts = off;   off = align_up(off + rows * kMaxSplit * 32 * 4, 256);
+  pl.off_cand = off;     off = align_up(off + rows * (size_t)(kSubTotal + kMaxSplit * 32) * 8, 256);
   pl.off_fb = off;       off = align_up(off + 64, 256);
   pl.off_fblist = off;   off = align_up(off + rows * 4, 256);
+  pl.off_widelist = off; off = align_up(off + rows * 4, 256);
   pl.off_scratch = off;  off = align_up(off + (size_t)kFallbackBlocks * (size_t)S * 4, 256);
   pl.total = off;
   return pl;
 }
 
+// Concurrent workgroups of the filter kernel on the current device (cached per device).
+int filter_slots(const void* kernel) {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+  if (cache[dev] > 0) return cache[dev];
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu <= 0)
+    per_cu = 2;
+  cache[dev] = cus * per_cu;
+  return cache[dev];
+}
+
+// Picks the key split count: the fraction of the last wave of workgroups that is busy,
+// highest first, fewer splits on ties; each split keeps >= 8 stages of 64 keys.
+int choose_nsplit(int64_t tiles, int64_t S, int slots, bool sample) {
+  if (!sample) return 1;
+  int best = 1;
+  double best_eff = -1.0;
+  for (int ns = 1; ns <= kMaxSplit; ns <<= 1) {
+    if (ns > 1 && S / (ns * (int64_t)kBN) < 8) break;
+    const double waves = (double)(tiles * ns) / slots;
+    const double eff = waves / ceil(waves);
+    if (eff > best_eff + 1e-9) {
+      best_eff = eff;
+      best = ns;
+    }
+  }
+  return best;
+}
+
 template <typename E, int HI, bool HAS_MASK>
-int run_typed(const ScoreParams& base, const Plan& pl, int64_t B, int32_t* out_idx, void* out_scores,
+int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, void* out_scores,
               uint8_t* ws, hipStream_t st) {
-  int* fb_count = reinterpret_cast<int*>(ws + pl.off_fb);
+  int* fb_count = reinterpret_cast<int*>(ws + pl.off_fb);  // [0] brute force, [1] wide select
   hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(64), 0, st, fb_count, 0);
   GW_HIP_LAUNCH_CHECK("set_int_kernel");
-  const dim3 sgrid((base.T + kBM - 1) / kBM, 1, (unsigned)B);
+  const int64_t tiles = (base.T + kBM - 1) / kBM;
+  const int64_t rows = B * (int64_t)base.T;
+  pl.nsplit = choose_nsplit(tiles * B, base.S, filter_slots((const void*)indexer_score_kernel<E, HI, false, HAS_MASK>),
+                            pl.sample);
+  pl.cap = kSubTotal / (32 * pl.nsplit);
   float* tau = reinterpret_cast<float*>(ws + pl.off_tau);
   if (pl.sample) {
     ScoreParams sp = base;
@@ -492,40 +793,52 @@ int run_typed(const ScoreParams& base, const Plan& pl, int64_t B, int32_t* out_i
     sp.Ms = pl.Ms;
     sp.tau = nullptr;
     sp.tau_mode = kTauArray;
-    hipLaunchKernelGGL((indexer_score_kernel<E, HI, true, HAS_MASK>), sgrid, dim3(256), 0, st, sp);
+    sp.nsplit = 1;
+    sp.nstages = (pl.Ms + kBN - 1) / kBN;
+    hipLaunchKernelGGL((indexer_score_kernel<E, HI, true, HAS_MASK>), dim3((unsigned)tiles, 1, (unsigned)B), dim3(256),
+                       0, st, sp);
     GW_HIP_LAUNCH_CHECK("indexer_score_kernel<sample>");
-    SelectParams tp{};
-    tp.samp = sp.samp;
-    tp.Ms = pl.Ms;
-    tp.rank = pl.rank;
-    tp.tau = tau;
-    tp.T = base.T;
-    hipLaunchKernelGGL((indexer_select_kernel<E, false>), dim3(base.T, (unsigned)B), dim3(256), 0, st, tp);
-    GW_HIP_LAUNCH_CHECK("indexer_select_kernel<tau>");
+    const dim3 tgrid((unsigned)((rows + 3) / 4));
+    if (pl.Ms == 4096)
+      hipLaunchKernelGGL((indexer_tau_kernel<64>), tgrid, dim3(256), 0, st, sp.samp, pl.Ms, pl.rank, 8, tau, rows);
+    else
+      hipLaunchKernelGGL((indexer_tau_kernel<32>), tgrid, dim3(256), 0, st, sp.samp, pl.Ms, pl.rank, 8, tau, rows);
+    GW_HIP_LAUNCH_CHECK("indexer_tau_kernel");
   }
   ScoreParams fp = base;
   fp.tau = pl.sample ? tau : nullptr;
   fp.cand = reinterpret_cast<int2*>(ws + pl.off_cand);
   fp.counts = reinterpret_cast<int*>(ws + pl.off_counts);
   fp.nsplit = pl.nsplit;
-  fp.split_len = pl.split_len;
   fp.cap = pl.cap;
-  const dim3 fgrid((base.T + kBM - 1) / kBM, pl.nsplit, (unsigned)B);
-  hipLaunchKernelGGL((indexer_score_kernel<E, HI, false, HAS_MASK>), fgrid, dim3(256), 0, st, fp);
+  fp.nstages = (base.S + kBN - 1) / kBN;
+  hipLaunchKernelGGL((indexer_score_kernel<E, HI, false, HAS_MASK>),
+                     dim3((unsigned)tiles, (unsigned)pl.nsplit, (unsigned)B), dim3(256), 0, st, fp);
   GW_HIP_LAUNCH_CHECK("indexer_score_kernel<filter>");
   SelectParams fs{};
   fs.cand = fp.cand;
   fs.counts = fp.counts;
-  fs.nsplit = pl.nsplit;
+  fs.nsub = pl.nsplit * 32;
   fs.cap = pl.cap;
   fs.out_idx = out_idx;
   fs.out_scores = static_cast<uint16_t*>(out_scores);
   fs.Kk = pl.Kk;
   fs.fb_count = fb_count;
   fs.fb_list = reinterpret_cast<int*>(ws + pl.off_fblist);
-  fs.T = base.T;
-  hipLaunchKernelGGL((indexer_select_kernel<E, true>), dim3(base.T, (unsigned)B), dim3(256), 0, st, fs);
-  GW_HIP_LAUNCH_CHECK("indexer_select_kernel<final>");
+  fs.wide_count = fb_count + 1;
+  fs.wide_list = reinterpret_cast<int*>(ws + pl.off_widelist);
+  fs.rows = rows;
+  fs.force_wide = base.force_wide;
+  const dim3 sgrid2((unsigned)((rows + 3) / 4));
+  if (fs.nsub <= 64)
+    hipLaunchKernelGGL((indexer_select_kernel<E, 1>), sgrid2, dim3(256), 0, st, fs);
+  else if (fs.nsub == 128)
+    hipLaunchKernelGGL((indexer_select_kernel<E, 2>), sgrid2, dim3(256), 0, st, fs);
+  else
+    hipLaunchKernelGGL((indexer_select_kernel<E, 4>), sgrid2, dim3(256), 0, st, fs);
+  GW_HIP_LAUNCH_CHECK("indexer_select_kernel");
+  hipLaunchKernelGGL((indexer_select_wide_kernel<E>), dim3(kFallbackBlocks), dim3(256), 0, st, fs);
+  GW_HIP_LAUNCH_CHECK("indexer_select_wide_kernel");
   FallbackParams bp{};
   bp.q = base.q;
   bp.k = base.k;
@@ -561,7 +874,7 @@ int dispatch_hi(int hi, const ScoreParams& base, const Plan& pl, int64_t B, int3
 
 extern "C" size_t gw_indexer_topk_workspace_size(int64_t B, int64_t T, int64_t S, int64_t topk) {
   if (B <= 0 || T <= 0 || S <= 0 || topk <= 0) return 0;
-  return gw::make_plan(B, T, S, topk).total;
+  return gw::make_layout(B, T, S, topk).total;
 }
 
 extern "C" int gw_indexer_topk_fwd(int dtype, const void* q, const void* k, const void* w,
@@ -578,7 +891,7 @@ extern "C" int gw_indexer_topk_fwd(int dtype, const void* q, const void* k, cons
     return set_error(GW_ERR_UNSUPPORTED, "indexer heads x dim %lld x %lld not supported (1/2/4/8 x 64)",
                      (long long)Hi, (long long)Di);
   GW_CHECK_ARG(softmax_scale > 0.f, "softmax_scale must be positive, got %g", (double)softmax_scale);
-  GW_CHECK_ARG((flags & ~3) == 0 && flags != 3, "invalid flags %d", flags);
+  GW_CHECK_ARG((flags & ~7) == 0 && (flags & 3) != 3, "invalid flags %d", flags);
   if (B == 0 || T == 0) return GW_OK;
   GW_CHECK_ARG(S >= 1, "empty key set");
   const int64_t Kk = topk < S ? topk : S;
@@ -586,8 +899,9 @@ extern "C" int gw_indexer_topk_fwd(int dtype, const void* q, const void* k, cons
     return set_error(GW_ERR_UNSUPPORTED, "topk %lld exceeds the supported maximum %d", (long long)Kk, kMaxTopk);
   GW_CHECK_ARG(q && k && w && out_indices && out_scores, "null tensor pointer");
   GW_CHECK_ARG(aligned16(q) && aligned16(k), "q and k must be 16-byte aligned");
-  GW_CHECK_ARG(B <= 65535 && T < (1ll << 31) && S < (1ll << 30), "size exceeds grid or int32 range");
-  const Plan pl = make_plan(B, T, S, topk);
+  GW_CHECK_ARG(B <= 65535 && T < (1ll << 31) && S < (1ll << 30) && B * T < (1ll << 31),
+               "size exceeds grid or int32 range");
+  const Plan pl = make_layout(B, T, S, topk);
   GW_CHECK_ARG(workspace != nullptr && workspace_bytes >= pl.total, "workspace needs %zu bytes, got %zu",
                pl.total, workspace_bytes);
   GW_CHECK_ARG(gw::aligned16(workspace), "workspace must be 16-byte aligned");
@@ -603,6 +917,7 @@ extern "C" int gw_indexer_topk_fwd(int dtype, const void* q, const void* k, cons
   base.tau_mode = (flags & GW_TOPK_FLAG_TAU_PLUS_INF) ? kTauPlusInf
                   : (flags & GW_TOPK_FLAG_TAU_MINUS_INF) ? kTauMinusInf
                                                          : kTauArray;
+  base.force_wide = (flags & GW_TOPK_FLAG_FORCE_WIDE) ? 1 : 0;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool has_mask = mask != nullptr;

@@ -30,6 +30,7 @@ __all__ = ["sparse_topk_indexer_func", "sparse_topk_indexer_inference_func", "Sp
 
 FLAG_TAU_PLUS_INF = 1
 FLAG_TAU_MINUS_INF = 2
+FLAG_FORCE_WIDE = 4
 
 
 def _normalize_mask(mask: Optional[torch.Tensor], bsz: int, tgt_len: int, src_len: int, dtype):

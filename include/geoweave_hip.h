@@ -99,14 +99,17 @@ int gw_sparse_attn_fwd(int dtype,
  * q: [B,T,Hi,Di], k: [B,S,Hi,Di], w: [B,S,Hi], mask: [B,T,S], all contiguous, same dtype.
  * Supported: Di = 64, Hi in {1,2,4,8}, topk <= 2048, softmax_scale > 0.
  * workspace: gw_indexer_topk_workspace_size(B, T, S, topk) bytes, 16-byte aligned.
- * flags: 0 normally. Test hooks that force the exact brute-force path:
+ * flags: 0 normally. Test hooks that force the exact fallback paths:
  *   GW_TOPK_FLAG_TAU_PLUS_INF  - no key passes the candidate filter (every query falls
  *                                back to the brute-force path);
- *   GW_TOPK_FLAG_TAU_MINUS_INF - every key passes (candidate lists overflow when a key
- *                                split exceeds its capacity).
+ *   GW_TOPK_FLAG_TAU_MINUS_INF - every key passes (the per-query candidate lists overflow
+ *                                once S exceeds their 8192 slots: brute force again);
+ *   GW_TOPK_FLAG_FORCE_WIDE    - every query with complete candidates is selected by the
+ *                                LDS path meant for rows the register path cannot hold.
  */
 #define GW_TOPK_FLAG_TAU_PLUS_INF 1
 #define GW_TOPK_FLAG_TAU_MINUS_INF 2
+#define GW_TOPK_FLAG_FORCE_WIDE 4
 
 size_t gw_indexer_topk_workspace_size(int64_t B, int64_t T, int64_t S, int64_t topk);
 int gw_indexer_topk_fwd(int dtype, const void* q, const void* k, const void* w, const void* mask,

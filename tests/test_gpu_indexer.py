@@ -96,11 +96,19 @@ def test_additive_mask(gpu_device):
     _check(q, k, w, idx, sc, 400, mask=mask.float())
 
 
-@pytest.mark.parametrize("flags", [sti.FLAG_TAU_PLUS_INF, sti.FLAG_TAU_MINUS_INF])
-def test_forced_fallback_paths_are_exact(gpu_device, flags):
+@pytest.mark.parametrize("flags,tokens", [(sti.FLAG_TAU_PLUS_INF, None), (sti.FLAG_TAU_MINUS_INF, None),
+                                          (sti.FLAG_TAU_MINUS_INF, 12000), (sti.FLAG_FORCE_WIDE, None),
+                                          (sti.FLAG_FORCE_WIDE, 2000)])
+def test_forced_fallback_paths_are_exact(gpu_device, flags, tokens):
     # PLUS_INF: no candidate passes, every query takes the brute-force path.
-    # MINUS_INF: every key passes; the per-split lists (1024 slots for 1408 keys) overflow.
-    q, k, w = workloads.indexer_inputs(4, 1, torch.bfloat16)
+    # MINUS_INF at N=5496: every key is a candidate and the lists hold them all.
+    # MINUS_INF at N=12000: every key passes and the per-(query, column) lists
+    # (8192 slots per query) overflow, so every query takes the brute-force path.
+    # FORCE_WIDE: every query is selected by the LDS path (with sampling at N=5496,
+    # without at N=2000) instead of the register path.
+    q, k, w = workloads.indexer_inputs(4, 1, torch.bfloat16, tokens=tokens)
+    if tokens is not None:
+        q = q[:, :1024].contiguous()
     idx, sc = _gpu_topk(q, k, w, 1024, flags=flags)
     _check(q, k, w, idx, sc, 1024)
 
