@@ -176,6 +176,9 @@ def main() -> int:
     ap.add_argument("--with-attn-sum", action="store_true",
                     help="also time the training forward that writes attn_sum")
     ap.add_argument("--no-train", action="store_true", help="skip the C4 training-step timing")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run 3 plain device copies of 1 GiB (reference kernel for rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE scaling)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -309,6 +312,13 @@ def main() -> int:
         "timing": "HIP events on the launch stream; steady state, caches not flushed",
     }
     result.update(extra)
+    if args.calibrate_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if not args.no_train:
         del idx, o
         print("[bench] C4 training step", file=sys.stderr, flush=True)

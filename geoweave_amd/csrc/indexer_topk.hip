@@ -121,7 +121,7 @@ struct ScoreParams {
   const uint16_t* mask;  // [B, T, S] or null
   const float* tau;      // [B*T] or null (-inf)
   float* samp;           // SAMPLE: [B*T, Ms]
-  int2* cand;            // FILTER: [B*T, nsplit*32, cap+1] (slot cap: overflow sink)
+  int2* cand;            // FILTER: [B*T, nsplit, cap+1, 32] (slot cap: overflow sink)
   int* counts;           // FILTER: [B*T, nsplit*32] appends per sublist (may exceed cap)
   int T, S;
   int nsplit, cap;
@@ -197,22 +197,24 @@ __global__ __launch_bounds__(256, (HI <= 4 ? 2 : 1)) void indexer_score_kernel(c
     }
     tau_s[wave * kQW + lane] = tv;
   }
-  uint32_t cnt[16];  // appends so far x 8 (bytes)
+  uint32_t cnt[16];  // appends so far x 256 (bytes between slots)
 #pragma unroll
   for (int r = 0; r < 16; ++r) cnt[r] = 0;
 
-  // Sublist addressing (FILTER): element offset from the wave's base =
-  //   (row_in_wave * nsub + col) * SS + slot, row_in_wave = 8*(r/4) + 4*half + r%4.
+  // Candidate layout [row][split][slot][key column] (int2): the 32 columns of one slot are
+  // 256 contiguous bytes. Element offset from the wave's base =
+  //   row_in_wave * row_stride + slot * 32 + col, row_in_wave = 8*(r/4) + 4*half + r%4.
   const int nsub = nsplit * 32;
   const int SS = p.cap + 1;
   char* wbase = nullptr;       // uniform
   uint32_t lane_off = 0;       // bytes
   uint32_t row_step = 0;       // bytes per query row (uniform)
-  const uint32_t cap8 = (uint32_t)p.cap * 8u;
+  const uint32_t cap256 = (uint32_t)p.cap * 256u;
   if constexpr (!SAMPLE) {
-    wbase = reinterpret_cast<char*>(p.cand + ((int64_t)b * T + q0) * nsub * SS + (int64_t)split * 32 * SS);
-    row_step = (uint32_t)nsub * (uint32_t)SS * 8u;
-    lane_off = (uint32_t)(4 * half) * row_step + (uint32_t)col * (uint32_t)SS * 8u;
+    const int64_t row_stride = (int64_t)nsub * SS;  // int2 per query row
+    wbase = reinterpret_cast<char*>(p.cand + ((int64_t)b * T + q0) * row_stride + (int64_t)split * SS * 32);
+    row_step = (uint32_t)row_stride * 8u;
+    lane_off = (uint32_t)(4 * half) * row_step + (uint32_t)col * 8u;
   }
 
   // Loader geometry: load i of this thread fills LDS bytes [(i*4 + wave)*1024 + 16*lane, +16),
@@ -321,9 +323,9 @@ __global__ __launch_bounds__(256, (HI <= 4 ? 2 : 1)) void indexer_score_kernel(c
             const int r = 4 * g + j;
             if (s[r] >= tv[j]) {  // NaN (key past the end) never passes
               const uint32_t rr = (uint32_t)(8 * g + j);
-              const uint32_t off = lane_off + rr * row_step + min(cnt[r], cap8);
+              const uint32_t off = lane_off + rr * row_step + min(cnt[r], cap256);
               *reinterpret_cast<int2*>(wbase + off) = make_int2(__float_as_int(s[r]), key);
-              cnt[r] += 8u;
+              cnt[r] += 256u;
             }
           }
         }
@@ -340,7 +342,7 @@ __global__ __launch_bounds__(256, (HI <= 4 ? 2 : 1)) void indexer_score_kernel(c
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = q0 + 8 * (r / 4) + 4 * half + (r % 4);
-      if (row < T) p.counts[((int64_t)b * T + row) * nsub + split * 32 + col] = (int)(cnt[r] >> 3);
+      if (row < T) p.counts[((int64_t)b * T + row) * nsub + split * 32 + col] = (int)(cnt[r] >> 8);
     }
   }
 }
@@ -438,12 +440,14 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
   int cnt[NSEG];
   int stride = 1;
   bool bad = false;
+  // Sublist (split, col) of the row: slot m at row_base + (split * SS + m) * 32 + col.
+  const int2* row_base = p.cand + row * (int64_t)p.nsub * SS;
   if (p.nsub == 32) {
     const int sub = lane & 31, part = lane >> 5;
     const int cc = p.counts[row * 32 + sub];
     bad = cc > p.cap;
     const int c = min(cc, p.cap);
-    src[0] = p.cand + (row * 32 + sub) * SS + part;
+    src[0] = row_base + part * 32 + sub;
     cnt[0] = c > part ? (c - part + 1) / 2 : 0;
     stride = 2;
 #pragma unroll
@@ -458,7 +462,7 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
       const int cc = p.counts[row * p.nsub + sub];
       bad |= cc > p.cap;
       cnt[j] = min(cc, p.cap);
-      src[j] = p.cand + (row * p.nsub + sub) * SS;
+      src[j] = row_base + (int64_t)(sub >> 5) * SS * 32 + (sub & 31);
     }
   }
   int nl = 0, cmax_l = 0;
@@ -497,7 +501,7 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
 #pragma unroll
         for (int m = m0; m < min(m0 + 8, KS); ++m) {
           const bool live = m < cnt[j];
-          const uint32_t key = f2key(__int_as_float(src[j][(live ? m : 0) * stride].x));
+          const uint32_t key = f2key(__int_as_float(src[j][(live ? m : 0) * stride * 32].x));
           kv[j][m] = live ? key : 0u;
         }
       }
@@ -568,7 +572,7 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
           const int slot_out = base + lanes_below(selm);
           base += __popcll(selm);
           if (sel) {
-            const int2 cdt = src[j][m * stride];
+            const int2 cdt = src[j][m * stride * 32];
             oi[slot_out] = cdt.y;
             os[slot_out] = (uint16_t)pack1(E{}, __int_as_float(cdt.x));
           }
@@ -604,10 +608,10 @@ __global__ __launch_bounds__(256) void indexer_select_wide_kernel(const SelectPa
     __syncthreads();
     const int total = offs[p.nsub];
     for (int sub = tid; sub < p.nsub; sub += kSelThreads) {
-      const int2* src = p.cand + (row * p.nsub + sub) * SS;
+      const int2* src = p.cand + row * (int64_t)p.nsub * SS + (int64_t)(sub >> 5) * SS * 32 + (sub & 31);
       const int o = offs[sub], n = offs[sub + 1] - o;
       for (int i = 0; i < n; ++i) {
-        const int2 e = src[i];
+        const int2 e = src[(int64_t)i * 32];
         keys[o + i] = f2key(__int_as_float(e.x));
         vals[o + i] = e.y;
       }
