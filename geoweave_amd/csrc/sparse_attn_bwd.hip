@@ -12,14 +12,15 @@
 //
 // Two passes over the (t, j) pairs instead of one pass with fp32 atomics:
 //  dq pass  (query-major, the forward's layout: one wave per query and group of heads,
-//            gathering the selected K and V rows). It also writes total[b,t,h] for the
-//            key pass. With dattn, total is only known after the sweep, so the wave
-//            accumulates A1 = sum_j (dp_j) p_j k_s and A2 = sum_j p_j k_s and forms
+//            gathering the selected K and V rows). It also writes {lse * log2(e), total}
+//            per (b, t, h) for the key pass (one 8-byte load per entry there). With
+//            dattn, total is only known after the sweep, so the wave accumulates
+//            A1 = sum_j dp_j p_j k_s and A2 = sum_j p_j k_s and forms
 //            dq = scale * (A1 - total * A2) at the end: one K/V gather instead of the
 //            reference's two (:640-676 then :678-740).
 //  dkv pass (key-major over the CSR of kv_csr.hip: one wave per work item = up to 2048
 //            entries of one key, and group of heads). The key's K and V rows stay in
-//            registers; the wave gathers q, dO, lse and total of each entry's query,
+//            registers; the wave gathers q, dO and {lse, total} of each entry's query,
 //            recomputes p_j and ds_j, and accumulates dk and dv in fp32. A key whose
 //            entries span several items writes fp32 partials that a reduce kernel sums
 //            in item order.
@@ -43,7 +44,7 @@ struct AttnBwdParams {
   const uint16_t* dattn;  // [B, T, K] contiguous or null
   const int32_t* pos;
   const float* lse;  // [B, T, H]
-  float* total;      // [B, T, H]
+  float2* lse_tot;   // [B, T, H] {lse * log2(e), total}
   uint16_t* dq;
   uint16_t* dk;
   uint16_t* dv;
@@ -198,7 +199,7 @@ __global__ __launch_bounds__(256) void sparse_attn_bwd_dq_kernel(const AttnBwdPa
       out[i] = a * p.scale;
     }
     *reinterpret_cast<uint4*>(p.dq + b * p.dqsb + (int64_t)t * p.dqst + h * p.dqsh + c * 8) = pack8<E>(out);
-    if (c == 0) p.total[((int64_t)b * p.T + t) * p.H + h] = total;
+    if (c == 0) p.lse_tot[((int64_t)b * p.T + t) * p.H + h] = make_float2(lse2, total);
   }
 }
 
@@ -234,65 +235,57 @@ __global__ __launch_bounds__(256) void sparse_attn_bwd_dkv_kernel(const AttnBwdP
   }
   const uint16_t* qb = p.q + b * p.qsb + hs * p.qsh + c * 8;
   const uint16_t* dob = p.dout + b * p.dosb + hs * p.dosh + c * 8;
-  const float* lseb = p.lse + (int64_t)b * p.T * p.H + hs;
-  const float* totb = p.total + (int64_t)b * p.T * p.H + hs;
+  const float2* ltb = p.lse_tot + (int64_t)b * p.T * p.H + hs;
   const uint16_t* dab = DATTN ? p.dattn + (int64_t)b * p.T * p.K : nullptr;
 
   float ak[8], av[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) ak[i] = av[i] = 0.f;
 
-  struct Slot {
-    uint4 q, d;
-    float lse2, tot, da;
-    bool ok;
-  };
-  auto load = [&](Slot (&sl)[U], int i0) {
+  // Entries of the next block are prefetched; the q/dO/{lse,total} gathers of a block are
+  // issued together at the top of its iteration (other waves cover their latency).
+  int2 en[U];
+  auto load_entries = [&](int2 (&ee)[U], int i0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int i = i0 + u * G + g;
-      Slot& x = sl[u];
-      x.ok = i < it.end;
-      if (x.ok) {
-        const int2 e = p.csr.entries[i];
-        const int64_t tt = e.x;
-        x.q = *reinterpret_cast<const uint4*>(qb + tt * p.qst);
-        x.d = *reinterpret_cast<const uint4*>(dob + tt * p.dost);
-        x.lse2 = lseb[tt * p.H] * kLog2e;
-        x.tot = totb[tt * p.H];
-        x.da = DATTN ? to_f32(E{}, dab[tt * p.K + e.y]) : 0.f;
-      } else {
-        x.q = x.d = make_uint4(0, 0, 0, 0);
-        x.lse2 = 0.f;
-        x.tot = 0.f;
-        x.da = 0.f;
-      }
+      ee[u] = i < it.end ? p.csr.entries[i] : make_int2(-1, 0);
     }
   };
-
-  Slot cur[U];
-  load(cur, it.beg);
+  load_entries(en, it.beg);
   for (int i0 = it.beg; i0 < it.end; i0 += STEP) {
-    Slot nxt[U];
-    load(nxt, i0 + STEP);
+    int2 ec[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) ec[u] = en[u];
+    load_entries(en, i0 + STEP);
+    uint4 qv[U], dv[U];
+    float2 lt[U];
+    float da[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const Slot& x = cur[u];
-      const float sd = group_sum<LPH>(dot8<E>(x.q, kv));
-      const float pj = (x.ok && head_ok) ? fexp2(sd * p.scale_log2 - x.lse2) : 0.f;
-      const float dp = group_sum<LPH>(dot8<E>(vv, x.d)) + x.da;
-      const float ds = (dp - x.tot) * pj;
+      const bool ok = ec[u].x >= 0;
+      const int64_t tt = ok ? ec[u].x : 0;
+      qv[u] = *reinterpret_cast<const uint4*>(qb + tt * p.qst);
+      dv[u] = *reinterpret_cast<const uint4*>(dob + tt * p.dost);
+      lt[u] = ltb[tt * p.H];
+      da[u] = (DATTN && ok) ? to_f32(E{}, dab[tt * p.K + ec[u].y]) : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool ok = ec[u].x >= 0 && head_ok;
+      const float sd = group_sum<LPH>(dot8<E>(qv[u], kv));
+      const float pj = ok ? fexp2(sd * p.scale_log2 - lt[u].x) : 0.f;
+      const float dp = group_sum<LPH>(dot8<E>(vv, dv[u])) + da[u];
+      const float ds = (dp - lt[u].y) * pj;
       float qf[8], df[8];
-      unpack8<E>(x.q, qf);
-      unpack8<E>(x.d, df);
+      unpack8<E>(qv[u], qf);
+      unpack8<E>(dv[u], df);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         ak[i] = fmaf(ds, qf[i], ak[i]);
         av[i] = fmaf(pj, df[i], av[i]);
       }
     }
-#pragma unroll
-    for (int u = 0; u < U; ++u) cur[u] = nxt[u];
   }
 
 #pragma unroll
@@ -389,14 +382,14 @@ int pow2_ceil(int x) {
 }
 
 struct BwdWs {
-  size_t total_off, part_off, bytes;
+  size_t lt_off, part_off, bytes;
 };
 
 BwdWs bwd_ws(int64_t B, int64_t T, int64_t S, int64_t H, int64_t D, int64_t K) {
   BwdWs w;
   const CsrLayout L = csr_layout(B, T, S, K);
-  w.total_off = 0;
-  w.part_off = ((size_t)B * T * H * 4 + 255) / 256 * 256;
+  w.lt_off = 0;
+  w.part_off = ((size_t)B * T * H * 8 + 255) / 256 * 256;
   w.bytes = w.part_off + (size_t)L.max_parts * 2 * H * D * 4;
   return w;
 }
@@ -460,7 +453,7 @@ extern "C" int gw_sparse_attn_bwd(int dtype, const void* q, const int64_t* q_str
   p.pos = kv_pos;
   p.lse = lse;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
-  p.total = reinterpret_cast<float*>(ws + w.total_off);
+  p.lse_tot = reinterpret_cast<float2*>(ws + w.lt_off);
   p.part = reinterpret_cast<float*>(ws + w.part_off);
   p.dq = static_cast<uint16_t*>(dq);
   p.dk = static_cast<uint16_t*>(dk);
