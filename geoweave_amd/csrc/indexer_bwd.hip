@@ -67,30 +67,47 @@ __global__ __launch_bounds__(256) void indexer_bwd_dq_kernel(const IdxBwdParams 
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
 
-  struct Slot {
+  // Three-stage pipeline: indices (and gradients) two blocks ahead, key rows and gates
+  // one block ahead, compute on the current block.
+  struct Idx {
+    int s;
+    float g;
+  };
+  struct Row {
     uint4 k;
     float gw;  // g * w * scale
   };
-  auto load = [&](Slot (&sl)[U], int j0) {
+  auto load_idx = [&](Idx (&xi)[U], int j0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int j = j0 + u * G + g;
-      Slot& x = sl[u];
       const int s = j < p.K ? irow[j] : -1;
-      if (s >= 0 && s < p.S) {
-        x.k = *reinterpret_cast<const uint4*>(kb + (int64_t)s * HI * kDI);
-        x.gw = to_f32(E{}, grow[j]) * to_f32(E{}, wb[(int64_t)s * HI]) * p.scale;
+      xi[u].s = (s >= 0 && s < p.S) ? s : -1;
+      xi[u].g = j < p.K ? to_f32(E{}, grow[j]) : 0.f;
+    }
+  };
+  auto load_row = [&](Row (&xr)[U], const Idx (&xi)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = xi[u].s;
+      if (s >= 0) {
+        xr[u].k = *reinterpret_cast<const uint4*>(kb + (int64_t)s * HI * kDI);
+        xr[u].gw = xi[u].g * to_f32(E{}, wb[(int64_t)s * HI]) * p.scale;
       } else {
-        x.k = make_uint4(0, 0, 0, 0);
-        x.gw = 0.f;
+        xr[u].k = make_uint4(0, 0, 0, 0);
+        xr[u].gw = 0.f;
       }
     }
   };
-  Slot cur[U];
-  load(cur, 0);
+  Idx in[U];
+  Row cur[U];
+  load_idx(in, 0);
+  load_row(cur, in);
+  load_idx(in, STEP);
   for (int j0 = 0; j0 < p.K; j0 += STEP) {
-    Slot nxt[U];
-    load(nxt, j0 + STEP);
+    Row nxt[U];
+    load_row(nxt, in);
+    load_idx(in, j0 + 2 * STEP);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const float z = group_sum<8>(dot8<E>(qv, cur[u].k)) * p.scale;

@@ -143,51 +143,54 @@ constexpr int kRadixBits = 6;
 constexpr int kRadixBins = 1 << kRadixBits;
 constexpr int kRadixPasses = 6;  // 36 bits cover any t*K + j < 2^31
 
-union SortShared {
-  uint64_t buf[kSortCap];                 // bitonic path
-  int hist[kRadixBins * 256];             // radix path: hist[digit * 256 + thread]
-};
+// Sorts each key's entries by (t, j), in two kernels so that the common short lists do
+// not pay for the long-list histogram's LDS. Lists of up to kSortCap entries are sorted in
+// LDS with a bitonic network (csr_sort_short_kernel). Longer ones (keys chosen by very many
+// queries) go through a stable LSD radix sort on t*K + j, one workgroup per key
+// (csr_sort_long_kernel): every thread owns a contiguous sub-range, per-thread digit counts
+// are scanned digit-major, and each thread scatters its sub-range in order, so every pass
+// is stable. The passes alternate between the list and the same range of `scratch` and
+// end in the list.
+__global__ __launch_bounds__(256) void csr_sort_short_kernel(const int* off, int nk, int2* entries) {
+  __shared__ uint64_t buf[kSortCap];
+  const int key = blockIdx.x;
+  if (key >= nk) return;
+  const int beg = off[key], n = off[key + 1] - beg;
+  if (n <= 1 || n > kSortCap) return;
+  const int tid = threadIdx.x;
+  int2* seg = entries + beg;
+  int np = 1;
+  while (np < n) np <<= 1;
+  for (int i = tid; i < np; i += 256) buf[i] = i < n ? pack_tj(seg[i]) : ~0ull;
+  __syncthreads();
+  for (int size = 2; size <= np; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = tid; i < np / 2; i += 256) {
+        const int lo = 2 * i - (i & (stride - 1));
+        const int hi = lo + stride;
+        const bool up = (lo & size) == 0;
+        const uint64_t x = buf[lo], y = buf[hi];
+        if ((x > y) == up) {
+          buf[lo] = y;
+          buf[hi] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int i = tid; i < n; i += 256) seg[i] = unpack_tj(buf[i]);
+}
 
-// Sorts each key's entries by (t, j). Segments of up to kSortCap entries are sorted in
-// LDS with a bitonic network. Longer ones (keys chosen by very many queries) go through
-// a stable LSD radix sort on t*K + j, one workgroup per key: every thread owns a
-// contiguous sub-range, per-thread digit counts are scanned digit-major, and each thread
-// scatters its sub-range in order, so every pass is stable. The passes alternate
-// between the segment and the same range of `scratch` and end in the segment.
-__global__ __launch_bounds__(256) void csr_sort_kernel(const int* off, int nk, int K, int2* entries,
-                                                       int2* scratch) {
-  __shared__ SortShared sm;
+__global__ __launch_bounds__(256) void csr_sort_long_kernel(const int* off, int nk, int K, int2* entries,
+                                                            int2* scratch) {
+  __shared__ int hist[kRadixBins * 256];  // hist[digit * 256 + thread]
   __shared__ int wave_tot[4];
   const int key = blockIdx.x;
   if (key >= nk) return;
   const int beg = off[key], n = off[key + 1] - beg;
-  if (n <= 1) return;
+  if (n <= kSortCap) return;
   const int tid = threadIdx.x;
   int2* seg = entries + beg;
-  if (n <= kSortCap) {
-    int np = 1;
-    while (np < n) np <<= 1;
-    uint64_t* buf = sm.buf;
-    for (int i = tid; i < np; i += 256) buf[i] = i < n ? pack_tj(seg[i]) : ~0ull;
-    __syncthreads();
-    for (int size = 2; size <= np; size <<= 1) {
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        for (int i = tid; i < np / 2; i += 256) {
-          const int lo = 2 * i - (i & (stride - 1));
-          const int hi = lo + stride;
-          const bool up = (lo & size) == 0;
-          const uint64_t x = buf[lo], y = buf[hi];
-          if ((x > y) == up) {
-            buf[lo] = y;
-            buf[hi] = x;
-          }
-        }
-        __syncthreads();
-      }
-    }
-    for (int i = tid; i < n; i += 256) seg[i] = unpack_tj(buf[i]);
-    return;
-  }
   const int per = (n + 255) / 256;
   const int i0 = min(n, tid * per), i1 = min(n, i0 + per);
   int2* src = seg;
@@ -195,17 +198,17 @@ __global__ __launch_bounds__(256) void csr_sort_kernel(const int* off, int nk, i
   const int lane = tid & 63, wave = tid >> 6;
   for (int pass = 0; pass < kRadixPasses; ++pass) {
     const int shift = pass * kRadixBits;
-    for (int d = 0; d < kRadixBins; ++d) sm.hist[d * 256 + tid] = 0;
+    for (int d = 0; d < kRadixBins; ++d) hist[d * 256 + tid] = 0;
     for (int i = i0; i < i1; ++i) {
       const int2 e = src[i];
       const uint32_t kv = (uint32_t)e.x * (uint32_t)K + (uint32_t)e.y;
-      sm.hist[((kv >> shift) & (kRadixBins - 1)) * 256 + tid] += 1;
+      hist[((kv >> shift) & (kRadixBins - 1)) * 256 + tid] += 1;
     }
     __syncthreads();
     // Exclusive scan of hist in flat (digit-major) order: thread x owns cells
     // [x * kRadixBins, (x + 1) * kRadixBins).
     int local = 0;
-    for (int c = 0; c < kRadixBins; ++c) local += sm.hist[tid * kRadixBins + c];
+    for (int c = 0; c < kRadixBins; ++c) local += hist[tid * kRadixBins + c];
     int incl = local;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -217,15 +220,15 @@ __global__ __launch_bounds__(256) void csr_sort_kernel(const int* off, int nk, i
     int run = incl - local;
     for (int w = 0; w < wave; ++w) run += wave_tot[w];
     for (int c = 0; c < kRadixBins; ++c) {
-      const int v = sm.hist[tid * kRadixBins + c];
-      sm.hist[tid * kRadixBins + c] = run;
+      const int v = hist[tid * kRadixBins + c];
+      hist[tid * kRadixBins + c] = run;
       run += v;
     }
     __syncthreads();
     for (int i = i0; i < i1; ++i) {
       const int2 e = src[i];
       const uint32_t kv = (uint32_t)e.x * (uint32_t)K + (uint32_t)e.y;
-      int& slot = sm.hist[((kv >> shift) & (kRadixBins - 1)) * 256 + tid];
+      int& slot = hist[((kv >> shift) & (kRadixBins - 1)) * 256 + tid];
       dst[slot] = e;
       ++slot;
     }
@@ -330,7 +333,9 @@ extern "C" int gw_kv_csr_build(const int32_t* pos, int64_t pos_stride_b, int64_t
   hipLaunchKernelGGL(csr_fill_kernel, egrid, dim3(256), 0, st, pos, pos_stride_b, pos_stride_t, (int)T, (int)S,
                      (int)K, n, count, off, entries);
   GW_HIP_LAUNCH_CHECK("csr_fill_kernel");
-  hipLaunchKernelGGL(csr_sort_kernel, dim3(nk), dim3(256), 0, st, off, nk, (int)K, entries, scratch);
-  GW_HIP_LAUNCH_CHECK("csr_sort_kernel");
+  hipLaunchKernelGGL(csr_sort_short_kernel, dim3(nk), dim3(256), 0, st, off, nk, entries);
+  GW_HIP_LAUNCH_CHECK("csr_sort_short_kernel");
+  hipLaunchKernelGGL(csr_sort_long_kernel, dim3(nk), dim3(256), 0, st, off, nk, (int)K, entries, scratch);
+  GW_HIP_LAUNCH_CHECK("csr_sort_long_kernel");
   return GW_OK;
 }
