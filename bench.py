@@ -66,14 +66,16 @@ def read_traffic_summary(path: Path):
 def train_step_c4(steps: int = 5, warmup: int = 2, views: int = 24, batch: int = 2, topk: int = 1024):
     """Config C4: one training step of the layer's hot path through autograd, B=2, S=24
     views (N=32,976), bf16: indexer top-k forward, sparse attention forward with
-    attn_sum, a loss over o, attn_sum and the top-k scores (the KL-loss path's inputs),
-    and the backward of both (CSR build, attention dq/dkv, indexer dq/dkw). Times each
+    attn_sum, the indexer KL loss on the layer's normalised attention mass
+    (dsa_attention.py:5395-5411: attn cast to q's dtype, p = attn / (sum + eps),
+    sparse_indexer_kl_loss(p, topk_scores)), and the backward of o (a random dO) and of
+    the KL loss (KL backward, CSR build, attention dq/dkv, indexer dq/dkw). Times each
     phase with HIP events on the launch stream."""
     import torch
 
     from geoweave_amd import _csr, workloads
     from geoweave_amd.custom_flash_attn.sparse_index_flash_attn import sparse_index_flash_attn_func
-    from geoweave_amd.custom_indexer import sparse_topk_indexer_func
+    from geoweave_amd.custom_indexer import sparse_indexer_kl_loss, sparse_topk_indexer_func
 
     dev = torch.device("cuda", 0)
     lay = workloads.layer_inputs(views, batch, torch.bfloat16)
@@ -81,9 +83,8 @@ def train_step_c4(steps: int = 5, warmup: int = 2, views: int = 24, batch: int =
     g = torch.Generator().manual_seed(views)
     B, T, H, D = q.shape
     do = torch.randn(B, T, H, D, generator=g).bfloat16().to(dev)
-    dattn = torch.randn(B, T, topk, generator=g).to(dev)
-    gsc = torch.randn(B, T, topk, generator=g).bfloat16().to(dev)
     stream = torch.cuda.current_stream(dev)
+    eps = 1e-6
 
     def one(ev=None):
         for x in (qi, ki, wi, q, k, v):
@@ -95,7 +96,63 @@ def train_step_c4(steps: int = 5, warmup: int = 2, views: int = 24, batch: int =
         o, attn = sparse_index_flash_attn_func(q, k, v, idx, None, False, 0.125)
         if ev:
             ev[1].record(stream)
-        torch.autograd.backward([o, attn, sc], [do, dattn, gsc])
+        p = attn.to(q.dtype)
+        p = p / (p.sum(dim=-1, keepdim=True) + eps)
+        kl = sparse_indexer_kl_loss(p, sc, eps)
+        if ev:
+            ev[2].record(stream)
+        torch.autograd.backward([o, kl], [do, None])
+        if ev:
+            ev[3].record(stream)
+
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    for i in range(steps):
+        one(evs[i])
+    torch.cuda.synchronize()
+    fwd = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+    kl_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
+    bwd = statistics.mean(e[2].elapsed_time(e[3]) for e in evs)
+    gather = batch * T * topk * H * D * 2 * 2
+    return {
+        "workload": f"C4 training step: B={batch}, S={views} views (N={T}), H={H}, D={D}, top-k {topk}, bf16, "
+                    "indexer + attention forward (attn_sum on), indexer KL loss, backward through autograd",
+        "fwd_ms": round(fwd, 3),
+        "kl_loss_fwd_ms": round(kl_ms, 3),
+        "bwd_ms": round(bwd, 3),
+        "step_ms": round(fwd + kl_ms + bwd, 3),
+        "attn_gathered_bytes_fwd": gather,
+        "attn_gathered_bytes_bwd": 2 * gather,
+    }
+
+
+def long_context_c3(steps: int = 5, warmup: int = 2, views: int = 64, topk: int = 1024):
+    """Config C3: the inference step (indexer top-k + sparse attention forward) at S=64
+    views (N=87,936), B=1, bf16; HIP-event timing per phase on the launch stream."""
+    import torch
+
+    from geoweave_amd import workloads
+    from geoweave_amd.custom_flash_attn.sparse_index_flash_attn import (
+        sparse_index_flash_attn_inference_func,
+    )
+    from geoweave_amd.custom_indexer import sparse_topk_indexer_inference_func
+
+    dev = torch.device("cuda", 0)
+    lay = workloads.layer_inputs(views, 1, torch.bfloat16)
+    qi, ki, wi, q, k, v = (x.to(dev) for x in (lay.q_idx, lay.k_idx, lay.w_idx, lay.q, lay.k, lay.v))
+    del lay
+    stream = torch.cuda.current_stream(dev)
+    empty_mask = qi.new_empty(0)
+
+    def one(ev=None):
+        if ev:
+            ev[0].record(stream)
+        idx, _ = sparse_topk_indexer_inference_func(qi, ki, wi, empty_mask, topk, 0.125, 256, 0)
+        if ev:
+            ev[1].record(stream)
+        sparse_index_flash_attn_inference_func(q, k, v, idx, softmax_scale=0.125)
         if ev:
             ev[2].record(stream)
 
@@ -106,17 +163,18 @@ def train_step_c4(steps: int = 5, warmup: int = 2, views: int = 24, batch: int =
     for i in range(steps):
         one(evs[i])
     torch.cuda.synchronize()
-    fwd = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
-    bwd = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
-    gather = batch * T * topk * H * D * 2 * 2
+    idx_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+    att_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
+    B, T, H, D = q.shape
+    att_bytes = attn_fwd_algorithmic_bytes(B, T, H, D, topk)
     return {
-        "workload": f"C4 training step: B={batch}, S={views} views (N={T}), H={H}, D={D}, top-k {topk}, bf16, "
-                    "indexer + attention forward (attn_sum on) and backward through autograd",
-        "fwd_ms": round(fwd, 3),
-        "bwd_ms": round(bwd, 3),
-        "step_ms": round(fwd + bwd, 3),
-        "attn_gathered_bytes_fwd": gather,
-        "attn_gathered_bytes_bwd": 2 * gather,
+        "workload": f"C3 long context: B=1, S={views} views (N={T}), H={H}, D={D}, top-k {topk}, bf16, "
+                    "indexer + sparse attention forward",
+        "value_ms": round(idx_ms + att_ms, 3),
+        "indexer_ms": round(idx_ms, 3),
+        "attn_fwd_ms": round(att_ms, 3),
+        "attn_fwd_gbs": round(att_bytes / (att_ms * 1e-3) / 1e9, 1),
+        "indexer_tflops": round(indexer_algorithmic_flops(B, T, T, qi.shape[2], qi.shape[3]) / (idx_ms * 1e-3) / 1e12, 2),
     }
 
 
@@ -176,6 +234,7 @@ def main() -> int:
     ap.add_argument("--with-attn-sum", action="store_true",
                     help="also time the training forward that writes attn_sum")
     ap.add_argument("--no-train", action="store_true", help="skip the C4 training-step timing")
+    ap.add_argument("--no-long", action="store_true", help="skip the C3 (S=64) long-context timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run 3 plain device copies of 1 GiB (reference kernel for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE scaling)")
@@ -319,6 +378,10 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if not args.no_long:
+        print("[bench] C3 long context", file=sys.stderr, flush=True)
+        result["long_context_c3"] = long_context_c3()
+        torch.cuda.empty_cache()
     if not args.no_train:
         del idx, o
         print("[bench] C4 training step", file=sys.stderr, flush=True)

@@ -17,6 +17,7 @@ LIB_PATH = Path(__file__).resolve().with_name("libgeoweave_hip.so")
 GW_OK = 0
 GW_DTYPE_BF16 = 0
 GW_DTYPE_FP16 = 1
+GW_DTYPE_FP32 = 2
 
 _i64 = ctypes.c_int64
 _p = ctypes.c_void_p
@@ -53,6 +54,11 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.c_int, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
          ctypes.c_float, _p, _sz, _p, _sz, _p],
+    ),
+    "gw_indexer_kl_fwd": (ctypes.c_int, [ctypes.c_int, _p, _p, _i64, _i64, ctypes.c_float, _p, _p]),
+    "gw_indexer_kl_bwd": (
+        ctypes.c_int,
+        [ctypes.c_int, _p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _p],
     ),
 }
 

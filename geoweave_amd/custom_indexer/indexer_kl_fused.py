@@ -1,0 +1,104 @@
+"""Indexer KL training loss on gfx950: the drop-in for the reference module
+``easyvolcap/utils/custom_indexer/indexer_kl_fused.py``.
+
+``sparse_indexer_kl_loss(attn_sum, logits, eps=1e-6) -> fp32 scalar`` (reference ``:285-298``):
+the mean over the ``B*T`` rows of ``KL(p || softmax(logits))`` with ``p = attn_sum /
+(attn_sum.sum(-1) + eps)`` and ``log(p + eps)`` in the entropy term, differentiable w.r.t.
+``attn_sum`` and ``logits``. The DSA layer calls it with ``p`` = the attention mass each
+query puts on its top-k keys and ``logits`` = the indexer's top-k scores
+(``easyvolcap/official_vggt/layers/dsa_attention.py:4688-4715``).
+
+Differences from the reference, all at its edges: it falls back to a torch formula for CPU
+tensors and shape mismatches (``:286-295``); here those raise, since this package has no
+CPU path. The backward reads ``dL/dloss`` on the device instead of calling ``.item()``
+(``:252``), so it does not synchronise the host.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+__all__ = ["sparse_indexer_kl_loss", "SparseIndexerKLLossFunc"]
+
+
+def _dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return _lib.GW_DTYPE_FP32
+    return _lib.dtype_code(dtype)
+
+
+def _prepare(attn_sum: torch.Tensor, logits: torch.Tensor):
+    if not (torch.is_tensor(attn_sum) and torch.is_tensor(logits)):
+        raise TypeError("attn_sum and logits must be tensors")
+    if attn_sum.dim() != 3 or tuple(attn_sum.shape) != tuple(logits.shape):
+        raise ValueError(
+            f"attn_sum {tuple(attn_sum.shape)} and logits {tuple(logits.shape)} must be equal [B, T, K]"
+        )
+    if not (attn_sum.is_cuda and logits.is_cuda):
+        raise ValueError("attn_sum and logits must be GPU tensors")
+    # reference: indexer_kl_fused.py:167-172 (contiguous rows, logits cast to attn's dtype)
+    attn_sum = attn_sum.contiguous()
+    logits = logits.to(attn_sum.dtype).contiguous()
+    return attn_sum, logits
+
+
+def kl_loss_forward(attn_sum: torch.Tensor, logits: torch.Tensor, eps: float) -> torch.Tensor:
+    """Per-row losses, fp32 ``[B*T]`` (gw_indexer_kl_fwd on the current stream)."""
+    rows = attn_sum.shape[0] * attn_sum.shape[1]
+    K = attn_sum.shape[2]
+    row_loss = torch.empty(rows, device=attn_sum.device, dtype=torch.float32)
+    lib = _lib.load()
+    _lib.check(
+        lib.gw_indexer_kl_fwd(
+            _dtype_code(attn_sum.dtype), attn_sum.data_ptr(), logits.data_ptr(), rows, K, float(eps),
+            row_loss.data_ptr(), _lib.stream_handle(attn_sum.device),
+        ),
+        "gw_indexer_kl_fwd",
+    )
+    return row_loss
+
+
+def kl_loss_backward(attn_sum: torch.Tensor, logits: torch.Tensor, grad_out: torch.Tensor, eps: float):
+    """(d_attn, d_logits) in the input dtype; ``grad_out`` is dL/dloss on the device."""
+    rows = attn_sum.shape[0] * attn_sum.shape[1]
+    K = attn_sum.shape[2]
+    g = grad_out.detach().reshape(()).to(device=attn_sum.device, dtype=torch.float32).contiguous()
+    d_attn = torch.empty_like(attn_sum)
+    d_logits = torch.empty_like(logits)
+    lib = _lib.load()
+    _lib.check(
+        lib.gw_indexer_kl_bwd(
+            _dtype_code(attn_sum.dtype), attn_sum.data_ptr(), logits.data_ptr(), g.data_ptr(), rows, K,
+            float(eps), d_attn.data_ptr(), d_logits.data_ptr(), _lib.stream_handle(attn_sum.device),
+        ),
+        "gw_indexer_kl_bwd",
+    )
+    return d_attn, d_logits
+
+
+class SparseIndexerKLLossFunc(torch.autograd.Function):
+    """Autograd wrapper (reference ``_SparseIndexerKLLossFunc``, ``indexer_kl_fused.py:164-282``)."""
+
+    @staticmethod
+    def forward(ctx, attn_sum: torch.Tensor, logits: torch.Tensor, eps: float):
+        a, z = _prepare(attn_sum, logits)
+        row_loss = kl_loss_forward(a, z, eps)
+        ctx.save_for_backward(a, z)
+        ctx.eps = float(eps)
+        ctx.logits_dtype = logits.dtype
+        return row_loss.mean()
+
+    @staticmethod
+    def backward(ctx, grad_out: torch.Tensor):
+        a, z = ctx.saved_tensors
+        d_attn, d_logits = kl_loss_backward(a, z, grad_out, ctx.eps)
+        return d_attn, d_logits.to(ctx.logits_dtype), None
+
+
+def sparse_indexer_kl_loss(attn_sum: torch.Tensor, logits: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """Mean KL(p || softmax(logits)) over rows (reference ``indexer_kl_fused.py:285-298``)."""
+    if torch.is_tensor(attn_sum) and attn_sum.numel() == 0 and attn_sum.dim() == 3:
+        # reference: indexer_kl_fused.py:296-297
+        return attn_sum.new_zeros(())
+    return SparseIndexerKLLossFunc.apply(attn_sum, logits, float(eps))

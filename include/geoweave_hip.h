@@ -35,6 +35,7 @@ extern "C" {
 
 #define GW_DTYPE_BF16 0
 #define GW_DTYPE_FP16 1
+#define GW_DTYPE_FP32 2 /* accepted only by the gw_indexer_kl_* entry points */
 
 /* Message for the last failed call on this thread ("" if none). */
 const char* gw_last_error(void);
@@ -200,6 +201,27 @@ int gw_indexer_topk_bwd(int dtype, const void* q, const void* k, const void* w,
                         const void* csr, size_t csr_bytes,
                         void* workspace, size_t workspace_bytes,
                         void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * Indexer KL training loss, forward and backward.
+ *
+ * Replaces sparse_indexer_kl_loss / _SparseIndexerKLLossFunc
+ * (easyvolcap/utils/custom_indexer/indexer_kl_fused.py:164-298: _kl_stats_kernel +
+ * _kl_row_loss_kernel forward, _kl_row_bwd_kernel backward), the fused form of the loss
+ * the DSA layer computes at easyvolcap/official_vggt/layers/dsa_attention.py:4688-4715.
+ * attn_sum and logits: contiguous [rows, K] in one dtype (bf16, fp16 or fp32; the
+ * reference casts logits to attn_sum's dtype, indexer_kl_fused.py:171-172); math in fp32.
+ * Per row: p = attn / (sum attn + eps), lq = log_softmax(logits),
+ * row_loss[r] = sum_j p_j (log(p_j + eps) - lq_j) (fp32). The loss is mean(row_loss).
+ * Backward: grad_out is a device fp32 scalar dL/dloss (read on the device: no host
+ * synchronisation, where the reference calls .item(), indexer_kl_fused.py:252);
+ * d_attn, d_logits: [rows, K] in the input dtype. K <= 4096.
+ */
+int gw_indexer_kl_fwd(int dtype, const void* attn_sum, const void* logits, int64_t rows, int64_t K,
+                      float eps, float* row_loss, void* stream);
+int gw_indexer_kl_bwd(int dtype, const void* attn_sum, const void* logits, const float* grad_out,
+                      int64_t rows, int64_t K, float eps, void* d_attn, void* d_logits,
+                      void* stream);
 
 #ifdef __cplusplus
 }

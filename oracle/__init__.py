@@ -17,6 +17,9 @@ torch`` path (reference: ``geoweave/inference.py:56-58`` sets ``use_topk_kernel=
 * ``attention.sparse_attention``: gathered sparse softmax attention with invalid-position
   masking and ``attn_sum`` (reference ``tests/sparse_index_flash_attn_tests.py:47-71``,
   ``easyvolcap/official_vggt/layers/dsa_attention.py:4717-4753,1774-1816``);
+* ``kl_loss.kl_row_losses`` / ``kl_loss.kl_loss_bwd``: the indexer KL training loss and its
+  explicit gradient (reference ``easyvolcap/utils/custom_indexer/indexer_kl_fused.py:8-298``),
+  pinned by scipy.stats.entropy (eps = 0), autograd and finite differences;
 * ``attention.sparse_attention_bwd``: explicit backward formulas of the reference kernel
   (reference ``easyvolcap/utils/custom_flash_attn/sparse_index_flash_attn.py:534-743``),
   cross-checked against autograd on the forward restatement.

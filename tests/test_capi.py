@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.gw_abi_version() == 100
+    assert lib.gw_abi_version() == 101
 
 
 def test_one_hip_runtime_in_process():
@@ -90,7 +90,8 @@ def test_python_preconditions_match_reference_errors():
 
 def test_dropin_modules_export_every_name_the_reference_callers_import():
     # easyvolcap/official_vggt/layers/dsa_attention.py:29-45 imports these six names in one
-    # try block; easyvolcap/official_vggt/layers/indexer.py:10-14 imports these two.
+    # try block and :24-27 the KL loss; easyvolcap/official_vggt/layers/indexer.py:10-14
+    # imports the two top-k entries.
     from geoweave_amd.custom_flash_attn import sparse_index_flash_attn as m
     from geoweave_amd import custom_indexer
 
@@ -101,3 +102,18 @@ def test_dropin_modules_export_every_name_the_reference_callers_import():
     assert m.sparse_index_flash_attn_value_gate_bhtd_func is None
     assert callable(custom_indexer.sparse_topk_indexer_func)
     assert callable(custom_indexer.sparse_topk_indexer_inference_func)
+    assert callable(custom_indexer.sparse_indexer_kl_loss)
+
+
+def test_kl_loss_rejects_cpu_tensors_and_shape_mismatch():
+    # The reference falls back to a torch formula here (indexer_kl_fused.py:286-295); this
+    # package has no CPU path, so it raises instead.
+    from geoweave_amd.custom_indexer import sparse_indexer_kl_loss
+
+    a = torch.rand(1, 3, 8)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        sparse_indexer_kl_loss(a, torch.randn(1, 3, 8))
+    with pytest.raises(ValueError, match="must be equal"):
+        sparse_indexer_kl_loss(a, torch.randn(1, 3, 9))
+    empty = torch.zeros(1, 0, 8)
+    assert float(sparse_indexer_kl_loss(empty, empty)) == 0.0

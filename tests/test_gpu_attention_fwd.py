@@ -127,7 +127,7 @@ def test_inference_entry_and_stream(gpu_device):
     torch.testing.assert_close(o.float().cpu(), ro, **TOL)
 
 
-@pytest.mark.parametrize("views", [16])
+@pytest.mark.parametrize("views", [16, 64])
 def test_full_size_sampled_rows(gpu_device, views):
     # Full layer size: exact comparison on a sample of query rows plus the
     # size-independent invariant sum_j attn_sum[t, j] = H on every row.

@@ -151,3 +151,16 @@ def test_full_size_sampled_rows(gpu_device, views):
     assert bool((srt[:, 1:] != srt[:, :-1]).all()), "duplicate index in a row"
     rows = torch.randperm(n, generator=torch.Generator().manual_seed(views))[:384]
     _check(q, k, w, idx, sc, 1024, rows=rows)
+
+
+def test_long_context_s64_sampled_rows(gpu_device):
+    # Config C3 size (N = 87936, the 4096-key sample path): exact check on 192 random
+    # rows, plus in-range / distinct indices on every row.
+    q, k, w = workloads.indexer_inputs(64, 1, torch.bfloat16)
+    n = q.shape[1]
+    idx, sc = _gpu_topk(q, k, w, 1024)
+    assert int(idx.min()) >= 0 and int(idx.max()) < n
+    srt = idx[0].long().sort(-1).values
+    assert bool((srt[:, 1:] != srt[:, :-1]).all()), "duplicate index in a row"
+    rows = torch.randperm(n, generator=torch.Generator().manual_seed(64))[:192]
+    _check(q, k, w, idx, sc, 1024, rows=rows)

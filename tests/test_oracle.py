@@ -259,3 +259,92 @@ def test_key_subset_backward_helpers_match_full_backward():
     hk, hw = oidx.indexer_topk_bwd_keys(q, k, w, pos, gs, keys, 0.3)
     torch.testing.assert_close(hk, ik[:, keys], atol=1e-5, rtol=1e-5)
     torch.testing.assert_close(hw, iw[:, keys], atol=1e-5, rtol=1e-5)
+
+
+def test_kl_oracle_forward_equals_scipy_entropy_and_brute_force():
+    # eps = 0 reduces the row loss to the textbook KL(p || softmax(z)) = scipy.stats.entropy.
+    from scipy.stats import entropy
+    from oracle import kl_loss as okl
+
+    g = torch.Generator().manual_seed(11)
+    a = torch.rand(2, 3, 17, generator=g, dtype=torch.float64) + 1e-3
+    z = torch.randn(2, 3, 17, generator=g, dtype=torch.float64) * 3
+    rows = okl.kl_row_losses(a, z, eps=0.0)
+    for r, (ar, zr) in enumerate(zip(a.reshape(-1, 17), z.reshape(-1, 17))):
+        q = torch.softmax(zr, -1)
+        assert abs(float(rows[r]) - entropy(ar.numpy(), q.numpy())) < 1e-12
+    # eps > 0: a pure-Python loop over the reference's per-element formula
+    # (indexer_kl_fused.py:76-91) with log-sum-exp written out.
+    eps = 1e-2
+    ar = [float(x) for x in a[1, 2]]
+    zr = [float(x) for x in z[1, 2]]
+    tot = sum(ar)
+    lse = math.log(sum(math.exp(x) for x in zr))
+    want = sum((x / (tot + eps)) * (math.log(x / (tot + eps) + eps) - (y - lse)) for x, y in zip(ar, zr))
+    assert abs(float(okl.kl_row_losses(a, z, eps)[5]) - want) < 1e-12
+    assert abs(float(okl.kl_loss(a, z, eps)) - float(okl.kl_row_losses(a, z, eps).mean())) < 1e-15
+
+
+def test_kl_oracle_invariants():
+    from oracle import kl_loss as okl
+
+    g = torch.Generator().manual_seed(12)
+    z = torch.randn(1, 4, 32, generator=g, dtype=torch.float64)
+    # p == softmax(z) and eps -> 0: the loss vanishes and so does d_logits.
+    p = torch.softmax(z, -1)
+    assert float(okl.kl_loss(p, z, eps=0.0).abs()) < 1e-14
+    _, dz = okl.kl_loss_bwd(p, z, 1.0, eps=0.0)
+    assert float(dz.abs().max()) < 1e-14
+    # a shift of the logits per row changes nothing; with eps = 0 neither does a scale of attn.
+    a = torch.rand(1, 4, 32, generator=g, dtype=torch.float64)
+    base = okl.kl_row_losses(a, z, 0.0)
+    assert torch.allclose(okl.kl_row_losses(a, z + torch.randn(1, 4, 1, generator=g, dtype=torch.float64) * 50, 0.0), base, atol=1e-11)
+    assert torch.allclose(okl.kl_row_losses(a * 7.5, z, 0.0), base, atol=1e-12)
+    # KL >= 0 (Gibbs).
+    assert float(base.min()) >= -1e-14
+    # d_logits sums to zero per row; d_attn is orthogonal to attn when eps = 0 (scale invariance).
+    da, dz = okl.kl_loss_bwd(a, z, 1.0, eps=0.0)
+    assert float(dz.sum(-1).abs().max()) < 1e-15
+    assert float((da * a).sum(-1).abs().max()) < 1e-14
+
+
+def test_kl_oracle_backward_matches_autograd_and_finite_differences():
+    from oracle import kl_loss as okl
+
+    g = torch.Generator().manual_seed(13)
+    eps = 1e-3
+    a = (torch.rand(2, 3, 9, generator=g, dtype=torch.float64) * torch.rand(2, 3, 1, generator=g, dtype=torch.float64))
+    a[0, 1, :4] = 0.0  # zero mass entries, where log(p + eps) matters
+    z = torch.randn(2, 3, 9, generator=g, dtype=torch.float64) * 2
+    ag = a.clone().requires_grad_(True)
+    zg = z.clone().requires_grad_(True)
+    # autograd through the reference's torch formula (indexer_kl_fused.py:158-161)
+    p = ag / (ag.sum(-1, keepdim=True) + eps)
+    loss = (p * (torch.log(p + eps) - torch.log_softmax(zg, -1))).sum(-1).mean()
+    (loss * 2.5).backward()
+    da, dz = okl.kl_loss_bwd(a, z, 2.5, eps)
+    torch.testing.assert_close(da, ag.grad, rtol=1e-10, atol=1e-13)
+    # The reference's d_logits is gs * (softmax(z) - p) (indexer_kl_fused.py:152); the exact
+    # derivative is gs * (softmax(z) * sum(p) - p) with sum(p) = S / (S + eps) < 1. The
+    # oracle follows the reference; the difference is exactly gs * softmax(z) * (sum(p) - 1).
+    gs = 2.5 / 6
+    sum_p = (a / (a.sum(-1, keepdim=True) + eps)).sum(-1, keepdim=True)
+    dz_exact = dz + gs * torch.softmax(z, -1) * (sum_p - 1)
+    torch.testing.assert_close(dz_exact, zg.grad, rtol=1e-10, atol=1e-13)
+    assert float((dz - zg.grad).abs().max()) > 1e-5  # the omitted factor is visible here
+    # with eps = 0 the reference's formula is the exact gradient
+    zg0 = z.clone().requires_grad_(True)
+    p0 = a / a.sum(-1, keepdim=True)
+    ((p0 * (torch.log(p0) .nan_to_num(neginf=0.0) - torch.log_softmax(zg0, -1))).sum(-1).mean() * 2.5).backward()
+    torch.testing.assert_close(okl.kl_loss_bwd(a, z, 2.5, 0.0)[1], zg0.grad, rtol=1e-10, atol=1e-13)
+    # central differences on a few coordinates
+    h = 1e-6
+    for idx in [(0, 0, 0), (0, 1, 2), (1, 2, 8)]:
+        for t, d in ((a, da), (z, dz_exact)):
+            tp, tm = t.clone(), t.clone()
+            tp[idx] += h
+            tm[idx] -= h
+            args_p = (tp, z) if t is a else (a, tp)
+            args_m = (tm, z) if t is a else (a, tm)
+            fd = (float(okl.kl_loss(*args_p, eps)) - float(okl.kl_loss(*args_m, eps))) / (2 * h) * 2.5
+            assert abs(fd - float(d[idx])) < 1e-6 * max(1.0, abs(fd))
