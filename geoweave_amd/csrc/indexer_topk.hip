@@ -40,6 +40,8 @@
 // over the splits, so every sublist receives about (candidates / (32 * nsplit)) entries.
 #include <math.h>
 
+#include <mutex>
+
 #include "gw_common.h"
 #include "gw_select.h"
 
@@ -47,14 +49,20 @@ namespace gw {
 namespace {
 
 constexpr int kQW = 32;            // queries per wave
-constexpr int kWaves = 4;
-constexpr int kBM = kQW * kWaves;  // queries per workgroup
 constexpr int kBN = 64;            // keys per LDS stage (and split interleave granule)
 constexpr int kDI = 64;            // indexer head dim
 constexpr int kSubTotal = 8192;    // candidate slots per query over all sublists
 constexpr int kMaxSplit = 8;
 constexpr int kMaxTopk = 2048;
 constexpr int kFallbackBlocks = 256;
+// Candidate layout: query rows are grouped 32 at a time (rows of one batch element, T
+// padded to a multiple of 32); group g holds [split][slot (cap + 1)][row (32)][key column
+// (32)] int2 {score bits, key}, so slot m of sublist (split, col) for the group's row rr
+// is at ((split * SS + m) * 32 + rr) * 32 + col. Slot cap is the overflow sink. One
+// wave's 32 query rows are one group: an append advances its offset by a fixed 8 KB and
+// the row enters as a constant, which keeps the epilogue's address math to one min.
+constexpr int kCandGroupRows = 32;
+constexpr int kCandSlotInt2 = kCandGroupRows * 32;  // int2 per slot of a group
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -121,9 +129,10 @@ struct ScoreParams {
   const uint16_t* mask;  // [B, T, S] or null
   const float* tau;      // [B*T] or null (-inf)
   float* samp;           // SAMPLE: [B*T, Ms]
-  int2* cand;            // FILTER: [B*T, nsplit, cap+1, 32] (slot cap: overflow sink)
+  int2* cand;            // FILTER: candidate groups, see kCandGroupRows
   int* counts;           // FILTER: [B*T, nsplit*32] appends per sublist (may exceed cap)
   int T, S;
+  int Tp;                // T rounded up to kCandGroupRows
   int nsplit, cap;
   int nstages;           // 64-key stages of the sweep
   int Ms;
@@ -147,19 +156,34 @@ __device__ __forceinline__ int sweep_key(int i, const ScoreParams& p) {
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
 
+// Workgroup shape of the score kernel: NW waves of 32 queries share every key tile (a
+// key tile read from L2 serves NW * 32 queries). HI <= 4 keeps its register file within
+// 256 per lane, so 8 waves (two per SIMD) fit one workgroup; HI = 8 needs 4.
+template <int HI>
+struct ScoreShape {
+  static constexpr int NW = HI <= 4 ? 8 : 4;
+  static constexpr int BM = NW * kQW;        // queries per workgroup
+  static constexpr int THREADS = NW * 64;
+  static constexpr int MIN_WAVES_PER_EU = HI <= 4 ? 2 : 1;
+};
+
 template <typename E, int HI, bool SAMPLE, bool HAS_MASK>
-__global__ __launch_bounds__(256, (HI <= 4 ? 2 : 1)) void indexer_score_kernel(const ScoreParams p) {
+__global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_PER_EU) void indexer_score_kernel(
+    const ScoreParams p) {
+  constexpr int NW = ScoreShape<HI>::NW;
+  constexpr int BM = ScoreShape<HI>::BM;
+  constexpr int THREADS = ScoreShape<HI>::THREADS;
   constexpr int ROW_BYTES = HI * kDI * 2;
   constexpr int CHUNKS = ROW_BYTES / 16;              // 16-byte chunks per key row (>= 8)
   constexpr int TILE_BYTES = kBN * ROW_BYTES;
-  constexpr int LOADS = TILE_BYTES / (256 * 16);      // direct loads per thread per stage
+  constexpr int LOADS = TILE_BYTES / (THREADS * 16);  // direct loads per thread per stage
   constexpr int WVALS = kBN * HI;
-  constexpr int WLOADS = (WVALS + 255) / 256;
-  static_assert(LOADS * 256 * 16 == TILE_BYTES, "key tile must split evenly over the threads");
+  constexpr int WLOADS = (WVALS + THREADS - 1) / THREADS;
+  static_assert(LOADS * THREADS * 16 == TILE_BYTES, "key tile must split evenly over the threads");
 
   __shared__ __attribute__((aligned(16))) uint8_t ktile[2][TILE_BYTES];
   __shared__ float wtile[2][WVALS];
-  __shared__ __attribute__((aligned(16))) float tau_s[kBM];
+  __shared__ __attribute__((aligned(16))) float tau_s[BM];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -167,7 +191,7 @@ __global__ __launch_bounds__(256, (HI <= 4 ? 2 : 1)) void indexer_score_kernel(c
   const int b = blockIdx.z;
   const int split = SAMPLE ? 0 : (int)blockIdx.y;
   const int nsplit = SAMPLE ? 1 : p.nsplit;
-  const int q0 = blockIdx.x * kBM + wave * kQW;
+  const int q0 = blockIdx.x * BM + wave * kQW;
   const int T = p.T, S = p.S;
   const int nkeys = SAMPLE ? p.Ms : S;
   const int col = lane & 31;
@@ -197,68 +221,88 @@ __global__ __launch_bounds__(256, (HI <= 4 ? 2 : 1)) void indexer_score_kernel(c
     }
     tau_s[wave * kQW + lane] = tv;
   }
-  uint32_t cnt[16];  // appends so far x 256 (bytes between slots)
-#pragma unroll
-  for (int r = 0; r < 16; ++r) cnt[r] = 0;
-
-  // Candidate layout [row][split][slot][key column] (int2): the 32 columns of one slot are
-  // 256 contiguous bytes. Element offset from the wave's base =
-  //   row_in_wave * row_stride + slot * 32 + col, row_in_wave = 8*(r/4) + 4*half + r%4.
+  // The wave's 32 rows are candidate group (b * Tp + q0) / 32. Row rr = 8*(r/4) + 4*half
+  // + r%4 of accumulator element r sits at byte (split*SS + slot) * 8192 + rr * 256 +
+  // col * 8 of the group; cnt[r] is this lane's byte offset of the next slot (the
+  // slot index times 8192 plus lane_base, so the clamp to the sink is one min).
   const int nsub = nsplit * 32;
   const int SS = p.cap + 1;
-  char* wbase = nullptr;       // uniform
-  uint32_t lane_off = 0;       // bytes
-  uint32_t row_step = 0;       // bytes per query row (uniform)
-  const uint32_t cap256 = (uint32_t)p.cap * 256u;
+  char* wbase = nullptr;   // uniform
+  uint32_t lane_base = 0, lim = 0;
   if constexpr (!SAMPLE) {
-    const int64_t row_stride = (int64_t)nsub * SS;  // int2 per query row
-    wbase = reinterpret_cast<char*>(p.cand + ((int64_t)b * T + q0) * row_stride + (int64_t)split * SS * 32);
-    row_step = (uint32_t)row_stride * 8u;
-    lane_off = (uint32_t)(4 * half) * row_step + (uint32_t)col * 8u;
+    const int64_t group = ((int64_t)b * p.Tp + q0) / kCandGroupRows;
+    wbase = reinterpret_cast<char*>(p.cand + group * ((int64_t)nsplit * SS * kCandSlotInt2));
+    lane_base = (uint32_t)split * (uint32_t)SS * 8192u + (uint32_t)half * 1024u + (uint32_t)col * 8u;
+    lim = lane_base + (uint32_t)p.cap * 8192u;
   }
-
-  // Loader geometry: load i of this thread fills LDS bytes [(i*4 + wave)*1024 + 16*lane, +16),
-  // which hold chunk (pc) of key row (kl); the source is logical chunk pc ^ (kl & 7).
-  int ld_kl[LOADS], ld_lc[LOADS];
+  uint32_t cnt[16];
 #pragma unroll
-  for (int i = 0; i < LOADS; ++i) {
-    const int pos = (i * 4 + wave) * 1024 + 16 * lane;
-    ld_kl[i] = pos / ROW_BYTES;
-    ld_lc[i] = ((pos % ROW_BYTES) / 16) ^ (ld_kl[i] & 7);
-  }
+  for (int r = 0; r < 16; ++r) cnt[r] = lane_base;
+
+  // Loader geometry: load i of this thread fills LDS bytes [(i*NW + wave)*1024 + 16*lane, +16),
+  // which hold physical chunk lane % CHUNKS of key row kl0 + i*RPI; its source is logical
+  // chunk (lane % CHUNKS) ^ (row & 7). kl0 < RPI and RPI is a power of two, so (row & 7)
+  // differs from (kl0 & 7) by the constant XOR (i*RPI) & 7 (0 unless HI = 8).
+  constexpr int RPW = 1024 / ROW_BYTES;  // key rows per 1 KB wave chunk
+  constexpr int RPI = NW * RPW;          // key rows per load step
+  const int kl0 = wave * RPW + (lane * 16) / ROW_BYTES;
+  const int lc0 = (lane % CHUNKS) ^ (kl0 & 7);
+  const uint32_t voff0 = (uint32_t)(kl0 * ROW_BYTES + lc0 * 16);
+  const uint32_t voff1 = (uint32_t)(kl0 * ROW_BYTES + (lc0 ^ (RPI & 7)) * 16);
   // Operand read offsets: key row (nb*32 + col), logical chunk h*8 + 2*ks + half.
   uint32_t rd_off[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) rd_off[ks] = col * ROW_BYTES + 16 * ((2 * ks + half) ^ (col & 7));
 
-  float wreg[WLOADS];
-  // Keys past the end: K rows are loaded from the last valid key (harmless), and the gate
-  // is NaN (FILTER: the score is NaN and fails every `>= tau`) or 0 (SAMPLE: not stored).
+  // Gate values travel as raw 16-bit patterns until wstore converts them at the end of the
+  // stage: converting at load time would make the wave wait (vmcnt) for the key tile
+  // loads issued just before. Keys past the end: K rows are loaded from the last valid key
+  // (harmless), and the gate is NaN (FILTER: the score is NaN and fails every `>= tau`)
+  // or 0 (SAMPLE: not stored).
+  constexpr uint32_t kNoGate = 0xFFFFFFFFu;
+  uint32_t wraw[WLOADS];
   auto gload = [&](int kb, int buf) {
     const int live = min(kBN, nkeys - kb);
+    if (!SAMPLE && live == kBN) {
+      // Full stage of consecutive keys: uniform base + lane offset + i * NW KB.
+      const char* kbase = reinterpret_cast<const char*>(p.k + ((int64_t)b * S + kb) * (HI * kDI));
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int kl = min(ld_kl[i], live - 1);
-      const int key = sweep_key<SAMPLE>(kb + kl, p);
-      const uint16_t* src = p.k + ((int64_t)b * S + key) * (HI * kDI) + ld_lc[i] * 8;
-      __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(&ktile[buf][(i * 4 + wave) * 1024]), 16, 0, 0);
+      for (int i = 0; i < LOADS; ++i) {
+        const char* src = kbase + i * (NW * 1024) + (((i * RPI) & 7) ? voff1 : voff0);
+        __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(&ktile[buf][(i * NW + wave) * 1024]), 16, 0, 0);
+      }
+    } else {
+      // Sample keys or the last stage: rows past the end re-read the last valid key.
+#pragma unroll
+      for (int i = 0; i < LOADS; ++i) {
+        const int kl = min(kl0 + i * RPI, live - 1);
+        const int key = sweep_key<SAMPLE>(kb + kl, p);
+        const int lc = lc0 ^ ((i * RPI) & 7);
+        const uint16_t* src = p.k + ((int64_t)b * S + key) * (HI * kDI) + lc * 8;
+        __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(&ktile[buf][(i * NW + wave) * 1024]), 16, 0, 0);
+      }
     }
 #pragma unroll
     for (int i = 0; i < WLOADS; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + THREADS * i;
       const int kl = c / HI, h = c % HI;
-      float wv = SAMPLE ? 0.f : __builtin_nanf("");
+      uint32_t wv = kNoGate;
       if (c < WVALS && kl < live) {
         const int key = sweep_key<SAMPLE>(kb + kl, p);
-        wv = to_f32(E{}, p.w[((int64_t)b * S + key) * HI + h]) * p.scale;
+        wv = p.w[((int64_t)b * S + key) * HI + h];
       }
-      wreg[i] = wv;
+      wraw[i] = wv;
     }
   };
   auto wstore = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < WLOADS; ++i)
-      if (tid + 256 * i < WVALS) wtile[buf][tid + 256 * i] = wreg[i];
+    for (int i = 0; i < WLOADS; ++i) {
+      if (tid + THREADS * i < WVALS) {
+        const float wv = wraw[i] == kNoGate ? (SAMPLE ? 0.f : __builtin_nanf(""))
+                                            : to_f32(E{}, (uint16_t)wraw[i]) * p.scale;
+        wtile[buf][tid + THREADS * i] = wv;
+      }
+    }
   };
 
   int st = split;
@@ -269,80 +313,107 @@ __global__ __launch_bounds__(256, (HI <= 4 ? 2 : 1)) void indexer_score_kernel(c
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct LDS loads have landed
   __syncthreads();
 
+  // Appends of one 32-key tile (FILTER). The second tile of a stage is appended one
+  // iteration late, after the stage-end vmcnt(0) + barrier: vmcnt counts stores as well
+  // as the direct LDS loads it waits for, so every store issued before that wait is
+  // followed by at least one tile of MFMA work rather than waited on at once.
+  float tau_r[16];  // thresholds of this lane's 16 rows (filled after the first barrier)
+  auto append = [&](const float (&sv)[16], int key) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 4 * g + j;
+        if (sv[r] >= tau_r[r]) {  // NaN (key past the end) never passes
+          char* wb = wbase + (8 * g + j) * 256;
+          *reinterpret_cast<int2*>(wb + min(cnt[r], lim)) = make_int2(__float_as_int(sv[r]), key);
+          cnt[r] += 8192u;
+        }
+      }
+    }
+  };
+  // Scores of the tile of 32 keys at kb + nb*32 (+ mask); SAMPLE stores them directly.
+  auto tile_scores = [&](float (&s)[16], int kb, int nb, int buf) {
+    const int kl = nb * 32 + col;
+    const uint8_t* tile = &ktile[buf][nb * 32 * ROW_BYTES];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = 0.f;
+#pragma unroll
+    for (int h = 0; h < HI; ++h) {
+      f32x16 acc = f32x16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const uint4 bop = *reinterpret_cast<const uint4*>(tile + rd_off[ks] + h * 128);
+        acc = mfma32(E{}, a[h][ks], bop, acc);
+      }
+      const float wv = wtile[buf][kl * HI + h];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = fmaf(wv, relu_bits(acc[r]), s[r]);
+    }
+    const int kidx = kb + kl;
+    const bool kvalid = kidx < nkeys;
+    const int key = sweep_key<SAMPLE>(kidx, p);
+    if constexpr (HAS_MASK) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = q0 + 8 * (r / 4) + 4 * half + (r % 4);
+        if (kvalid && row < T) s[r] += to_f32(E{}, p.mask[((int64_t)b * T + row) * S + key]);
+      }
+    }
+    if constexpr (SAMPLE) {
+      if (kvalid) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = q0 + 8 * (r / 4) + 4 * half + (r % 4);
+          if (row < T) p.samp[((int64_t)b * T + row) * p.Ms + kidx] = s[r];
+        }
+      }
+    }
+  };
+  static_assert(kBN == 64, "two 32-key tiles per stage");
+
+  if constexpr (!SAMPLE) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 t4 = *reinterpret_cast<const float4*>(&tau_s[wave * kQW + 8 * g + 4 * half]);
+      tau_r[4 * g + 0] = t4.x;
+      tau_r[4 * g + 1] = t4.y;
+      tau_r[4 * g + 2] = t4.z;
+      tau_r[4 * g + 3] = t4.w;
+    }
+  }
+  float sp[16];      // FILTER: scores of the pending tile
+  int key_prev = -1; // uniform >= 0: key column base of the pending tile (+ col per lane)
   int buf = 0;
   for (; st < p.nstages; st += nsplit) {
     const int kb = st * kBN;
     const bool more = st + nsplit < p.nstages;
     if (more) gload((st + nsplit) * kBN, buf ^ 1);
-
-#pragma unroll
-    for (int nb = 0; nb < kBN / 32; ++nb) {
-      const int kl = nb * 32 + col;
-      const uint8_t* tile = &ktile[buf][nb * 32 * ROW_BYTES];
-      float s[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = 0.f;
-#pragma unroll
-      for (int h = 0; h < HI; ++h) {
-        f32x16 acc = f32x16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const uint4 bop = *reinterpret_cast<const uint4*>(tile + rd_off[ks] + h * 128);
-          acc = mfma32(E{}, a[h][ks], bop, acc);
-        }
-        const float wv = wtile[buf][kl * HI + h];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[r] = fmaf(wv, relu_bits(acc[r]), s[r]);
-      }
-      const int kidx = kb + kl;
-      const bool kvalid = kidx < nkeys;
-      const int key = sweep_key<SAMPLE>(kidx, p);
-
-      if constexpr (HAS_MASK) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = q0 + 8 * (r / 4) + 4 * half + (r % 4);
-          if (kvalid && row < T) s[r] += to_f32(E{}, p.mask[((int64_t)b * T + row) * S + key]);
-        }
-      }
-      if constexpr (SAMPLE) {
-        if (kvalid) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int row = q0 + 8 * (r / 4) + 4 * half + (r % 4);
-            if (row < T) p.samp[((int64_t)b * T + row) * p.Ms + kidx] = s[r];
-          }
-        }
-      } else {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const float4 t4 = *reinterpret_cast<const float4*>(&tau_s[wave * kQW + 8 * g + 4 * half]);
-          const float tv[4] = {t4.x, t4.y, t4.z, t4.w};
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int r = 4 * g + j;
-            if (s[r] >= tv[j]) {  // NaN (key past the end) never passes
-              const uint32_t rr = (uint32_t)(8 * g + j);
-              const uint32_t off = lane_off + rr * row_step + min(cnt[r], cap256);
-              *reinterpret_cast<int2*>(wbase + off) = make_int2(__float_as_int(s[r]), key);
-              cnt[r] += 256u;
-            }
-          }
-        }
-      }
+    if constexpr (!SAMPLE) {
+      if (key_prev >= 0) append(sp, key_prev + col);
     }
+    float s0[16];
+    tile_scores(s0, kb, 0, buf);
+    if constexpr (!SAMPLE) append(s0, kb + col);
+    tile_scores(sp, kb, 1, buf);
+    key_prev = kb + 32;
 
+    // Keep the gate conversion (which waits for this stage's loads) after the tile work.
+    __builtin_amdgcn_sched_barrier(0);
     if (more) wstore(buf ^ 1);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): next stage's direct LDS loads have landed
     __syncthreads();
     buf ^= 1;
+  }
+  if constexpr (!SAMPLE) {
+    if (key_prev >= 0) append(sp, key_prev + col);
   }
 
   if constexpr (!SAMPLE) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = q0 + 8 * (r / 4) + 4 * half + (r % 4);
-      if (row < T) p.counts[((int64_t)b * T + row) * nsub + split * 32 + col] = (int)(cnt[r] >> 8);
+      if (row < T) p.counts[((int64_t)b * T + row) * nsub + split * 32 + col] = (int)((cnt[r] - lane_base) >> 13);
     }
   }
 }
@@ -400,6 +471,7 @@ struct SelectParams {
   const int2* cand;
   const int* counts;
   int nsub, cap;
+  int T, Tp;
   int32_t* out_idx;
   uint16_t* out_scores;
   int Kk;
@@ -410,6 +482,15 @@ struct SelectParams {
   int64_t rows;
   int force_wide;  // test hook: every complete row takes the LDS selection
 };
+
+// First element of a row's candidates: slot m of sublist (split, col) is at
+// + (split * SS + m) * kCandSlotInt2 + col.
+__device__ __forceinline__ const int2* cand_row(const SelectParams& p, int64_t row) {
+  const int64_t b = row / p.T, t = row - b * p.T;
+  const int64_t crow = b * p.Tp + t;
+  const int SS = p.cap + 1;
+  return p.cand + (crow / kCandGroupRows) * ((int64_t)p.nsub * SS * kCandGroupRows) + (crow % kCandGroupRows) * 32;
+}
 
 // Exclusive prefix over the wave of x; `total` receives the wave sum.
 __device__ __forceinline__ int wave_excl_scan(int x, int& total) {
@@ -440,14 +521,14 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
   int cnt[NSEG];
   int stride = 1;
   bool bad = false;
-  // Sublist (split, col) of the row: slot m at row_base + (split * SS + m) * 32 + col.
-  const int2* row_base = p.cand + row * (int64_t)p.nsub * SS;
+  // Sublist (split, col) of the row: slot m at row_base + (split * SS + m) * kCandSlotInt2 + col.
+  const int2* row_base = cand_row(p, row);
   if (p.nsub == 32) {
     const int sub = lane & 31, part = lane >> 5;
     const int cc = p.counts[row * 32 + sub];
     bad = cc > p.cap;
     const int c = min(cc, p.cap);
-    src[0] = row_base + part * 32 + sub;
+    src[0] = row_base + part * kCandSlotInt2 + sub;
     cnt[0] = c > part ? (c - part + 1) / 2 : 0;
     stride = 2;
 #pragma unroll
@@ -462,7 +543,7 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
       const int cc = p.counts[row * p.nsub + sub];
       bad |= cc > p.cap;
       cnt[j] = min(cc, p.cap);
-      src[j] = row_base + (int64_t)(sub >> 5) * SS * 32 + (sub & 31);
+      src[j] = row_base + (int64_t)(sub >> 5) * SS * kCandSlotInt2 + (sub & 31);
     }
   }
   int nl = 0, cmax_l = 0;
@@ -501,7 +582,7 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
 #pragma unroll
         for (int m = m0; m < min(m0 + 8, KS); ++m) {
           const bool live = m < cnt[j];
-          const uint32_t key = f2key(__int_as_float(src[j][(live ? m : 0) * stride * 32].x));
+          const uint32_t key = f2key(__int_as_float(src[j][(live ? m : 0) * stride * kCandSlotInt2].x));
           kv[j][m] = live ? key : 0u;
         }
       }
@@ -572,7 +653,7 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
           const int slot_out = base + lanes_below(selm);
           base += __popcll(selm);
           if (sel) {
-            const int2 cdt = src[j][m * stride * 32];
+            const int2 cdt = src[j][m * stride * kCandSlotInt2];
             oi[slot_out] = cdt.y;
             os[slot_out] = (uint16_t)pack1(E{}, __int_as_float(cdt.x));
           }
@@ -608,10 +689,10 @@ __global__ __launch_bounds__(256) void indexer_select_wide_kernel(const SelectPa
     __syncthreads();
     const int total = offs[p.nsub];
     for (int sub = tid; sub < p.nsub; sub += kSelThreads) {
-      const int2* src = p.cand + row * (int64_t)p.nsub * SS + (int64_t)(sub >> 5) * SS * 32 + (sub & 31);
+      const int2* src = cand_row(p, row) + (int64_t)(sub >> 5) * SS * kCandSlotInt2 + (sub & 31);
       const int o = offs[sub], n = offs[sub + 1] - o;
       for (int i = 0; i < n; ++i) {
-        const int2 e = src[(int64_t)i * 32];
+        const int2 e = src[(int64_t)i * kCandSlotInt2];
         keys[o + i] = f2key(__int_as_float(e.x));
         vals[o + i] = e.y;
       }
@@ -734,11 +815,12 @@ Plan make_layout(int64_t B, int64_t T, int64_t S, int64_t topk) {
     pl.rank = r > pl.Ms ? pl.Ms : r;
   }
   const size_t rows = (size_t)B * (size_t)T;
+  const size_t rows_pad = (size_t)B * (size_t)((T + kCandGroupRows - 1) / kCandGroupRows * kCandGroupRows);
   size_t off = 0;
   pl.off_tau = off;      off = align_up(off + rows * 4, 256);
   pl.off_samp = off;     off = align_up(off + (pl.sample ? rows * (size_t)pl.Ms * 4 : 0), 256);
   pl.off_counts = off;   off = align_up(off + rows * kMaxSplit * 32 * 4, 256);
-  pl.off_cand = off;     off = align_up(off + rows * (size_t)(kSubTotal + kMaxSplit * 32) * 8, 256);
+  pl.off_cand = off;     off = align_up(off + rows_pad * (size_t)(kSubTotal + kMaxSplit * 32) * 8, 256);
   pl.off_fb = off;       off = align_up(off + 64, 256);
   pl.off_fblist = off;   off = align_up(off + rows * 4, 256);
   pl.off_widelist = off; off = align_up(off + rows * 4, 256);
@@ -747,18 +829,31 @@ Plan make_layout(int64_t B, int64_t T, int64_t S, int64_t topk) {
   return pl;
 }
 
-// Concurrent workgroups of the filter kernel on the current device (cached per device).
-int filter_slots(const void* kernel) {
-  static int cache[64] = {0};
+// Concurrent workgroups of a filter kernel instance on the current device (cached per
+// device and kernel).
+int filter_slots(const void* kernel, int threads) {
+  struct Entry {
+    const void* kernel;
+    int dev, slots;
+  };
+  static Entry cache[64];
+  static int n_cache = 0;
+  static std::mutex mu;
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
-  if (cache[dev] > 0) return cache[dev];
+  if (hipGetDevice(&dev) != hipSuccess) return 512;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < n_cache; ++i)
+      if (cache[i].kernel == kernel && cache[i].dev == dev) return cache[i].slots;
+  }
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu <= 0)
-    per_cu = 2;
-  cache[dev] = cus * per_cu;
-  return cache[dev];
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess || per_cu <= 0)
+    per_cu = 1;
+  const int slots = cus * per_cu;
+  std::lock_guard<std::mutex> lock(mu);
+  if (n_cache < 64) cache[n_cache++] = Entry{kernel, dev, slots};
+  return slots;
 }
 
 // Picks the key split count: the fraction of the last wave of workgroups that is busy,
@@ -785,9 +880,11 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   int* fb_count = reinterpret_cast<int*>(ws + pl.off_fb);  // [0] brute force, [1] wide select
   hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(64), 0, st, fb_count, 0);
   GW_HIP_LAUNCH_CHECK("set_int_kernel");
-  const int64_t tiles = (base.T + kBM - 1) / kBM;
+  constexpr int BM = ScoreShape<HI>::BM;
+  constexpr int THREADS = ScoreShape<HI>::THREADS;
+  const int64_t tiles = (base.T + BM - 1) / BM;
   const int64_t rows = B * (int64_t)base.T;
-  pl.nsplit = choose_nsplit(tiles * B, base.S, filter_slots((const void*)indexer_score_kernel<E, HI, false, HAS_MASK>),
+  pl.nsplit = choose_nsplit(tiles * B, base.S, filter_slots((const void*)indexer_score_kernel<E, HI, false, HAS_MASK>, THREADS),
                             pl.sample);
   pl.cap = kSubTotal / (32 * pl.nsplit);
   float* tau = reinterpret_cast<float*>(ws + pl.off_tau);
@@ -799,7 +896,7 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
     sp.tau_mode = kTauArray;
     sp.nsplit = 1;
     sp.nstages = (pl.Ms + kBN - 1) / kBN;
-    hipLaunchKernelGGL((indexer_score_kernel<E, HI, true, HAS_MASK>), dim3((unsigned)tiles, 1, (unsigned)B), dim3(256),
+    hipLaunchKernelGGL((indexer_score_kernel<E, HI, true, HAS_MASK>), dim3((unsigned)tiles, 1, (unsigned)B), dim3(THREADS),
                        0, st, sp);
     GW_HIP_LAUNCH_CHECK("indexer_score_kernel<sample>");
     const dim3 tgrid((unsigned)((rows + 3) / 4));
@@ -817,13 +914,15 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   fp.cap = pl.cap;
   fp.nstages = (base.S + kBN - 1) / kBN;
   hipLaunchKernelGGL((indexer_score_kernel<E, HI, false, HAS_MASK>),
-                     dim3((unsigned)tiles, (unsigned)pl.nsplit, (unsigned)B), dim3(256), 0, st, fp);
+                     dim3((unsigned)tiles, (unsigned)pl.nsplit, (unsigned)B), dim3(THREADS), 0, st, fp);
   GW_HIP_LAUNCH_CHECK("indexer_score_kernel<filter>");
   SelectParams fs{};
   fs.cand = fp.cand;
   fs.counts = fp.counts;
   fs.nsub = pl.nsplit * 32;
   fs.cap = pl.cap;
+  fs.T = base.T;
+  fs.Tp = base.Tp;
   fs.out_idx = out_idx;
   fs.out_scores = static_cast<uint16_t*>(out_scores);
   fs.Kk = pl.Kk;
@@ -903,8 +1002,10 @@ extern "C" int gw_indexer_topk_fwd(int dtype, const void* q, const void* k, cons
     return set_error(GW_ERR_UNSUPPORTED, "topk %lld exceeds the supported maximum %d", (long long)Kk, kMaxTopk);
   GW_CHECK_ARG(q && k && w && out_indices && out_scores, "null tensor pointer");
   GW_CHECK_ARG(aligned16(q) && aligned16(k), "q and k must be 16-byte aligned");
-  GW_CHECK_ARG(B <= 65535 && T < (1ll << 31) && S < (1ll << 30) && B * T < (1ll << 31),
-               "size exceeds grid or int32 range");
+  GW_CHECK_ARG(B <= 65535 && T < (1ll << 30) && B * T < (1ll << 30), "size exceeds grid or int32 range");
+  // A sublist's byte cursor advances 8 KB per append and must stay below 2^32.
+  if (S > (1ll << 24))
+    return set_error(GW_ERR_UNSUPPORTED, "S=%lld exceeds the supported maximum %lld", (long long)S, 1ll << 24);
   const Plan pl = make_layout(B, T, S, topk);
   GW_CHECK_ARG(workspace != nullptr && workspace_bytes >= pl.total, "workspace needs %zu bytes, got %zu",
                pl.total, workspace_bytes);
@@ -916,6 +1017,7 @@ extern "C" int gw_indexer_topk_fwd(int dtype, const void* q, const void* k, cons
   base.w = static_cast<const uint16_t*>(w);
   base.mask = static_cast<const uint16_t*>(mask);
   base.T = (int)T;
+  base.Tp = (int)((T + kCandGroupRows - 1) / kCandGroupRows * kCandGroupRows);
   base.S = (int)S;
   base.scale = softmax_scale;
   base.tau_mode = (flags & GW_TOPK_FLAG_TAU_PLUS_INF) ? kTauPlusInf

@@ -75,6 +75,14 @@ def test_layer_inputs_fp16_batch2(gpu_device):
     _check(q, k, w, idx, sc, 512)
 
 
+def test_sampled_path_batch3_ragged_rows(gpu_device):
+    # B = 3 with T = 4500 (not a multiple of the 32-row candidate groups) and S > 4096 (the
+    # sampled threshold): every row of every batch element is checked.
+    q, k, w = workloads.indexer_inputs(4, 3, torch.bfloat16, tokens=4500)
+    idx, sc = _gpu_topk(q, k, w, 1024)
+    _check(q, k, w, idx, sc, 1024)
+
+
 @pytest.mark.parametrize("heads", [1, 2, 8])
 def test_other_head_counts(gpu_device, heads):
     g = torch.Generator().manual_seed(heads)
