@@ -178,6 +178,106 @@ def long_context_c3(steps: int = 5, warmup: int = 2, views: int = 64, topk: int 
     }
 
 
+def layer_forward_s32(steps: int = 5, warmup: int = 2, views: int = 32, topk: int = 1024):
+    """The whole sparse global-attention layer forward at S=32 views (N=43,968), B=1, bf16,
+    random-init weights: fused projection GEMM (hipBLASLt via torch), layer glue
+    (gw_dsa_glue_fwd), indexer top-k, sparse attention, output projection. HIP events per
+    phase on the launch stream. Also times the same glue written as separate torch ops
+    (LayerNorm, rotary gathers and concatenations, casts: the reference's unfused order,
+    dsa_attention.py:4928-4948 and indexer.py:302-328) for the fusion comparison."""
+    import torch
+    import torch.nn.functional as F
+
+    from geoweave_amd import dsa_layer, workloads
+    from geoweave_amd.custom_flash_attn.sparse_index_flash_attn import (
+        sparse_index_flash_attn_inference_func,
+    )
+    from geoweave_amd.custom_indexer import sparse_topk_indexer_inference_func
+
+    dev = torch.device("cuda", 0)
+    m = workloads.init_layer_(dsa_layer.SparseGlobalAttention(topk=topk)).to(dev)
+    x, pos = workloads.layer_module_inputs(views)
+    x, pos = x.to(dev), pos.to(dev)
+    B, N, dim = x.shape
+    lay = m.layout
+    w, b = m.fused_projection(torch.bfloat16)
+    pw = m.proj.weight.detach().to(torch.bfloat16)
+    pb = m.proj.bias.detach().to(torch.bfloat16)
+    norms = [dsa_layer._ln_params(n) for n in (m.q_norm, m.k_norm, m.indexer.k_norm)]
+    n_rope = int(pos.max()) + 1
+    cos, sin = dsa_layer.rope2d_tables(n_rope, 100.0, dev)
+    empty = x.new_empty(0)
+    stream = torch.cuda.current_stream(dev)
+
+    def one(ev=None):
+        rec = (lambda i: ev[i].record(stream)) if ev else (lambda i: None)
+        rec(0)
+        y = F.linear(x, w, b)
+        rec(1)
+        q, k, v, iq, ik, iw = dsa_layer.dsa_glue_forward(y, lay, *norms, 1e-5, pos, 100.0, n_rope)
+        rec(2)
+        idx, _ = sparse_topk_indexer_inference_func(iq, ik, iw, empty, topk, 0.125, 256, 0)
+        rec(3)
+        o, _ = sparse_index_flash_attn_inference_func(q, k, v, idx, softmax_scale=0.125)
+        rec(4)
+        F.linear(o.reshape(B, N, dim), pw, pb)
+        rec(5)
+
+    def rope_torch(t, p):  # t [B, N, h, 64] -> rotary as rope.py:133-200 in torch ops
+        t = t.permute(0, 2, 1, 3)
+        out = []
+        for half, pp in ((t[..., :32], p[..., 0]), (t[..., 32:], p[..., 1])):
+            c = torch.cat((cos, cos), -1)[pp.long()][:, None]
+            s_ = torch.cat((sin, sin), -1)[pp.long()][:, None]
+            out.append(half * c + torch.cat((-half[..., 16:], half[..., :16]), -1) * s_)
+        return torch.cat(out, -1).permute(0, 2, 1, 3)
+
+    def torch_glue(y):
+        H, Hi = lay.H, lay.Hi
+        q = y[..., lay.q_off:lay.q_off + H * 64].reshape(B, N, H, 64).float()
+        k = y[..., lay.k_off:lay.k_off + H * 64].reshape(B, N, H, 64).float()
+        iq = y[..., lay.iq_off:lay.iq_off + Hi * 64].reshape(B, N, Hi, 64).float()
+        ik = y[..., lay.ik_off:lay.ik_off + Hi * 64].reshape(B, N, Hi, 64).float()
+        q = F.layer_norm(q, (64,), norms[0][0], norms[0][1], 1e-5)
+        k = F.layer_norm(k, (64,), norms[1][0], norms[1][1], 1e-5)
+        ik = F.layer_norm(ik, (64,), norms[2][0], norms[2][1], 1e-5)
+        outs = [rope_torch(t, pos).to(torch.bfloat16).contiguous() for t in (q, k, iq, ik)]
+        return outs + [y[..., lay.iw_off:lay.iw_off + Hi].contiguous()]
+
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(steps)]
+    for i in range(steps):
+        one(evs[i])
+    torch.cuda.synchronize()
+    ph = [statistics.mean(e[j].elapsed_time(e[j + 1]) for e in evs) for j in range(5)]
+    y = F.linear(x, w, b)
+    for _ in range(warmup):
+        torch_glue(y)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        torch_glue(y)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    torch_glue_ms = e0.elapsed_time(e1) / steps
+    H, Hi = lay.H, lay.Hi
+    glue_bytes = B * N * ((2 * H + 2 * Hi) * 64 + Hi) * 2 * 2 + B * N * 8
+    return {
+        "workload": f"whole sparse global-attention layer forward: B={B}, S={views} views (N={N}), dim {dim}, "
+                    f"H={H}, indexer {Hi}x64, top-k {topk}, bf16, random-init weights",
+        "value_ms": round(sum(ph), 3),
+        "proj_gemm_ms": round(ph[0], 3),
+        "glue_ms": round(ph[1], 3),
+        "glue_gbs": round(glue_bytes / (ph[1] * 1e-3) / 1e9, 1),
+        "indexer_ms": round(ph[2], 3),
+        "attn_fwd_ms": round(ph[3], 3),
+        "out_proj_ms": round(ph[4], 3),
+        "torch_glue_ms": round(torch_glue_ms, 3),
+    }
+
+
 def cpu_baseline(views: int, budget_s: float, rows_per_chunk: int = 128):
     """Times the fp32 CPU oracle (indexer scores + top-k + sparse attention) on query
     rows of the same layer until ``budget_s`` seconds have elapsed; scales to all rows."""
@@ -235,6 +335,7 @@ def main() -> int:
                     help="also time the training forward that writes attn_sum")
     ap.add_argument("--no-train", action="store_true", help="skip the C4 training-step timing")
     ap.add_argument("--no-long", action="store_true", help="skip the C3 (S=64) long-context timing")
+    ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer (projection + glue) timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run 3 plain device copies of 1 GiB (reference kernel for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE scaling)")
@@ -378,6 +479,9 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if not args.no_layer:
+        print("[bench] whole layer forward", file=sys.stderr, flush=True)
+        result["layer_fwd_s32"] = layer_forward_s32()
     if not args.no_long:
         print("[bench] C3 long context", file=sys.stderr, flush=True)
         result["long_context_c3"] = long_context_c3()

@@ -60,6 +60,11 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.c_int, _p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _p],
     ),
+    "gw_dsa_glue_fwd": (
+        ctypes.c_int,
+        [ctypes.c_int, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+         _p, _p, _p, _p, _p, _p, ctypes.c_float, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p],
+    ),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,213 @@
+"""The sparse global-attention layer on gfx950: fused projection, layer glue, indexer
+top-k and sparse attention.
+
+Counterpart of the sparse inference path of the reference ``DSAAttention``
+(``easyvolcap/official_vggt/layers/dsa_attention.py:47-5403``) with its
+``LightningIndexer`` (``easyvolcap/official_vggt/layers/indexer.py:40-330``), keeping the
+reference's parameter names (``qkv``, ``q_norm``, ``k_norm``, ``proj``,
+``indexer.{q_proj, k_proj, w_proj, k_norm}``) so that its state dict loads as is:
+
+1. ``y = x W^T + b`` with ``W = [qkv | indexer q | indexer k | indexer w]``: one library
+   GEMM (``_project_qkv_and_indexer_fused``, ``dsa_attention.py:583-625``); the fused
+   weight's row count is padded to a multiple of 8 so every column block starts on a
+   16-byte boundary.
+2. ``gw_dsa_glue_fwd``: per-head LayerNorm, 2D RoPE and the 16-bit cast of q/k (attention)
+   and q/k/w (indexer) in one pass (``:4928-4948``, ``indexer.py:302-328``); v is read in
+   place from ``y`` through strides.
+3. ``gw_indexer_topk_fwd`` (top-k), ``gw_sparse_attn_fwd`` (attention), then ``proj``.
+
+The layer runs in one 16-bit dtype (bf16 by default); the glue's LayerNorm and RoPE are
+fp32 math on the 16-bit projection with one rounding at the end.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib
+from .custom_flash_attn.sparse_index_flash_attn import sparse_index_flash_attn_inference_func
+from .custom_indexer.sparse_topk_indexer import sparse_topk_indexer_inference_func
+
+__all__ = ["GlueLayout", "rope2d_tables", "dsa_glue_forward", "LightningIndexerProjections",
+           "SparseGlobalAttention"]
+
+
+class GlueLayout:
+    """Column blocks of the fused projection output (reference ``dsa_attention.py:590-600``)."""
+
+    def __init__(self, H: int, D: int, Hi: int, Di: int):
+        if D != 64 or Di != 64:
+            raise NotImplementedError("the glue kernel handles 64-wide heads")
+        self.H, self.D, self.Hi, self.Di = H, D, Hi, Di
+        self.q_off = 0
+        self.k_off = H * D
+        self.v_off = 2 * H * D
+        self.iq_off = 3 * H * D
+        self.ik_off = self.iq_off + Hi * Di
+        self.iw_off = self.ik_off + Hi * Di
+        self.width = self.iw_off + Hi
+        self.ldy = (self.width + 7) // 8 * 8
+
+
+def rope2d_tables(max_position: int, base: float, device, feature_dim: int = 32) -> Tuple[torch.Tensor, torch.Tensor]:
+    """fp32 (cos, sin) ``[max_position, feature_dim // 2]``, built as
+    ``RotaryPositionEmbedding2D._compute_frequency_components`` builds them (``rope.py:86-117``)
+    for fp32 tokens (one copy of the reference's ``cat(t, t)``)."""
+    exponents = torch.arange(0, feature_dim, 2, device=device).float() / feature_dim
+    inv_freq = 1.0 / (base ** exponents)
+    positions = torch.arange(max_position, device=device, dtype=inv_freq.dtype)
+    angles = torch.einsum("i,j->ij", positions, inv_freq)
+    return angles.cos().contiguous(), angles.sin().contiguous()
+
+
+def _ln_params(norm: Optional[nn.Module]):
+    if norm is None or isinstance(norm, nn.Identity):
+        return None, None
+    if not isinstance(norm, nn.LayerNorm) or norm.normalized_shape != (64,):
+        raise NotImplementedError("q/k norms must be LayerNorm(64) or Identity")
+    w = norm.weight.detach().float().contiguous() if norm.weight is not None else None
+    b = norm.bias.detach().float().contiguous() if norm.bias is not None else None
+    if w is None or b is None:
+        dev = norm.weight.device if norm.weight is not None else None
+        w = torch.ones(64, device=dev) if w is None else w
+        b = torch.zeros(64, device=w.device) if b is None else b
+    return w, b
+
+
+def dsa_glue_forward(
+    y: torch.Tensor,
+    layout: GlueLayout,
+    q_norm=(None, None),
+    k_norm=(None, None),
+    idx_k_norm=(None, None),
+    ln_eps: float = 1e-5,
+    pos: Optional[torch.Tensor] = None,
+    rope_base: float = 100.0,
+    rope_len: Optional[int] = None,
+):
+    """(q, k, v, idx_q, idx_k, idx_w) from the fused projection ``y [B, N, ldy]`` via
+    ``gw_dsa_glue_fwd``. q/k ``[B, N, H, 64]`` and idx_q/idx_k ``[B, N, Hi, 64]`` are new
+    contiguous tensors, idx_w ``[B, N, Hi]``; v is a strided view of ``y``. ``pos`` is
+    ``[B, N, 2]`` (y, x) integer positions or None (no rope); ``rope_len`` is the table
+    length (default ``max(pos) + 1`` like the reference, ``rope.py:190``, which reads it on
+    the host)."""
+    if y.dim() != 3 or y.shape[-1] != layout.ldy or y.stride(-1) != 1 or y.stride(1) != layout.ldy:
+        raise ValueError(f"y must be a contiguous [B, N, {layout.ldy}] projection")
+    if not y.is_cuda:
+        raise ValueError("y must be a GPU tensor")
+    B, N = y.shape[0], y.shape[1]
+    H, Hi = layout.H, layout.Hi
+    dev = y.device
+    q = torch.empty(B, N, H, 64, device=dev, dtype=y.dtype)
+    k = torch.empty_like(q)
+    iq = torch.empty(B, N, Hi, 64, device=dev, dtype=y.dtype)
+    ik = torch.empty_like(iq)
+    iw = torch.empty(B, N, Hi, device=dev, dtype=y.dtype)
+    pos32 = cos = sin = None
+    n_rope = 0
+    if pos is not None:
+        if tuple(pos.shape) != (B, N, 2):
+            raise ValueError(f"pos shape {tuple(pos.shape)} != ({B}, {N}, 2)")
+        pos32 = pos.to(device=dev, dtype=torch.int32).contiguous()
+        n_rope = int(rope_len) if rope_len is not None else int(pos32.max()) + 1
+        cos, sin = rope2d_tables(n_rope, rope_base, dev)
+    lib = _lib.load()
+    _lib.check(
+        lib.gw_dsa_glue_fwd(
+            _lib.dtype_code(y.dtype), y.data_ptr(), B * N, layout.ldy, layout.q_off, layout.k_off,
+            layout.iq_off, layout.ik_off, layout.iw_off, H, Hi, 64,
+            _lib.ptr(q_norm[0]), _lib.ptr(q_norm[1]), _lib.ptr(k_norm[0]), _lib.ptr(k_norm[1]),
+            _lib.ptr(idx_k_norm[0]), _lib.ptr(idx_k_norm[1]), float(ln_eps),
+            _lib.ptr(pos32), _lib.ptr(cos), _lib.ptr(sin), n_rope,
+            q.data_ptr(), k.data_ptr(), iq.data_ptr(), ik.data_ptr(), iw.data_ptr(),
+            _lib.stream_handle(dev),
+        ),
+        "gw_dsa_glue_fwd",
+    )
+    v = y[..., layout.v_off:layout.v_off + H * 64].view(B, N, H, 64)
+    return q, k, v, iq, ik, iw
+
+
+class LightningIndexerProjections(nn.Module):
+    """Parameters of the reference ``LightningIndexer`` (``indexer.py:55-61``): q/k/w
+    projections and the k LayerNorm; the gate starts at w = 1 (``:63-68``)."""
+
+    def __init__(self, dim: int, n_heads: int = 4, head_dim: int = 64, qk_norm: bool = True):
+        super().__init__()
+        self.n_heads = n_heads
+        self.head_dim = head_dim
+        self.q_proj = nn.Linear(dim, n_heads * head_dim)
+        self.k_proj = nn.Linear(dim, n_heads * head_dim)
+        self.w_proj = nn.Linear(dim, n_heads)
+        nn.init.zeros_(self.w_proj.weight)
+        nn.init.ones_(self.w_proj.bias)
+        self.k_norm = nn.LayerNorm(head_dim) if qk_norm else nn.Identity()
+        self.scale = head_dim ** -0.5
+
+
+class SparseGlobalAttention(nn.Module):
+    """Sparse global attention (inference): ``forward(x [B, N, dim], pos [B, N, 2] | None)
+    -> [B, N, dim]``. Each query attends to the ``topk`` keys its lightning indexer ranks
+    highest (``min(topk, N)``, reference ``dsa_attention.py:4996``)."""
+
+    def __init__(self, dim: int = 1024, num_heads: int = 16, qkv_bias: bool = True, proj_bias: bool = True,
+                 qk_norm: bool = True, rope_base: Optional[float] = 100.0, indexer_heads: int = 4,
+                 indexer_dim: int = 64, topk: int = 1024):
+        super().__init__()
+        self.dim = dim
+        self.num_heads = num_heads
+        self.head_dim = dim // num_heads
+        self.scale = self.head_dim ** -0.5
+        self.qkv = nn.Linear(dim, 3 * dim, bias=qkv_bias)
+        self.q_norm = nn.LayerNorm(self.head_dim) if qk_norm else nn.Identity()
+        self.k_norm = nn.LayerNorm(self.head_dim) if qk_norm else nn.Identity()
+        self.proj = nn.Linear(dim, dim, bias=proj_bias)
+        self.indexer = LightningIndexerProjections(dim, indexer_heads, indexer_dim, qk_norm)
+        self.rope_base = rope_base
+        self.topk = topk
+        self.layout = GlueLayout(num_heads, self.head_dim, indexer_heads, indexer_dim)
+        self._fused = None
+
+    def fused_projection(self, dtype: torch.dtype):
+        """(W [ldy, dim], b [ldy]) in ``dtype``: ``[qkv | q_proj | k_proj | w_proj]`` plus zero
+        rows up to ``ldy`` (``_get_fused_proj_params``, ``dsa_attention.py:583-600``). Cached
+        until a parameter changes."""
+        lins = (self.qkv, self.indexer.q_proj, self.indexer.k_proj, self.indexer.w_proj)
+        key = (dtype,) + tuple((l.weight.data_ptr(), l.weight._version,
+                                0 if l.bias is None else l.bias._version) for l in lins)
+        if self._fused is not None and self._fused[0] == key:
+            return self._fused[1], self._fused[2]
+        pad = self.layout.ldy - self.layout.width
+        w = torch.cat([l.weight.detach() for l in lins], 0)
+        b = torch.cat([l.bias.detach() if l.bias is not None else torch.zeros(l.out_features, device=w.device)
+                       for l in lins], 0)
+        if pad:
+            w = torch.cat([w, w.new_zeros(pad, w.shape[1])], 0)
+            b = torch.cat([b, b.new_zeros(pad)], 0)
+        w, b = w.to(dtype).contiguous(), b.to(dtype).contiguous()
+        self._fused = (key, w, b)
+        return w, b
+
+    @torch.no_grad()
+    def forward(self, x: torch.Tensor, pos: Optional[torch.Tensor] = None, topk: Optional[int] = None,
+                return_topk: bool = False):
+        if x.dtype not in (torch.bfloat16, torch.float16):
+            raise TypeError("SparseGlobalAttention runs in bfloat16 or float16")
+        B, N, _ = x.shape
+        w, b = self.fused_projection(x.dtype)
+        y = F.linear(x, w, b)
+        q, k, v, iq, ik, iw = dsa_glue_forward(
+            y, self.layout, _ln_params(self.q_norm), _ln_params(self.k_norm), _ln_params(self.indexer.k_norm),
+            self.q_norm.eps if isinstance(self.q_norm, nn.LayerNorm) else 1e-5,
+            pos if self.rope_base else None, self.rope_base or 100.0)
+        kk = min(int(topk or self.topk), N)
+        idx, _ = sparse_topk_indexer_inference_func(iq, ik, iw, iq.new_empty(0), kk, float(self.indexer.scale),
+                                                    256, 0)
+        o, _ = sparse_index_flash_attn_inference_func(q, k, v, idx, softmax_scale=self.scale)
+        out = F.linear(o.reshape(B, N, self.dim), self.proj.weight.to(x.dtype),
+                       None if self.proj.bias is None else self.proj.bias.to(x.dtype))
+        return (out, idx) if return_topk else out

@@ -127,3 +127,44 @@ def layer_inputs(views: int, batch: int = 1, dtype: torch.dtype = torch.bfloat16
     qi, ki, wi = indexer_inputs(views, batch, dtype, tokens)
     q, k, v = attention_inputs(views, batch, dtype, tokens)
     return LayerInputs(qi, ki, wi, q, k, v, views, batch)
+
+
+PATCH_GRID = 37
+SPECIAL_TOKENS = 5
+
+
+def patch_positions(views: int, batch: int = 1) -> torch.Tensor:
+    """int32 ``[B, S * P, 2]`` (y, x) rotary positions of the global-attention tokens: per
+    view 5 special tokens at (0, 0), then the 37 x 37 patch grid at (row + 1, col + 1)
+    (reference ``easyvolcap/official_vggt/models/aggregator.py:515-526``)."""
+    ys, xs = torch.meshgrid(torch.arange(PATCH_GRID), torch.arange(PATCH_GRID), indexing="ij")
+    grid = torch.stack([ys.reshape(-1), xs.reshape(-1)], -1) + 1
+    one = torch.cat([torch.zeros(SPECIAL_TOKENS, 2, dtype=grid.dtype), grid], 0)
+    return one.repeat(views, 1).unsqueeze(0).expand(batch, -1, -1).to(torch.int32).contiguous()
+
+
+def layer_module_inputs(views: int, batch: int = 1, dtype: torch.dtype = torch.bfloat16, seed: Optional[int] = None):
+    """(x ``[B, N, 1024]`` ~ N(0, 1) in ``dtype``, positions) for a full layer forward."""
+    g = _gen(BASE_SEED + views if seed is None else seed)
+    x = torch.randn(batch, views * TOKENS_PER_VIEW, DIM, generator=g).to(dtype)
+    return x, patch_positions(views, batch)
+
+
+def init_layer_(layer: torch.nn.Module, seed: int = BASE_SEED) -> torch.nn.Module:
+    """Random-init a SparseGlobalAttention in place (no checkpoint exists offline): linear
+    weights ~ N(0, 1/dim) (unit-variance projections), biases ~ N(0, 0.02), LayerNorm
+    gains 1 + N(0, 0.1), the indexer gate bias 1 (its reference init, ``indexer.py:63-68``)
+    with weights ~ N(0, 0.25/dim)."""
+    g = _gen(seed)
+    with torch.no_grad():
+        for name, p in layer.named_parameters():
+            if p.dim() == 2:
+                scale = (0.25 if "w_proj" in name else 1.0) / p.shape[1] ** 0.5
+                p.copy_(torch.randn(p.shape, generator=g) * scale)
+            elif "norm" in name and name.endswith("weight"):
+                p.copy_(1 + 0.1 * torch.randn(p.shape, generator=g))
+            elif "w_proj" in name:
+                p.fill_(1.0)
+            else:
+                p.copy_(0.02 * torch.randn(p.shape, generator=g))
+    return layer

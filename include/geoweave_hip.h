@@ -223,6 +223,31 @@ int gw_indexer_kl_bwd(int dtype, const void* attn_sum, const void* logits, const
                       int64_t rows, int64_t K, float eps, void* d_attn, void* d_logits,
                       void* stream);
 
+/* ------------------------------------------------------------------------------------
+ * DSA layer glue, forward: per-head LayerNorm + 2D RoPE + 16-bit cast of the attention
+ * q/k and the indexer q/k/w, read from one fused projection output.
+ *
+ * Replaces the torch glue of DSAAttention._project_qkv_and_indexer_fused
+ * (easyvolcap/official_vggt/layers/dsa_attention.py:583-625) plus :4928-4948 (q_norm,
+ * k_norm, rope, score_dtype cast) and LightningIndexer.project
+ * (easyvolcap/official_vggt/layers/indexer.py:302-328), with RotaryPositionEmbedding2D
+ * (easyvolcap/official_vggt/layers/rope.py:62-200).
+ * y: [rows, ldy] (dtype) = x W^T + b with W = [qkv | indexer q | indexer k | indexer w];
+ * the *_off arguments are column offsets (multiples of 8, ldy % 8 == 0); the v block is
+ * not touched (read it in place through strides). D = 64. LayerNorm weight/bias pairs are
+ * fp32 [64] or both NULL (identity), eps ln_eps. pos: int32 [rows, 2] (y, x) or NULL (no
+ * rope); rope_cos/rope_sin: fp32 [rope_len, 16] tables cos/sin(p * base^(-2i/32)), as
+ * rope.py:86-117 builds them. Outputs (dtype, contiguous): q_out, k_out [rows, H, 64],
+ * idx_q_out, idx_k_out [rows, Hi, 64], idx_w_out [rows, Hi].
+ */
+int gw_dsa_glue_fwd(int dtype, const void* y, int64_t rows, int64_t ldy, int64_t q_off, int64_t k_off,
+                    int64_t iq_off, int64_t ik_off, int64_t iw_off, int64_t H, int64_t Hi, int64_t D,
+                    const float* q_norm_w, const float* q_norm_b, const float* k_norm_w,
+                    const float* k_norm_b, const float* idx_k_norm_w, const float* idx_k_norm_b,
+                    float ln_eps, const int32_t* pos, const float* rope_cos, const float* rope_sin,
+                    int64_t rope_len, void* q_out, void* k_out, void* idx_q_out, void* idx_k_out,
+                    void* idx_w_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

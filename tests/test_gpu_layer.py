@@ -1,0 +1,123 @@
+"""GPU parity of the DSA layer glue (gw_dsa_glue_fwd) and of the sparse global-attention
+layer built on it, against the fp32 CPU oracle (oracle/layer_glue.py, oracle/indexer.py,
+oracle/attention.py).
+
+Bar: the glue is fp32 math on the same 16-bit projection the oracle reads, rounded once
+to bf16/fp16: within 2e-2 (abs + rel) of the oracle, the path's 16-bit bar. The layer is
+checked stage by stage on the GPU's own intermediate tensors (as the C4 check feeds the
+GPU indices to both sides): index sets tie-aware exact, the output within 2e-2.
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from geoweave_amd import dsa_layer
+from oracle import attention as oatt
+from oracle import indexer as oidx
+from oracle import layer_glue as olg
+from oracle.topk_check import check_topk_rows
+
+pytestmark = pytest.mark.gpu
+
+TOL = dict(atol=2e-2, rtol=2e-2)
+
+
+def _glue_case(B, N, H, Hi, dtype, seed, with_ln=True, with_rope=True, maxpos=38):
+    g = torch.Generator().manual_seed(seed)
+    lay = dsa_layer.GlueLayout(H, 64, Hi, 64)
+    y = (torch.randn(B, N, lay.ldy, generator=g) * 2 + 0.5).to(dtype)
+    norms = {}
+    for key in ("q", "k", "idx_k"):
+        norms[key] = (torch.rand(64, generator=g) + 0.5, torch.randn(64, generator=g) * 0.1) if with_ln else None
+    pos = None
+    if with_rope:
+        pos = torch.randint(0, maxpos, (B, N, 2), generator=g)
+        pos[:, :3] = 0  # special tokens sit at position (0, 0) (aggregator.py:521-526)
+    return lay, y, norms, pos
+
+
+def _run_glue(lay, y, norms, pos):
+    dev = "cuda"
+    nd = lambda key: (None, None) if norms[key] is None else tuple(t.to(dev) for t in norms[key])
+    out = dsa_layer.dsa_glue_forward(y.to(dev), lay, nd("q"), nd("k"), nd("idx_k"), 1e-5,
+                                     None if pos is None else pos.to(dev))
+    torch.cuda.synchronize()
+    return [t.float().cpu() for t in out]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("with_ln,with_rope", [(True, True), (False, True), (True, False), (False, False)])
+def test_glue_matches_oracle(gpu_device, dtype, with_ln, with_rope):
+    lay, y, norms, pos = _glue_case(2, 300, 16, 4, dtype, seed=5 + with_ln + 2 * with_rope,
+                                    with_ln=with_ln, with_rope=with_rope)
+    got = _run_glue(lay, y, norms, pos)
+    want = olg.fused_projection_glue(None, None, None, dict(H=16, D=64, Hi=4, Di=64), norms, pos,
+                                     y=y[..., :lay.width].float())
+    for name, a, b in zip(("q", "k", "v", "idx_q", "idx_k", "idx_w"), got, want):
+        torch.testing.assert_close(a, b, **TOL, msg=lambda m: f"{name}: {m}")
+
+
+def test_glue_at_layer_size_sampled_rows(gpu_device):
+    # S = 32 views of 1374 tokens, the layer's bf16 projection; oracle on sampled rows.
+    lay, y, norms, pos = _glue_case(1, 32 * 1374, 16, 4, torch.bfloat16, seed=32)
+    got = _run_glue(lay, y, norms, pos)
+    rows = torch.randperm(y.shape[1], generator=torch.Generator().manual_seed(1))[:2048]
+    want = olg.fused_projection_glue(None, None, None, dict(H=16, D=64, Hi=4, Di=64), norms, pos[:, rows],
+                                     y=y[:, rows, :lay.width].float())
+    for a, b in zip(got, want):
+        torch.testing.assert_close(a[:, rows], b, **TOL)
+
+
+def test_glue_rejects_bad_layouts(gpu_device):
+    lay = dsa_layer.GlueLayout(16, 64, 4, 64)
+    y = torch.zeros(1, 8, lay.ldy - 8, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        dsa_layer.dsa_glue_forward(y, lay)
+
+
+def _layer(dim=1024, seed=0):
+    torch.manual_seed(seed)
+    m = dsa_layer.SparseGlobalAttention(dim=dim, num_heads=dim // 64, topk=256)
+    with torch.no_grad():
+        for p in m.parameters():
+            p.copy_(torch.randn_like(p) * (0.03 if p.dim() > 1 else 0.5))
+        m.q_norm.weight.add_(1.0)
+        m.k_norm.weight.add_(1.0)
+        m.indexer.k_norm.weight.add_(1.0)
+        m.indexer.w_proj.bias.fill_(1.0)
+    return m
+
+
+def test_sparse_global_attention_layer_stage_by_stage(gpu_device):
+    B, N, dim = 1, 1500, 1024
+    m = _layer(dim).cuda()
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(B, N, dim, generator=g).bfloat16()
+    pos = torch.randint(0, 38, (B, N, 2), generator=g)
+    out, idx = m(x.cuda(), pos.cuda(), return_topk=True)
+    torch.cuda.synchronize()
+
+    # 1) projection + glue on the GPU vs the oracle on the same bf16 projection y
+    w, b = m.fused_projection(torch.bfloat16)
+    y = F.linear(x.cuda(), w, b)
+    lay = m.layout
+    norms = {"q": (m.q_norm.weight.detach().float().cpu(), m.q_norm.bias.detach().float().cpu()),
+             "k": (m.k_norm.weight.detach().float().cpu(), m.k_norm.bias.detach().float().cpu()),
+             "idx_k": (m.indexer.k_norm.weight.detach().float().cpu(), m.indexer.k_norm.bias.detach().float().cpu())}
+    gq, gk, gv, giq, gik, giw = dsa_layer.dsa_glue_forward(
+        y, lay, *[tuple(t.cuda() for t in norms[key]) for key in ("q", "k", "idx_k")], 1e-5, pos.cuda())
+    want = olg.fused_projection_glue(None, None, None, dict(H=16, D=64, Hi=4, Di=64), norms, pos,
+                                     y=y[..., :lay.width].float().cpu())
+    for a, bb in zip((gq, gk, gv, giq, gik, giw), want):
+        torch.testing.assert_close(a.float().cpu(), bb, **TOL)
+
+    # 2) the layer's indices: exact top-256 of the oracle scores over the GPU's indexer q/k/w
+    ref_scores = oidx.indexer_scores(giq.cpu(), gik.cpu(), giw.cpu(), None, 0.125)[0]
+    rep = check_topk_rows(ref_scores, idx[0].cpu(), 256)
+    assert rep.ok, rep
+
+    # 3) attention over those indices, then the output projection, in fp32 on the CPU
+    o, _, _ = oatt.sparse_attention(gq.cpu(), gk.cpu(), gv.cpu(), idx.cpu(), 0.125)
+    ref = F.linear(o.to(torch.bfloat16).float().reshape(B, N, dim), m.proj.weight.detach().bfloat16().float().cpu(),
+                   m.proj.bias.detach().bfloat16().float().cpu())
+    torch.testing.assert_close(out.float().cpu(), ref, **TOL)

@@ -348,3 +348,78 @@ def test_kl_oracle_backward_matches_autograd_and_finite_differences():
             args_m = (tm, z) if t is a else (a, tm)
             fd = (float(okl.kl_loss(*args_p, eps)) - float(okl.kl_loss(*args_m, eps))) / (2 * h) * 2.5
             assert abs(fd - float(d[idx])) < 1e-6 * max(1.0, abs(fd))
+
+
+def test_rope2d_oracle_identity_relative_position_and_brute_force():
+    from oracle import layer_glue as olg
+
+    g = torch.Generator().manual_seed(21)
+    B, H, N, D = 1, 2, 6, 64
+    t = torch.randn(B, H, N, D, generator=g, dtype=torch.float64).float()
+    # position (0, 0) is the identity
+    z = torch.zeros(B, N, 2, dtype=torch.long)
+    torch.testing.assert_close(olg.rope2d(t, z), t, rtol=0, atol=0)
+    # brute force over the reference's formula (rope.py:120-152): per 32-dim half with
+    # position p and frequency f_i = 100^(-2i/32): out[i] = x[i] cos - x[i+16] sin,
+    # out[i+16] = x[i+16] cos + x[i] sin
+    pos = torch.randint(0, 40, (B, N, 2), generator=g)
+    got = olg.rope2d(t, pos)
+    for h in range(H):
+        for n in range(N):
+            for half, p in ((0, int(pos[0, n, 0])), (1, int(pos[0, n, 1]))):
+                for i in range(16):
+                    f = 1.0 / (100.0 ** (2 * i / 32))
+                    c, s = math.cos(p * f), math.sin(p * f)
+                    a, b = float(t[0, h, n, 32 * half + i]), float(t[0, h, n, 32 * half + 16 + i])
+                    assert abs(float(got[0, h, n, 32 * half + i]) - (a * c - b * s)) < 1e-5
+                    assert abs(float(got[0, h, n, 32 * half + 16 + i]) - (b * c + a * s)) < 1e-5
+    # rotations preserve the norm, and scores depend only on position differences
+    torch.testing.assert_close(got.norm(dim=-1), t.norm(dim=-1), rtol=1e-5, atol=1e-5)
+    q = torch.randn(1, 1, 2, D, generator=g)
+    k = torch.randn(1, 1, 2, D, generator=g)
+    p1 = torch.tensor([[[3, 7], [5, 2]]])
+    p2 = p1 + torch.tensor([[[4, 9]]])
+    s1 = (olg.rope2d(q, p1)[0, 0, 0] * olg.rope2d(k, p1)[0, 0, 1]).sum()
+    s2 = (olg.rope2d(q, p2)[0, 0, 0] * olg.rope2d(k, p2)[0, 0, 1]).sum()
+    assert abs(float(s1) - float(s2)) < 1e-4
+
+
+def test_layer_glue_oracle_matches_the_unfused_reference_order():
+    # The fused projection (dsa_attention.py:583-625) equals the unfused path: qkv linear
+    # -> reshape(B, N, 3, H, D) (:229-233), q_norm/k_norm, rope (:4935-4940); indexer
+    # q_proj/k_proj/w_proj, k_norm, rope (indexer.py:302-320).
+    from oracle import layer_glue as olg
+
+    g = torch.Generator().manual_seed(22)
+    B, N, dim, H, D, Hi = 1, 10, 128, 2, 64, 2
+    x = torch.randn(B, N, dim, generator=g)
+    qkv_w, qkv_b = torch.randn(3 * H * D, dim, generator=g) * 0.1, torch.randn(3 * H * D, generator=g)
+    iq_w, ik_w, iw_w = (torch.randn(n, dim, generator=g) * 0.1 for n in (Hi * D, Hi * D, Hi))
+    iq_b, ik_b, iw_b = (torch.randn(n, generator=g) for n in (Hi * D, Hi * D, Hi))
+    lnp = {k: (torch.rand(D, generator=g) + 0.5, torch.randn(D, generator=g)) for k in ("q", "k", "idx_k")}
+    pos = torch.randint(0, 12, (B, N, 2), generator=g)
+    W = torch.cat([qkv_w, iq_w, ik_w, iw_w])
+    bb = torch.cat([qkv_b, iq_b, ik_b, iw_b])
+    q, k, v, iq, ik, iw = olg.fused_projection_glue(x, W, bb, dict(H=H, D=D, Hi=Hi, Di=D), lnp, pos)
+    qkv = F.linear(x, qkv_w, qkv_b).reshape(B, N, 3, H, D).permute(2, 0, 3, 1, 4)
+    rq, rk, rv = qkv.unbind(0)
+    rq = F.layer_norm(rq, (D,), *lnp["q"], 1e-5)
+    rk = F.layer_norm(rk, (D,), *lnp["k"], 1e-5)
+    rq, rk = olg.rope2d(rq, pos), olg.rope2d(rk, pos)
+    torch.testing.assert_close(q, rq.transpose(1, 2), rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(k, rk.transpose(1, 2), rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(v, rv.transpose(1, 2), rtol=1e-5, atol=1e-5)
+    riq = F.linear(x, iq_w, iq_b).view(B, N, Hi, D)
+    rik = F.layer_norm(F.linear(x, ik_w, ik_b).view(B, N, Hi, D), (D,), *lnp["idx_k"], 1e-5)
+    rp = lambda t: olg.rope2d(t.permute(0, 2, 1, 3), pos).permute(0, 2, 1, 3)
+    torch.testing.assert_close(iq, rp(riq), rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(ik, rp(rik), rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(iw, F.linear(x, iw_w, iw_b), rtol=1e-5, atol=1e-5)
+    # LayerNorm itself against a hand loop on one vector
+    vec = F.linear(x, ik_w, ik_b).view(B, N, Hi, D)[0, 3, 1]
+    mu = sum(float(a) for a in vec) / D
+    var = sum((float(a) - mu) ** 2 for a in vec) / D
+    want = [(float(a) - mu) / math.sqrt(var + 1e-5) * float(w) + float(b2)
+            for a, w, b2 in zip(vec, *lnp["idx_k"])]
+    got = F.layer_norm(vec, (D,), *lnp["idx_k"], 1e-5)
+    assert max(abs(float(a) - b2) for a, b2 in zip(got, want)) < 1e-4
