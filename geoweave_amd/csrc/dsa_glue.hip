@@ -18,7 +18,8 @@
 //   p.x; within each 32-dim half, for i < 16 with c = cos[p][i], s = sin[p][i]:
 //     out[i] = x[i] c - x[i+16] s,   out[i+16] = x[i+16] c + x[i] s
 //   (rope.py:120-152: x * cos + cat(-x2, x1) * sin with cos/sin = cat(t, t) tables).
-// One thread per (row, head vector); the whole vector lives in registers.
+#include <algorithm>
+
 #include "gw_common.h"
 
 namespace gw {
@@ -50,88 +51,133 @@ struct GlueParams {
   int64_t rows;
 };
 
-__device__ __forceinline__ void layer_norm64(float (&x)[kGlueD], const float* g, const float* bta, float eps) {
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < kGlueD; ++i) s += x[i];
-  const float mean = s * (1.f / kGlueD);
-  float v = 0.f;
-#pragma unroll
-  for (int i = 0; i < kGlueD; ++i) {
-    const float d = x[i] - mean;
-    v += d * d;
-  }
-  const float rstd = 1.f / sqrtf(v * (1.f / kGlueD) + eps);
-#pragma unroll
-  for (int i = 0; i < kGlueD; ++i) x[i] = (x[i] - mean) * rstd * g[i] + bta[i];
-}
+// Eight lanes per head vector: lane j of a group holds dims [8j, 8j + 8) as one 16-byte
+// chunk, so a wave moves 1 KB of consecutive columns per load or store; each wave takes
+// kGlueVecs * 8 consecutive vectors per step (all loads issued first) in a grid-stride
+// loop, with the LayerNorm parameters and rotary tables staged in LDS once per block.
+// LayerNorm sums over the 8 lanes with DPP; the rotary partner of dims [8j, 8j + 8)
+// within each 32-dim half is lane j ^ 2 (dims i and i + 16), one DPP quad permute.
+constexpr int kGlueVecs = 4;
+constexpr int kGlueMaxRope = 256;  // rotary positions staged in LDS (else read from global)
 
-__device__ __forceinline__ void rope_half(float (&x)[kGlueD], int base, const float* c, const float* s) {
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const float a = x[base + i], bb = x[base + 16 + i];
-    x[base + i] = a * c[i] - bb * s[i];
-    x[base + 16 + i] = bb * c[i] + a * s[i];
+struct GlueVec {
+  uint32_t row;
+  int head, out_heads, col;
+  int norm;  // -1: none, 0: attention q, 1: attention k, 2: indexer k
+  uint16_t* out;
+  bool live, gate;
+};
+
+__device__ __forceinline__ GlueVec glue_vec(const GlueParams& p, uint32_t vid, uint32_t nvec, uint32_t slots) {
+  GlueVec v{};
+  v.live = vid < nvec;
+  if (!v.live) vid = 0;
+  v.row = vid / slots;
+  const int slot = (int)(vid - v.row * slots);
+  v.norm = -1;
+  if (slot < p.H) {
+    v.head = slot;
+    v.col = p.q_off + v.head * kGlueD;
+    v.norm = p.qn_w ? 0 : -1;
+    v.out = p.q_out;
+    v.out_heads = p.H;
+  } else if (slot < 2 * p.H) {
+    v.head = slot - p.H;
+    v.col = p.k_off + v.head * kGlueD;
+    v.norm = p.kn_w ? 1 : -1;
+    v.out = p.k_out;
+    v.out_heads = p.H;
+  } else if (slot < 2 * p.H + p.Hi) {
+    v.head = slot - 2 * p.H;
+    v.col = p.iq_off + v.head * kGlueD;
+    v.out = p.iq_out;
+    v.out_heads = p.Hi;
+    v.gate = true;  // the indexer gate of this head travels with its query vector
+  } else {
+    v.head = slot - 2 * p.H - p.Hi;
+    v.col = p.ik_off + v.head * kGlueD;
+    v.norm = p.ikn_w ? 2 : -1;
+    v.out = p.ik_out;
+    v.out_heads = p.Hi;
   }
+  return v;
 }
 
 template <typename E>
 __global__ __launch_bounds__(256) void dsa_glue_kernel(const GlueParams p) {
-  const int slots = 2 * p.H + 2 * p.Hi;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= p.rows * slots) return;
-  const int64_t row = gid / slots;
-  const int slot = (int)(gid - row * slots);
-
-  int col, head;
-  const float* g = nullptr;
-  const float* bta = nullptr;
-  uint16_t* out;
-  int out_heads;
-  if (slot < p.H) {
-    head = slot;
-    col = p.q_off + head * kGlueD;
-    g = p.qn_w;
-    bta = p.qn_b;
-    out = p.q_out;
-    out_heads = p.H;
-  } else if (slot < 2 * p.H) {
-    head = slot - p.H;
-    col = p.k_off + head * kGlueD;
-    g = p.kn_w;
-    bta = p.kn_b;
-    out = p.k_out;
-    out_heads = p.H;
-  } else if (slot < 2 * p.H + p.Hi) {
-    head = slot - 2 * p.H;
-    col = p.iq_off + head * kGlueD;
-    out = p.iq_out;
-    out_heads = p.Hi;
-    // The indexer gate of this head travels with its query vector.
-    p.iw_out[row * p.Hi + head] = p.y[row * p.ldy + p.iw_off + head];
-  } else {
-    head = slot - 2 * p.H - p.Hi;
-    col = p.ik_off + head * kGlueD;
-    g = p.ikn_w;
-    bta = p.ikn_b;
-    out = p.ik_out;
-    out_heads = p.Hi;
+  __shared__ float ln_s[3][2][kGlueD];  // (q, k, indexer k) x (weight, bias)
+  __shared__ float rope_s[2][kGlueMaxRope * 16];
+  const float* lnw[3] = {p.qn_w, p.kn_w, p.ikn_w};
+  const float* lnb[3] = {p.qn_b, p.kn_b, p.ikn_b};
+  for (int i = threadIdx.x; i < 3 * kGlueD; i += blockDim.x) {
+    const int t = i / kGlueD, d = i % kGlueD;
+    ln_s[t][0][d] = lnw[t] ? lnw[t][d] : 1.f;
+    ln_s[t][1][d] = lnb[t] ? lnb[t][d] : 0.f;
   }
-
-  const uint4* src = reinterpret_cast<const uint4*>(p.y + row * p.ldy + col);
-  float x[kGlueD];
-#pragma unroll
-  for (int c = 0; c < kGlueD / 8; ++c) unpack8<E>(src[c], x + 8 * c);
-  if (g != nullptr) layer_norm64(x, g, bta, p.ln_eps);
-  if (p.pos != nullptr) {
-    const int py = min(max(p.pos[row * 2 + 0], 0), p.rope_len - 1);
-    const int px = min(max(p.pos[row * 2 + 1], 0), p.rope_len - 1);
-    rope_half(x, 0, p.rope_cos + py * 16, p.rope_sin + py * 16);
-    rope_half(x, 32, p.rope_cos + px * 16, p.rope_sin + px * 16);
+  const bool rope_lds = p.pos != nullptr && p.rope_len <= kGlueMaxRope;
+  if (rope_lds) {
+    for (int i = threadIdx.x; i < p.rope_len * 16; i += blockDim.x) {
+      rope_s[0][i] = p.rope_cos[i];
+      rope_s[1][i] = p.rope_sin[i];
+    }
   }
-  uint4* dst = reinterpret_cast<uint4*>(out + (row * out_heads + head) * kGlueD);
+  __syncthreads();
+  const float* cos_t = rope_lds ? rope_s[0] : p.rope_cos;
+  const float* sin_t = rope_lds ? rope_s[1] : p.rope_sin;
+
+  const uint32_t slots = 2 * p.H + 2 * p.Hi;
+  const uint32_t nvec = (uint32_t)(p.rows * slots);
+  const int lane = threadIdx.x & 63;
+  const int j = lane & 7;  // 16-byte chunk of each vector
+  const int grp = lane >> 3;
+  const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
+  constexpr uint32_t kStep = 8 * kGlueVecs;
+  for (uint32_t w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); w * kStep < nvec; w += nwaves) {
+    GlueVec v[kGlueVecs];
+    uint4 raw[kGlueVecs];
 #pragma unroll
-  for (int c = 0; c < kGlueD / 8; ++c) dst[c] = pack8<E>(x + 8 * c);
+    for (int u = 0; u < kGlueVecs; ++u) {
+      v[u] = glue_vec(p, w * kStep + u * 8 + grp, nvec, slots);
+      raw[u] = *reinterpret_cast<const uint4*>(p.y + (int64_t)v[u].row * p.ldy + v[u].col + 8 * j);
+    }
+#pragma unroll
+    for (int u = 0; u < kGlueVecs; ++u) {
+      if (!v[u].live) continue;  // uniform over the 8-lane group
+      const int64_t row = v[u].row;
+      float x[8];
+      unpack8<E>(raw[u], x);
+      if (v[u].gate && j == 0) p.iw_out[row * p.Hi + v[u].head] = p.y[row * p.ldy + p.iw_off + v[u].head];
+      if (v[u].norm >= 0) {  // uniform over the 8-lane group
+        const float* g = &ln_s[v[u].norm][0][8 * j];
+        const float* bta = &ln_s[v[u].norm][1][8 * j];
+        float s = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += x[e];
+        const float mean = group_sum<8>(s) * (1.f / kGlueD);
+        float var = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = x[e] - mean;
+          var += d * d;
+        }
+        const float rstd = 1.f / sqrtf(group_sum<8>(var) * (1.f / kGlueD) + p.ln_eps);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = (x[e] - mean) * rstd * g[e] + bta[e];
+      }
+      if (p.pos != nullptr) {
+        const int pp = min(max(p.pos[row * 2 + (j >> 2)], 0), p.rope_len - 1);  // y below dim 32, x above
+        const float* c = cos_t + pp * 16 + 8 * (j & 1);
+        const float* sn = sin_t + pp * 16 + 8 * (j & 1);
+        const float sign = (j & 2) ? 1.f : -1.f;  // dims [0, 16) take -x[i + 16] sin, [16, 32) +x[i] sin
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float partner = dpp<kDppXor2>(x[e]);
+          x[e] = x[e] * c[e] + sign * partner * sn[e];
+        }
+      }
+      *reinterpret_cast<uint4*>(v[u].out + (row * v[u].out_heads + v[u].head) * kGlueD + 8 * j) = pack8<E>(x);
+    }
+  }
 }
 
 }  // namespace
@@ -166,7 +212,7 @@ extern "C" int gw_dsa_glue_fwd(int dtype, const void* y, int64_t rows, int64_t l
   GW_CHECK_ARG(pos == nullptr || (rope_cos && rope_sin && rope_len >= 1), "rope tables missing");
   GW_CHECK_ARG(aligned16(q_out) && aligned16(k_out) && aligned16(idx_q_out) && aligned16(idx_k_out),
                "outputs must be 16-byte aligned");
-  GW_CHECK_ARG(rows * (2 * H + 2 * Hi) / 256 < (1ll << 31) - 1, "too many rows for one launch");
+  GW_CHECK_ARG(rows * (2 * H + 2 * Hi) < (1ll << 31) - 64, "rows x head vectors exceeds the 32-bit index range");
   GlueParams p{};
   p.y = static_cast<const uint16_t*>(y);
   p.ldy = ldy;
@@ -194,8 +240,9 @@ extern "C" int gw_dsa_glue_fwd(int dtype, const void* y, int64_t rows, int64_t l
   p.ik_out = static_cast<uint16_t*>(idx_k_out);
   p.iw_out = static_cast<uint16_t*>(idx_w_out);
   p.rows = rows;
-  const int64_t threads = rows * (2 * H + 2 * Hi);
-  const dim3 grid((unsigned)((threads + 255) / 256));
+  const int64_t vectors = rows * (2 * H + 2 * Hi);
+  const int64_t waves = (vectors + 8 * kGlueVecs - 1) / (8 * kGlueVecs);
+  const dim3 grid((unsigned)std::min<int64_t>((waves + 3) / 4, 2048));
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == GW_DTYPE_BF16)
     hipLaunchKernelGGL((dsa_glue_kernel<BF16>), grid, dim3(256), 0, st, p);

@@ -53,10 +53,23 @@ class GlueLayout:
         self.ldy = (self.width + 7) // 8 * 8
 
 
+_ROPE_CACHE = {}
+
+
 def rope2d_tables(max_position: int, base: float, device, feature_dim: int = 32) -> Tuple[torch.Tensor, torch.Tensor]:
     """fp32 (cos, sin) ``[max_position, feature_dim // 2]``, built as
     ``RotaryPositionEmbedding2D._compute_frequency_components`` builds them (``rope.py:86-117``)
-    for fp32 tokens (one copy of the reference's ``cat(t, t)``)."""
+    for fp32 tokens (one copy of the reference's ``cat(t, t)``), and cached per
+    (length, base, device) as the reference caches them (``rope.py:101-115``)."""
+    key = (int(max_position), float(base), str(torch.device(device)), int(feature_dim))
+    hit = _ROPE_CACHE.get(key)
+    if hit is None:
+        hit = _rope2d_tables(max_position, base, device, feature_dim)
+        _ROPE_CACHE[key] = hit
+    return hit
+
+
+def _rope2d_tables(max_position: int, base: float, device, feature_dim: int):
     exponents = torch.arange(0, feature_dim, 2, device=device).float() / feature_dim
     inv_freq = 1.0 / (base ** exponents)
     positions = torch.arange(max_position, device=device, dtype=inv_freq.dtype)
