@@ -15,10 +15,13 @@
 //                           probability (about 1.7 x topk keys on average).
 //  K1 score_kernel<FILTER>: MFMA scores against all keys; the epilogue appends
 //                           (score, key) pairs with score >= tau to candidate sublists.
-//  K2 select_kernel:        one workgroup per query: exact top-k of the candidates
-//                           (register-resident bisection on the order-preserving score
-//                           bits). A query whose sublists overflowed or hold fewer than
-//                           topk entries is queued for K3 instead.
+//  K2 select_kernel:        one wave per query: exact top-k of the candidates held in
+//                           registers (bisection on the order-preserving score bits,
+//                           ballot-ordered emit). A query whose sublists overflowed or
+//                           hold fewer than topk entries is queued for K3; one whose
+//                           candidates exceed the register slots is queued for K2b.
+//  K2b select_wide_kernel:  persistent workgroups: all candidates of a queued query in
+//                           LDS, block radix select.
 //  K3 fallback_kernel:      exact brute force for queued queries (scores to scratch, radix
 //                           select) - correct for any input, used rarely.
 // Exactness: if count(score >= tau) >= topk, every member of the top-k scores >= tau and
@@ -26,8 +29,8 @@
 // broken deterministically (candidate order: sublist, then position).
 //
 // MFMA layout (v_mfma_f32_32x32x16_{bf16,f16}): C[32 queries x 32 keys]; A = q rows
-// (stationary in VGPRs for the whole key sweep), B = key rows staged through LDS (padded
-// rows, conflict-free 16-byte reads). Lane l owns key column l%32 and query rows
+// (stationary in VGPRs for the whole key sweep), B = key rows staged through LDS
+// (XOR-swizzled 16-byte chunks, conflict-free operand reads). Lane l owns key column l%32 and query rows
 // 8*(r/4) + 4*(l/32) + r%4 of accumulator element r. Every (query row, key column) cell
 // of the tile therefore belongs to exactly one lane, for every key tile of the sweep, so
 // the candidates of one (query, column) go to a sublist that only that lane appends to:
