@@ -278,6 +278,77 @@ def layer_forward_s32(steps: int = 5, warmup: int = 2, views: int = 32, topk: in
     }
 
 
+def aggregator_c5(steps: int = 2, warmup: int = 1, views: int = 32, topk: int = 1024):
+    """Config C5: the VGGT-1B-style aggregator forward (DINOv2-style ViT-L/14 patch
+    embedding, 24 frame + 24 global blocks, dim 1024, 16 heads, MLP ratio 4, global blocks
+    9-19 sparse with top-k 1024), random-init weights, bf16, S=32 seeded 518 x 518 images.
+    Reports end-to-end latency (eager and replayed as one HIP graph) and the time inside the
+    sparse global attention calls (HIP events around each call)."""
+    import torch
+
+    from geoweave_amd import aggregator as agg
+
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(20261201)
+    with torch.device(dev):
+        m = agg.Aggregator(indexer_layers="9-19", topk=topk)
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            if p.dim() >= 2:
+                p.normal_(0.0, p[0].numel() ** -0.5)
+            elif name.endswith("gamma"):
+                p.fill_(0.1)
+            elif "norm" in name and name.endswith("weight"):
+                p.normal_(1.0, 0.1)
+            elif "w_proj" in name:
+                p.fill_(1.0)
+            else:
+                p.normal_(0.0, 0.02)
+    m = m.to(torch.bfloat16)
+    g = torch.Generator(device=dev).manual_seed(20261201 + views)
+    images = torch.rand(1, views, 3, 518, 518, generator=g, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sparse_blocks = [b for b in m.global_blocks if b.sparse]
+
+    for _ in range(warmup):
+        m(images)
+    torch.cuda.synchronize()
+    e2e, sparse_ms = [], []
+    for _ in range(steps):
+        for b in sparse_blocks:
+            b.timing = []
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        m(images)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        e2e.append(e0.elapsed_time(e1))
+        sparse_ms.append(sum(a.elapsed_time(b) for blk in sparse_blocks for a, b in blk.timing))
+    for b in sparse_blocks:
+        b.timing = None
+    graph = agg.AggregatorGraph(m)
+    graph(images)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        graph(images)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    graph_ms = e0.elapsed_time(e1) / steps
+    n_params = sum(p.numel() for p in m.parameters())
+    e2e_ms, sp_ms = statistics.mean(e2e), statistics.mean(sparse_ms)
+    return {
+        "workload": f"C5 VGGT-1B-style aggregator forward: S={views} views of 518x518, 24 frame + 24 global blocks, "
+                    f"dim 1024, 16 heads, global blocks 9-19 sparse (top-k {topk}), ViT-L/14 patch embedding, "
+                    f"{n_params / 1e9:.2f} B random-init parameters, bf16",
+        "e2e_ms": round(e2e_ms, 2),
+        "e2e_graph_ms": round(graph_ms, 2),
+        "sparse_global_attention_ms": round(sp_ms, 2),
+        "sparse_global_attention_share": round(sp_ms / e2e_ms, 4),
+    }
+
+
 def cpu_baseline(views: int, budget_s: float, rows_per_chunk: int = 128):
     """Times the fp32 CPU oracle (indexer scores + top-k + sparse attention) on query
     rows of the same layer until ``budget_s`` seconds have elapsed; scales to all rows."""
@@ -336,6 +407,7 @@ def main() -> int:
     ap.add_argument("--no-train", action="store_true", help="skip the C4 training-step timing")
     ap.add_argument("--no-long", action="store_true", help="skip the C3 (S=64) long-context timing")
     ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer (projection + glue) timing")
+    ap.add_argument("--no-c5", action="store_true", help="skip the C5 (full aggregator) timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run 3 plain device copies of 1 GiB (reference kernel for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE scaling)")
@@ -482,6 +554,9 @@ def main() -> int:
     if not args.no_layer:
         print("[bench] whole layer forward", file=sys.stderr, flush=True)
         result["layer_fwd_s32"] = layer_forward_s32()
+    if not args.no_c5:
+        print("[bench] C5 aggregator", file=sys.stderr, flush=True)
+        result["aggregator_c5"] = aggregator_c5()
     if not args.no_long:
         print("[bench] C3 long context", file=sys.stderr, flush=True)
         result["long_context_c3"] = long_context_c3()

@@ -194,10 +194,10 @@ extern "C" int gw_dsa_glue_fwd(int dtype, const void* y, int64_t rows, int64_t l
   clear_error();
   GW_CHECK_ARG(dtype == GW_DTYPE_BF16 || dtype == GW_DTYPE_FP16, "unsupported dtype code %d", dtype);
   if (D != kGlueD) return set_error(GW_ERR_UNSUPPORTED, "head dim %lld not supported (64)", (long long)D);
-  GW_CHECK_ARG(rows >= 0 && H >= 1 && Hi >= 1 && H <= 64 && Hi <= 64, "invalid sizes rows=%lld H=%lld Hi=%lld",
+  GW_CHECK_ARG(rows >= 0 && H >= 1 && Hi >= 0 && H <= 64 && Hi <= 64, "invalid sizes rows=%lld H=%lld Hi=%lld",
                (long long)rows, (long long)H, (long long)Hi);
   if (rows == 0) return GW_OK;
-  GW_CHECK_ARG(y && q_out && k_out && idx_q_out && idx_k_out && idx_w_out, "null tensor pointer");
+  GW_CHECK_ARG(y && q_out && k_out && (Hi == 0 || (idx_q_out && idx_k_out && idx_w_out)), "null tensor pointer");
   GW_CHECK_ARG(ldy % 8 == 0 && aligned16(y), "projection rows must be 16-byte aligned (ldy %% 8 == 0)");
   const int64_t offs[4] = {q_off, k_off, iq_off, ik_off};
   const int64_t widths[4] = {H * D, H * D, Hi * D, Hi * D};
@@ -211,7 +211,7 @@ extern "C" int gw_dsa_glue_fwd(int dtype, const void* y, int64_t rows, int64_t l
                "LayerNorm weight and bias must both be given or both be null");
   GW_CHECK_ARG(pos == nullptr || (rope_cos && rope_sin && rope_len >= 1), "rope tables missing");
   GW_CHECK_ARG(aligned16(q_out) && aligned16(k_out) && aligned16(idx_q_out) && aligned16(idx_k_out),
-               "outputs must be 16-byte aligned");
+               "outputs must be 16-byte aligned");  // null (Hi = 0) counts as aligned
   GW_CHECK_ARG(rows * (2 * H + 2 * Hi) < (1ll << 31) - 64, "rows x head vectors exceeds the 32-bit index range");
   GlueParams p{};
   p.y = static_cast<const uint16_t*>(y);

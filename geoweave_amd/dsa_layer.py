@@ -37,7 +37,8 @@ __all__ = ["GlueLayout", "rope2d_tables", "dsa_glue_forward", "LightningIndexerP
 
 
 class GlueLayout:
-    """Column blocks of the fused projection output (reference ``dsa_attention.py:590-600``)."""
+    """Column blocks of the fused projection output (reference ``dsa_attention.py:590-600``);
+    ``Hi = 0`` is a dense attention layer's plain qkv projection."""
 
     def __init__(self, H: int, D: int, Hi: int, Di: int):
         if D != 64 or Di != 64:
@@ -117,9 +118,9 @@ def dsa_glue_forward(
     dev = y.device
     q = torch.empty(B, N, H, 64, device=dev, dtype=y.dtype)
     k = torch.empty_like(q)
-    iq = torch.empty(B, N, Hi, 64, device=dev, dtype=y.dtype)
-    ik = torch.empty_like(iq)
-    iw = torch.empty(B, N, Hi, device=dev, dtype=y.dtype)
+    iq = torch.empty(B, N, Hi, 64, device=dev, dtype=y.dtype) if Hi else None
+    ik = torch.empty_like(iq) if Hi else None
+    iw = torch.empty(B, N, Hi, device=dev, dtype=y.dtype) if Hi else None
     pos32 = cos = sin = None
     n_rope = 0
     if pos is not None:
@@ -136,7 +137,7 @@ def dsa_glue_forward(
             _lib.ptr(q_norm[0]), _lib.ptr(q_norm[1]), _lib.ptr(k_norm[0]), _lib.ptr(k_norm[1]),
             _lib.ptr(idx_k_norm[0]), _lib.ptr(idx_k_norm[1]), float(ln_eps),
             _lib.ptr(pos32), _lib.ptr(cos), _lib.ptr(sin), n_rope,
-            q.data_ptr(), k.data_ptr(), iq.data_ptr(), ik.data_ptr(), iw.data_ptr(),
+            q.data_ptr(), k.data_ptr(), _lib.ptr(iq), _lib.ptr(ik), _lib.ptr(iw),
             _lib.stream_handle(dev),
         ),
         "gw_dsa_glue_fwd",
@@ -207,7 +208,13 @@ class SparseGlobalAttention(nn.Module):
 
     @torch.no_grad()
     def forward(self, x: torch.Tensor, pos: Optional[torch.Tensor] = None, topk: Optional[int] = None,
-                return_topk: bool = False):
+                return_topk: bool = False, topk_indices: Optional[torch.Tensor] = None,
+                rope_len: Optional[int] = None):
+        """``topk_indices`` (int32 ``[B, N, >= k]``): use another layer's selection and skip
+        this layer's indexer (the reference's ``reuse_topk_indices``,
+        ``dsa_attention.py:5014-5032``). ``rope_len``: rotary table length (default
+        ``max(pos) + 1``, read on the host; pass it to keep the forward free of host syncs,
+        e.g. under graph capture)."""
         if x.dtype not in (torch.bfloat16, torch.float16):
             raise TypeError("SparseGlobalAttention runs in bfloat16 or float16")
         B, N, _ = x.shape
@@ -216,10 +223,17 @@ class SparseGlobalAttention(nn.Module):
         q, k, v, iq, ik, iw = dsa_glue_forward(
             y, self.layout, _ln_params(self.q_norm), _ln_params(self.k_norm), _ln_params(self.indexer.k_norm),
             self.q_norm.eps if isinstance(self.q_norm, nn.LayerNorm) else 1e-5,
-            pos if self.rope_base else None, self.rope_base or 100.0)
+            pos if self.rope_base else None, self.rope_base or 100.0, rope_len)
         kk = min(int(topk or self.topk), N)
-        idx, _ = sparse_topk_indexer_inference_func(iq, ik, iw, iq.new_empty(0), kk, float(self.indexer.scale),
-                                                    256, 0)
+        if topk_indices is not None:
+            if topk_indices.dim() != 3 or tuple(topk_indices.shape[:2]) != (B, N) or topk_indices.shape[2] < kk:
+                raise ValueError(f"reused top-k indices {tuple(topk_indices.shape)} do not cover ({B}, {N}, {kk})")
+            idx = topk_indices[..., :kk]
+            if idx.dtype != torch.int32:
+                idx = idx.to(torch.int32)
+        else:
+            idx, _ = sparse_topk_indexer_inference_func(iq, ik, iw, iq.new_empty(0), kk,
+                                                        float(self.indexer.scale), 256, 0)
         o, _ = sparse_index_flash_attn_inference_func(q, k, v, idx, softmax_scale=self.scale)
         out = F.linear(o.reshape(B, N, self.dim), self.proj.weight.to(x.dtype),
                        None if self.proj.bias is None else self.proj.bias.to(x.dtype))

@@ -238,7 +238,9 @@ int gw_indexer_kl_bwd(int dtype, const void* attn_sum, const void* logits, const
  * fp32 [64] or both NULL (identity), eps ln_eps. pos: int32 [rows, 2] (y, x) or NULL (no
  * rope); rope_cos/rope_sin: fp32 [rope_len, 16] tables cos/sin(p * base^(-2i/32)), as
  * rope.py:86-117 builds them. Outputs (dtype, contiguous): q_out, k_out [rows, H, 64],
- * idx_q_out, idx_k_out [rows, Hi, 64], idx_w_out [rows, Hi].
+ * idx_q_out, idx_k_out [rows, Hi, 64], idx_w_out [rows, Hi]. Hi = 0 (a dense attention
+ * layer's q/k glue, easyvolcap/official_vggt/layers/attention.py:70-85) is allowed; the
+ * idx_* outputs may then be NULL.
  */
 int gw_dsa_glue_fwd(int dtype, const void* y, int64_t rows, int64_t ldy, int64_t q_off, int64_t k_off,
                     int64_t iq_off, int64_t ik_off, int64_t iw_off, int64_t H, int64_t Hi, int64_t D,

@@ -117,3 +117,31 @@ def test_kl_loss_rejects_cpu_tensors_and_shape_mismatch():
         sparse_indexer_kl_loss(a, torch.randn(1, 3, 9))
     empty = torch.zeros(1, 0, 8)
     assert float(sparse_indexer_kl_loss(empty, empty)) == 0.0
+
+
+def test_reuse_topk_group_and_layer_parsers_follow_the_reference_syntax():
+    # easyvolcap/official_vggt/models/aggregator.py:267-292 and :327-362
+    from geoweave_amd.aggregator import parse_indexer_layers, parse_reuse_topk_groups
+
+    assert parse_indexer_layers("9-19") == set(range(9, 20))
+    assert parse_indexer_layers("1,3, 5-7") == {1, 3, 5, 6, 7}
+    assert parse_indexer_layers("all") is None and parse_indexer_layers("*") is None
+    assert parse_indexer_layers("") == set() and parse_indexer_layers(None) is None
+    assert parse_indexer_layers([2, "4"]) == {2, 4}
+    assert parse_reuse_topk_groups("9:10,11") == {10: 9}  # "11" alone names no reuse
+    assert parse_reuse_topk_groups("9:10-12") == {10: 9, 11: 9, 12: 9}
+    assert parse_reuse_topk_groups("9-12") == {10: 9, 11: 9, 12: 9}
+    assert parse_reuse_topk_groups("12-9") == {10: 9, 11: 9, 12: 9}
+    assert parse_reuse_topk_groups(["9:9-10", "14-15"]) == {10: 9, 15: 14}
+    assert parse_reuse_topk_groups("") == {} and parse_reuse_topk_groups(None) is None
+
+
+def test_special_tokens_first_view_uses_slot_zero():
+    # aggregator.py:723-746
+    from geoweave_amd.aggregator import slice_expand_and_flatten
+
+    tok = torch.arange(2 * 3 * 4, dtype=torch.float32).view(1, 2, 3, 4)
+    out = slice_expand_and_flatten(tok, 2, 3).view(2, 3, 3, 4)
+    for b in range(2):
+        assert torch.equal(out[b, 0], tok[0, 0])
+        assert torch.equal(out[b, 1], tok[0, 1]) and torch.equal(out[b, 2], tok[0, 1])
