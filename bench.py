@@ -167,7 +167,36 @@ def long_context_c3(steps: int = 5, warmup: int = 2, views: int = 64, topk: int 
     att_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
     B, T, H, D = q.shape
     att_bytes = attn_fwd_algorithmic_bytes(B, T, H, D, topk)
+
+    # The query-chunked stream (dsa_attention.py:1017-1283): same work, the indices and the
+    # indexer workspace live per chunk of 16384 queries. Peak memory above the inputs.
+    from geoweave_amd.dsa_layer import sparse_attention_streaming
+
+    def peak_of(fn):
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated(dev)
+        torch.cuda.reset_peak_memory_stats(dev)
+        fn()
+        torch.cuda.synchronize()
+        return (torch.cuda.max_memory_allocated(dev) - base) / 1e9
+
+    chunk = 16384
+    stream = lambda: sparse_attention_streaming(q, k, v, qi, ki, wi, topk, chunk, 0.125, 0.125)
+    stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(torch.cuda.current_stream(dev))
+    for _ in range(steps):
+        stream()
+    e1.record(torch.cuda.current_stream(dev))
+    torch.cuda.synchronize()
+    stream_ms = e0.elapsed_time(e1) / steps
+    peak_whole = peak_of(lambda: one())
+    peak_stream = peak_of(stream)
     return {
+        "stream_query_chunk": chunk,
+        "stream_ms": round(stream_ms, 3),
+        "peak_extra_gb_whole": round(peak_whole, 2),
+        "peak_extra_gb_stream": round(peak_stream, 2),
         "workload": f"C3 long context: B=1, S={views} views (N={T}), H={H}, D={D}, top-k {topk}, bf16, "
                     "indexer + sparse attention forward",
         "value_ms": round(idx_ms + att_ms, 3),

@@ -32,8 +32,8 @@ from . import _lib
 from .custom_flash_attn.sparse_index_flash_attn import sparse_index_flash_attn_inference_func
 from .custom_indexer.sparse_topk_indexer import sparse_topk_indexer_inference_func
 
-__all__ = ["GlueLayout", "rope2d_tables", "dsa_glue_forward", "LightningIndexerProjections",
-           "SparseGlobalAttention"]
+__all__ = ["GlueLayout", "rope2d_tables", "dsa_glue_forward", "sparse_attention_streaming",
+           "LightningIndexerProjections", "SparseGlobalAttention"]
 
 
 class GlueLayout:
@@ -146,6 +146,26 @@ def dsa_glue_forward(
     return q, k, v, iq, ik, iw
 
 
+def sparse_attention_streaming(q, k, v, idx_q, idx_k, idx_w, topk: int, query_chunk: int,
+                               indexer_scale: float, softmax_scale: float) -> torch.Tensor:
+    """Indexer top-k and sparse attention ``query_chunk`` queries at a time (reference
+    ``DSAAttention._run_sparse_streaming_direct``, ``dsa_attention.py:1017-1283``): each
+    chunk's top-k indices live only while its attention runs, so peak memory for indices and
+    the indexer workspace scales with the chunk, not with N. Per-row results equal the
+    unchunked path's (rows are independent); q/idx_q ``[B, N, ...]``, k/v/idx_k/idx_w over all
+    keys. Returns o ``[B, N, H, D]``."""
+    B, N = q.shape[0], q.shape[1]
+    out = torch.empty(q.shape, device=q.device, dtype=q.dtype)
+    empty = idx_q.new_empty(0)
+    for s0 in range(0, N, query_chunk):
+        s1 = min(s0 + query_chunk, N)
+        idx, _ = sparse_topk_indexer_inference_func(idx_q[:, s0:s1], idx_k, idx_w, empty, topk, indexer_scale,
+                                                    256, 0)
+        o, _ = sparse_index_flash_attn_inference_func(q[:, s0:s1], k, v, idx, softmax_scale=softmax_scale)
+        out[:, s0:s1] = o
+    return out
+
+
 class LightningIndexerProjections(nn.Module):
     """Parameters of the reference ``LightningIndexer`` (``indexer.py:55-61``): q/k/w
     projections and the k LayerNorm; the gate starts at w = 1 (``:63-68``)."""
@@ -209,12 +229,15 @@ class SparseGlobalAttention(nn.Module):
     @torch.no_grad()
     def forward(self, x: torch.Tensor, pos: Optional[torch.Tensor] = None, topk: Optional[int] = None,
                 return_topk: bool = False, topk_indices: Optional[torch.Tensor] = None,
-                rope_len: Optional[int] = None):
+                rope_len: Optional[int] = None, query_chunk: Optional[int] = None):
         """``topk_indices`` (int32 ``[B, N, >= k]``): use another layer's selection and skip
         this layer's indexer (the reference's ``reuse_topk_indices``,
         ``dsa_attention.py:5014-5032``). ``rope_len``: rotary table length (default
         ``max(pos) + 1``, read on the host; pass it to keep the forward free of host syncs,
-        e.g. under graph capture)."""
+        e.g. under graph capture). ``query_chunk``: select and attend ``query_chunk`` queries
+        at a time (the reference's query-chunked sparse stream, ``dsa_attention.py:1017-1283``):
+        the same result with the indexer workspace and the index tensor bounded by the chunk;
+        ``return_topk`` then returns None for the indices."""
         if x.dtype not in (torch.bfloat16, torch.float16):
             raise TypeError("SparseGlobalAttention runs in bfloat16 or float16")
         B, N, _ = x.shape
@@ -225,6 +248,12 @@ class SparseGlobalAttention(nn.Module):
             self.q_norm.eps if isinstance(self.q_norm, nn.LayerNorm) else 1e-5,
             pos if self.rope_base else None, self.rope_base or 100.0, rope_len)
         kk = min(int(topk or self.topk), N)
+        if query_chunk is not None and 0 < int(query_chunk) < N and topk_indices is None:
+            o = sparse_attention_streaming(q, k, v, iq, ik, iw, kk, int(query_chunk), float(self.indexer.scale),
+                                           self.scale)
+            out = F.linear(o.reshape(B, N, self.dim), self.proj.weight.to(x.dtype),
+                           None if self.proj.bias is None else self.proj.bias.to(x.dtype))
+            return (out, None) if return_topk else out
         if topk_indices is not None:
             if topk_indices.dim() != 3 or tuple(topk_indices.shape[:2]) != (B, N) or topk_indices.shape[2] < kk:
                 raise ValueError(f"reused top-k indices {tuple(topk_indices.shape)} do not cover ({B}, {N}, {kk})")

@@ -121,3 +121,18 @@ def test_sparse_global_attention_layer_stage_by_stage(gpu_device):
     ref = F.linear(o.to(torch.bfloat16).float().reshape(B, N, dim), m.proj.weight.detach().bfloat16().float().cpu(),
                    m.proj.bias.detach().bfloat16().float().cpu())
     torch.testing.assert_close(out.float().cpu(), ref, **TOL)
+
+
+def test_query_chunked_stream_equals_the_whole_layer(gpu_device):
+    # The query-chunked sparse stream (dsa_attention.py:1017-1283) selects and attends per
+    # chunk of queries; rows are independent, so the output equals the unchunked layer's
+    # (up to the summation order of equal index sets).
+    B, N, dim = 1, 2500, 1024
+    m = _layer(dim).cuda()
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(B, N, dim, generator=g).bfloat16().cuda()
+    pos = torch.randint(0, 38, (B, N, 2), generator=g).cuda()
+    whole = m(x, pos)
+    chunked = m(x, pos, query_chunk=700)  # ragged last chunk
+    torch.cuda.synchronize()
+    torch.testing.assert_close(chunked.float(), whole.float(), atol=1e-2, rtol=1e-2)
