@@ -307,6 +307,57 @@ def layer_forward_s32(steps: int = 5, warmup: int = 2, views: int = 32, topk: in
     }
 
 
+def layer_train_c4(steps: int = 3, warmup: int = 1, views: int = 24, batch: int = 2, topk: int = 1024):
+    """The whole layer trained at the C4 shape (B=2, S=24 views, N=32,976), random-init
+    weights, bf16: ``SparseGlobalAttention.forward_train`` (fused projection, glue, indexer
+    top-k with scores, attention with attn_sum, output projection), the indexer KL loss on
+    the normalised attention mass, and the backward through every stage (GEMMs, glue,
+    attention, indexer, KL). HIP events on the launch stream."""
+    import torch
+
+    from geoweave_amd import dsa_layer, workloads
+    from geoweave_amd.custom_indexer import sparse_indexer_kl_loss
+
+    dev = torch.device("cuda", 0)
+    m = workloads.init_layer_(dsa_layer.SparseGlobalAttention(topk=topk)).to(dev).to(torch.bfloat16)
+    x, pos = workloads.layer_module_inputs(views, batch)
+    x, pos = x.to(dev).requires_grad_(), pos.to(dev)
+    g = torch.Generator(device=dev).manual_seed(views)
+    G = torch.randn(x.shape, generator=g, device=dev, dtype=torch.bfloat16)
+    rope_len = int(pos.max()) + 1
+    stream = torch.cuda.current_stream(dev)
+
+    def one(ev=None):
+        rec = (lambda i: ev[i].record(stream)) if ev else (lambda i: None)
+        m.zero_grad(set_to_none=True)
+        x.grad = None
+        rec(0)
+        out, attn, scores, _ = m.forward_train(x, pos, rope_len=rope_len)
+        p = attn.to(torch.bfloat16)
+        p = p / (p.sum(-1, keepdim=True) + 1e-6)
+        kl = sparse_indexer_kl_loss(p, scores, 1e-6)
+        rec(1)
+        torch.autograd.backward([out, kl], [G, None])
+        rec(2)
+
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    for i in range(steps):
+        one(evs[i])
+    torch.cuda.synchronize()
+    fwd = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+    bwd = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
+    return {
+        "workload": f"whole-layer training step: B={batch}, S={views} views (N={x.shape[1]}), dim 1024, 16 heads, "
+                    f"indexer 4x64, top-k {topk}, bf16, random-init weights, output-gradient + indexer KL loss",
+        "fwd_ms": round(fwd, 3),
+        "bwd_ms": round(bwd, 3),
+        "step_ms": round(fwd + bwd, 3),
+    }
+
+
 def aggregator_c5(steps: int = 2, warmup: int = 1, views: int = 32, topk: int = 1024):
     """Config C5: the VGGT-1B-style aggregator forward (DINOv2-style ViT-L/14 patch
     embedding, 24 frame + 24 global blocks, dim 1024, 16 heads, MLP ratio 4, global blocks
@@ -583,6 +634,9 @@ def main() -> int:
     if not args.no_layer:
         print("[bench] whole layer forward", file=sys.stderr, flush=True)
         result["layer_fwd_s32"] = layer_forward_s32()
+    if not args.no_train:
+        print("[bench] whole-layer training step", file=sys.stderr, flush=True)
+        result["layer_train_c4"] = layer_train_c4()
     if not args.no_c5:
         print("[bench] C5 aggregator", file=sys.stderr, flush=True)
         result["aggregator_c5"] = aggregator_c5()

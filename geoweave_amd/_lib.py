@@ -65,6 +65,13 @@ _SIGNATURES = {
         [ctypes.c_int, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
          _p, _p, _p, _p, _p, _p, ctypes.c_float, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p],
     ),
+    "gw_dsa_glue_bwd_workspace_size": (_sz, [_i64, _i64, _i64]),
+    "gw_dsa_glue_bwd": (
+        ctypes.c_int,
+        [ctypes.c_int, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+         _p, _p, _p, _p, _p, _p, ctypes.c_float, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p,
+         _p, _sz, _p],
+    ),
 }
 
 _lock = threading.Lock()

@@ -180,6 +180,149 @@ __global__ __launch_bounds__(256) void dsa_glue_kernel(const GlueParams p) {
   }
 }
 
+// Backward of the glue, one head vector per 8 lanes as in the forward. With
+// u = LN(x) (x_hat * g + b, or x without a norm) and o = R(p) u the rotation:
+//   du = R(p)^T do:  du[i] = do[i] c + do[i+16] s,  du[i+16] = do[i+16] c - do[i] s
+//   dg += du * x_hat,  db += du,  dx_hat = du * g,
+//   dx = rstd * (dx_hat - mean(dx_hat) - x_hat * mean(dx_hat * x_hat))
+// dy receives dx in the q, k, indexer q/k blocks and the gate gradient in the w block
+// (the v block is not written). dg/db are summed per workgroup into ws[block][3][2][64]
+// in a fixed order, then over workgroups by dsa_glue_ln_reduce_kernel.
+struct GlueBwdParams {
+  GlueParams f;            // forward inputs (y, layout, norms, rope); outputs unused
+  const uint16_t* dq;      // [rows, H, 64]
+  const uint16_t* dk;
+  const uint16_t* diq;     // [rows, Hi, 64]
+  const uint16_t* dik;
+  const uint16_t* diw;     // [rows, Hi]
+  uint16_t* dy;            // [rows, ldy]
+  float* ws;               // [gridDim.x][3][2][64]
+};
+
+template <typename E>
+__global__ __launch_bounds__(256) void dsa_glue_bwd_kernel(const GlueBwdParams bp) {
+  const GlueParams& p = bp.f;
+  __shared__ float ln_s[3][2][kGlueD];
+  __shared__ float rope_s[2][kGlueMaxRope * 16];
+  __shared__ float red[4][3][2][kGlueD];  // per-wave partial dg/db
+  const float* lnw[3] = {p.qn_w, p.kn_w, p.ikn_w};
+  const float* lnb[3] = {p.qn_b, p.kn_b, p.ikn_b};
+  for (int i = threadIdx.x; i < 3 * kGlueD; i += blockDim.x) {
+    const int t = i / kGlueD, d = i % kGlueD;
+    ln_s[t][0][d] = lnw[t] ? lnw[t][d] : 1.f;
+    ln_s[t][1][d] = lnb[t] ? lnb[t][d] : 0.f;
+  }
+  const bool rope_lds = p.pos != nullptr && p.rope_len <= kGlueMaxRope;
+  if (rope_lds) {
+    for (int i = threadIdx.x; i < p.rope_len * 16; i += blockDim.x) {
+      rope_s[0][i] = p.rope_cos[i];
+      rope_s[1][i] = p.rope_sin[i];
+    }
+  }
+  __syncthreads();
+  const float* cos_t = rope_lds ? rope_s[0] : p.rope_cos;
+  const float* sin_t = rope_lds ? rope_s[1] : p.rope_sin;
+
+  float acc[3][2][8];
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[t][0][e] = acc[t][1][e] = 0.f;
+
+  const uint32_t slots = 2 * p.H + 2 * p.Hi;
+  const uint32_t nvec = (uint32_t)(p.rows * slots);
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int j = lane & 7;
+  const int grp = lane >> 3;
+  const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
+  for (uint32_t w = blockIdx.x * (blockDim.x >> 6) + wv; w * 8 < nvec; w += nwaves) {
+    const GlueVec v = glue_vec(p, w * 8 + grp, nvec, slots);
+    if (!v.live) continue;  // uniform over the 8-lane group
+    const int64_t row = v.row;
+    const int slot = (int)(w * 8 + grp - v.row * slots);
+    const uint16_t* gsrc;
+    if (slot < p.H) gsrc = bp.dq;
+    else if (slot < 2 * p.H) gsrc = bp.dk;
+    else if (slot < 2 * p.H + p.Hi) gsrc = bp.diq;
+    else gsrc = bp.dik;
+    float x[8], d[8];
+    unpack8<E>(*reinterpret_cast<const uint4*>(p.y + row * p.ldy + v.col + 8 * j), x);
+    unpack8<E>(*reinterpret_cast<const uint4*>(gsrc + (row * v.out_heads + v.head) * kGlueD + 8 * j), d);
+    if (v.gate && j == 0) bp.dy[row * p.ldy + p.iw_off + v.head] = bp.diw[row * p.Hi + v.head];
+    if (p.pos != nullptr) {  // du = R^T do
+      const int pp = min(max(p.pos[row * 2 + (j >> 2)], 0), p.rope_len - 1);
+      const float* c = cos_t + pp * 16 + 8 * (j & 1);
+      const float* sn = sin_t + pp * 16 + 8 * (j & 1);
+      const float sign = (j & 2) ? -1.f : 1.f;  // dims [0, 16) take +do[i+16] s, [16, 32) -do[i] s
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float partner = dpp<kDppXor2>(d[e]);
+        d[e] = d[e] * c[e] + sign * partner * sn[e];
+      }
+    }
+    if (v.norm >= 0) {
+      const float* g = &ln_s[v.norm][0][8 * j];
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += x[e];
+      const float mean = group_sum<8>(s) * (1.f / kGlueD);
+      float var = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float t = x[e] - mean;
+        var += t * t;
+      }
+      const float rstd = 1.f / sqrtf(group_sum<8>(var) * (1.f / kGlueD) + p.ln_eps);
+      float xh[8], dxh[8], m1 = 0.f, m2 = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xh[e] = (x[e] - mean) * rstd;
+        dxh[e] = d[e] * g[e];
+        m1 += dxh[e];
+        m2 += dxh[e] * xh[e];
+      }
+      m1 = group_sum<8>(m1) * (1.f / kGlueD);
+      m2 = group_sum<8>(m2) * (1.f / kGlueD);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        acc[v.norm][0][e] += d[e] * xh[e];
+        acc[v.norm][1][e] += d[e];
+        d[e] = rstd * (dxh[e] - m1 - xh[e] * m2);
+      }
+    }
+    *reinterpret_cast<uint4*>(bp.dy + row * p.ldy + v.col + 8 * j) = pack8<E>(d);
+  }
+  // Block sums of dg/db: lanes with the same chunk j (8 groups of a wave) first, then the
+  // four waves, in a fixed order.
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float x = acc[t][k][e];
+        x += __shfl_xor(x, 8);
+        x += __shfl_xor(x, 16);
+        x += __shfl_xor(x, 32);
+        if (grp == 0) red[wv][t][k][8 * j + e] = x;
+      }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 3 * 2 * kGlueD; i += blockDim.x) {
+    const float* r = &red[0][0][0][0] + i;
+    const int stride = 3 * 2 * kGlueD;
+    bp.ws[(int64_t)blockIdx.x * stride + i] = ((r[0] + r[stride]) + r[2 * stride]) + r[3 * stride];
+  }
+}
+
+__global__ __launch_bounds__(256) void dsa_glue_ln_reduce_kernel(const float* ws, int nblocks, float* dln) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= 3 * 2 * kGlueD) return;
+  float s = 0.f;
+  for (int b = 0; b < nblocks; ++b) s += ws[(int64_t)b * 3 * 2 * kGlueD + i];
+  dln[i] = s;
+}
+
 }  // namespace
 }  // namespace gw
 
@@ -249,5 +392,88 @@ extern "C" int gw_dsa_glue_fwd(int dtype, const void* y, int64_t rows, int64_t l
   else
     hipLaunchKernelGGL((dsa_glue_kernel<FP16>), grid, dim3(256), 0, st, p);
   GW_HIP_LAUNCH_CHECK("dsa_glue_kernel");
+  return GW_OK;
+}
+
+extern "C" size_t gw_dsa_glue_bwd_workspace_size(int64_t rows, int64_t H, int64_t Hi) {
+  const int64_t vectors = rows * (2 * H + 2 * Hi);
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>((vectors + 31) / 32, 2048));
+  return (size_t)blocks * 3 * 2 * 64 * sizeof(float);
+}
+
+extern "C" int gw_dsa_glue_bwd(int dtype, const void* y, int64_t rows, int64_t ldy, int64_t q_off, int64_t k_off,
+                               int64_t iq_off, int64_t ik_off, int64_t iw_off, int64_t H, int64_t Hi, int64_t D,
+                               const float* q_norm_w, const float* q_norm_b, const float* k_norm_w,
+                               const float* k_norm_b, const float* idx_k_norm_w, const float* idx_k_norm_b,
+                               float ln_eps, const int32_t* pos, const float* rope_cos, const float* rope_sin,
+                               int64_t rope_len, const void* dq, const void* dk, const void* d_idx_q,
+                               const void* d_idx_k, const void* d_idx_w, void* dy, float* d_norm,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace gw;
+  clear_error();
+  GW_CHECK_ARG(dtype == GW_DTYPE_BF16 || dtype == GW_DTYPE_FP16, "unsupported dtype code %d", dtype);
+  if (D != kGlueD) return set_error(GW_ERR_UNSUPPORTED, "head dim %lld not supported (64)", (long long)D);
+  GW_CHECK_ARG(rows >= 0 && H >= 1 && Hi >= 0 && H <= 64 && Hi <= 64, "invalid sizes rows=%lld H=%lld Hi=%lld",
+               (long long)rows, (long long)H, (long long)Hi);
+  GW_CHECK_ARG(d_norm != nullptr, "null d_norm");
+  GW_CHECK_ARG(y && dy && dq && dk && (Hi == 0 || (d_idx_q && d_idx_k && d_idx_w)), "null tensor pointer");
+  GW_CHECK_ARG(ldy % 8 == 0 && aligned16(y) && aligned16(dy), "rows must be 16-byte aligned (ldy %% 8 == 0)");
+  const int64_t offs[4] = {q_off, k_off, iq_off, ik_off};
+  const int64_t widths[4] = {H * D, H * D, Hi * D, Hi * D};
+  for (int i = 0; i < 4; ++i)
+    GW_CHECK_ARG(offs[i] >= 0 && offs[i] % 8 == 0 && offs[i] + widths[i] <= ldy,
+                 "column block %d at %lld (+%lld) must be 8-aligned and inside ldy=%lld", i, (long long)offs[i],
+                 (long long)widths[i], (long long)ldy);
+  GW_CHECK_ARG(iw_off >= 0 && iw_off + Hi <= ldy, "indexer gate columns outside the row");
+  GW_CHECK_ARG((q_norm_w == nullptr) == (q_norm_b == nullptr) && (k_norm_w == nullptr) == (k_norm_b == nullptr) &&
+                   (idx_k_norm_w == nullptr) == (idx_k_norm_b == nullptr),
+               "LayerNorm weight and bias must both be given or both be null");
+  GW_CHECK_ARG(pos == nullptr || (rope_cos && rope_sin && rope_len >= 1), "rope tables missing");
+  GW_CHECK_ARG(aligned16(dq) && aligned16(dk) && aligned16(d_idx_q) && aligned16(d_idx_k),
+               "gradients must be 16-byte aligned");
+  GW_CHECK_ARG(rows * (2 * H + 2 * Hi) < (1ll << 31) - 64, "rows x head vectors exceeds the 32-bit index range");
+  const size_t need = gw_dsa_glue_bwd_workspace_size(rows, H, Hi);
+  GW_CHECK_ARG(workspace && workspace_bytes >= need && aligned16(workspace), "workspace needs %zu bytes", need);
+  GlueBwdParams bp{};
+  GlueParams& p = bp.f;
+  p.y = static_cast<const uint16_t*>(y);
+  p.ldy = ldy;
+  p.q_off = (int)q_off;
+  p.k_off = (int)k_off;
+  p.iq_off = (int)iq_off;
+  p.ik_off = (int)ik_off;
+  p.iw_off = (int)iw_off;
+  p.H = (int)H;
+  p.Hi = (int)Hi;
+  p.qn_w = q_norm_w;
+  p.qn_b = q_norm_b;
+  p.kn_w = k_norm_w;
+  p.kn_b = k_norm_b;
+  p.ikn_w = idx_k_norm_w;
+  p.ikn_b = idx_k_norm_b;
+  p.ln_eps = ln_eps;
+  p.pos = pos;
+  p.rope_cos = rope_cos;
+  p.rope_sin = rope_sin;
+  p.rope_len = (int)rope_len;
+  p.rows = rows;
+  bp.dq = static_cast<const uint16_t*>(dq);
+  bp.dk = static_cast<const uint16_t*>(dk);
+  bp.diq = static_cast<const uint16_t*>(d_idx_q);
+  bp.dik = static_cast<const uint16_t*>(d_idx_k);
+  bp.diw = static_cast<const uint16_t*>(d_idx_w);
+  bp.dy = static_cast<uint16_t*>(dy);
+  bp.ws = static_cast<float*>(workspace);
+  const int64_t vectors = rows * (2 * H + 2 * Hi);
+  const int nblocks = (int)std::max<int64_t>(1, std::min<int64_t>((vectors + 31) / 32, 2048));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == GW_DTYPE_BF16)
+    hipLaunchKernelGGL((dsa_glue_bwd_kernel<BF16>), dim3(nblocks), dim3(256), 0, st, bp);
+  else
+    hipLaunchKernelGGL((dsa_glue_bwd_kernel<FP16>), dim3(nblocks), dim3(256), 0, st, bp);
+  GW_HIP_LAUNCH_CHECK("dsa_glue_bwd_kernel");
+  hipLaunchKernelGGL(dsa_glue_ln_reduce_kernel, dim3(2), dim3(256), 0, st, static_cast<const float*>(workspace),
+                     nblocks, d_norm);
+  GW_HIP_LAUNCH_CHECK("dsa_glue_ln_reduce_kernel");
   return GW_OK;
 }

@@ -29,8 +29,11 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _lib
-from .custom_flash_attn.sparse_index_flash_attn import sparse_index_flash_attn_inference_func
-from .custom_indexer.sparse_topk_indexer import sparse_topk_indexer_inference_func
+from .custom_flash_attn.sparse_index_flash_attn import (
+    sparse_index_flash_attn_func,
+    sparse_index_flash_attn_inference_func,
+)
+from .custom_indexer.sparse_topk_indexer import sparse_topk_indexer_func, sparse_topk_indexer_inference_func
 
 __all__ = ["GlueLayout", "rope2d_tables", "dsa_glue_forward", "sparse_attention_streaming",
            "LightningIndexerProjections", "SparseGlobalAttention"]
@@ -166,6 +169,66 @@ def sparse_attention_streaming(q, k, v, idx_q, idx_k, idx_w, topk: int, query_ch
     return out
 
 
+def _glue_args(y, layout, norms, ln_eps, pos32, cos, sin, n_rope):
+    B, N = y.shape[0], y.shape[1]
+    (qw, qb), (kw, kb), (iw_, ib) = norms
+    return [_lib.dtype_code(y.dtype), y.data_ptr(), B * N, layout.ldy, layout.q_off, layout.k_off,
+            layout.iq_off, layout.ik_off, layout.iw_off, layout.H, layout.Hi, 64,
+            _lib.ptr(qw), _lib.ptr(qb), _lib.ptr(kw), _lib.ptr(kb), _lib.ptr(iw_), _lib.ptr(ib), float(ln_eps),
+            _lib.ptr(pos32), _lib.ptr(cos), _lib.ptr(sin), n_rope]
+
+
+class GlueFunction(torch.autograd.Function):
+    """Autograd wrapper of the glue: ``forward(y, qn_w, qn_b, kn_w, kn_b, ikn_w, ikn_b,
+    layout, ln_eps, pos32, cos, sin, n_rope) -> (q, k, idx_q, idx_k, idx_w)``; the backward
+    (``gw_dsa_glue_bwd``) returns dy (zero in the v block and the padding, where the v
+    view's own gradient is added by autograd) and the LayerNorm weight/bias gradients. The
+    LayerNorm parameters are fp32 tensors (pass ``param.float()`` to train them)."""
+
+    @staticmethod
+    def forward(ctx, y, qn_w, qn_b, kn_w, kn_b, ikn_w, ikn_b, layout, ln_eps, pos32, cos, sin, n_rope):
+        B, N = y.shape[0], y.shape[1]
+        H, Hi = layout.H, layout.Hi
+        q = torch.empty(B, N, H, 64, device=y.device, dtype=y.dtype)
+        k = torch.empty_like(q)
+        iq = torch.empty(B, N, Hi, 64, device=y.device, dtype=y.dtype)
+        ik = torch.empty_like(iq)
+        iw = torch.empty(B, N, Hi, device=y.device, dtype=y.dtype)
+        norms = ((qn_w, qn_b), (kn_w, kn_b), (ikn_w, ikn_b))
+        lib = _lib.load()
+        _lib.check(lib.gw_dsa_glue_fwd(*_glue_args(y, layout, norms, ln_eps, pos32, cos, sin, n_rope),
+                                       q.data_ptr(), k.data_ptr(), iq.data_ptr(), ik.data_ptr(), iw.data_ptr(),
+                                       _lib.stream_handle(y.device)), "gw_dsa_glue_fwd")
+        ctx.save_for_backward(y, qn_w, qn_b, kn_w, kn_b, ikn_w, ikn_b, pos32, cos, sin)
+        ctx.layout, ctx.ln_eps, ctx.n_rope = layout, ln_eps, n_rope
+        ctx.has_norm = (qn_w is not None, kn_w is not None, ikn_w is not None)
+        return q, k, iq, ik, iw
+
+    @staticmethod
+    def backward(ctx, dq, dk, diq, dik, diw):
+        y, qn_w, qn_b, kn_w, kn_b, ikn_w, ikn_b, pos32, cos, sin = ctx.saved_tensors
+        layout = ctx.layout
+        B, N = y.shape[0], y.shape[1]
+        grads = []
+        for g, shape in ((dq, (B, N, layout.H, 64)), (dk, (B, N, layout.H, 64)), (diq, (B, N, layout.Hi, 64)),
+                         (dik, (B, N, layout.Hi, 64)), (diw, (B, N, layout.Hi))):
+            g = torch.zeros(shape, device=y.device, dtype=y.dtype) if g is None else g.to(y.dtype).contiguous()
+            grads.append(g)
+        dy = torch.zeros_like(y)
+        dln = torch.empty(3, 2, 64, device=y.device, dtype=torch.float32)
+        lib = _lib.load()
+        nbytes = lib.gw_dsa_glue_bwd_workspace_size(B * N, layout.H, layout.Hi)
+        ws = torch.empty(nbytes, device=y.device, dtype=torch.uint8)
+        norms = ((qn_w, qn_b), (kn_w, kn_b), (ikn_w, ikn_b))
+        _lib.check(lib.gw_dsa_glue_bwd(*_glue_args(y, layout, norms, ctx.ln_eps, pos32, cos, sin, ctx.n_rope),
+                                       *[g.data_ptr() for g in grads], dy.data_ptr(), dln.data_ptr(), ws.data_ptr(),
+                                       nbytes, _lib.stream_handle(y.device)), "gw_dsa_glue_bwd")
+        out = [dy]
+        for t, has in enumerate(ctx.has_norm):
+            out += [dln[t, 0], dln[t, 1]] if has else [None, None]
+        return (*out, None, None, None, None, None, None)
+
+
 class LightningIndexerProjections(nn.Module):
     """Parameters of the reference ``LightningIndexer`` (``indexer.py:55-61``): q/k/w
     projections and the k LayerNorm; the gate starts at w = 1 (``:63-68``)."""
@@ -267,3 +330,43 @@ class SparseGlobalAttention(nn.Module):
         out = F.linear(o.reshape(B, N, self.dim), self.proj.weight.to(x.dtype),
                        None if self.proj.bias is None else self.proj.bias.to(x.dtype))
         return (out, idx) if return_topk else out
+
+    def forward_train(self, x: torch.Tensor, pos: Optional[torch.Tensor] = None, topk: Optional[int] = None,
+                      rope_len: Optional[int] = None):
+        """Differentiable forward (training): ``-> (out, attn_sum, topk_scores, topk_indices)``.
+        Gradients reach x and every parameter: the fused projection (autograd of the GEMM),
+        the glue (``GlueFunction``: ``gw_dsa_glue_bwd``), the attention
+        (``sparse_index_flash_attn_func``) and, through ``topk_scores``, the indexer
+        (``sparse_topk_indexer_func``); ``attn_sum`` and ``topk_scores`` feed the indexer KL
+        loss as in ``dsa_attention.py:5404-5411``."""
+        if x.dtype not in (torch.bfloat16, torch.float16):
+            raise TypeError("SparseGlobalAttention runs in bfloat16 or float16")
+        B, N, _ = x.shape
+        lins = (self.qkv, self.indexer.q_proj, self.indexer.k_proj, self.indexer.w_proj)
+        pad = self.layout.ldy - self.layout.width
+        w = torch.cat([l.weight for l in lins] + ([x.new_zeros(pad, self.dim)] if pad else []), 0).to(x.dtype)
+        b = torch.cat([l.bias for l in lins] + ([x.new_zeros(pad)] if pad else []), 0).to(x.dtype)
+        y = F.linear(x, w, b)
+        lay = self.layout
+        pos32 = cos = sin = None
+        n_rope = 0
+        if pos is not None and self.rope_base:
+            pos32 = pos.to(device=x.device, dtype=torch.int32).contiguous()
+            n_rope = int(rope_len) if rope_len is not None else int(pos32.max()) + 1
+            cos, sin = rope2d_tables(n_rope, self.rope_base, x.device)
+
+        def ln(norm):
+            if isinstance(norm, nn.Identity):
+                return None, None
+            return norm.weight.float(), norm.bias.float()
+
+        eps = self.q_norm.eps if isinstance(self.q_norm, nn.LayerNorm) else 1e-5
+        q, k, iq, ik, iw = GlueFunction.apply(y, *ln(self.q_norm), *ln(self.k_norm), *ln(self.indexer.k_norm), lay, eps,
+                                              pos32, cos, sin, n_rope)
+        v = y[..., lay.v_off:lay.v_off + lay.H * 64].view(B, N, lay.H, 64)
+        kk = min(int(topk or self.topk), N)
+        idx, scores = sparse_topk_indexer_func(iq, ik, iw, iq.new_empty(0), kk, float(self.indexer.scale), 256, 0)
+        o, attn = sparse_index_flash_attn_func(q, k, v, idx, None, False, self.scale)
+        out = F.linear(o.reshape(B, N, self.dim), self.proj.weight.to(x.dtype),
+                       None if self.proj.bias is None else self.proj.bias.to(x.dtype))
+        return out, attn, scores, idx

@@ -250,6 +250,29 @@ int gw_dsa_glue_fwd(int dtype, const void* y, int64_t rows, int64_t ldy, int64_t
                     int64_t rope_len, void* q_out, void* k_out, void* idx_q_out, void* idx_k_out,
                     void* idx_w_out, void* stream);
 
+/* ------------------------------------------------------------------------------------
+ * DSA layer glue, backward (training through the layer).
+ *
+ * Gradient of gw_dsa_glue_fwd, i.e. of the reference's q_norm/k_norm + rope + cast glue
+ * (dsa_attention.py:4928-4948, indexer.py:302-328; autograd of those torch ops in the
+ * reference). Inputs: the forward's arguments (y, layout, LayerNorm parameters, positions,
+ * rope tables) and the output gradients dq, dk [rows, H, 64], d_idx_q, d_idx_k
+ * [rows, Hi, 64], d_idx_w [rows, Hi] (dtype, contiguous). Writes dy [rows, ldy] (dtype) in
+ * the q, k, indexer q/k/w column blocks only (the v block and the padding are not written:
+ * the caller zero-fills them or adds the attention's dv there), and d_norm fp32 [3][2][64]
+ * = (d weight, d bias) of (q_norm, k_norm, indexer k_norm), summed over all rows and heads
+ * in a fixed order (bitwise reproducible). workspace: gw_dsa_glue_bwd_workspace_size bytes.
+ */
+size_t gw_dsa_glue_bwd_workspace_size(int64_t rows, int64_t H, int64_t Hi);
+int gw_dsa_glue_bwd(int dtype, const void* y, int64_t rows, int64_t ldy, int64_t q_off, int64_t k_off,
+                    int64_t iq_off, int64_t ik_off, int64_t iw_off, int64_t H, int64_t Hi, int64_t D,
+                    const float* q_norm_w, const float* q_norm_b, const float* k_norm_w,
+                    const float* k_norm_b, const float* idx_k_norm_w, const float* idx_k_norm_b,
+                    float ln_eps, const int32_t* pos, const float* rope_cos, const float* rope_sin,
+                    int64_t rope_len, const void* dq, const void* dk, const void* d_idx_q,
+                    const void* d_idx_k, const void* d_idx_w, void* dy, float* d_norm,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -134,6 +134,36 @@ def sparse_attention_bwd(
     return dq, dk, dv
 
 
+def sparse_attention_differentiable(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    kv_positions: torch.Tensor,
+    softmax_scale: Optional[float] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(o, attn_sum) of the textbook forward as differentiable torch ops on the inputs'
+    autograd graph (small shapes only): the forward of ``_reference_sparse_attn``
+    (reference ``tests/sparse_index_flash_attn_tests.py:47-71``) with attn_sum = sum of p over
+    heads (``sparse_index_flash_attn.py:375-458``)."""
+    bsz, tgt_len, n_heads, head_dim = q.shape
+    src_len = k.shape[1]
+    scale = _scale(head_dim, softmax_scale)
+    pos = kv_positions.long()
+    valid = _valid(pos, src_len)
+    safe = torch.where(valid, pos, torch.zeros_like(pos))
+    outs = []
+    sums = []
+    for b in range(bsz):
+        k_sel = k[b][safe[b]]
+        v_sel = v[b][safe[b]]
+        s = torch.einsum("thd,tkhd->thk", q[b], k_sel) * scale
+        s = s.masked_fill(~valid[b][:, None, :], float("-inf"))
+        p = torch.softmax(s, dim=-1).masked_fill(~valid[b][:, None, :], 0.0)
+        outs.append(torch.einsum("thk,tkhd->thd", p, v_sel))
+        sums.append(p.sum(dim=1))
+    return torch.stack(outs), torch.stack(sums)
+
+
 def sparse_attention_autograd(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -152,24 +182,7 @@ def sparse_attention_autograd(
     q = q.detach().float().requires_grad_()
     k = k.detach().float().requires_grad_()
     v = v.detach().float().requires_grad_()
-    bsz, tgt_len, n_heads, head_dim = q.shape
-    src_len = k.shape[1]
-    scale = _scale(head_dim, softmax_scale)
-    pos = kv_positions.long()
-    valid = _valid(pos, src_len)
-    safe = torch.where(valid, pos, torch.zeros_like(pos))
-    outs = []
-    sums = []
-    for b in range(bsz):
-        k_sel = k[b][safe[b]]
-        v_sel = v[b][safe[b]]
-        s = torch.einsum("thd,tkhd->thk", q[b], k_sel) * scale
-        s = s.masked_fill(~valid[b][:, None, :], float("-inf"))
-        p = torch.softmax(s, dim=-1).masked_fill(~valid[b][:, None, :], 0.0)
-        outs.append(torch.einsum("thk,tkhd->thd", p, v_sel))
-        sums.append(p.sum(dim=1))
-    o = torch.stack(outs)
-    attn_sum = torch.stack(sums)
+    o, attn_sum = sparse_attention_differentiable(q, k, v, kv_positions, softmax_scale)
     loss = (o * do.float()).sum()
     if dattn is not None:
         loss = loss + (attn_sum * dattn.float()).sum()

@@ -66,3 +66,13 @@ def kl_loss_bwd(
     d_attn = (g - gbar) * gs / denom
     d_logits = (torch.exp(log_q) - p) * gs
     return d_attn.reshape(attn_sum.shape), d_logits.reshape(logits.shape)
+
+
+def kl_loss_autograd(attn_sum: torch.Tensor, logits: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """The reference's torch formula as differentiable ops in the inputs' dtype
+    (``indexer_kl_fused.py:158-161``): ``p = attn / (sum attn + eps)``,
+    ``mean((p * (log(p + eps) - log_softmax(logits))).sum(-1))``. Its logits gradient is the
+    exact one (see ``kl_loss_bwd`` for the fused kernel's)."""
+    p = attn_sum / (attn_sum.sum(dim=-1, keepdim=True) + eps)
+    log_q = torch.log_softmax(logits, dim=-1)
+    return (p * (torch.log(p + eps) - log_q)).sum(dim=-1).mean()

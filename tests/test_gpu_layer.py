@@ -136,3 +136,101 @@ def test_query_chunked_stream_equals_the_whole_layer(gpu_device):
     chunked = m(x, pos, query_chunk=700)  # ragged last chunk
     torch.cuda.synchronize()
     torch.testing.assert_close(chunked.float(), whole.float(), atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("with_ln,with_rope", [(True, True), (False, True), (True, False)])
+def test_glue_backward_matches_autograd_of_the_oracle(gpu_device, with_ln, with_rope):
+    lay, y, norms, pos = _glue_case(2, 257, 16, 4, torch.bfloat16, seed=40 + with_ln + 2 * with_rope,
+                                    with_ln=with_ln, with_rope=with_rope)
+    g = torch.Generator().manual_seed(41)
+    gq, gk = (torch.randn(2, 257, 16, 64, generator=g).bfloat16() for _ in range(2))
+    giq, gik = (torch.randn(2, 257, 4, 64, generator=g).bfloat16() for _ in range(2))
+    giw = torch.randn(2, 257, 4, generator=g).bfloat16()
+    dev = "cuda"
+    yd = y.to(dev).requires_grad_()
+    nd = {k: None if v is None else tuple(t.to(dev).requires_grad_() for t in v) for k, v in norms.items()}
+    pos32 = cos = sin = None
+    n_rope = 0
+    if pos is not None:
+        pos32 = pos.to(dev, torch.int32)
+        n_rope = int(pos.max()) + 1
+        cos, sin = dsa_layer.rope2d_tables(n_rope, 100.0, dev)
+    flat = lambda key: (None, None) if nd[key] is None else nd[key]
+    outs = dsa_layer.GlueFunction.apply(yd, *flat("q"), *flat("k"), *flat("idx_k"), lay, 1e-5, pos32, cos, sin,
+                                        n_rope)
+    torch.autograd.backward(outs, [t.to(dev) for t in (gq, gk, giq, gik, giw)])
+    torch.cuda.synchronize()
+
+    yr = y[..., :lay.width].float().requires_grad_()
+    nr = {k: None if v is None else tuple(t.clone().requires_grad_() for t in v) for k, v in norms.items()}
+    q, k, v, iq, ik, iw = olg.fused_projection_glue(None, None, None, dict(H=16, D=64, Hi=4, Di=64), nr, pos, y=yr)
+    loss = sum((a * b.float()).sum() for a, b in zip((q, k, iq, ik, iw), (gq, gk, giq, gik, giw)))
+    loss.backward()
+    got = yd.grad.float().cpu()
+    torch.testing.assert_close(got[..., :lay.width], yr.grad, **TOL)
+    assert float(got[..., lay.v_off:lay.v_off + 16 * 64].abs().max()) == 0.0  # v block left to the v view
+    assert float(got[..., lay.width:].abs().max()) == 0.0
+    if with_ln:
+        for key in ("q", "k", "idx_k"):
+            for a, b in zip(nd[key], nr[key]):
+                err = float((a.grad.cpu() - b.grad).norm() / b.grad.norm())
+                assert err < 2e-3, (key, err)
+
+
+def test_layer_training_gradients_match_the_fp32_pipeline(gpu_device):
+    # forward_train + KL loss through every HIP backward (glue, indexer, attention, KL) vs
+    # autograd of the fp32 CPU pipeline on the same bf16 inputs/weights and the GPU's own
+    # top-k indices. Bar: per-tensor relative error (norm) within 2e-2.
+    from geoweave_amd.custom_indexer import sparse_indexer_kl_loss
+    from oracle import kl_loss as okl
+
+    B, N, dim, K = 1, 600, 256, 64
+    torch.manual_seed(3)
+    m = dsa_layer.SparseGlobalAttention(dim=dim, num_heads=4, topk=K)
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            p.copy_(torch.randn_like(p) * (dim ** -0.5 if p.dim() == 2 else 0.1))
+        for norm in (m.q_norm, m.k_norm, m.indexer.k_norm):
+            norm.weight.add_(1.0)
+        m.indexer.w_proj.bias.fill_(1.0)
+    m = m.to(torch.bfloat16)
+    ref_m = {n: p.detach().float().clone().requires_grad_() for n, p in m.named_parameters()}
+    m = m.cuda()
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(B, N, dim, generator=g).bfloat16()
+    pos = torch.randint(0, 12, (B, N, 2), generator=g)
+    G = torch.randn(B, N, dim, generator=g) * 0.1
+
+    xd = x.cuda().requires_grad_()
+    out, attn, scores, idx = m.forward_train(xd, pos.cuda())
+    p = attn.to(torch.bfloat16)
+    p = p / (p.sum(-1, keepdim=True) + 1e-6)
+    loss = (out.float() * G.cuda()).sum() + sparse_indexer_kl_loss(p, scores, 1e-6)
+    loss.backward()
+    torch.cuda.synchronize()
+
+    # fp32 reference pipeline with the GPU's indices
+    xr = x.float().requires_grad_()
+    W = torch.cat([ref_m[f"{n}.weight"] for n in ("qkv", "indexer.q_proj", "indexer.k_proj", "indexer.w_proj")])
+    bvec = torch.cat([ref_m[f"{n}.bias"] for n in ("qkv", "indexer.q_proj", "indexer.k_proj", "indexer.w_proj")])
+    norms = {"q": (ref_m["q_norm.weight"], ref_m["q_norm.bias"]), "k": (ref_m["k_norm.weight"], ref_m["k_norm.bias"]),
+             "idx_k": (ref_m["indexer.k_norm.weight"], ref_m["indexer.k_norm.bias"])}
+    q, k, v, iq, ik, iw = olg.fused_projection_glue(xr, W, bvec, dict(H=4, D=64, Hi=4, Di=64), norms, pos)
+    idx_c = idx.cpu()
+    sc = oidx.selected_scores(iq, ik, iw, idx_c, 0.125)
+    o, attn_r = oatt.sparse_attention_differentiable(q, k, v, idx_c, 0.125)
+    outr = torch.nn.functional.linear(o.reshape(B, N, dim), ref_m["proj.weight"], ref_m["proj.bias"])
+    pr = attn_r / (attn_r.sum(-1, keepdim=True) + 1e-6)
+    lossr = (outr * G).sum() + okl.kl_loss_autograd(pr, sc, 1e-6)
+    lossr.backward()
+
+    def rel(a, b):
+        return float((a.float().cpu() - b).norm() / b.norm())
+
+    assert rel(out.detach(), outr.detach()) < 2e-2
+    assert rel(xd.grad, xr.grad) < 2e-2
+    params = dict(m.named_parameters())
+    for name in ("qkv.weight", "qkv.bias", "q_norm.weight", "k_norm.bias", "proj.weight",
+                 "indexer.q_proj.weight", "indexer.k_proj.weight", "indexer.k_norm.weight", "indexer.w_proj.weight"):
+        assert params[name].grad is not None, name
+        assert rel(params[name].grad, ref_m[name].grad) < 2e-2, (name, rel(params[name].grad, ref_m[name].grad))
