@@ -154,8 +154,9 @@ __device__ __forceinline__ int sweep_key(int i, const ScoreParams& p) {
 // Key tiles reach LDS through direct global->LDS loads (global_load_lds_dwordx4: lane l
 // of a wave writes 16 bytes at the wave's LDS base + 16*l), so no staging registers are
 // needed. Rows are stored unpadded with the 16-byte chunks of key row kl XOR-swizzled by
-// (kl & 7): the MFMA operand reads (32 consecutive key rows at one logical chunk) then
-// hit 8 distinct 16-byte bank groups per 8 lanes.
+// (kl & SWZ), SWZ = 15 for rows of >= 16 chunks (HI >= 2), else 7: the MFMA operand reads
+// (32 consecutive key rows at one logical chunk) then hit 16 distinct 16-byte bank groups
+// per 16 lanes (8 for HI = 1), one LDS pass per 256 bytes.
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
 
@@ -244,18 +245,26 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
 
   // Loader geometry: load i of this thread fills LDS bytes [(i*NW + wave)*1024 + 16*lane, +16),
   // which hold physical chunk lane % CHUNKS of key row kl0 + i*RPI; its source is logical
-  // chunk (lane % CHUNKS) ^ (row & 7). kl0 < RPI and RPI is a power of two, so (row & 7)
-  // differs from (kl0 & 7) by the constant XOR (i*RPI) & 7 (0 unless HI = 8).
+  // chunk (lane % CHUNKS) ^ (row & SWZ). kl0 < RPI and RPI is a power of two, so
+  // (row & SWZ) differs from (kl0 & SWZ) by the constant XOR (i*RPI) & SWZ.
+  constexpr int SWZ = CHUNKS >= 16 ? 15 : 7;
   constexpr int RPW = 1024 / ROW_BYTES;  // key rows per 1 KB wave chunk
   constexpr int RPI = NW * RPW;          // key rows per load step
   const int kl0 = wave * RPW + (lane * 16) / ROW_BYTES;
-  const int lc0 = (lane % CHUNKS) ^ (kl0 & 7);
-  const uint32_t voff0 = (uint32_t)(kl0 * ROW_BYTES + lc0 * 16);
-  const uint32_t voff1 = (uint32_t)(kl0 * ROW_BYTES + (lc0 ^ (RPI & 7)) * 16);
-  // Operand read offsets: key row (nb*32 + col), logical chunk h*8 + 2*ks + half.
-  uint32_t rd_off[4];
+  const int lc0 = (lane % CHUNKS) ^ (kl0 & SWZ);
+  auto voff = [&](int i) { return (uint32_t)(kl0 * ROW_BYTES + (lc0 ^ ((i * RPI) & SWZ)) * 16); };
+  // Operand read offsets: key row (nb*32 + col), logical chunk h*8 + 2*ks + half, physical
+  // chunk (h*8 + 2*ks + half) ^ (col & SWZ) = 8*(h ^ c3) + ((2*ks + half) ^ (col & 7)) with
+  // c3 = bit 3 of col when SWZ = 15: head h sits at 128*h + 128*c3 (h even) or
+  // 128*h - 128*c3 (h odd), so the head part stays an immediate offset.
+  const int c3 = SWZ == 15 ? ((col >> 3) & 1) : 0;
+  uint32_t rd_even[4], rd_odd[4];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) rd_off[ks] = col * ROW_BYTES + 16 * ((2 * ks + half) ^ (col & 7));
+  for (int ks = 0; ks < 4; ++ks) {
+    const uint32_t base = col * ROW_BYTES + 16 * ((2 * ks + half) ^ (col & 7));
+    rd_even[ks] = base + 128 * c3;
+    rd_odd[ks] = base - 128 * c3;
+  }
 
   // Gate values travel as raw 16-bit patterns until wstore converts them at the end of the
   // stage: converting at load time would make the wave wait (vmcnt) for the key tile
@@ -271,7 +280,7 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
       const char* kbase = reinterpret_cast<const char*>(p.k + ((int64_t)b * S + kb) * (HI * kDI));
 #pragma unroll
       for (int i = 0; i < LOADS; ++i) {
-        const char* src = kbase + i * (NW * 1024) + (((i * RPI) & 7) ? voff1 : voff0);
+        const char* src = kbase + i * (NW * 1024) + voff(i);
         __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(&ktile[buf][(i * NW + wave) * 1024]), 16, 0, 0);
       }
     } else {
@@ -280,7 +289,7 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
       for (int i = 0; i < LOADS; ++i) {
         const int kl = min(kl0 + i * RPI, live - 1);
         const int key = sweep_key<SAMPLE>(kb + kl, p);
-        const int lc = lc0 ^ ((i * RPI) & 7);
+        const int lc = lc0 ^ ((i * RPI) & SWZ);
         const uint16_t* src = p.k + ((int64_t)b * S + key) * (HI * kDI) + lc * 8;
         __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(&ktile[buf][(i * NW + wave) * 1024]), 16, 0, 0);
       }
@@ -346,7 +355,7 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
       f32x16 acc = f32x16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const uint4 bop = *reinterpret_cast<const uint4*>(tile + rd_off[ks] + h * 128);
+        const uint4 bop = *reinterpret_cast<const uint4*>(tile + ((h & 1) ? rd_odd[ks] : rd_even[ks]) + h * 128);
         acc = mfma32(E{}, a[h][ks], bop, acc);
       }
       const float wv = wtile[buf][kl * HI + h];
