@@ -14,7 +14,7 @@ constexpr int kCsrChunk = 2048;
 struct CsrLayout {
   int64_t nk = 0;  // keys = B * S
   size_t header = 0, count = 0, off = 0, item_off = 0, part_off = 0, item_key = 0, entries = 0, scratch = 0,
-         total = 0;
+         hist = 0, raw = 0, total = 0;
   int64_t max_items = 0;  // upper bound of header[0]
   int64_t max_parts = 0;  // upper bound of header[1]
 };
