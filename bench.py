@@ -358,6 +358,35 @@ def layer_train_c4(steps: int = 3, warmup: int = 1, views: int = 24, batch: int 
     }
 
 
+def source_downsample_s32(qi, ki, wi, views: int, topk: int, steps: int = 10, warmup: int = 2):
+    """The approximate coarse selector (source downsample, factor 2, inference only) on the
+    metric's S=32 indexer inputs: pooled keys, indexer top-k over the 12,864 source rows and
+    the expansion to top-k fine tokens, timed with HIP events. Not part of the metric (the
+    metric is the exact top-k); reported so the approximate mode's cost is on record."""
+    import torch
+
+    from geoweave_amd import source_downsample as sd
+
+    cfg = sd.SourceDownsample(tokens_per_view=qi.shape[1] // views, num_views=views, patch_start_idx=5, factor=2)
+    layout = sd.build_layout(cfg)
+    stream = torch.cuda.current_stream(qi.device)
+    for _ in range(warmup):
+        sd.select_topk(qi, ki, wi, topk, 0.125, cfg)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        sd.select_topk(qi, ki, wi, topk, 0.125, cfg)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return {
+        "workload": f"approximate top-{topk} by source downsample (factor 2): S={views} views, "
+                    f"{qi.shape[1]} queries x {layout.source_len} source rows, then expansion",
+        "select_ms": round(e0.elapsed_time(e1) / steps, 3),
+        "source_rows": layout.source_len,
+        "coarse_topk": sd.coarse_budget(layout, topk, cfg),
+    }
+
+
 def aggregator_c5(steps: int = 2, warmup: int = 1, views: int = 32, topk: int = 1024):
     """Config C5: the VGGT-1B-style aggregator forward (DINOv2-style ViT-L/14 patch
     embedding, 24 frame + 24 global blocks, dim 1024, 16 heads, MLP ratio 4, global blocks
@@ -488,6 +517,7 @@ def main() -> int:
     ap.add_argument("--no-long", action="store_true", help="skip the C3 (S=64) long-context timing")
     ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer (projection + glue) timing")
     ap.add_argument("--no-c5", action="store_true", help="skip the C5 (full aggregator) timing")
+    ap.add_argument("--no-sd", action="store_true", help="skip the approximate (source-downsample) top-k timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run 3 plain device copies of 1 GiB (reference kernel for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE scaling)")
@@ -624,6 +654,9 @@ def main() -> int:
         "timing": "HIP events on the launch stream; steady state, caches not flushed",
     }
     result.update(extra)
+    if not args.no_sd:
+        print("[bench] source-downsample selector", file=sys.stderr, flush=True)
+        result["approx_topk_s32"] = source_downsample_s32(qi, ki, wi, views, topk)
     if args.calibrate_copy:
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)

@@ -33,7 +33,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from . import dsa_layer
+from . import dsa_layer, source_downsample
 
 __all__ = ["parse_indexer_layers", "parse_reuse_topk_groups", "slice_expand_and_flatten", "Aggregator",
            "AggregatorGraph"]
@@ -192,7 +192,7 @@ class Block(nn.Module):
 
     timing = None  # a list to collect (start, end) HIP events around the attention call
 
-    def forward(self, x, pos=None, rope_len=None, topk_indices=None):
+    def forward(self, x, pos=None, rope_len=None, topk_indices=None, source_downsample=None):
         idx = None
         h = self.norm1(x)
         ev = None
@@ -200,7 +200,8 @@ class Block(nn.Module):
             ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             ev[0].record()
         if self.sparse:
-            a, idx = self.attn(h, pos, return_topk=True, topk_indices=topk_indices, rope_len=rope_len)
+            a, idx = self.attn(h, pos, return_topk=True, topk_indices=topk_indices, rope_len=rope_len,
+                               source_downsample=source_downsample)
         else:
             a = self.attn(h, pos, rope_len)
         if ev is not None:
@@ -260,8 +261,13 @@ class Aggregator(nn.Module):
     def __init__(self, dim: int = 1024, depth: int = 24, num_heads: int = 16, mlp_ratio: float = 4.0,
                  num_register_tokens: int = 4, qk_norm: bool = True, rope_freq: float = 100.0,
                  indexer_layers="9-19", reuse_topk_groups=None, topk: int = 1024, patch_depth: int = 24,
-                 img_size: int = 518, patch_size: int = 14):
+                 img_size: int = 518, patch_size: int = 14, source_downsample_factor: int = 1,
+                 source_downsample_options: Optional[Dict] = None):
         super().__init__()
+        # Approximate coarse selection in the sparse layers (off at factor 1, the reference
+        # default; dsa_attention.py:122-132): the per-forward layout is filled in below.
+        self.source_downsample_factor = int(source_downsample_factor)
+        self.source_downsample_options = dict(source_downsample_options or {})
         self.depth = depth
         self.patch_size = patch_size
         grid = img_size // patch_size
@@ -306,13 +312,20 @@ class Aggregator(nn.Module):
         pos_global = pos.reshape(B, S * P, 2)
         cached: Dict[int, torch.Tensor] = {}
         sources = set(self.reuse_topk_source_by_layer.values())
+        sd = None
+        if self.source_downsample_factor > 1:
+            sd = source_downsample.SourceDownsample(tokens_per_view=P, num_views=S,
+                                                    patch_start_idx=self.patch_start_idx,
+                                                    factor=self.source_downsample_factor, grid_h=grid, grid_w=grid,
+                                                    **self.source_downsample_options)
         outputs = []
         for i in range(self.depth):
             tokens, _ = self.frame_blocks[i](tokens.reshape(B * S, P, C), pos, rope_len)
             frame_out = tokens.reshape(B, S, P, C)
             blk = self.global_blocks[i]
             reuse = cached.get(self.reuse_topk_source_by_layer.get(i, -1)) if blk.sparse else None
-            tokens, idx = blk(tokens.reshape(B, S * P, C), pos_global, rope_len, topk_indices=reuse)
+            tokens, idx = blk(tokens.reshape(B, S * P, C), pos_global, rope_len, topk_indices=reuse,
+                              source_downsample=sd)
             if blk.sparse and i in sources:
                 cached[i] = idx
             outputs.append(torch.cat([frame_out, tokens.reshape(B, S, P, C)], dim=-1))

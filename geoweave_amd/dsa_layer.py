@@ -34,6 +34,7 @@ from .custom_flash_attn.sparse_index_flash_attn import (
     sparse_index_flash_attn_inference_func,
 )
 from .custom_indexer.sparse_topk_indexer import sparse_topk_indexer_func, sparse_topk_indexer_inference_func
+from . import source_downsample as sdown
 
 __all__ = ["GlueLayout", "rope2d_tables", "dsa_glue_forward", "sparse_attention_streaming",
            "LightningIndexerProjections", "SparseGlobalAttention"]
@@ -150,20 +151,31 @@ def dsa_glue_forward(
 
 
 def sparse_attention_streaming(q, k, v, idx_q, idx_k, idx_w, topk: int, query_chunk: int,
-                               indexer_scale: float, softmax_scale: float) -> torch.Tensor:
+                               indexer_scale: float, softmax_scale: float,
+                               source_downsample: Optional["sdown.SourceDownsample"] = None) -> torch.Tensor:
     """Indexer top-k and sparse attention ``query_chunk`` queries at a time (reference
     ``DSAAttention._run_sparse_streaming_direct``, ``dsa_attention.py:1017-1283``): each
     chunk's top-k indices live only while its attention runs, so peak memory for indices and
     the indexer workspace scales with the chunk, not with N. Per-row results equal the
     unchunked path's (rows are independent); q/idx_q ``[B, N, ...]``, k/v/idx_k/idx_w over all
-    keys. Returns o ``[B, N, H, D]``."""
+    keys. Returns o ``[B, N, H, D]``. ``source_downsample``: select each chunk's keys with the
+    coarse selector (pooled keys built once for all chunks, as the reference's stream does,
+    ``dsa_attention.py:1369-1435``)."""
     B, N = q.shape[0], q.shape[1]
     out = torch.empty(q.shape, device=q.device, dtype=q.dtype)
     empty = idx_q.new_empty(0)
+    prepared = None
+    if source_downsample is not None and int(source_downsample.factor) > 1:
+        prepared = sdown.prepare(idx_k, idx_w, source_downsample)
     for s0 in range(0, N, query_chunk):
         s1 = min(s0 + query_chunk, N)
-        idx, _ = sparse_topk_indexer_inference_func(idx_q[:, s0:s1], idx_k, idx_w, empty, topk, indexer_scale,
-                                                    256, 0)
+        idx = None
+        if prepared is not None:
+            idx = sdown.select_topk(idx_q[:, s0:s1], idx_k, idx_w, topk, indexer_scale, source_downsample,
+                                    prepared=prepared)
+        if idx is None:
+            idx, _ = sparse_topk_indexer_inference_func(idx_q[:, s0:s1], idx_k, idx_w, empty, topk, indexer_scale,
+                                                        256, 0)
         o, _ = sparse_index_flash_attn_inference_func(q[:, s0:s1], k, v, idx, softmax_scale=softmax_scale)
         out[:, s0:s1] = o
     return out
@@ -292,7 +304,8 @@ class SparseGlobalAttention(nn.Module):
     @torch.no_grad()
     def forward(self, x: torch.Tensor, pos: Optional[torch.Tensor] = None, topk: Optional[int] = None,
                 return_topk: bool = False, topk_indices: Optional[torch.Tensor] = None,
-                rope_len: Optional[int] = None, query_chunk: Optional[int] = None):
+                rope_len: Optional[int] = None, query_chunk: Optional[int] = None,
+                source_downsample: Optional["sdown.SourceDownsample"] = None):
         """``topk_indices`` (int32 ``[B, N, >= k]``): use another layer's selection and skip
         this layer's indexer (the reference's ``reuse_topk_indices``,
         ``dsa_attention.py:5014-5032``). ``rope_len``: rotary table length (default
@@ -300,7 +313,11 @@ class SparseGlobalAttention(nn.Module):
         e.g. under graph capture). ``query_chunk``: select and attend ``query_chunk`` queries
         at a time (the reference's query-chunked sparse stream, ``dsa_attention.py:1017-1283``):
         the same result with the indexer workspace and the index tensor bounded by the chunk;
-        ``return_topk`` then returns None for the indices."""
+        ``return_topk`` then returns None for the indices. ``source_downsample``
+        (``source_downsample.SourceDownsample``): select keys with the approximate coarse
+        selector over pooled keys (the reference's ``source_downsample_*`` indexer options,
+        inference only, ``dsa_attention.py:4279-4318``); the full indexer runs when its
+        layout does not describe this input."""
         if x.dtype not in (torch.bfloat16, torch.float16):
             raise TypeError("SparseGlobalAttention runs in bfloat16 or float16")
         B, N, _ = x.shape
@@ -313,7 +330,7 @@ class SparseGlobalAttention(nn.Module):
         kk = min(int(topk or self.topk), N)
         if query_chunk is not None and 0 < int(query_chunk) < N and topk_indices is None:
             o = sparse_attention_streaming(q, k, v, iq, ik, iw, kk, int(query_chunk), float(self.indexer.scale),
-                                           self.scale)
+                                           self.scale, source_downsample)
             out = F.linear(o.reshape(B, N, self.dim), self.proj.weight.to(x.dtype),
                            None if self.proj.bias is None else self.proj.bias.to(x.dtype))
             return (out, None) if return_topk else out
@@ -324,8 +341,12 @@ class SparseGlobalAttention(nn.Module):
             if idx.dtype != torch.int32:
                 idx = idx.to(torch.int32)
         else:
-            idx, _ = sparse_topk_indexer_inference_func(iq, ik, iw, iq.new_empty(0), kk,
-                                                        float(self.indexer.scale), 256, 0)
+            idx = None
+            if source_downsample is not None:
+                idx = sdown.select_topk(iq, ik, iw, kk, float(self.indexer.scale), source_downsample)
+            if idx is None:
+                idx, _ = sparse_topk_indexer_inference_func(iq, ik, iw, iq.new_empty(0), kk,
+                                                            float(self.indexer.scale), 256, 0)
         o, _ = sparse_index_flash_attn_inference_func(q, k, v, idx, softmax_scale=self.scale)
         out = F.linear(o.reshape(B, N, self.dim), self.proj.weight.to(x.dtype),
                        None if self.proj.bias is None else self.proj.bias.to(x.dtype))

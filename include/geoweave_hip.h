@@ -273,6 +273,41 @@ int gw_dsa_glue_bwd(int dtype, const void* y, int64_t rows, int64_t ldy, int64_t
                     const void* d_idx_k, const void* d_idx_w, void* dy, float* d_norm,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------------------
+ * Source-downsample coarse selector (inference only, off unless requested): the device
+ * steps around an indexer top-k over pooled source rows. Replaces the torch pooling of
+ * DSAAttention._prepare_source_downsample_projected and the torch expansion of
+ * _expand_source_downsample_chunk (easyvolcap/official_vggt/layers/dsa_attention.py:
+ * 3386-3542 and :4079-4128; "legacy" strategy, :4187-4217).
+ *
+ * source_to_fine: int32 [L, M], the fine tokens (< S) each source row covers, -1 past
+ * the row's count (built on the host from the view/grid layout, :3069-3259).
+ *
+ * gw_source_downsample_pool: source_k [B, L, Hi, Di] and source_w [B, L, Hi] (dtype,
+ *   contiguous) = the mean of each row's fine rows of k [B, S, Hi, Di] and w [B, S, Hi]
+ *   (contiguous): fp32 sum in listed order / count, rounded once (F.avg_pool2d over a cell,
+ *   or the mean of its representative points; special and edge rows are copies).
+ *   Supported: Hi <= 8, Hi * Di a multiple of 8.
+ * gw_source_downsample_expand: out int32 [B, T, target] (contiguous) from the chosen
+ *   source rows coarse_idx [B, T, Kc] (element (b,t,c) at b*idx_stride_b + t*idx_stride_t
+ *   + c) taken in their given order or, when coarse_scores (dtype, same layout) is given,
+ *   by score descending and row index ascending on ties (the reference's order is that of
+ *   an unsorted torch.topk, i.e. unspecified; Kc <= 4096 then): round_robin != 0 lists the
+ *   m-th token of every
+ *   chosen row for m = 0, 1, ... (full cells), else row by row; invalid slots are skipped
+ *   and the list is cut to target; a query with fewer valid tokens repeats its last
+ *   min(count, pad_window) tokens cyclically, or gets -1 everywhere if it has none.
+ *   Supported: target <= 4096.
+ */
+int gw_source_downsample_pool(int dtype, const void* k, const void* w, int64_t B, int64_t S, int64_t Hi,
+                              int64_t Di, const int32_t* source_to_fine, int64_t L, int64_t M,
+                              void* source_k, void* source_w, void* stream);
+int gw_source_downsample_expand(int dtype, const int32_t* coarse_idx, const void* coarse_scores,
+                                int64_t idx_stride_b, int64_t idx_stride_t,
+                                int64_t B, int64_t T, int64_t Kc, const int32_t* source_to_fine,
+                                int64_t L, int64_t M, int round_robin, int64_t target,
+                                int64_t pad_window, int32_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

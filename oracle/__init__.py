@@ -20,6 +20,9 @@ torch`` path (reference: ``geoweave/inference.py:56-58`` sets ``use_topk_kernel=
 * ``kl_loss.kl_row_losses`` / ``kl_loss.kl_loss_bwd``: the indexer KL training loss and its
   explicit gradient (reference ``easyvolcap/utils/custom_indexer/indexer_kl_fused.py:8-298``),
   pinned by scipy.stats.entropy (eps = 0), autograd and finite differences;
+* ``source_downsample``: the source-downsample coarse selector (layout, pooled keys,
+  coarse budget, expansion; reference ``dsa_attention.py:3069-3542,3328-3384,4079-4217``),
+  pinned by hand-written layouts and expansions and by ``F.avg_pool2d``;
 * ``attention.sparse_attention_bwd``: explicit backward formulas of the reference kernel
   (reference ``easyvolcap/utils/custom_flash_attn/sparse_index_flash_attn.py:534-743``),
   cross-checked against autograd on the forward restatement.

@@ -96,3 +96,22 @@ def test_graph_replays_match_eager(gpu_device):
         print(f"[replay] {rep}", flush=True)
         for a, b in zip(got, eager):
             torch.testing.assert_close(a.float(), b.float(), atol=1e-2, rtol=1e-2)
+
+
+def test_source_downsample_option(gpu_device):
+    # factor 2 over the 5 x 5 patch grid of each view: the sparse layers select through the
+    # coarse selector (2 x 2 pooled cells + edge rows + specials); the rest of the model is
+    # unchanged, and at factor 1 the option is off.
+    exact = _model(indexer_layers="1-3", topk=32)
+    coarse = _model(indexer_layers="1-3", topk=32)
+    coarse.source_downsample_factor = 2
+    x = _images(seed=4)
+    out_e, _ = exact(x)
+    out_c, _ = coarse(x)
+    coarse.source_downsample_factor = 1
+    out_off, _ = coarse(x)
+    torch.cuda.synchronize()
+    for a, b, c in zip(out_e, out_c, out_off):
+        assert a.shape == b.shape and torch.isfinite(b.float()).all()
+        assert torch.equal(a, c)
+    assert any(not torch.equal(a, b) for a, b in zip(out_e[1:], out_c[1:]))

@@ -1,0 +1,138 @@
+"""GPU parity of the source-downsample coarse selector (inference only) against the oracle
+restatement (oracle/source_downsample.py): pooled keys and gates bit-exact, the expansion
+of given source rows bit-exact (round robin, row by row, padding, empty rows), the coarse
+top-k set tie-aware against the oracle scores, and the layer's use of the selection.
+"""
+import numpy as np
+import pytest
+import torch
+
+from geoweave_amd import dsa_layer, source_downsample as sd, workloads
+from geoweave_amd.custom_indexer import sparse_topk_indexer_inference_func
+from oracle import indexer as oidx
+from oracle import source_downsample as osd
+from oracle.topk_check import check_topk_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(tpv, views, seed, dtype=torch.bfloat16, B=1):
+    g = torch.Generator().manual_seed(seed)
+    n = tpv * views
+    q = torch.randn(B, n, 4, 64, generator=g).to(dtype)
+    k = torch.randn(B, n, 4, 64, generator=g).to(dtype)
+    w = (1 + 0.3 * torch.randn(B, n, 4, generator=g)).to(dtype)
+    return q, k, w
+
+
+@pytest.mark.parametrize("tpv,views,psi,factor,rep,dtype", [
+    (5 + 37 * 37, 2, 5, 2, False, torch.bfloat16),
+    (5 + 37 * 37, 2, 5, 4, False, torch.float16),
+    (5 + 37 * 37, 2, 5, 4, True, torch.bfloat16),
+    (1 + 10 * 10, 3, 1, 3, False, torch.bfloat16),
+])
+def test_pooled_sources_bit_exact(gpu_device, tpv, views, psi, factor, rep, dtype):
+    q, k, w = _inputs(tpv, views, 11, dtype, B=2)
+    cfg = sd.SourceDownsample(tpv, views, psi, factor=factor, representative_points=rep)
+    layout, table, sk, sw = sd.prepare(k.cuda(), w.cuda(), cfg)
+    lay = osd.source_layout(tpv, views, psi, factor, representative_points=rep)
+    assert np.array_equal(layout.source_to_fine, lay["source_to_fine"])
+    rk, rw = osd.pool_sources(k, w, lay)
+    torch.cuda.synchronize()
+    assert torch.equal(sk.cpu(), rk) and torch.equal(sw.cpu(), rw)
+
+
+@pytest.mark.parametrize("factor,rep,target,pad", [(2, False, 300, 64), (2, False, 2000, 64), (4, True, 700, 16),
+                                                   (4, False, 64, 64)])
+def test_expand_bit_exact(gpu_device, factor, rep, target, pad):
+    tpv, views, psi = 5 + 37 * 37, 2, 5
+    cfg = sd.SourceDownsample(tpv, views, psi, factor=factor, representative_points=rep, pad_window=pad)
+    layout = sd.build_layout(cfg)
+    table = torch.from_numpy(layout.source_to_fine).cuda()
+    lay = osd.source_layout(tpv, views, psi, factor, representative_points=rep)
+    g = torch.Generator().manual_seed(factor * 100 + target)
+    B, T, Kc = 2, 40, 96
+    cidx = torch.stack([torch.randperm(layout.source_len, generator=g)[:Kc] for _ in range(B * T)]).view(B, T, Kc)
+    cidx[0, 0] = torch.arange(Kc)            # special and edge rows only (one token each)
+    cidx[1, 3, :] = 0                        # repeated row
+    got = sd.expand(cidx.to(torch.int32).cuda(), layout, table, min(target, tpv * views), pad)
+    want = osd.expand(cidx, lay, target, tpv * views, pad)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu().long(), want)
+
+
+def test_select_matches_oracle(gpu_device):
+    tpv, views, psi, topk = 5 + 37 * 37, 4, 5, 512
+    q, k, w = _inputs(tpv, views, 21)
+    cfg = sd.SourceDownsample(tpv, views, psi, factor=2)
+    qd, kd, wd = q.cuda(), k.cuda(), w.cuda()
+    layout, table, sk, sw = sd.prepare(kd, wd, cfg)
+    lay = osd.source_layout(tpv, views, psi, 2)
+    kc = sd.coarse_budget(layout, topk, cfg)
+    assert kc == osd.coarse_topk(lay, topk)
+    cidx, csc = sparse_topk_indexer_inference_func(qd, sk, sw, qd.new_empty(0), kc, 0.125, 256, 0)
+    fine = sd.select_topk(qd, kd, wd, topk, 0.125, cfg)
+    torch.cuda.synchronize()
+    # the coarse sets: tie-aware against the oracle scores over the pooled sources
+    rk, rw = osd.pool_sources(k, w, lay)
+    rows = torch.randperm(q.shape[1], generator=torch.Generator().manual_seed(3))[:256]
+    scores = oidx.indexer_scores(q[:, rows], rk, rw, None, 0.125)
+    rep = check_topk_rows(scores[0], cidx[0, rows].cpu(), kc)
+    assert rep.ok, rep.first_bad
+    # the fine tokens: the oracle's expansion of the GPU's coarse rows, taken by score
+    want = osd.expand(osd.order_by_score(cidx.cpu(), csc.cpu()), lay, topk, tpv * views)
+    assert torch.equal(fine.cpu().long(), want)
+    # given order (no scores): the oracle's expansion of the rows as they come
+    layout_t = torch.from_numpy(layout.source_to_fine).cuda()
+    plain = sd.expand(cidx, layout, layout_t, topk, 64)
+    assert torch.equal(plain.cpu().long(), osd.expand(cidx.cpu().long(), lay, topk, tpv * views))
+    # query chunks give the same rows
+    fine_c = sd.select_topk(qd, kd, wd, topk, 0.125, cfg, query_chunk=1000)
+    assert torch.equal(fine_c, fine)
+
+
+def test_layer_uses_the_selection_and_falls_back(gpu_device):
+    torch.manual_seed(0)
+    views, topk = 2, 256
+    m = workloads.init_layer_(dsa_layer.SparseGlobalAttention(topk=topk)).cuda()
+    x, pos = workloads.layer_module_inputs(views)
+    x, pos = x.cuda(), pos.cuda()
+    N = x.shape[1]
+    cfg = sd.SourceDownsample(tokens_per_view=N // views, num_views=views, patch_start_idx=5, factor=2)
+    with torch.no_grad():
+        out, idx = m(x, pos, return_topk=True, source_downsample=cfg)
+        again = m(x, pos, topk_indices=idx)
+        chunked = m(x, pos, source_downsample=cfg, query_chunk=700)
+        full, idx_full = m(x, pos, return_topk=True)
+        # a layout that does not match the input: the full indexer runs
+        bad = sd.SourceDownsample(tokens_per_view=N // views + 1, num_views=views, patch_start_idx=5, factor=2)
+        out_bad, idx_bad = m(x, pos, return_topk=True, source_downsample=bad)
+    torch.cuda.synchronize()
+    assert idx.shape == (1, N, topk) and int(idx.min()) >= 0 and int(idx.max()) < N
+    assert torch.equal(out, again)
+    torch.testing.assert_close(chunked.float(), out.float(), atol=0, rtol=0)
+    assert torch.equal(idx_bad, idx_full) and torch.equal(out_bad, full)
+    # An approximation: with random weights and inputs neighbouring tokens are unrelated, so
+    # pooled keys carry little of the fine scores; the selection still beats chance (k / N).
+    overlap = np.mean([len(set(a) & set(b)) / topk for a, b in zip(idx[0, ::97].tolist(), idx_full[0, ::97].tolist())])
+    print(f"[source-downsample] overlap with exact top-k: {overlap:.3f} (chance {topk / N:.3f})", flush=True)
+    assert overlap > 1.5 * topk / N
+
+
+@pytest.mark.parametrize("Kc", [40, 300, 1500])
+def test_expand_orders_by_score(gpu_device, Kc):
+    # register sort (Kc <= 1024) and LDS sort (longer lists); bf16 scores with many ties
+    tpv, views, psi = 5 + 37 * 37, 4, 5
+    cfg = sd.SourceDownsample(tpv, views, psi, factor=2)
+    layout = sd.build_layout(cfg)
+    table = torch.from_numpy(layout.source_to_fine).cuda()
+    lay = osd.source_layout(tpv, views, psi, 2)
+    g = torch.Generator().manual_seed(Kc)
+    B, T = 1, 24
+    cidx = torch.stack([torch.randperm(layout.source_len, generator=g)[:Kc] for _ in range(B * T)]).view(B, T, Kc)
+    sc = (torch.randint(0, 50, (B, T, Kc), generator=g).float() / 8).bfloat16()
+    target = min(4 * Kc, 4096)
+    got = sd.expand(cidx.to(torch.int32).cuda(), layout, table, target, 64, sc.cuda())
+    want = osd.expand(osd.order_by_score(cidx, sc), lay, target, tpv * views)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu().long(), want)

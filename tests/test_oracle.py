@@ -423,3 +423,104 @@ def test_layer_glue_oracle_matches_the_unfused_reference_order():
             for a, w, b2 in zip(vec, *lnp["idx_k"])]
     got = F.layer_norm(vec, (D,), *lnp["idx_k"], 1e-5)
     assert max(abs(float(a) - b2) for a, b2 in zip(got, want)) < 1e-4
+
+
+# ------------------------------------------------------------- source-downsample selector
+
+
+def test_source_layout_tiny_case_by_hand():
+    # 2 views of 2 special tokens + a 3 x 3 patch grid, factor 2: the pooled area is the
+    # top-left 2 x 2 cell; the other 5 patches of a view are edge rows.
+    from oracle import source_downsample as osd
+
+    lay = osd.source_layout(11, 2, 2, 2)
+    rows = [[t for t in r if t >= 0] for r in lay["source_to_fine"].tolist()]
+    assert rows == [[0], [1], [11], [12],  # specials, view-major
+                    [4], [7], [8], [9], [10], [15], [18], [19], [20], [21],  # edges, row-major per view
+                    [2, 3, 5, 6], [13, 14, 16, 17]]  # one cell per view, (dy, dx) order
+    assert (lay["special_count"], lay["edge_count"], lay["coarse_count"]) == (4, 10, 2)
+    assert lay["expand_round_robin"] and lay["max_block_tokens"] == 4
+
+
+@pytest.mark.parametrize("factor,rep", [(2, False), (3, False), (4, False), (4, True), (8, True)])
+def test_source_layout_covers_each_token_once(factor, rep):
+    from oracle import source_downsample as osd
+
+    tpv, views, psi, grid = 5 + 37 * 37, 3, 5, 37
+    lay = osd.source_layout(tpv, views, psi, factor, representative_points=rep)
+    stf = lay["source_to_fine"]
+    toks = stf[stf >= 0]
+    assert len(set(toks.tolist())) == toks.size  # no token in two rows
+    if not rep:
+        assert sorted(toks.tolist()) == list(range(tpv * views))  # a partition of all tokens
+        assert lay["max_block_tokens"] == factor * factor
+    else:
+        # representative points lie inside their own cell; specials and edges are complete
+        off = lay["special_count"] + lay["edge_count"]
+        cells = stf[off:]
+        pooled = grid // factor * factor
+        for r, row in enumerate(cells[: pooled // factor * pooled // factor]):
+            cy, cx = divmod(r, pooled // factor)
+            for t in row[row >= 0]:
+                y, x = divmod(int(t) - psi, grid)
+                assert cy * factor <= y < (cy + 1) * factor and cx * factor <= x < (cx + 1) * factor
+        assert not lay["expand_round_robin"]
+    assert lay["source_len"] == lay["special_count"] + lay["edge_count"] + lay["coarse_count"]
+
+
+def test_source_pooling_equals_avg_pool2d_and_copies():
+    from oracle import source_downsample as osd
+
+    g = torch.Generator().manual_seed(5)
+    tpv, views, psi, grid, f = 5 + 9 * 9, 2, 5, 9, 2
+    k = torch.randn(1, tpv * views, 2, 64, generator=g).bfloat16()
+    w = (1 + 0.3 * torch.randn(1, tpv * views, 2, generator=g)).bfloat16()
+    lay = osd.source_layout(tpv, views, psi, f)
+    sk, sw = osd.pool_sources(k, w, lay)
+    img = k.float().view(views, tpv, 128)[:, psi:].reshape(views, grid, grid, 128).permute(0, 3, 1, 2)
+    ref = F.avg_pool2d(img[:, :, :8, :8], f).permute(0, 2, 3, 1).reshape(-1, 2, 64).bfloat16()
+    off = lay["special_count"] + lay["edge_count"]
+    assert torch.equal(sk[0, off:], ref)
+    imgw = w.float().view(views, tpv, 2)[:, psi:].reshape(views, grid, grid, 2).permute(0, 3, 1, 2)
+    refw = F.avg_pool2d(imgw[:, :, :8, :8], f).permute(0, 2, 3, 1).reshape(-1, 2).bfloat16()
+    assert torch.equal(sw[0, off:], refw)
+    single = torch.from_numpy(lay["source_to_fine"][:off, 0])
+    assert torch.equal(sk[0, :off], k[0, single]) and torch.equal(sw[0, :off], w[0, single])
+
+
+def test_source_coarse_budget_by_hand():
+    from oracle import source_downsample as osd
+
+    # VGGT at S = 32, factor 2: 160 specials, 73 edges x 32, 324 cells x 32; 43968 tokens over
+    # 12864 rows -> ceil(1024 / 3.41791 * 1.1) = 330.
+    lay = osd.source_layout(1374, 32, 5, 2)
+    assert (lay["source_len"], osd.coarse_topk(lay, 1024)) == (12864, 330)
+    # Specials (160) outnumber the budget (ceil(256 / 7.667 * 1.1) = 37): 160 + ceil(96 / 16 * 1.1).
+    lay = osd.source_layout(20 + 16 * 16, 8, 20, 4)
+    assert osd.coarse_topk(lay, 256) == 160 + 7
+    assert osd.coarse_topk(lay, 256, explicit=10**6) == lay["source_len"]
+
+
+def test_source_expand_by_hand():
+    from oracle import source_downsample as osd
+
+    lay = osd.source_layout(11, 2, 2, 2)  # rows as in the tiny case above
+    c = torch.tensor([[[14, 0, 15]]])
+    # round robin: m = 0 -> 2, 0, 13; m = 1 -> 3, (special has one token), 14; m = 2 -> 5, 16; m = 3 -> 6, 17
+    assert osd.expand(c, lay, 6, 22).tolist() == [[[2, 0, 13, 3, 14, 5]]]
+    # 9 valid tokens for a target of 12: repeat the last min(9, 4) = 4 cyclically
+    assert osd.expand(c, lay, 12, 22, pad_window=4).tolist() == [[[2, 0, 13, 3, 14, 5, 16, 6, 17, 5, 16, 6]]]
+    # row-by-row order (representative points)
+    lay_rep = osd.source_layout(2 + 8 * 8, 1, 2, 8, representative_points=True)
+    r0 = lay_rep["special_count"] + lay_rep["edge_count"]
+    got = osd.expand(torch.tensor([[[r0, 1]]]), lay_rep, 5, 66)[0, 0].tolist()
+    cell = [t for t in lay_rep["source_to_fine"][r0].tolist() if t >= 0]
+    assert got == cell + [1]
+
+
+def test_source_order_by_score_by_hand():
+    from oracle import source_downsample as osd
+
+    c = torch.tensor([[[5, 3, 9, 1]]])
+    s = torch.tensor([[[1.0, 2.0, 1.0, 2.0]]])
+    assert osd.order_by_score(c, s).tolist() == [[[1, 3, 5, 9]]]
