@@ -76,6 +76,7 @@ def train_step_c4(steps: int = 5, warmup: int = 2, views: int = 24, batch: int =
     from geoweave_amd import _csr, workloads
     from geoweave_amd.custom_flash_attn.sparse_index_flash_attn import sparse_index_flash_attn_func
     from geoweave_amd.custom_indexer import sparse_indexer_kl_loss, sparse_topk_indexer_func
+    from geoweave_amd.custom_indexer.indexer_kl_fused import sparse_attention_kl_loss
 
     dev = torch.device("cuda", 0)
     lay = workloads.layer_inputs(views, batch, torch.bfloat16)
@@ -86,35 +87,44 @@ def train_step_c4(steps: int = 5, warmup: int = 2, views: int = 24, batch: int =
     stream = torch.cuda.current_stream(dev)
     eps = 1e-6
 
-    def one(ev=None):
+    def one(ev=None, fused=False):
         for x in (qi, ki, wi, q, k, v):
             x.grad = None
         _csr.clear_cache()
         if ev:
             ev[0].record(stream)
         idx, sc = sparse_topk_indexer_func(qi, ki, wi, None, topk, 0.125, 256, 0)
-        o, attn = sparse_index_flash_attn_func(q, k, v, idx, None, False, 0.125)
-        if ev:
-            ev[1].record(stream)
-        p = attn.to(q.dtype)
-        p = p / (p.sum(dim=-1, keepdim=True) + eps)
-        kl = sparse_indexer_kl_loss(p, sc, eps)
-        if ev:
-            ev[2].record(stream)
+        if fused:
+            # KL on the attention mass computed in the attention epilogue (one launch)
+            o, attn, kl = sparse_attention_kl_loss(q, k, v, idx, sc, eps, 0.125)
+            if ev:
+                ev[1].record(stream)
+                ev[2].record(stream)
+        else:
+            o, attn = sparse_index_flash_attn_func(q, k, v, idx, None, False, 0.125)
+            if ev:
+                ev[1].record(stream)
+            p = attn.to(q.dtype)
+            p = p / (p.sum(dim=-1, keepdim=True) + eps)
+            kl = sparse_indexer_kl_loss(p, sc, eps)
+            if ev:
+                ev[2].record(stream)
         torch.autograd.backward([o, kl], [do, None])
         if ev:
             ev[3].record(stream)
 
-    for _ in range(warmup):
-        one()
-    torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
-    for i in range(steps):
-        one(evs[i])
-    torch.cuda.synchronize()
-    fwd = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
-    kl_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
-    bwd = statistics.mean(e[2].elapsed_time(e[3]) for e in evs)
+    def timed(fused):
+        for _ in range(warmup):
+            one(fused=fused)
+        torch.cuda.synchronize()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+        for i in range(steps):
+            one(evs[i], fused)
+        torch.cuda.synchronize()
+        return [statistics.mean(e[j].elapsed_time(e[j + 1]) for e in evs) for j in range(3)]
+
+    fwd, kl_ms, bwd = timed(False)
+    f_fwd, _, f_bwd = timed(True)
     gather = batch * T * topk * H * D * 2 * 2
     return {
         "workload": f"C4 training step: B={batch}, S={views} views (N={T}), H={H}, D={D}, top-k {topk}, bf16, "
@@ -123,6 +133,13 @@ def train_step_c4(steps: int = 5, warmup: int = 2, views: int = 24, batch: int =
         "kl_loss_fwd_ms": round(kl_ms, 3),
         "bwd_ms": round(bwd, 3),
         "step_ms": round(fwd + kl_ms + bwd, 3),
+        "fused_kl": {
+            "note": "indexer KL on the fp32 attention mass computed in the attention epilogue "
+                    "(sparse_attention_kl_loss) instead of a separate loss kernel on the bf16-normalised mass",
+            "fwd_ms": round(f_fwd, 3),
+            "bwd_ms": round(f_bwd, 3),
+            "step_ms": round(f_fwd + f_bwd, 3),
+        },
         "attn_gathered_bytes_fwd": gather,
         "attn_gathered_bytes_bwd": 2 * gather,
     }

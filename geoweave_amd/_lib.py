@@ -72,6 +72,12 @@ _SIGNATURES = {
          _p, _p, _p, _p, _p, _p, ctypes.c_float, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p,
          _p, _sz, _p],
     ),
+    "gw_sparse_attn_fwd_kl": (
+        ctypes.c_int,
+        [ctypes.c_int, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64, _i64, _p, _i64p, _p, _p,
+         _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p, ctypes.c_int, _i64, _i64,
+         ctypes.c_float, _p, _p, _sz, _p],
+    ),
     "gw_source_downsample_pool": (
         ctypes.c_int,
         [ctypes.c_int, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p, _p, _p],

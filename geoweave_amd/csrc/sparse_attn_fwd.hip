@@ -18,6 +18,13 @@
 // writes attn_sum once. This replaces the reference's second K gather + per-head atomics
 // (_attn_sum_kernel, sparse_index_flash_attn.py:375-458) with 2 * K * H * 4 bytes of
 // workspace traffic per query.
+//
+// Indexer KL loss fused into that epilogue (optional, training): with the query's attn_sum
+// row still in registers, the workgroup also reads the row's indexer logits z (the top-k
+// scores) and writes row_loss = KL(p || softmax(z)), p = attn_sum / (sum attn_sum + eps),
+// the per-row term of sparse_indexer_kl_loss (indexer_kl_fused.py:8-155): one pass for
+// sum(attn_sum) and max(z), one for sum exp(z - max z), one for the terms, each reduced over
+// the query's head-group waves in a fixed order.
 #include <math.h>
 
 #include "gw_common.h"
@@ -42,6 +49,12 @@ struct AttnFwdParams {
   int64_t vsb, vss, vsh;
   int64_t osb, ost, osh;
   int64_t psb, pst;
+  // fused KL (KL kernels only)
+  const void* logits;
+  int logits_dt;  // GW_DTYPE_*
+  int64_t lsb, lst;
+  float kl_eps;
+  float* row_loss;
   int T, S, H, K;
   int NG;   // head groups (waves) per query
   int QPB;  // queries per workgroup
@@ -50,9 +63,32 @@ struct AttnFwdParams {
 
 constexpr int kMaxHeadsLds = 64;
 constexpr int kMaxQpb = 4;
+constexpr int kKlRegs = 16;  // attn_sum entries per thread held for the fused KL
 
-template <typename E, int D, int HPW, bool ATTN>
+__device__ __forceinline__ float kl_lane(float x, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
+__device__ __forceinline__ float kl_wave_sum(float x) {
+  x = group_sum<16>(x);
+  return (kl_lane(x, 0) + kl_lane(x, 16)) + (kl_lane(x, 32) + kl_lane(x, 48));
+}
+__device__ __forceinline__ float kl_wave_max(float x) {
+  x = fmaxf(x, dpp<kDppXor1>(x));
+  x = fmaxf(x, dpp<kDppXor2>(x));
+  x = fmaxf(x, dpp<kDppHalfMirror>(x));
+  x = fmaxf(x, dpp<kDppMirror>(x));
+  return fmaxf(fmaxf(kl_lane(x, 0), kl_lane(x, 16)), fmaxf(kl_lane(x, 32), kl_lane(x, 48)));
+}
+__device__ __forceinline__ float kl_load(int dt, const void* base, int64_t i) {
+  if (dt == GW_DTYPE_FP32) return static_cast<const float*>(base)[i];
+  const uint32_t u = static_cast<const uint16_t*>(base)[i];
+  if (dt == GW_DTYPE_BF16) return __uint_as_float(u << 16);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)u);
+}
+
+template <typename E, int D, int HPW, bool ATTN, bool KL>
 __global__ __launch_bounds__(256) void sparse_attn_fwd_kernel(const AttnFwdParams p) {
+  static_assert(ATTN || !KL, "the fused KL needs attn_sum");
   constexpr int LPH = D / 8;
   constexpr int HL = HPW * LPH;
   constexpr int G = 64 / HL;
@@ -188,7 +224,7 @@ __global__ __launch_bounds__(256) void sparse_attn_fwd_kernel(const AttnFwdParam
     }
   }
 
-  if constexpr (ATTN) {
+  if constexpr (ATTN && !KL) {
     __threadfence_block();
     __syncthreads();
     if (t_ok) {
@@ -207,16 +243,90 @@ __global__ __launch_bounds__(256) void sparse_attn_fwd_kernel(const AttnFwdParam
       }
     }
   }
+  if constexpr (KL) {
+    // attn_sum as above, entry j = lid + r * nthr held in av[r] (the host checks
+    // K <= kKlRegs * nthr), then the KL row loss. Barriers are reached by every thread.
+    __shared__ float kl_red[kMaxQpb][4][2];
+    __threadfence_block();
+    __syncthreads();
+    const int nthr = p.NG * 64;
+    const int lid = hg * 64 + lane;
+    float av[kKlRegs], zv[kKlRegs];
+    float sa = 0.f, mz = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < kKlRegs; ++r) {
+      av[r] = 0.f;
+      zv[r] = -INFINITY;
+      const int j = lid + r * nthr;
+      if (t_ok && j < p.K) {
+        const float* srow = p.ws + (((int64_t)b * p.T + t) * (int64_t)p.K + j) * p.H;
+        float sum = 0.f;
+        for (int hx = 0; hx < p.H; ++hx) {
+          const float l2 = lse2_s[ql][hx];
+          if (l2 != -INFINITY) sum += fexp2(srow[hx] - l2);
+        }
+        p.attn_sum[((int64_t)b * p.T + t) * (int64_t)p.K + j] = sum;
+        av[r] = sum;
+        zv[r] = kl_load(p.logits_dt, p.logits, b * p.lsb + (int64_t)t * p.lst + j);
+        sa += sum;
+        mz = fmaxf(mz, zv[r]);
+      }
+    }
+    sa = kl_wave_sum(sa);
+    mz = kl_wave_max(mz);
+    if (lane == 0) {
+      kl_red[ql][hg][0] = sa;
+      kl_red[ql][hg][1] = mz;
+    }
+    __syncthreads();
+    float sa_t = 0.f, mz_t = -INFINITY;
+    for (int g2 = 0; g2 < p.NG; ++g2) {
+      sa_t += kl_red[ql][g2][0];
+      mz_t = fmaxf(mz_t, kl_red[ql][g2][1]);
+    }
+    const float denom = sa_t + p.kl_eps;
+    float se = 0.f;
+#pragma unroll
+    for (int r = 0; r < kKlRegs; ++r) {
+      if (t_ok && lid + r * nthr < p.K) se += expf(zv[r] - mz_t);
+    }
+    se = kl_wave_sum(se);
+    __syncthreads();  // every wave has read kl_red
+    if (lane == 0) kl_red[ql][hg][0] = se;
+    __syncthreads();
+    float se_t = 0.f;
+    for (int g2 = 0; g2 < p.NG; ++g2) se_t += kl_red[ql][g2][0];
+    const float lse = mz_t + logf(se_t);
+    float acc = 0.f;
+#pragma unroll
+    for (int r = 0; r < kKlRegs; ++r) {
+      if (t_ok && lid + r * nthr < p.K) {
+        const float pj = av[r] / denom;
+        acc += pj * (logf(pj + p.kl_eps) - (zv[r] - lse));
+      }
+    }
+    acc = kl_wave_sum(acc);
+    __syncthreads();
+    if (lane == 0) kl_red[ql][hg][0] = acc;
+    __syncthreads();
+    if (t_ok && lid == 0) {
+      float loss = 0.f;
+      for (int g2 = 0; g2 < p.NG; ++g2) loss += kl_red[ql][g2][0];
+      p.row_loss[(int64_t)b * p.T + t] = loss;
+    }
+  }
 }
 
 template <typename E, int D, int HPW>
 int launch_typed(const AttnFwdParams& p, int B, bool attn, hipStream_t stream) {
   dim3 grid((p.T + p.QPB - 1) / p.QPB, B);
   dim3 block(64 * p.NG * p.QPB);
-  if (attn)
-    hipLaunchKernelGGL((sparse_attn_fwd_kernel<E, D, HPW, true>), grid, block, 0, stream, p);
+  if (p.row_loss)
+    hipLaunchKernelGGL((sparse_attn_fwd_kernel<E, D, HPW, true, true>), grid, block, 0, stream, p);
+  else if (attn)
+    hipLaunchKernelGGL((sparse_attn_fwd_kernel<E, D, HPW, true, false>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((sparse_attn_fwd_kernel<E, D, HPW, false>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((sparse_attn_fwd_kernel<E, D, HPW, false, false>), grid, block, 0, stream, p);
   GW_HIP_LAUNCH_CHECK("sparse_attn_fwd_kernel launch");
   return GW_OK;
 }
@@ -253,16 +363,22 @@ extern "C" size_t gw_sparse_attn_fwd_workspace_size(int64_t B, int64_t T, int64_
   return (size_t)B * (size_t)T * (size_t)K * (size_t)H * sizeof(float);
 }
 
-extern "C" int gw_sparse_attn_fwd(int dtype, const void* q, const int64_t* q_strides,
-                                  const void* k, const int64_t* k_strides, const void* v,
-                                  const int64_t* v_strides, const int32_t* kv_pos,
-                                  int64_t pos_stride_b, int64_t pos_stride_t, void* o,
-                                  const int64_t* o_strides, float* lse, float* attn_sum,
-                                  int64_t B, int64_t T, int64_t S, int64_t H, int64_t D,
-                                  int64_t K, float softmax_scale, void* workspace,
-                                  size_t workspace_bytes, void* stream) {
-  using namespace gw;
-  clear_error();
+namespace gw {
+namespace {
+
+struct KlArgs {
+  const void* logits;
+  int dtype;
+  int64_t stride_b, stride_t;
+  float eps;
+  float* row_loss;
+};
+
+int attn_fwd_impl(int dtype, const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                  const void* v, const int64_t* v_strides, const int32_t* kv_pos, int64_t pos_stride_b,
+                  int64_t pos_stride_t, void* o, const int64_t* o_strides, float* lse, float* attn_sum, int64_t B,
+                  int64_t T, int64_t S, int64_t H, int64_t D, int64_t K, float softmax_scale, void* workspace,
+                  size_t workspace_bytes, const KlArgs* kl, void* stream) {
   GW_CHECK_ARG(dtype == GW_DTYPE_BF16 || dtype == GW_DTYPE_FP16, "unsupported dtype code %d", dtype);
   GW_CHECK_ARG(B >= 0 && T >= 0 && S >= 0 && H >= 1 && K >= 0,
                "invalid sizes B=%lld T=%lld S=%lld H=%lld K=%lld", (long long)B, (long long)T,
@@ -308,6 +424,11 @@ extern "C" int gw_sparse_attn_fwd(int dtype, const void* q, const int64_t* q_str
   p.osb = o_strides[0]; p.ost = o_strides[1]; p.osh = o_strides[2];
   p.psb = pos_stride_b;
   p.pst = pos_stride_t;
+  p.logits = nullptr;
+  p.logits_dt = GW_DTYPE_FP32;
+  p.lsb = p.lst = 0;
+  p.kl_eps = 0.f;
+  p.row_loss = nullptr;
   p.T = (int)T;
   p.S = (int)S;
   p.H = (int)H;
@@ -317,7 +438,55 @@ extern "C" int gw_sparse_attn_fwd(int dtype, const void* q, const int64_t* q_str
   p.QPB = 4 / p.NG;
   if (p.QPB < 1) p.QPB = 1;
   p.scale_log2 = softmax_scale * kLog2e;
+  if (kl != nullptr) {
+    GW_CHECK_ARG(want_attn, "the fused KL loss needs attn_sum");
+    GW_CHECK_ARG(kl->logits != nullptr && kl->row_loss != nullptr, "null logits or row_loss pointer");
+    GW_CHECK_ARG(kl->dtype == GW_DTYPE_BF16 || kl->dtype == GW_DTYPE_FP16 || kl->dtype == GW_DTYPE_FP32,
+                 "unsupported logits dtype code %d", kl->dtype);
+    GW_CHECK_ARG(kl->eps >= 0.f, "eps must be non-negative, got %g", (double)kl->eps);
+    if (K > (int64_t)kKlRegs * p.NG * 64)
+      return set_error(GW_ERR_UNSUPPORTED, "fused KL supports K <= %d for %lld heads, got %lld",
+                       kKlRegs * p.NG * 64, (long long)H, (long long)K);
+    p.logits = kl->logits;
+    p.logits_dt = kl->dtype;
+    p.lsb = kl->stride_b;
+    p.lst = kl->stride_t;
+    p.kl_eps = kl->eps;
+    p.row_loss = kl->row_loss;
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == GW_DTYPE_BF16) return dispatch_d<BF16>(p, (int)B, (int)D, hpw, want_attn, st);
   return dispatch_d<FP16>(p, (int)B, (int)D, hpw, want_attn, st);
+}
+
+}  // namespace
+}  // namespace gw
+
+extern "C" int gw_sparse_attn_fwd(int dtype, const void* q, const int64_t* q_strides,
+                                  const void* k, const int64_t* k_strides, const void* v,
+                                  const int64_t* v_strides, const int32_t* kv_pos,
+                                  int64_t pos_stride_b, int64_t pos_stride_t, void* o,
+                                  const int64_t* o_strides, float* lse, float* attn_sum,
+                                  int64_t B, int64_t T, int64_t S, int64_t H, int64_t D,
+                                  int64_t K, float softmax_scale, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  gw::clear_error();
+  return gw::attn_fwd_impl(dtype, q, q_strides, k, k_strides, v, v_strides, kv_pos, pos_stride_b, pos_stride_t, o,
+                           o_strides, lse, attn_sum, B, T, S, H, D, K, softmax_scale, workspace, workspace_bytes,
+                           nullptr, stream);
+}
+
+extern "C" int gw_sparse_attn_fwd_kl(int dtype, const void* q, const int64_t* q_strides, const void* k,
+                                     const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                                     const int32_t* kv_pos, int64_t pos_stride_b, int64_t pos_stride_t, void* o,
+                                     const int64_t* o_strides, float* lse, float* attn_sum, int64_t B, int64_t T,
+                                     int64_t S, int64_t H, int64_t D, int64_t K, float softmax_scale,
+                                     const void* logits, int logits_dtype, int64_t logits_stride_b,
+                                     int64_t logits_stride_t, float eps, float* row_loss, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  gw::clear_error();
+  const gw::KlArgs kl{logits, logits_dtype, logits_stride_b, logits_stride_t, eps, row_loss};
+  return gw::attn_fwd_impl(dtype, q, q_strides, k, k_strides, v, v_strides, kv_pos, pos_stride_b, pos_stride_t, o,
+                           o_strides, lse, attn_sum, B, T, S, H, D, K, softmax_scale, workspace, workspace_bytes,
+                           &kl, stream);
 }

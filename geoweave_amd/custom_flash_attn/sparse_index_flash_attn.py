@@ -110,11 +110,16 @@ def _flash_attn_forward(
     softmax_scale: Optional[float] = None,
     return_attn: bool = True,
     q_layout: str = "bthd",
+    kl_logits: Optional[torch.Tensor] = None,
+    kl_eps: float = 1e-6,
+    kl_row_loss: Optional[torch.Tensor] = None,
 ):
     """Returns (o, attn_sum | None, lse [B,T,H] fp32, softmax_scale).
 
     o has q's shape and dtype and is contiguous (reference :2064-2067); attn_sum is fp32
-    ``[B, T, K]`` (reference :2070-2075)."""
+    ``[B, T, K]`` (reference :2070-2075). With ``kl_logits`` ([B, T, K], unit last stride)
+    the indexer KL row losses are computed in the same launch (gw_sparse_attn_fwd_kl) into
+    ``kl_row_loss`` (fp32 [B*T])."""
     batch, seqlen_q, seqlen_k, nheads, d = _check_inputs(q, k, v, kv_positions, bias, causal, q_layout)
     q, k, v = _prep(q), _prep(k), _prep(v)
     if kv_positions.stride(-1) != 1:
@@ -138,7 +143,7 @@ def _flash_attn_forward(
         lse.fill_(-math.inf)
         return o, attn_sum, lse, softmax_scale
     lib = _lib.load()
-    rc = lib.gw_sparse_attn_fwd(
+    common = (
         _lib.dtype_code(q.dtype),
         q.data_ptr(), _lib.strides3(*_bthd_strides(q, q_layout)),
         k.data_ptr(), _lib.strides3(*_bthd_strides(k, q_layout)),
@@ -148,10 +153,16 @@ def _flash_attn_forward(
         lse.data_ptr(), _lib.ptr(attn_sum),
         batch, seqlen_q, seqlen_k, nheads, d, num_kv,
         float(softmax_scale),
-        _lib.ptr(ws), ws_bytes,
-        _lib.stream_handle(q.device),
     )
-    _lib.check(rc, "gw_sparse_attn_fwd")
+    if kl_logits is None:
+        rc = lib.gw_sparse_attn_fwd(*common, _lib.ptr(ws), ws_bytes, _lib.stream_handle(q.device))
+        _lib.check(rc, "gw_sparse_attn_fwd")
+    else:
+        code = _lib.GW_DTYPE_FP32 if kl_logits.dtype == torch.float32 else _lib.dtype_code(kl_logits.dtype)
+        rc = lib.gw_sparse_attn_fwd_kl(*common, kl_logits.data_ptr(), code, kl_logits.stride(0),
+                                       kl_logits.stride(1), float(kl_eps), kl_row_loss.data_ptr(),
+                                       _lib.ptr(ws), ws_bytes, _lib.stream_handle(q.device))
+        _lib.check(rc, "gw_sparse_attn_fwd_kl")
     return o, attn_sum, lse, softmax_scale
 
 

@@ -19,7 +19,7 @@ import torch
 
 from .. import _lib
 
-__all__ = ["sparse_indexer_kl_loss", "SparseIndexerKLLossFunc"]
+__all__ = ["sparse_indexer_kl_loss", "SparseIndexerKLLossFunc", "sparse_attention_kl_loss"]
 
 
 def _dtype_code(dtype: torch.dtype) -> int:
@@ -102,3 +102,66 @@ def sparse_indexer_kl_loss(attn_sum: torch.Tensor, logits: torch.Tensor, eps: fl
         # reference: indexer_kl_fused.py:296-297
         return attn_sum.new_zeros(())
     return SparseIndexerKLLossFunc.apply(attn_sum, logits, float(eps))
+
+
+class _AttnWithKLRows(torch.autograd.Function):
+    """Sparse attention forward that also writes the KL row losses (gw_sparse_attn_fwd_kl);
+    the backward is the attention's own, with dattn_sum from the KL node below."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, kv_positions, logits, eps, softmax_scale):
+        from ..custom_flash_attn.sparse_index_flash_attn import _flash_attn_forward
+
+        if kv_positions.stride(-1) != 1:
+            kv_positions = kv_positions.contiguous()
+        if logits.stride(-1) != 1:
+            logits = logits.contiguous()
+        B, T = kv_positions.shape[0], kv_positions.shape[1]
+        row_loss = torch.empty(B * T, device=q.device, dtype=torch.float32)
+        o, attn_sum, lse, ctx.softmax_scale = _flash_attn_forward(
+            q, k, v, kv_positions, softmax_scale=softmax_scale, return_attn=True, q_layout="bthd",
+            kl_logits=logits, kl_eps=eps, kl_row_loss=row_loss,
+        )
+        ctx.save_for_backward(q, k, v, kv_positions, o, lse)
+        ctx.mark_non_differentiable(row_loss)
+        return o, attn_sum, row_loss
+
+    @staticmethod
+    def backward(ctx, do, dattn_sum, _d_row_loss):
+        from ..custom_flash_attn.sparse_index_flash_attn import _flash_attn_backward
+
+        q, k, v, kv_positions, o, lse = ctx.saved_tensors
+        dq, dk, dv = _flash_attn_backward(do, q, k, v, kv_positions, o, lse, dattn_sum, ctx.softmax_scale, "bthd")
+        return dq, dk, dv, None, None, None, None
+
+
+class _KLFromRowLosses(torch.autograd.Function):
+    """The mean of row losses computed in the attention epilogue; backward as
+    SparseIndexerKLLossFunc (gw_indexer_kl_bwd on attn_sum and the fp32 logits)."""
+
+    @staticmethod
+    def forward(ctx, attn_sum, logits, row_loss, eps):
+        a, z = _prepare(attn_sum, logits)
+        ctx.save_for_backward(a, z)
+        ctx.eps = float(eps)
+        ctx.logits_dtype = logits.dtype
+        return row_loss.mean()
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        a, z = ctx.saved_tensors
+        d_attn, d_logits = kl_loss_backward(a, z, grad_out, ctx.eps)
+        return d_attn, d_logits.to(ctx.logits_dtype), None, None
+
+
+def sparse_attention_kl_loss(q, k, v, kv_positions, logits, eps: float = 1e-6, softmax_scale=None):
+    """``(o, attn_sum, loss)``: ``sparse_index_flash_attn_func(q, k, v, kv_positions)``
+    followed by ``sparse_indexer_kl_loss(attn_sum, logits, eps)`` (reference
+    ``dsa_attention.py:5395-5411`` with the attention mass as p), with the loss's forward
+    fused into the attention's attn_sum epilogue: attn_sum is not read back for the loss.
+    Same values and gradients as the two calls (the fused sums run in another order);
+    ``logits`` is the indexer's ``topk_scores`` aligned with ``kv_positions``."""
+    if logits.shape != kv_positions.shape:
+        raise ValueError(f"logits {tuple(logits.shape)} must match kv_positions {tuple(kv_positions.shape)}")
+    o, attn_sum, row_loss = _AttnWithKLRows.apply(q, k, v, kv_positions, logits, float(eps), softmax_scale)
+    return o, attn_sum, _KLFromRowLosses.apply(attn_sum, logits, row_loss, float(eps))

@@ -274,6 +274,35 @@ int gw_dsa_glue_bwd(int dtype, const void* y, int64_t rows, int64_t ldy, int64_t
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------------------
+ * Sparse-index attention forward with the indexer KL loss fused into the attn_sum epilogue
+ * (training). Same arguments and outputs as gw_sparse_attn_fwd (attn_sum required), plus:
+ * logits [B, T, K] of logits_dtype (GW_DTYPE_BF16/FP16/FP32; element (b,t,j) at
+ * b*logits_stride_b + t*logits_stride_t + j) - the indexer's top-k scores aligned with
+ * kv_pos - and row_loss fp32 [B*T] (contiguous):
+ *   row_loss[b*T+t] = sum_j p_j (log(p_j + eps) - log_softmax(z)_j),
+ *   p = attn_sum[b,t,:] / (sum_j attn_sum[b,t,j] + eps),  z = logits[b,t,:] in fp32,
+ * i.e. gw_indexer_kl_fwd on (attn_sum, logits cast to fp32), the per-row loss of
+ * sparse_indexer_kl_loss (easyvolcap/utils/custom_indexer/indexer_kl_fused.py:8-155) with
+ * the attention mass as p (easyvolcap/official_vggt/layers/dsa_attention.py:5404-5411),
+ * computed while the row is still on chip. Supported: K <= 1024 per head group (a group
+ * is 8 heads at D = 64, 4 at D = 128: K <= 2048 at H = 16, D = 64). The backward is
+ * gw_indexer_kl_bwd + gw_sparse_attn_bwd.
+ */
+int gw_sparse_attn_fwd_kl(int dtype,
+                          const void* q, const int64_t* q_strides,
+                          const void* k, const int64_t* k_strides,
+                          const void* v, const int64_t* v_strides,
+                          const int32_t* kv_pos, int64_t pos_stride_b, int64_t pos_stride_t,
+                          void* o, const int64_t* o_strides,
+                          float* lse, float* attn_sum,
+                          int64_t B, int64_t T, int64_t S, int64_t H, int64_t D, int64_t K,
+                          float softmax_scale,
+                          const void* logits, int logits_dtype, int64_t logits_stride_b,
+                          int64_t logits_stride_t, float eps, float* row_loss,
+                          void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/* ------------------------------------------------------------------------------------
  * Source-downsample coarse selector (inference only, off unless requested): the device
  * steps around an indexer top-k over pooled source rows. Replaces the torch pooling of
  * DSAAttention._prepare_source_downsample_projected and the torch expansion of

@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.gw_abi_version() == 102
+    assert lib.gw_abi_version() == 103
 
 
 def test_one_hip_runtime_in_process():

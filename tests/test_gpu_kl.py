@@ -147,3 +147,70 @@ def test_kl_loss_at_layer_size_sampled_rows(gpu_device):
     wda, wdz = okl.kl_loss_bwd(ac, zc, 512.0 / T, 1e-6)  # gs = 1 / T for the sampled rows
     _check_grads(da[0, sel.cuda()].cpu()[None], wda, torch.bfloat16)
     _check_grads(dz[0, sel.cuda()].cpu()[None], wdz, torch.bfloat16)
+
+
+# ------------------------------------------------- KL fused into the attention epilogue
+
+
+def _attn_inputs(B, T, S, H, K, seed, invalid=True):
+    from geoweave_amd import workloads
+
+    q, k, v = workloads.attention_inputs(1, B, torch.bfloat16, tokens=max(T, S), heads=H, seed=seed)
+    q, k, v = q[:, :T], k[:, :S], v[:, :S]
+    g = torch.Generator().manual_seed(seed + 1)
+    pos = torch.randint(0, S, (B, T, K), generator=g, dtype=torch.int32)
+    if invalid:
+        pos[0, 1, :] = -1            # a row with no valid key: attn_sum = 0, loss = 0
+        pos[0, 2, ::3] = S           # out of range -> p = 0 for those entries
+    z = (torch.randn(B, T, K, generator=g) * 2.0).bfloat16()
+    return [x.contiguous().cuda() for x in (q, k, v, pos, z)]
+
+
+@pytest.mark.parametrize("B,T,S,H,K", [(2, 300, 500, 16, 1024), (1, 257, 400, 16, 100), (1, 130, 300, 8, 1024),
+                                       (1, 64, 2100, 16, 2048)])
+def test_fused_kl_rows_match_standalone_and_oracle(gpu_device, B, T, S, H, K):
+    from geoweave_amd.custom_flash_attn.sparse_index_flash_attn import _flash_attn_forward
+
+    q, k, v, pos, z = _attn_inputs(B, T, S, H, K, seed=K + H)
+    rows = torch.empty(B * T, device=q.device, dtype=torch.float32)
+    o, a, lse, _ = _flash_attn_forward(q, k, v, pos, softmax_scale=0.125, kl_logits=z, kl_eps=1e-6, kl_row_loss=rows)
+    o2, a2, lse2, _ = _flash_attn_forward(q, k, v, pos, softmax_scale=0.125)
+    want = klf.kl_loss_forward(a2, z.float().contiguous(), 1e-6)
+    torch.cuda.synchronize()
+    # the attention outputs are those of the unfused launch, bit for bit
+    assert torch.equal(o, o2) and torch.equal(a, a2) and torch.equal(lse, lse2)
+    torch.testing.assert_close(rows, want, rtol=1e-5, atol=1e-6)
+    ref = okl.kl_row_losses(a2.cpu().double(), z.cpu().double(), 1e-6)
+    torch.testing.assert_close(rows.cpu().double(), ref.reshape(-1), rtol=1e-5, atol=1e-6)
+    assert float(rows[1]) == 0.0  # row (0, 1) has no valid key
+
+
+def test_fused_kl_gradients_equal_the_two_calls(gpu_device):
+    from geoweave_amd.custom_flash_attn import sparse_index_flash_attn as sifa
+
+    q, k, v, pos, z = _attn_inputs(1, 400, 600, 16, 256, seed=5)
+    do = torch.randn(q.shape, generator=torch.Generator().manual_seed(6)).bfloat16().cuda()
+    grads = []
+    for fused in (True, False):
+        qd, kd, vd, zd = (x.detach().clone().requires_grad_() for x in (q, k, v, z))
+        if fused:
+            o, attn, loss = klf.sparse_attention_kl_loss(qd, kd, vd, pos, zd, 1e-6, 0.125)
+        else:
+            o, attn = sifa.sparse_index_flash_attn_func(qd, kd, vd, pos, None, False, 0.125)
+            loss = sparse_indexer_kl_loss(attn, zd, 1e-6)
+        ((o.float() * do.float()).sum() + 3.0 * loss).backward()
+        grads.append((float(loss.detach()), qd.grad, kd.grad, vd.grad, zd.grad))
+    torch.cuda.synchronize()
+    (l1, *g1), (l2, *g2) = grads
+    assert abs(l1 - l2) <= 1e-5 * abs(l2) + 1e-7
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+
+
+def test_fused_kl_limits(gpu_device):
+    from geoweave_amd.custom_flash_attn.sparse_index_flash_attn import _flash_attn_forward
+
+    q, k, v, pos, z = _attn_inputs(1, 8, 4000, 8, 1025, seed=9, invalid=False)
+    rows = torch.empty(8, device=q.device, dtype=torch.float32)
+    with pytest.raises(RuntimeError, match="fused KL supports K <= 1024"):
+        _flash_attn_forward(q, k, v, pos, softmax_scale=0.125, kl_logits=z, kl_row_loss=rows)
