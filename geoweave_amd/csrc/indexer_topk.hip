@@ -14,33 +14,39 @@
 //                           topk keys of the whole row score >= tau with very high
 //                           probability (about 1.7 x topk keys on average).
 //  K1 score_kernel<FILTER>: MFMA scores against all keys; the epilogue appends
-//                           (score, key) pairs with score >= tau to candidate sublists.
+//                           (score, key) pairs with score >= tau to the query's candidate
+//                           list (one list per query and key split).
 //  K2 select_kernel:        one wave per query: exact top-k of the candidates held in
 //                           registers (bisection on the order-preserving score bits,
-//                           ballot-ordered emit). A query whose sublists overflowed or
-//                           hold fewer than topk entries is queued for K3; one whose
-//                           candidates exceed the register slots is queued for K2b.
+//                           ballot-ordered emit). A query whose lists overflowed or hold
+//                           fewer than topk entries is queued for K3; one whose candidates
+//                           exceed the register slots is queued for K2b.
 //  K2b select_wide_kernel:  persistent workgroups: all candidates of a queued query in
 //                           LDS, block radix select.
 //  K3 fallback_kernel:      exact brute force for queued queries (scores to scratch, radix
 //                           select) - correct for any input, used rarely.
 // Exactness: if count(score >= tau) >= topk, every member of the top-k scores >= tau and
 // is a candidate, so selecting among the candidates is exact. Ties at the k-th value are
-// broken deterministically (candidate order: sublist, then position).
+// broken deterministically (candidate order: split, then position in the list).
 //
 // MFMA layout (v_mfma_f32_32x32x16_{bf16,f16}): C[32 queries x 32 keys]; A = q rows
 // (stationary in VGPRs for the whole key sweep), B = key rows staged through LDS
-// (XOR-swizzled 16-byte chunks, conflict-free operand reads). Lane l owns key column l%32 and query rows
-// 8*(r/4) + 4*(l/32) + r%4 of accumulator element r. Every (query row, key column) cell
-// of the tile therefore belongs to exactly one lane, for every key tile of the sweep, so
-// the candidates of one (query, column) go to a sublist that only that lane appends to:
-// its fill count is a private register and an append is a compare, a clamp, an add and a
-// store, with no cross-lane coordination.
+// (XOR-swizzled 16-byte chunks, conflict-free operand reads). Lane l owns key column l%32
+// and query rows 8*(r/4) + 4*(l/32) + r%4 of accumulator element r.
+//
+// Candidate appends: about 2 % of scores pass tau, so most accumulator elements have a
+// passing lane somewhere in the wave and a store per element would issue a mostly empty
+// memory instruction per element. Instead each wave compacts its passing entries into an
+// LDS queue (a ballot and a lane count per element, one LDS write), and every 64 queued
+// entries are written out by one full store: each lane takes one entry, ranks it among
+// the lanes holding the same query row (ballots on the row bits) and writes it to that
+// row's list after the entries already written. Everything is in a fixed order, so the
+// lists are deterministic.
 //
 // Key splits: to fill the chip, the key range is divided over nsplit workgroups per
 // query tile. Split sp takes the 64-key stages sp, sp + nsplit, sp + 2*nsplit, ...; the
 // interleave spreads any locality of a query's favourite keys (e.g. its own view) evenly
-// over the splits, so every sublist receives about (candidates / (32 * nsplit)) entries.
+// over the splits, so every list receives about (candidates / nsplit) entries.
 #include <math.h>
 
 #include <mutex>
@@ -54,18 +60,13 @@ namespace {
 constexpr int kQW = 32;            // queries per wave
 constexpr int kBN = 64;            // keys per LDS stage (and split interleave granule)
 constexpr int kDI = 64;            // indexer head dim
-constexpr int kSubTotal = 8192;    // candidate slots per query over all sublists
+constexpr int kSubTotal = 8192;    // candidate slots per query over all key splits
 constexpr int kMaxSplit = 8;
 constexpr int kMaxTopk = 2048;
 constexpr int kFallbackBlocks = 256;
-// Candidate layout: query rows are grouped 32 at a time (rows of one batch element, T
-// padded to a multiple of 32); group g holds [split][slot (cap + 1)][row (32)][key column
-// (32)] int2 {score bits, key}, so slot m of sublist (split, col) for the group's row rr
-// is at ((split * SS + m) * 32 + rr) * 32 + col. Slot cap is the overflow sink. One
-// wave's 32 query rows are one group: an append advances its offset by a fixed 8 KB and
-// the row enters as a constant, which keeps the epilogue's address math to one min.
-constexpr int kCandGroupRows = 32;
-constexpr int kCandSlotInt2 = kCandGroupRows * 32;  // int2 per slot of a group
+// Candidate layout: int2 {score bits, key} lists cand[(row * nsplit + split) * cap + i],
+// row = b * T + t, cap = kSubTotal / nsplit; counts[row * nsplit + split] = entries
+// appended (more than cap means the list overflowed).
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -123,6 +124,11 @@ __device__ __forceinline__ uint32_t wave_max_u(uint32_t x) {
   return max(a, b);
 }
 
+// Number of set bits of a wave mask below this lane.
+__device__ __forceinline__ uint32_t lanes_below_u(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
 enum TauMode { kTauArray = 0, kTauPlusInf = 1, kTauMinusInf = 2 };
 
 struct ScoreParams {
@@ -132,10 +138,9 @@ struct ScoreParams {
   const uint16_t* mask;  // [B, T, S] or null
   const float* tau;      // [B*T] or null (-inf)
   float* samp;           // SAMPLE: [B*T, Ms]
-  int2* cand;            // FILTER: candidate groups, see kCandGroupRows
-  int* counts;           // FILTER: [B*T, nsplit*32] appends per sublist (may exceed cap)
+  int2* cand;            // FILTER: candidate lists, see kQueue
+  int* counts;           // FILTER: [B*T, nsplit] appends per list (may exceed cap)
   int T, S;
-  int Tp;                // T rounded up to kCandGroupRows
   int nsplit, cap;
   int nstages;           // 64-key stages of the sweep
   int Ms;
@@ -169,6 +174,11 @@ struct ScoreShape {
   static constexpr int BM = NW * kQW;        // queries per workgroup
   static constexpr int THREADS = NW * 64;
   static constexpr int MIN_WAVES_PER_EU = HI <= 4 ? 2 : 1;
+  // Per-wave LDS candidate queue (entries): written out when it holds FLUSH entries at a
+  // check after every 8 accumulator elements, so at most FLUSH - 1 + 8 * 64 < QUEUE are
+  // ever queued.
+  static constexpr int QUEUE = HI <= 4 ? 1024 : 640;
+  static constexpr int FLUSH = HI <= 4 ? 256 : 128;
 };
 
 template <typename E, int HI, bool SAMPLE, bool HAS_MASK>
@@ -188,6 +198,9 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
   __shared__ __attribute__((aligned(16))) uint8_t ktile[2][TILE_BYTES];
   __shared__ float wtile[2][WVALS];
   __shared__ __attribute__((aligned(16))) float tau_s[BM];
+  constexpr int QUEUE = ScoreShape<HI>::QUEUE;
+  __shared__ int2 cq[SAMPLE ? 1 : NW][SAMPLE ? 1 : QUEUE];  // FILTER: per-wave candidate queue
+  __shared__ int rcnt[SAMPLE ? 1 : NW][kQW];                 // FILTER: entries appended per row
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -225,24 +238,13 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
     }
     tau_s[wave * kQW + lane] = tv;
   }
-  // The wave's 32 rows are candidate group (b * Tp + q0) / 32. Row rr = 8*(r/4) + 4*half
-  // + r%4 of accumulator element r sits at byte (split*SS + slot) * 8192 + rr * 256 +
-  // col * 8 of the group; cnt[r] is this lane's byte offset of the next slot (the
-  // slot index times 8192 plus lane_base, so the clamp to the sink is one min).
-  const int nsub = nsplit * 32;
-  const int SS = p.cap + 1;
-  char* wbase = nullptr;   // uniform
-  uint32_t lane_base = 0, lim = 0;
+  // FILTER: list of query row q0 + rr at cand + (((b * T + q0 + rr) * nsplit + split) * cap.
+  const int64_t list0 = ((int64_t)b * T + q0) * nsplit + split;
+  const uint32_t half_tag = (uint32_t)(4 * half) << 24;  // row bits of this lane's half
+  uint32_t qn = 0;                                       // queued entries (wave-uniform)
   if constexpr (!SAMPLE) {
-    const int64_t group = ((int64_t)b * p.Tp + q0) / kCandGroupRows;
-    wbase = reinterpret_cast<char*>(p.cand + group * ((int64_t)nsplit * SS * kCandSlotInt2));
-    lane_base = (uint32_t)split * (uint32_t)SS * 8192u + (uint32_t)half * 1024u + (uint32_t)col * 8u;
-    lim = lane_base + (uint32_t)p.cap * 8192u;
+    if (lane < kQW) rcnt[wave][lane] = 0;
   }
-  uint32_t cnt[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) cnt[r] = lane_base;
-
   // Loader geometry: load i of this thread fills LDS bytes [(i*NW + wave)*1024 + 16*lane, +16),
   // which hold physical chunk lane % CHUNKS of key row kl0 + i*RPI; its source is logical
   // chunk (lane % CHUNKS) ^ (row & SWZ). kl0 < RPI and RPI is a power of two, so
@@ -330,18 +332,65 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
   // as the direct LDS loads it waits for, so every store issued before that wait is
   // followed by at least one tile of MFMA work rather than waited on at once.
   float tau_r[16];  // thresholds of this lane's 16 rows (filled after the first barrier)
-  auto append = [&](const float (&sv)[16], int key) {
+  // Writes the queued entries to their rows' lists: all of them (`all`) or every full
+  // chunk of 64, moving the rest (< 64) to the front; qn is wave-uniform. Queue entries
+  // are {score bits, key | row << 24}. A row's next slot comes from an LDS atomic on the
+  // wave's own row counters: one instruction's lanes and successive instructions are
+  // served in order, so the lists come out the same on every run. Up to four chunks go
+  // per round, their LDS reads and atomics issued back to back.
+  auto flush = [&](bool all) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t full = all ? qn : (qn & ~63u);
+    for (uint32_t h = 0; h < full; h += 256) {
+      int2 e[4];
+      int slot[4];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t i = h + 64 * c + lane;
+        e[c] = i < full ? cq[wave][i] : make_int2(0, -1);
+      }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = 4 * g + j;
-        if (sv[r] >= tau_r[r]) {  // NaN (key past the end) never passes
-          char* wb = wbase + (8 * g + j) * 256;
-          *reinterpret_cast<int2*>(wb + min(cnt[r], lim)) = make_int2(__float_as_int(sv[r]), key);
-          cnt[r] += 8192u;
+      for (int c = 0; c < 4; ++c)
+        slot[c] = e[c].y != -1 ? atomicAdd(&rcnt[wave][((uint32_t)e[c].y >> 24) & 31u], 1) : p.cap;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (slot[c] < p.cap) {
+          const uint32_t rr = ((uint32_t)e[c].y >> 24) & 31u;
+          p.cand[(list0 + (int64_t)rr * nsplit) * p.cap + slot[c]] = make_int2(e[c].x, e[c].y & 0xFFFFFF);
         }
       }
+    }
+    const uint32_t rem = qn - full;
+    if (rem > 0 && full > 0) {
+      int2 mv = make_int2(0, 0);
+      if ((uint32_t)lane < rem) mv = cq[wave][full + lane];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if ((uint32_t)lane < rem) cq[wave][lane] = mv;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    qn = rem;
+  };
+  // Queues the passing entries of a tile: a ballot, a count of the passing lanes below,
+  // one LDS write; the queue is written out once it holds FLUSH entries (checked after
+  // every 8 elements).
+  auto append = [&](const float (&sv)[16], int key) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const bool pass = sv[r] >= tau_r[r];  // NaN (key past the end) never passes
+      const uint64_t m = __ballot(pass);
+      if (pass) {
+        const uint32_t pos = qn + (uint32_t)lanes_below_u(m);
+        cq[wave][pos] = make_int2(__float_as_int(sv[r]),
+                                  key | (int)(half_tag + ((uint32_t)(8 * (r / 4) + (r % 4)) << 24)));
+      }
+      qn += (uint32_t)__popcll(m);
+      if ((r & 7) == 7 && qn >= (uint32_t)ScoreShape<HI>::FLUSH) flush(false);
     }
   };
   // Scores of the tile of 32 keys at kb + nb*32 (+ mask); SAMPLE stores them directly.
@@ -422,11 +471,11 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
   }
 
   if constexpr (!SAMPLE) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = q0 + 8 * (r / 4) + 4 * half + (r % 4);
-      if (row < T) p.counts[((int64_t)b * T + row) * nsub + split * 32 + col] = (int)((cnt[r] - lane_base) >> 13);
-    }
+    flush(true);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < kQW && q0 + lane < T) p.counts[list0 + (int64_t)lane * nsplit] = rcnt[wave][lane];
   }
 }
 
@@ -470,20 +519,18 @@ __global__ __launch_bounds__(256) void indexer_tau_kernel(const float* samp, int
 // ---------------------------------------------------------------------------------------
 // Exact top-k among the candidates: one wave per query row, candidates in registers.
 //
-// Lane l reads NSEG = max(1, nsub / 64) sublists: l, l + 64, ... (with nsub = 32, lanes
-// l and l + 32 share sublist l % 32, taking its even and odd entries). Each sublist's
-// entries land in a fixed register array of KS = kSelRegs / NSEG slots (expected fill:
-// about 1.7 x topk / nsub, e.g. 14 of 40 at nsub = 128). A row with an overflowed
-// sublist, a register array over KS, or fewer than topk candidates goes to the exact
-// fallback. No barriers: reductions are wave-wide.
+// The row's lists (one per key split) are read as one sequence: entry e of the sequence
+// goes to register slot e / 64 of lane e % 64, for up to 64 * kSelRegs entries (about
+// 1.7 x topk are expected). A row with an overflowed list or fewer than topk candidates
+// goes to the exact fallback; one with more candidates than the registers hold goes to
+// the LDS selection. No barriers: reductions are wave-wide.
 // ---------------------------------------------------------------------------------------
-constexpr int kSelRegs = 80;
+constexpr int kSelRegs = 48;
 
 struct SelectParams {
   const int2* cand;
   const int* counts;
-  int nsub, cap;
-  int T, Tp;
+  int nsplit, cap;
   int32_t* out_idx;
   uint16_t* out_scores;
   int Kk;
@@ -495,119 +542,88 @@ struct SelectParams {
   int force_wide;  // test hook: every complete row takes the LDS selection
 };
 
-// First element of a row's candidates: slot m of sublist (split, col) is at
-// + (split * SS + m) * kCandSlotInt2 + col.
-__device__ __forceinline__ const int2* cand_row(const SelectParams& p, int64_t row) {
-  const int64_t b = row / p.T, t = row - b * p.T;
-  const int64_t crow = b * p.Tp + t;
-  const int SS = p.cap + 1;
-  return p.cand + (crow / kCandGroupRows) * ((int64_t)p.nsub * SS * kCandGroupRows) + (crow % kCandGroupRows) * 32;
-}
-
-// Exclusive prefix over the wave of x; `total` receives the wave sum.
-__device__ __forceinline__ int wave_excl_scan(int x, int& total) {
-  const int lane = threadIdx.x & 63;
-  int incl = x;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(incl, o);
-    if (lane >= o) incl += y;
-  }
-  total = __builtin_amdgcn_readlane(incl, 63);
-  return incl - x;
-}
-
 // Number of set bits of a wave mask below this lane.
 __device__ __forceinline__ int lanes_below(uint64_t m) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-template <typename E, int NSEG>
+// Row lists as one sequence: off[s] = entries of the lists before split s (uniform);
+// entry e sits at cand + (row * nsplit + s) * cap + (e - off[s]) for the split s holding it.
+struct RowLists {
+  int64_t base;  // (row * nsplit) * cap
+  int off[kMaxSplit + 1];
+  int nsplit, cap;
+  __device__ __forceinline__ int64_t at(int e) const {
+    int64_t a = base + e;
+#pragma unroll
+    for (int s2 = 1; s2 < kMaxSplit; ++s2)
+      if (s2 < nsplit && e >= off[s2]) a += cap - (off[s2] - off[s2 - 1]);
+    return a;
+  }
+};
+
+__device__ __forceinline__ bool row_lists(const SelectParams& p, int64_t row, RowLists& rl) {
+  rl.base = row * p.nsplit * (int64_t)p.cap;
+  rl.nsplit = p.nsplit;
+  rl.cap = p.cap;
+  bool bad = false;
+  int acc = 0;
+#pragma unroll
+  for (int s2 = 0; s2 < kMaxSplit; ++s2) {
+    rl.off[s2] = acc;
+    if (s2 < p.nsplit) {
+      const int c = p.counts[row * p.nsplit + s2];
+      bad |= c > p.cap;
+      acc += min(c, p.cap);
+    }
+  }
+  rl.off[kMaxSplit] = acc;
+  return bad;
+}
+
+template <typename E>
 __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams p) {
-  constexpr int KS = NSEG == 4 ? 24 : kSelRegs / NSEG;  // register slots per sublist
+  constexpr int KS = kSelRegs;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (row >= p.rows) return;
-  const int SS = p.cap + 1;
-  const int2* src[NSEG];
-  int cnt[NSEG];
-  int stride = 1;
-  bool bad = false;
-  // Sublist (split, col) of the row: slot m at row_base + (split * SS + m) * kCandSlotInt2 + col.
-  const int2* row_base = cand_row(p, row);
-  if (p.nsub == 32) {
-    const int sub = lane & 31, part = lane >> 5;
-    const int cc = p.counts[row * 32 + sub];
-    bad = cc > p.cap;
-    const int c = min(cc, p.cap);
-    src[0] = row_base + part * kCandSlotInt2 + sub;
-    cnt[0] = c > part ? (c - part + 1) / 2 : 0;
-    stride = 2;
-#pragma unroll
-    for (int j = 1; j < NSEG; ++j) {
-      src[j] = src[0];
-      cnt[j] = 0;
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < NSEG; ++j) {
-      const int sub = lane + 64 * j;
-      const int cc = p.counts[row * p.nsub + sub];
-      bad |= cc > p.cap;
-      cnt[j] = min(cc, p.cap);
-      src[j] = row_base + (int64_t)(sub >> 5) * SS * kCandSlotInt2 + (sub & 31);
-    }
-  }
-  int nl = 0, cmax_l = 0;
-#pragma unroll
-  for (int j = 0; j < NSEG; ++j) {
-    nl += cnt[j];
-    cmax_l = max(cmax_l, cnt[j]);
-  }
-  const uint32_t total = wave_sum_u((uint32_t)nl);
-  if (wave_max_u(bad ? 1u : 0u) != 0 || (int)total < p.Kk) {
+  RowLists rl;
+  const bool bad = row_lists(p, row, rl);
+  const int total = rl.off[kMaxSplit];
+  if (bad || total < p.Kk) {
     // The candidates may miss part of the top-k: exact brute force.
     if (lane == 0) p.fb_list[atomicAdd(p.fb_count, 1)] = (int)row;
     return;
   }
-  if (p.force_wide || wave_max_u(cmax_l > KS ? 1u : 0u) != 0) {
+  if (p.force_wide || total > 64 * KS) {
     // Complete candidates, more than the registers hold: the LDS selection.
     if (lane == 0) p.wide_list[atomicAdd(p.wide_count, 1)] = (int)row;
     return;
   }
-  const int cmax = (int)wave_max_u((uint32_t)cmax_l);  // register slots in use, uniform
+  const int nch = (total + 63) / 64;  // register slots in use, uniform
 
-  // Branch-free loads: slots past a sublist's count read its first entry (inside the
-  // buffer) and are replaced by key 0, below the key of every finite score. Chunks of 8
-  // slots past the wave's largest count are skipped with a uniform branch.
-  uint32_t kv[NSEG][KS];
+  // Slots past the end hold key 0, below the key of every finite score; chunks of 8 slots
+  // past the last one in use are skipped with a uniform branch.
+  uint32_t kv[KS];
   uint32_t lmin = 0xFFFFFFFFu, lmax = 0u;
 #pragma unroll
   for (int m0 = 0; m0 < KS; m0 += 8) {
 #pragma unroll
-    for (int j = 0; j < NSEG; ++j)
+    for (int m = m0; m < m0 + 8; ++m) kv[m] = 0u;
+    if (m0 < nch) {
 #pragma unroll
-      for (int m = m0; m < min(m0 + 8, KS); ++m) kv[j][m] = 0u;
-    if (m0 < cmax) {
-#pragma unroll
-      for (int j = 0; j < NSEG; ++j) {
-#pragma unroll
-        for (int m = m0; m < min(m0 + 8, KS); ++m) {
-          const bool live = m < cnt[j];
-          const uint32_t key = f2key(__int_as_float(src[j][(live ? m : 0) * stride * kCandSlotInt2].x));
-          kv[j][m] = live ? key : 0u;
-        }
+      for (int m = m0; m < m0 + 8; ++m) {
+        const int e = m * 64 + lane;
+        if (e < total) kv[m] = f2key(__int_as_float(p.cand[rl.at(e)].x));
       }
     }
   }
   // Key range of the live slots: empty slots hold 0, which kv - 1 wraps to the maximum.
 #pragma unroll
-  for (int j = 0; j < NSEG; ++j)
-#pragma unroll
-    for (int m = 0; m < KS; ++m) {
-      lmin = min(lmin, kv[j][m] - 1u);
-      lmax = max(lmax, kv[j][m]);
-    }
+  for (int m = 0; m < KS; ++m) {
+    lmin = min(lmin, kv[m] - 1u);
+    lmax = max(lmax, kv[m]);
+  }
   lmin += 1u;
   // Bisection on the key value: count(key >= lo) >= Kk > count(key >= hi).
   uint64_t lo = wave_min_u(lmin), hi = (uint64_t)wave_max_u(lmax) + 1;
@@ -616,11 +632,9 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
     uint32_t cc = 0;
 #pragma unroll
     for (int m0 = 0; m0 < KS; m0 += 8) {
-      if (m0 < cmax) {
+      if (m0 < nch) {
 #pragma unroll
-        for (int j = 0; j < NSEG; ++j)
-#pragma unroll
-          for (int m = m0; m < min(m0 + 8, KS); ++m) cc += kv[j][m] >= mid;
+        for (int m = m0; m < m0 + 8; ++m) cc += kv[m] >= mid;
       }
     }
     const int n = (int)wave_sum_u(cc);
@@ -633,16 +647,14 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
   }
   const uint32_t thr = (uint32_t)lo;
   // Elements > thr are all selected; of those == thr, the first (Kk - count(> thr)) in
-  // candidate order (slot chunk, sublist, slot, lane). Output positions come from wave
-  // ballots, so each write goes to base + (selected lanes below this one).
+  // candidate order (split, position). Output positions come from wave ballots, so each
+  // write goes to base + (selected lanes below this one).
   int n_gt = 0;
 #pragma unroll
   for (int m0 = 0; m0 < KS; m0 += 8) {
-    if (m0 < cmax) {
+    if (m0 < nch) {
 #pragma unroll
-      for (int j = 0; j < NSEG; ++j)
-#pragma unroll
-        for (int m = m0; m < min(m0 + 8, KS); ++m) n_gt += __popcll(__ballot(kv[j][m] > thr));
+      for (int m = m0; m < m0 + 8; ++m) n_gt += __popcll(__ballot(kv[m] > thr));
     }
   }
   const int need_eq = p.Kk - n_gt;
@@ -651,24 +663,21 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
   int base = 0, eq_run = 0;
 #pragma unroll
   for (int m0 = 0; m0 < KS; m0 += 8) {
-    if (m0 < cmax) {
+    if (m0 < nch) {
 #pragma unroll
-      for (int j = 0; j < NSEG; ++j) {
-#pragma unroll
-        for (int m = m0; m < min(m0 + 8, KS); ++m) {
-          const bool eq = kv[j][m] == thr;
-          const uint64_t eqm = __ballot(eq);
-          const int eq_before = eq_run + lanes_below(eqm);
-          eq_run += __popcll(eqm);
-          const bool sel = kv[j][m] > thr || (eq && eq_before < need_eq);
-          const uint64_t selm = __ballot(sel);
-          const int slot_out = base + lanes_below(selm);
-          base += __popcll(selm);
-          if (sel) {
-            const int2 cdt = src[j][m * stride * kCandSlotInt2];
-            oi[slot_out] = cdt.y;
-            os[slot_out] = (uint16_t)pack1(E{}, __int_as_float(cdt.x));
-          }
+      for (int m = m0; m < m0 + 8; ++m) {
+        const bool eq = kv[m] == thr;
+        const uint64_t eqm = __ballot(eq);
+        const int eq_before = eq_run + lanes_below(eqm);
+        eq_run += __popcll(eqm);
+        const bool sel = kv[m] > thr || (eq && eq_before < need_eq);
+        const uint64_t selm = __ballot(sel);
+        const int slot_out = base + lanes_below(selm);
+        base += __popcll(selm);
+        if (sel) {
+          const int2 cdt = p.cand[rl.at(m * 64 + lane)];
+          oi[slot_out] = cdt.y;
+          os[slot_out] = (uint16_t)pack1(E{}, __int_as_float(cdt.x));
         }
       }
     }
@@ -683,28 +692,19 @@ template <typename E>
 __global__ __launch_bounds__(256) void indexer_select_wide_kernel(const SelectParams p) {
   __shared__ uint32_t keys[kSubTotal];
   __shared__ int vals[kSubTotal];
-  __shared__ int offs[kMaxSplit * 32 + 1];
   __shared__ SelectShared sh;
   const int tid = threadIdx.x;
   const int nitems = *((volatile const int*)p.wide_count);
-  const int SS = p.cap + 1;
   for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
     const int64_t row = p.wide_list[item];
-    if (tid == 0) {
-      int acc = 0;
-      for (int sub = 0; sub < p.nsub; ++sub) {
-        offs[sub] = acc;
-        acc += min(p.counts[row * p.nsub + sub], p.cap);
-      }
-      offs[p.nsub] = acc;
-    }
-    __syncthreads();
-    const int total = offs[p.nsub];
-    for (int sub = tid; sub < p.nsub; sub += kSelThreads) {
-      const int2* src = cand_row(p, row) + (int64_t)(sub >> 5) * SS * kCandSlotInt2 + (sub & 31);
-      const int o = offs[sub], n = offs[sub + 1] - o;
-      for (int i = 0; i < n; ++i) {
-        const int2 e = src[(int64_t)i * kCandSlotInt2];
+    RowLists rl;
+    row_lists(p, row, rl);
+    const int total = rl.off[kMaxSplit];
+    for (int s2 = 0; s2 < p.nsplit; ++s2) {
+      const int2* src = p.cand + rl.base + (int64_t)s2 * p.cap;
+      const int o = rl.off[s2], n = rl.off[s2 + 1] - o;
+      for (int i = tid; i < n; i += kSelThreads) {
+        const int2 e = src[i];
         keys[o + i] = f2key(__int_as_float(e.x));
         vals[o + i] = e.y;
       }
@@ -827,12 +827,11 @@ Plan make_layout(int64_t B, int64_t T, int64_t S, int64_t topk) {
     pl.rank = r > pl.Ms ? pl.Ms : r;
   }
   const size_t rows = (size_t)B * (size_t)T;
-  const size_t rows_pad = (size_t)B * (size_t)((T + kCandGroupRows - 1) / kCandGroupRows * kCandGroupRows);
   size_t off = 0;
   pl.off_tau = off;      off = align_up(off + rows * 4, 256);
   pl.off_samp = off;     off = align_up(off + (pl.sample ? rows * (size_t)pl.Ms * 4 : 0), 256);
-  pl.off_counts = off;   off = align_up(off + rows * kMaxSplit * 32 * 4, 256);
-  pl.off_cand = off;     off = align_up(off + rows_pad * (size_t)(kSubTotal + kMaxSplit * 32) * 8, 256);
+  pl.off_counts = off;   off = align_up(off + rows * kMaxSplit * 4, 256);
+  pl.off_cand = off;     off = align_up(off + rows * (size_t)kSubTotal * 8, 256);
   pl.off_fb = off;       off = align_up(off + 64, 256);
   pl.off_fblist = off;   off = align_up(off + rows * 4, 256);
   pl.off_widelist = off; off = align_up(off + rows * 4, 256);
@@ -898,7 +897,7 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   const int64_t rows = B * (int64_t)base.T;
   pl.nsplit = choose_nsplit(tiles * B, base.S, filter_slots((const void*)indexer_score_kernel<E, HI, false, HAS_MASK>, THREADS),
                             pl.sample);
-  pl.cap = kSubTotal / (32 * pl.nsplit);
+  pl.cap = kSubTotal / pl.nsplit;
   float* tau = reinterpret_cast<float*>(ws + pl.off_tau);
   if (pl.sample) {
     ScoreParams sp = base;
@@ -931,10 +930,8 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   SelectParams fs{};
   fs.cand = fp.cand;
   fs.counts = fp.counts;
-  fs.nsub = pl.nsplit * 32;
+  fs.nsplit = pl.nsplit;
   fs.cap = pl.cap;
-  fs.T = base.T;
-  fs.Tp = base.Tp;
   fs.out_idx = out_idx;
   fs.out_scores = static_cast<uint16_t*>(out_scores);
   fs.Kk = pl.Kk;
@@ -945,12 +942,7 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   fs.rows = rows;
   fs.force_wide = base.force_wide;
   const dim3 sgrid2((unsigned)((rows + 3) / 4));
-  if (fs.nsub <= 64)
-    hipLaunchKernelGGL((indexer_select_kernel<E, 1>), sgrid2, dim3(256), 0, st, fs);
-  else if (fs.nsub == 128)
-    hipLaunchKernelGGL((indexer_select_kernel<E, 2>), sgrid2, dim3(256), 0, st, fs);
-  else
-    hipLaunchKernelGGL((indexer_select_kernel<E, 4>), sgrid2, dim3(256), 0, st, fs);
+  hipLaunchKernelGGL((indexer_select_kernel<E>), sgrid2, dim3(256), 0, st, fs);
   GW_HIP_LAUNCH_CHECK("indexer_select_kernel");
   hipLaunchKernelGGL((indexer_select_wide_kernel<E>), dim3(kFallbackBlocks), dim3(256), 0, st, fs);
   GW_HIP_LAUNCH_CHECK("indexer_select_wide_kernel");
@@ -1029,7 +1021,6 @@ extern "C" int gw_indexer_topk_fwd(int dtype, const void* q, const void* k, cons
   base.w = static_cast<const uint16_t*>(w);
   base.mask = static_cast<const uint16_t*>(mask);
   base.T = (int)T;
-  base.Tp = (int)((T + kCandGroupRows - 1) / kCandGroupRows * kCandGroupRows);
   base.S = (int)S;
   base.scale = softmax_scale;
   base.tau_mode = (flags & GW_TOPK_FLAG_TAU_PLUS_INF) ? kTauPlusInf
