@@ -384,11 +384,21 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
     for (int r = 0; r < 16; ++r) {
       const bool pass = sv[r] >= tau_r[r];  // NaN (key past the end) never passes
       const uint64_t m = __ballot(pass);
-      if (pass) {
-        const uint32_t pos = qn + (uint32_t)lanes_below_u(m);
-        cq[wave][pos] = make_int2(__float_as_int(sv[r]),
-                                  key | (int)(half_tag + ((uint32_t)(8 * (r / 4) + (r % 4)) << 24)));
-      }
+      const uint32_t addr = (uint32_t)(uintptr_t)&cq[wave][0] + 8u * (qn + lanes_below_u(m));
+      const uint32_t kt = (uint32_t)key | (half_tag + ((uint32_t)(8 * (r / 4) + (r % 4)) << 24));
+      // The LDS write runs with exec = the passing lanes, set and restored inside one asm
+      // statement, so there is no branch around it (a branch per accumulator element splits
+      // the epilogue into small blocks). The compiler does not count this write in its
+      // lgkmcnt waits; LDS operations of a wave complete in issue order, so an extra
+      // operation can only make those waits stricter, never release one early.
+      uint64_t saved;
+      asm volatile(
+          "s_and_saveexec_b64 %0, %1\n\t"
+          "ds_write_b64 %2, %3\n\t"
+          "s_or_b64 exec, exec, %0"
+          : "=&s"(saved)
+          : "s"(m), "v"(addr), "v"(make_uint2(__float_as_uint(sv[r]), kt))
+          : "memory", "scc");
       qn += (uint32_t)__popcll(m);
       if ((r & 7) == 7 && qn >= (uint32_t)ScoreShape<HI>::FLUSH) flush(false);
     }
