@@ -20,8 +20,9 @@
 //            reference's two (:640-676 then :678-740).
 //  dkv pass (key-major over the CSR of kv_csr.hip: one wave per work item = up to 2048
 //            entries of one key, and group of heads). The key's K and V rows stay in
-//            registers; the wave gathers q, dO and {lse, total} of each entry's query,
-//            recomputes p_j and ds_j, and accumulates dk and dv in fp32. A key whose
+//            registers; the wave gathers q, dO and {lse, total} of each entry's query
+//            (4 entries per block, the next block's gathers in flight while one is
+//            consumed), recomputes p_j and ds_j, and accumulates dk and dv in fp32. A key whose
 //            entries span several items writes fp32 partials that a reduce kernel sums
 //            in item order.
 // Every sum runs in a fixed order, so the backward is bitwise reproducible.
@@ -208,7 +209,7 @@ __global__ __launch_bounds__(256) void sparse_attn_bwd_dkv_kernel(const AttnBwdP
   constexpr int LPH = D / 8;
   constexpr int HL = HPW * LPH;
   constexpr int G = 64 / HL;
-  constexpr int U = 8;
+  constexpr int U = 4;  // entries per block and lane group
   constexpr int STEP = U * G;
   static_assert(HL * G == 64, "lane decomposition must cover one wave");
 
@@ -242,9 +243,8 @@ __global__ __launch_bounds__(256) void sparse_attn_bwd_dkv_kernel(const AttnBwdP
 #pragma unroll
   for (int i = 0; i < 8; ++i) ak[i] = av[i] = 0.f;
 
-  // Entries of the next block are prefetched; the q/dO/{lse,total} gathers of a block are
-  // issued together at the top of its iteration (other waves cover their latency).
-  int2 en[U];
+  // Software-pipelined gathers: the q/dO/{lse,total} rows of block i+1 are issued before
+  // block i is consumed, and the entries of block i+2 before that.
   auto load_entries = [&](int2 (&ee)[U], int i0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -252,39 +252,61 @@ __global__ __launch_bounds__(256) void sparse_attn_bwd_dkv_kernel(const AttnBwdP
       ee[u] = i < it.end ? p.csr.entries[i] : make_int2(-1, 0);
     }
   };
-  load_entries(en, it.beg);
-  for (int i0 = it.beg; i0 < it.end; i0 += STEP) {
-    int2 ec[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) ec[u] = en[u];
-    load_entries(en, i0 + STEP);
-    uint4 qv[U], dv[U];
-    float2 lt[U];
-    float da[U];
+  auto gather = [&](uint4 (&qv)[U], uint4 (&dv)[U], float2 (&lt)[U], float (&da)[U], const int2 (&ee)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const bool ok = ec[u].x >= 0;
-      const int64_t tt = ok ? ec[u].x : 0;
-      qv[u] = *reinterpret_cast<const uint4*>(qb + tt * p.qst);
-      dv[u] = *reinterpret_cast<const uint4*>(dob + tt * p.dost);
-      lt[u] = ltb[tt * p.H];
-      da[u] = (DATTN && ok) ? to_f32(E{}, dab[tt * p.K + ec[u].y]) : 0.f;
+      const bool ok = ee[u].x >= 0;
+      const int64_t tt = ok ? ee[u].x : 0;
+      qv[u] = make_uint4(0, 0, 0, 0);
+      dv[u] = qv[u];
+      lt[u] = make_float2(0.f, 0.f);
+      da[u] = 0.f;
+      if (ok) {
+        qv[u] = *reinterpret_cast<const uint4*>(qb + tt * p.qst);
+        dv[u] = *reinterpret_cast<const uint4*>(dob + tt * p.dost);
+        lt[u] = ltb[tt * p.H];
+        if constexpr (DATTN) da[u] = to_f32(E{}, dab[tt * p.K + ee[u].y]);
+      }
     }
+  };
+  int2 ec[U], en[U];
+  uint4 qc[U], dc[U];
+  float2 lc[U];
+  float dac[U];
+  load_entries(ec, it.beg);
+  gather(qc, dc, lc, dac, ec);
+  load_entries(en, it.beg + STEP);
+  for (int i0 = it.beg; i0 < it.end; i0 += STEP) {
+    uint4 qn[U], dn[U];
+    float2 ln[U];
+    float dan[U];
+    gather(qn, dn, ln, dan, en);  // block i+1 (past the end: no traffic)
+    int2 enn[U];
+    load_entries(enn, i0 + 2 * STEP);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const bool ok = ec[u].x >= 0 && head_ok;
-      const float sd = group_sum<LPH>(dot8<E>(qv[u], kv));
-      const float pj = ok ? fexp2(sd * p.scale_log2 - lt[u].x) : 0.f;
-      const float dp = group_sum<LPH>(dot8<E>(vv, dv[u])) + da[u];
-      const float ds = (dp - lt[u].y) * pj;
+      const float sd = group_sum<LPH>(dot8<E>(qc[u], kv));
+      const float pj = ok ? fexp2(sd * p.scale_log2 - lc[u].x) : 0.f;
+      const float dp = group_sum<LPH>(dot8<E>(vv, dc[u])) + dac[u];
+      const float ds = (dp - lc[u].y) * pj;
       float qf[8], df[8];
-      unpack8<E>(qv[u], qf);
-      unpack8<E>(dv[u], df);
+      unpack8<E>(qc[u], qf);
+      unpack8<E>(dc[u], df);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         ak[i] = fmaf(ds, qf[i], ak[i]);
         av[i] = fmaf(pj, df[i], av[i]);
       }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      ec[u] = en[u];
+      en[u] = enn[u];
+      qc[u] = qn[u];
+      dc[u] = dn[u];
+      lc[u] = ln[u];
+      dac[u] = dan[u];
     }
   }
 
