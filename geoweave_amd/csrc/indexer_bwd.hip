@@ -47,7 +47,7 @@ template <typename E, int HI>
 __global__ __launch_bounds__(256) void indexer_bwd_dq_kernel(const IdxBwdParams p) {
   constexpr int HL = HI * 8;
   constexpr int G = 64 / HL;
-  constexpr int U = 8;
+  constexpr int U = 2;  // small blocks: 5+ waves per SIMD for the latency-bound gathers
   constexpr int STEP = U * G;
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -131,7 +131,7 @@ template <typename E, int HI>
 __global__ __launch_bounds__(256) void indexer_bwd_dkw_kernel(const IdxBwdParams p) {
   constexpr int HL = HI * 8;
   constexpr int G = 64 / HL;
-  constexpr int U = 8;
+  constexpr int U = 2;  // small blocks: 5+ waves per SIMD for the latency-bound gathers
   constexpr int STEP = U * G;
   const int lane = threadIdx.x & 63;
   const int item = blockIdx.x * 4 + (threadIdx.x >> 6);

@@ -21,8 +21,11 @@
 //  dkv pass (key-major over the CSR of kv_csr.hip: one wave per work item = up to 2048
 //            entries of one key, and group of heads). The key's K and V rows stay in
 //            registers; the wave gathers q, dO and {lse, total} of each entry's query
-//            (4 entries per block, the next block's gathers in flight while one is
-//            consumed), recomputes p_j and ds_j, and accumulates dk and dv in fp32. A key whose
+//            (2 entries per block, the next block's gathers in flight while one is
+//            consumed), recomputes p_j and ds_j, and accumulates dk and dv in fp32.
+// Both passes are latency-bound random gathers; their block sizes (4 keys per lane group
+// in the dq pass, 2 entries in the dkv pass) were chosen by measurement: smaller blocks
+// leave fewer bytes in flight per wave but let more waves run per SIMD. A key whose
 //            entries span several items writes fp32 partials that a reduce kernel sums
 //            in item order.
 // Every sum runs in a fixed order, so the backward is bitwise reproducible.
@@ -74,7 +77,7 @@ __global__ __launch_bounds__(256) void sparse_attn_bwd_dq_kernel(const AttnBwdPa
   constexpr int LPH = D / 8;
   constexpr int HL = HPW * LPH;
   constexpr int G = 64 / HL;
-  constexpr int U = 8;
+  constexpr int U = 4;  // keys per block and lane group (136 VGPRs: 3 waves per SIMD)
   constexpr int STEP = U * G;
   static_assert(HL * G == 64, "lane decomposition must cover one wave");
 
@@ -209,7 +212,7 @@ __global__ __launch_bounds__(256) void sparse_attn_bwd_dkv_kernel(const AttnBwdP
   constexpr int LPH = D / 8;
   constexpr int HL = HPW * LPH;
   constexpr int G = 64 / HL;
-  constexpr int U = 4;  // entries per block and lane group
+  constexpr int U = 2;  // entries per block and lane group (small blocks: more waves in flight)
   constexpr int STEP = U * G;
   static_assert(HL * G == 64, "lane decomposition must cover one wave");
 
