@@ -110,7 +110,7 @@ def test_additive_mask(gpu_device):
 def test_forced_fallback_paths_are_exact(gpu_device, flags, tokens):
     # PLUS_INF: no candidate passes, every query takes the brute-force path.
     # MINUS_INF at N=5496: every key is a candidate and the lists hold them all.
-    # MINUS_INF at N=12000: every key passes and the per-(query, column) lists
+    # MINUS_INF at N=12000: every key passes and the query's candidate lists
     # (8192 slots per query) overflow, so every query takes the brute-force path.
     # FORCE_WIDE: every query is selected by the LDS path (with sampling at N=5496,
     # without at N=2000) instead of the register path.
@@ -172,3 +172,20 @@ def test_long_context_s64_sampled_rows(gpu_device):
     assert bool((srt[:, 1:] != srt[:, :-1]).all()), "duplicate index in a row"
     rows = torch.randperm(n, generator=torch.Generator().manual_seed(64))[:192]
     _check(q, k, w, idx, sc, 1024, rows=rows)
+
+
+def test_massive_ties_and_zero_scores_stay_exact(gpu_device):
+    # Degenerate inputs like those of deep random-weight stacks: keys that repeat (ties in
+    # the thousands) and queries whose scores are zero for almost every key (relu of
+    # negative products). Such rows overflow the candidate lists or miss the sampled
+    # threshold and must take the exact path; every index set must hold up to the ties.
+    g = torch.Generator().manual_seed(41)
+    T, S, topk = 600, 9000, 1024
+    base = torch.randn(50, 4, 64, generator=g)
+    k = base[torch.randint(0, 50, (S,), generator=g)].unsqueeze(0)       # 50 distinct keys
+    q = torch.randn(1, T, 4, 64, generator=g)
+    q[0, :200] = -k[0, :200].mean(0).sign() * k[0].abs().mean(0)          # mostly zero scores
+    w = torch.ones(1, S, 4)
+    q, k, w = q.bfloat16(), k.bfloat16(), w.bfloat16()
+    idx, sc = _gpu_topk(q, k, w, topk)
+    _check(q, k, w, idx, sc, topk)
