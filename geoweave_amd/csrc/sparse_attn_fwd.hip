@@ -27,6 +27,7 @@
 // the query's head-group waves in a fixed order.
 #include <math.h>
 
+#include "gw_attn.h"
 #include "gw_common.h"
 
 namespace gw {
@@ -55,6 +56,9 @@ struct AttnFwdParams {
   int64_t lsb, lst;
   float kl_eps;
   float* row_loss;
+  // Optional: run only the 32-query blocks flagged here ([B][nqb][nchunk]).
+  const int* blk_flags;
+  int nqb, nchunk;
   int T, S, H, K;
   int NG;   // head groups (waves) per query
   int QPB;  // queries per workgroup
@@ -97,6 +101,16 @@ __global__ __launch_bounds__(256) void sparse_attn_fwd_kernel(const AttnFwdParam
   static_assert(HL * G == 64, "lane decomposition must cover one wave");
 
   __shared__ float lse2_s[kMaxQpb][kMaxHeadsLds];
+
+  if (p.blk_flags != nullptr) {
+    // All QPB (1, 2 or 4) queries of a workgroup sit in one 32-query block: the test is
+    // uniform over the workgroup.
+    const int qb = (int)((blockIdx.x * p.QPB) >> 5);
+    const int* f = p.blk_flags + ((int64_t)blockIdx.y * p.nqb + qb) * p.nchunk;
+    bool run = false;
+    for (int c = 0; c < p.nchunk; ++c) run |= f[c] != 0;
+    if (!run) return;
+  }
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -378,7 +392,8 @@ int attn_fwd_impl(int dtype, const void* q, const int64_t* q_strides, const void
                   const void* v, const int64_t* v_strides, const int32_t* kv_pos, int64_t pos_stride_b,
                   int64_t pos_stride_t, void* o, const int64_t* o_strides, float* lse, float* attn_sum, int64_t B,
                   int64_t T, int64_t S, int64_t H, int64_t D, int64_t K, float softmax_scale, void* workspace,
-                  size_t workspace_bytes, const KlArgs* kl, void* stream) {
+                  size_t workspace_bytes, const KlArgs* kl, void* stream, const int* blk_flags = nullptr,
+                  int nqb = 0, int nchunk = 0) {
   GW_CHECK_ARG(dtype == GW_DTYPE_BF16 || dtype == GW_DTYPE_FP16, "unsupported dtype code %d", dtype);
   GW_CHECK_ARG(B >= 0 && T >= 0 && S >= 0 && H >= 1 && K >= 0,
                "invalid sizes B=%lld T=%lld S=%lld H=%lld K=%lld", (long long)B, (long long)T,
@@ -429,6 +444,10 @@ int attn_fwd_impl(int dtype, const void* q, const int64_t* q_strides, const void
   p.lsb = p.lst = 0;
   p.kl_eps = 0.f;
   p.row_loss = nullptr;
+  p.blk_flags = blk_flags;
+  p.nqb = nqb;
+  p.nchunk = nchunk;
+  GW_CHECK_ARG(blk_flags == nullptr || (!want_attn && kl == nullptr), "block flags need the plain forward");
   p.T = (int)T;
   p.S = (int)S;
   p.H = (int)H;
@@ -489,4 +508,15 @@ extern "C" int gw_sparse_attn_fwd_kl(int dtype, const void* q, const int64_t* q_
   return gw::attn_fwd_impl(dtype, q, q_strides, k, k_strides, v, v_strides, kv_pos, pos_stride_b, pos_stride_t, o,
                            o_strides, lse, attn_sum, B, T, S, H, D, K, softmax_scale, workspace, workspace_bytes,
                            &kl, stream);
+}
+
+int gw::attn_fwd_flagged_blocks(int dtype, const void* q, const int64_t* q_strides, const void* k,
+                                const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                                const int32_t* kv_pos, int64_t pos_stride_b, int64_t pos_stride_t, void* o,
+                                const int64_t* o_strides, float* lse, int64_t B, int64_t T, int64_t S, int64_t H,
+                                int64_t D, int64_t K, float softmax_scale, const int* blk_flags, int nqb,
+                                int nchunk, void* stream) {
+  return gw::attn_fwd_impl(dtype, q, q_strides, k, k_strides, v, v_strides, kv_pos, pos_stride_b, pos_stride_t, o,
+                           o_strides, lse, nullptr, B, T, S, H, D, K, softmax_scale, nullptr, 0, nullptr, stream,
+                           blk_flags, nqb, nchunk);
 }

@@ -92,6 +92,19 @@ def _check_inputs(q, k, v, kv_positions, bias, causal, layout):
     return batch, seqlen_q, seqlen_k, nheads, d
 
 
+# Forward without attn_sum: "auto" picks the masked dense pass (gw_sparse_attn_fwd_dense)
+# when a query selects at least 1 / DENSE_MAX_RATIO of the keys, "dense" / "gather" force
+# one path (tests and measurements).
+FORWARD_PATH = "auto"
+DENSE_MAX_RATIO = 96
+
+
+def _use_dense(seqlen_k: int, num_kv: int, nheads: int, d: int) -> bool:
+    if FORWARD_PATH == "gather" or d != 64 or nheads % 2:
+        return False
+    return FORWARD_PATH == "dense" or seqlen_k <= DENSE_MAX_RATIO * num_kv
+
+
 def _prep(x: torch.Tensor) -> torch.Tensor:
     # Last dim contiguous and 16-byte aligned b/t/h strides (reference :3207-3209 makes
     # the last dim contiguous; the gfx950 kernel also needs 16-byte rows).
@@ -154,7 +167,13 @@ def _flash_attn_forward(
         batch, seqlen_q, seqlen_k, nheads, d, num_kv,
         float(softmax_scale),
     )
-    if kl_logits is None:
+    if kl_logits is None and attn_sum is None and _use_dense(seqlen_k, num_kv, nheads, d):
+        dense_bytes = int(lib.gw_sparse_attn_fwd_dense_workspace_size(batch, seqlen_q, seqlen_k, nheads, d))
+        dws = torch.empty(max(dense_bytes, 1), device=q.device, dtype=torch.uint8)
+        rc = lib.gw_sparse_attn_fwd_dense(*common[:13], *common[14:], dws.data_ptr(), dense_bytes,
+                                          _lib.stream_handle(q.device))
+        _lib.check(rc, "gw_sparse_attn_fwd_dense")
+    elif kl_logits is None:
         rc = lib.gw_sparse_attn_fwd(*common, _lib.ptr(ws), ws_bytes, _lib.stream_handle(q.device))
         _lib.check(rc, "gw_sparse_attn_fwd")
     else:

@@ -1,0 +1,148 @@
+"""GPU parity of the masked dense attention forward (gw_sparse_attn_fwd_dense) against the
+fp32 CPU oracle and the gather kernel.
+
+The dense pass computes every (query, key) product on the matrix cores and masks the keys a
+query did not select; o and lse must equal the sparse attention's. Tolerance: 2e-2 abs/rel for
+bf16/fp16 outputs (P enters the P·V product in the input dtype, as the gather kernel's fp32 p
+does not: both are within the bar), 1e-4 for lse. Cases: the layer's per-view shape in bf16
+and fp16, ragged -1 padding with T and S not multiples of 32 or 64, cross attention (T != S),
+empty rows, out-of-range and repeated positions (repeats go to the gather kernel inside the
+call), scores with a large dynamic range rising along the key order (the lazy maximum is raised
+and O rescaled on many tiles), bhtd strides, determinism, and a full-size layer on sampled rows.
+"""
+import contextlib
+
+import pytest
+import torch
+
+from geoweave_amd import workloads
+from geoweave_amd.custom_flash_attn import sparse_index_flash_attn as sifa
+from oracle import attention as oatt
+
+pytestmark = pytest.mark.gpu
+
+TOL = dict(atol=2e-2, rtol=2e-2)
+
+
+@contextlib.contextmanager
+def _path(name):
+    old = sifa.FORWARD_PATH
+    sifa.FORWARD_PATH = name
+    try:
+        yield
+    finally:
+        sifa.FORWARD_PATH = old
+
+
+def _run(q, k, v, pos, scale=None, layout="bthd", path="dense"):
+    qd, kd, vd, pd = (x.cuda() for x in (q, k, v, pos))
+    if layout == "bhtd":
+        qd, kd, vd = (x.transpose(1, 2).contiguous() for x in (qd, kd, vd))
+    with _path(path):
+        o, attn, lse, _ = sifa._flash_attn_forward(qd, kd, vd, pd, softmax_scale=scale, return_attn=False,
+                                                   q_layout=layout)
+    torch.cuda.synchronize()
+    assert attn is None
+    if layout == "bhtd":
+        o = o.transpose(1, 2)
+    return o.float().cpu(), lse.cpu()
+
+
+def _distinct_positions(B, T, S, K, seed):
+    # Row t lists (off_t + j * step) mod S: distinct when gcd(step, S) = 1.
+    g = torch.Generator().manual_seed(seed)
+    step = 7919 if S % 7919 else 7907
+    off = torch.randint(0, S, (B, T, 1), generator=g)
+    j = torch.arange(K).view(1, 1, K)
+    return ((off + j * step) % S).to(torch.int32).contiguous()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_one_view_layer_shape(gpu_device, dtype):
+    q, k, v = workloads.attention_inputs(1, 1, dtype)
+    n = q.shape[1]
+    pos = workloads.random_positions(1, n, n, 1024, seed=21)
+    print(f"[dense] one view N={n} dtype={dtype}", flush=True)
+    o, lse = _run(q, k, v, pos)
+    ro, _, rl = oatt.sparse_attention(q, k, v, pos)
+    torch.testing.assert_close(o, ro, **TOL)
+    torch.testing.assert_close(lse, rl, atol=1e-4, rtol=1e-4)
+    og, lg = _run(q, k, v, pos, path="gather")
+    torch.testing.assert_close(o, og, **TOL)
+    torch.testing.assert_close(lse, lg, atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("B,T,S,H,K,inv", [(2, 300, 300, 4, 77, 0.5), (1, 5, 700, 2, 64, 0.0),
+                                            (1, 100, 70, 16, 70, 0.3), (2, 257, 1000, 6, 200, 0.2)])
+def test_ragged_and_cross_attention(gpu_device, B, T, S, H, K, inv):
+    g = torch.Generator().manual_seed(T + S)
+    q = torch.randn(B, T, H, 64, generator=g).bfloat16()
+    k = torch.randn(B, S, H, 64, generator=g).bfloat16()
+    v = torch.randn(B, S, H, 64, generator=g).bfloat16()
+    pos = workloads.random_positions(B, T, S, K, seed=T, invalid_fraction=inv)
+    print(f"[dense] B={B} T={T} S={S} H={H} K={K}", flush=True)
+    o, lse = _run(q, k, v, pos, scale=0.1)
+    ro, _, rl = oatt.sparse_attention(q, k, v, pos, 0.1)
+    torch.testing.assert_close(o, ro, **TOL)
+    torch.testing.assert_close(lse, rl, atol=1e-4, rtol=1e-4)
+
+
+def test_masking_and_repeated_positions(gpu_device):
+    q, k, v = workloads.attention_inputs(1, 1, torch.bfloat16, tokens=200, seed=9)
+    pos = workloads.random_positions(1, 200, 200, 13, seed=10)
+    pos[0, 0, :] = -1          # no valid candidate: o = 0, lse = -inf
+    pos[0, 1, 5:] = 200        # past the end: masked
+    pos[0, 3, 0] = -5
+    pos[0, 70, :] = 7          # one position listed 13 times: counted 13 times (gather kernel)
+    pos[0, 150, 2] = pos[0, 150, 9]
+    o, lse = _run(q, k, v, pos)
+    ro, _, rl = oatt.sparse_attention(q, k, v, pos)
+    assert torch.all(o[0, 0] == 0) and torch.isinf(lse[0, 0]).all() and (lse[0, 0] < 0).all()
+    torch.testing.assert_close(o, ro, **TOL)
+    torch.testing.assert_close(lse, rl, atol=1e-4, rtol=1e-4)
+    # the repeated key dominates nothing: with one key listed 13 times the row is v[7]
+    torch.testing.assert_close(o[0, 70], v[0, 7].float(), **TOL)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_large_dynamic_range_rising_scores(gpu_device, dtype):
+    # Scores grow along the key order by ~60 units of log2 over the keys, so the lazy
+    # maximum of every row is raised on many tiles and O is rescaled each time.
+    T, S, H, K = 96, 2048, 2, 512
+    g = torch.Generator().manual_seed(5)
+    q = (torch.ones(1, T, H, 64) + 0.1 * torch.randn(1, T, H, 64, generator=g))
+    ramp = torch.linspace(-3.0, 3.0, S).view(1, S, 1, 1)
+    k = ramp * torch.ones(1, S, H, 64) + 0.1 * torch.randn(1, S, H, 64, generator=g)
+    v = torch.randn(1, S, H, 64, generator=g)
+    q, k, v = (x.to(dtype) for x in (q, k, v))
+    pos = workloads.random_positions(1, T, S, K, seed=6)
+    o, lse = _run(q, k, v, pos, scale=0.125)
+    ro, _, rl = oatt.sparse_attention(q, k, v, pos, 0.125)
+    torch.testing.assert_close(o, ro, **TOL)
+    torch.testing.assert_close(lse, rl, atol=1e-4, rtol=1e-4)
+
+
+def test_bhtd_matches_bthd_and_is_deterministic(gpu_device):
+    q, k, v = workloads.attention_inputs(1, 1, torch.bfloat16, tokens=512, seed=3)
+    pos = workloads.random_positions(1, 512, 512, 200, seed=4)
+    o1, l1 = _run(q, k, v, pos)
+    o2, l2 = _run(q, k, v, pos, layout="bhtd")
+    o3, l3 = _run(q, k, v, pos)
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    assert torch.equal(o1, o3) and torch.equal(l1, l3)
+
+
+@pytest.mark.parametrize("views", [16])
+def test_full_size_sampled_rows(gpu_device, views):
+    q, k, v = workloads.attention_inputs(views, 1, torch.bfloat16)
+    n = q.shape[1]
+    pos = _distinct_positions(1, n, n, 1024, seed=views)
+    print(f"[dense] full size N={n}", flush=True)
+    o, lse = _run(q, k, v, pos)
+    og, lg = _run(q, k, v, pos, path="gather")
+    torch.testing.assert_close(o, og, **TOL)
+    torch.testing.assert_close(lse, lg, atol=1e-4, rtol=1e-4)
+    rows = torch.randperm(n, generator=torch.Generator().manual_seed(1))[:128]
+    ro, _, rl = oatt.sparse_attention(q[:, rows], k, v, pos[:, rows])
+    torch.testing.assert_close(o[:, rows], ro, **TOL)
+    torch.testing.assert_close(lse[:, rows], rl, atol=1e-4, rtol=1e-4)
