@@ -20,14 +20,16 @@
 // final o = O / l and lse = m + log2(l) do not depend on which m was used.
 //
 // Pieces (all on the caller's stream):
-//   dense_mask_kernel  — maskT[b][qb][key]: bit i set when query qb*32 + i selected the key,
-//                        built per (32-query block, key chunk) with LDS atomics. A position
+//   dense_mask_kernel  — maskT[b][qb][key]: bit i set when query qb*32 + i selected the key
+//                        (LDS atomic OR per listed position, per chunk of keys). A position
 //                        listed twice for one query (the atomic returns the bit already set)
 //                        flags the block: the gather kernel then computes that block, since
 //                        the reference counts a repeated position twice.
 //   dense_vt_kernel    — V as [B][H][64][S_pad] (S_pad = S rounded up to 64, zero padded):
 //                        the P·V B operand is 8 consecutive keys of one column, one 16-byte load.
-//   dense_attn_kernel  — one wave per (32-query block, 2 heads).
+//   dense_attn_kernel  — 8 waves per workgroup, one per 32-query block, all on the same 2
+//                        heads: each K and V^T tile is read from memory once per workgroup
+//                        and shared through LDS.
 #include <math.h>
 
 #include "gw_attn.h"
@@ -39,7 +41,6 @@ namespace {
 
 constexpr float kDLog2e = 1.4426950408889634f;
 constexpr float kDLn2 = 0.6931471805599453f;
-constexpr int kMaskChunk = 16384;  // keys per mask-building workgroup (64 KiB of LDS words)
 constexpr int kDHpw = 2;           // heads per wave
 constexpr float kLazy = 8.f;       // p <= 2^kLazy before a rescale
 
@@ -57,10 +58,15 @@ __device__ __forceinline__ f32x16 mma(FP16, uint4 a, uint4 b, f32x16 c) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Selection mask, key-major per 32-query block.
+// Selection mask, key-major per 32-query block, built per (block, chunk of kMaskChunk keys)
+// with LDS atomics. The atomic returns the word as it was: a bit already set means the query
+// listed the key twice, and the block is flagged. Positions are read 8 rows at a time (16
+// bytes per lane when the table allows), so the loads of a group are in flight together.
 // ---------------------------------------------------------------------------------------
+constexpr int kMaskChunk = 16384;  // keys per workgroup (64 KiB of LDS words)
+
 __global__ __launch_bounds__(256) void dense_mask_kernel(const int32_t* __restrict__ pos, int64_t psb, int64_t pst,
-                                                         int T, int S, int K, int nqb, int nchunk,
+                                                         int T, int S, int K, int nqb, int nchunk, int vec,
                                                          uint32_t* __restrict__ mask, int* __restrict__ flags) {
   __shared__ uint32_t words[kMaskChunk];
   __shared__ int dup_any;
@@ -72,15 +78,38 @@ __global__ __launch_bounds__(256) void dense_mask_kernel(const int32_t* __restri
   __syncthreads();
   bool dup = false;
   const int rows = min(32, T - qb * 32);
+  const int32_t* pblk = pos + b * psb + (int64_t)(qb * 32) * pst;
+  // Positions outside [c0, c0 + len) (other chunks, negative padding, >= S) wrap to large
+  // unsigned offsets and are skipped.
+  auto put = [&](int32_t sidx, uint32_t bit) {
+    const uint32_t sl = (uint32_t)sidx - (uint32_t)c0;
+    if (sl < (uint32_t)len) dup |= (atomicOr(&words[sl], bit) & bit) != 0u;
+  };
+  if (vec) {
+    // K % 4 == 0 and 16-byte aligned rows: one int4 per lane and row.
+    const int n4 = K >> 2;
+    for (int j4 = threadIdx.x; j4 < n4; j4 += 256) {
 #pragma unroll 1
-  for (int i = 0; i < rows; ++i) {
-    const int32_t* prow = pos + b * psb + (int64_t)(qb * 32 + i) * pst;
-    const uint32_t bit = 1u << i;
-    for (int j = threadIdx.x; j < K; j += 256) {
-      // Positions outside [c0, c0 + len) (other chunks, negative padding, >= S) wrap to
-      // large unsigned offsets and are skipped.
-      const uint32_t s = (uint32_t)prow[j] - (uint32_t)c0;
-      if (s < (uint32_t)len) dup |= (atomicOr(&words[s], bit) & bit) != 0u;
+      for (int r0 = 0; r0 < rows; r0 += 8) {
+        int4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          v[u] = r0 + u < rows ? reinterpret_cast<const int4*>(pblk + (int64_t)(r0 + u) * pst)[j4] : make_int4(-1, -1, -1, -1);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const uint32_t bit = 1u << ((r0 + u) & 31);
+          put(v[u].x, bit);
+          put(v[u].y, bit);
+          put(v[u].z, bit);
+          put(v[u].w, bit);
+        }
+      }
+    }
+  } else {
+#pragma unroll 1
+    for (int i = 0; i < rows; ++i) {
+      const int32_t* prow = pblk + (int64_t)i * pst;
+      for (int j = threadIdx.x; j < K; j += 256) put(prow[j], 1u << i);
     }
   }
   if (dup) dup_any = 1;
@@ -163,6 +192,21 @@ __device__ __forceinline__ int tile_row(int r, int half) { return 8 * (r >> 2) +
 
 __device__ __forceinline__ uint16_t to_half_bits(BF16, float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 __device__ __forceinline__ uint16_t to_half_bits(FP16, float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// Sum of the 8 16-bit values of v added to c, in a fixed order (exact products with 1.0).
+__device__ __forceinline__ float sum8(BF16 e, uint4 v, float c) {
+  constexpr uint32_t one2 = 0x3F803F80u;
+  c = dot2(e, v.x, one2, c);
+  c = dot2(e, v.y, one2, c);
+  c = dot2(e, v.z, one2, c);
+  return dot2(e, v.w, one2, c);
+}
+__device__ __forceinline__ float sum8(FP16 e, uint4 v, float c) {
+  constexpr uint32_t one2 = 0x3C003C00u;
+  c = dot2(e, v.x, one2, c);
+  c = dot2(e, v.y, one2, c);
+  c = dot2(e, v.z, one2, c);
+  return dot2(e, v.w, one2, c);
+}
 __device__ __forceinline__ float from_half_bits(BF16, uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
 __device__ __forceinline__ float from_half_bits(FP16, uint16_t x) { return (float)__builtin_bit_cast(_Float16, x); }
 __device__ __forceinline__ uint32_t pack_pair(BF16 e, float lo, float hi) {
@@ -176,7 +220,7 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
 
 constexpr int kDW = 8;      // waves (32-query blocks) per workgroup, sharing each K/V tile
-constexpr int kPRow = 36;   // floats per P-tile row (32 keys + padding)
+constexpr int kPRow = 40;   // 16-bit elements per P-tile row (32 keys + padding: 80 bytes)
 
 // K tile: 32 keys x (2 heads x 64) bf16 = 32 rows of 256 bytes; the 16-byte chunk c of key
 // row kl sits at position c ^ (kl & 15). V^T tile: 128 rows (head, d) x 32 keys = 128 rows of
@@ -188,12 +232,14 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
   __shared__ __align__(16) uint8_t ktile[2][8192];
   __shared__ __align__(16) uint8_t vtile[2][8192];
   // Per wave: the S tile staged as float4 groups, lane-contiguous (element r of lane l at
-  // ((r >> 2) * 64 + l) * 4 + (r & 3)); the P tile in fp32 with padded rows; the compacted
-  // entry list. Lanes without an entry use dummy slots, so no per-entry step needs a branch:
-  // row 32 (m = +inf there, so p = 0), P slot kPRow * 32 + lane, list slot 1024 + lane.
+  // ((r >> 2) * 64 + l) * 4 + (r & 3)); P as two 16-bit tiles hi and lo (p = hi + lo to
+  // ~16 significant bits) with padded rows; the compacted entry list. Lanes without an
+  // entry use dummy slots, so no per-entry step needs a branch: row 32 (m = +inf there, so
+  // p = 0), P slot kPRow * 32 + lane, list slot 1024 + lane.
   __shared__ __align__(16) float stage_all[kDW][16 * 64];
-  __shared__ __align__(16) float ptile_all[kDW][kPRow * 32 + 64];
-  __shared__ int elist_all[kDW][32 * 32 + 64];
+  __shared__ __align__(16) uint16_t phi_all[kDW][kPRow * 32 + 64];
+  __shared__ __align__(16) uint16_t plo_all[kDW][kPRow * 32 + 64];
+  __shared__ uint16_t elist_all[kDW][32 * 32 + 64];
   __shared__ __align__(16) float mrow_all[kDW][HPW][36];
   __shared__ __align__(16) float lrow_all[kDW][HPW][36];
   __shared__ __align__(16) float arow_all[kDW][32];
@@ -202,8 +248,9 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   float* stage = stage_all[wave];
-  float* ptile = ptile_all[wave];
-  int* elist = elist_all[wave];
+  uint16_t* phi = phi_all[wave];
+  uint16_t* plo = plo_all[wave];
+  uint16_t* elist = elist_all[wave];
   float (*mrow)[36] = mrow_all[wave];
   float (*lrow)[36] = lrow_all[wave];
   float* arow = arow_all[wave];
@@ -248,9 +295,12 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
       lrow[hh][lane] = 0.f;
     }
   }
-  for (int i = lane; i < (kPRow * 32 + 64) / 4; i += 64) reinterpret_cast<float4*>(ptile)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int i = lane; i < (kPRow * 32 + 64) / 8; i += 64) {
+    reinterpret_cast<uint4*>(phi)[i] = make_uint4(0, 0, 0, 0);
+    reinterpret_cast<uint4*>(plo)[i] = make_uint4(0, 0, 0, 0);
+  }
   // Row sums: this lane's share of row `col` (keys 8*half + 0..7 and 16 + 8*half + 0..7 of
-  // each tile, the keys of its P·V operand), summed in a fixed order.
+  // each tile, the keys of its P·V operand), summed in a fixed order from hi and lo.
   float lpart[HPW];
 #pragma unroll
   for (int hh = 0; hh < HPW; ++hh) lpart[hh] = 0.f;
@@ -258,23 +308,27 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
   const uint32_t* mbase = p.mask + ((int64_t)b * p.nqb + (active ? qb : 0)) * p.S;
   const float sl2 = p.scale_log2;
 
-  // Tile loads: one 1 KB direct global->LDS load of K and one of V^T per wave.
+  // Tile loads: per wave one 16-byte chunk per lane of K and one of V^T (1 KB each), loaded
+  // into registers two tiles ahead and written to LDS one tile ahead.
   const int krow = 4 * wave + (lane >> 4);                 // key row of this lane's K chunk
   const int kchunk = (lane & 15) ^ (krow & 15);            // global chunk it loads
   const uint16_t* ksrc0 = p.k + b * p.ksb + (int64_t)(h0 + (kchunk >> 3)) * p.ksh + (kchunk & 7) * 8;
   const int vrow = 16 * wave + (lane >> 2);                // (head, d) row of this lane's V chunk
   const int vchunk = (lane & 3) ^ ((vrow >> 2) & 3);
   const uint16_t* vsrc0 = p.vt + (((int64_t)b * p.H + h0 + (vrow >> 6)) * 64 + (vrow & 63)) * p.Spad + vchunk * 8;
-  auto issue = [&](int kb0, int bf) {
+  auto gload = [&](int kb0, uint4& kr, uint4& vr) {
     const int key = min(kb0 + krow, p.S - 1);  // keys past S: any valid row (their P is 0)
-    __builtin_amdgcn_global_load_lds((glb_void_t*)(ksrc0 + (int64_t)key * p.kss),
-                                     (lds_void_t*)(&ktile[bf][wave * 1024]), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((glb_void_t*)(vsrc0 + kb0), (lds_void_t*)(&vtile[bf][wave * 1024]), 16, 0, 0);
+    kr = *reinterpret_cast<const uint4*>(ksrc0 + (int64_t)key * p.kss);
+    vr = *reinterpret_cast<const uint4*>(vsrc0 + kb0);
   };
-  auto mask_word = [&](int kb0) -> uint32_t {
-    const int kx = kb0 + col;
-    return (active && kx < p.S) ? mbase[kx] : 0u;
+  auto lstore = [&](int bf, const uint4& kr, const uint4& vr) {
+    *reinterpret_cast<uint4*>(&ktile[bf][wave * 1024 + lane * 16]) = kr;
+    *reinterpret_cast<uint4*>(&vtile[bf][wave * 1024 + lane * 16]) = vr;
   };
+  // Loads in the tile loop are unconditional (clamped addresses): with no control flow around
+  // them the compiler's memory waits count exactly the loads still needed.
+  // The raw word is loaded a tile ahead; its validity select waits until the word is used.
+  auto mask_raw = [&](int kb0) -> uint32_t { return mbase[min(kb0 + col, p.S - 1)]; };
   // Operand read offsets (bytes) within a tile.
   uint32_t koff[HPW][4], voff[HPW][2][2];
 #pragma unroll
@@ -306,16 +360,29 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
     return en;
   };
 
-  issue(0, 0);
-  uint32_t wnext = mask_word(0);
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's tile loads have landed
+  // Iteration n: tile n + 1 goes from registers to LDS buffer (n + 1) & 1 (last read in
+  // iteration n - 1), tile n + 3 is loaded into registers, tile n is computed from buffer
+  // n & 1; one barrier per tile. The wave's private LDS needs no barrier (one wave).
+  const int ntiles = (p.S + 31) / 32;
+  // Tiles n + 1 and n + 2 are in flight in two register pairs that alternate by iteration
+  // (no register copies, which would wait for the loads).
+  uint4 kra, vra, krb, vrb;
+  {
+    uint4 k0r, v0r;
+    gload(0, k0r, v0r);
+    lstore(0, k0r, v0r);
+  }
+  if (ntiles > 1) gload(32, kra, vra);
+  if (ntiles > 2) gload(64, krb, vrb);
+  uint32_t wraw = mask_raw(0);
   __syncthreads();
-  int buf = 0;
-  for (int k0 = 0; k0 < p.S; k0 += 32) {
-    const bool more = k0 + 32 < p.S;
-    if (more) issue(k0 + 32, buf ^ 1);
-    const uint32_t w = wnext;
-    if (more) wnext = mask_word(k0 + 32);
+  auto tile = [&](int n, uint4& kr, uint4& vr) {
+    const int k0 = n * 32;
+    const int buf = n & 1;
+    lstore(buf ^ 1, kr, vr);                   // past the last tile: never read
+    gload(min(k0 + 96, (ntiles - 1) * 32), kr, vr);
+    const uint32_t wnext = mask_raw(k0 + 32);  // past the last tile: unused
+    const uint32_t w = (active && k0 + col < p.S) ? wraw : 0u;
     // This lane's rows 8g + 4*half + i (g, i < 4) are bits 8g + 4*half + i of w; bit r of
     // m16 is accumulator element r.
     const uint32_t xw = w >> (4 * half);
@@ -332,7 +399,7 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
         uint32_t mm = m16;
         while (__ballot(mm != 0u) != 0ull) {
           const bool has = mm != 0u;
-          elist[has ? at : 1024 + lane] = ((__ffs(mm) - 1) << 6) | lane;
+          elist[has ? at : 1024 + lane] = (uint16_t)(((__ffs(mm) - 1) << 6) | lane);
           at += has ? 1 : 0;
           mm &= mm - 1u;
         }
@@ -340,11 +407,18 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
       lds_fence();
       const Ent e0 = decode(lane, nsel);  // entries 0..63; later chunks are decoded on the fly
 
+      // Both heads' score products first: head 1's MFMAs run while head 0's softmax does.
+      f32x16 sacc[HPW];
 #pragma unroll
       for (int hh = 0; hh < HPW; ++hh) {
-        f32x16 s = f32x16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        sacc[hh] = f32x16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) s = mma(E{}, a[hh][ks], *reinterpret_cast<const uint4*>(kt + koff[hh][ks]), s);
+        for (int ks = 0; ks < 4; ++ks)
+          sacc[hh] = mma(E{}, a[hh][ks], *reinterpret_cast<const uint4*>(kt + koff[hh][ks]), sacc[hh]);
+      }
+#pragma unroll
+      for (int hh = 0; hh < HPW; ++hh) {
+        const f32x16 s = sacc[hh];
 #pragma unroll
         for (int g = 0; g < 4; ++g)
           *reinterpret_cast<float4*>(&stage[(g * 64 + lane) * 4]) = make_float4(s[4 * g], s[4 * g + 1], s[4 * g + 2], s[4 * g + 3]);
@@ -353,9 +427,14 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
         // A row's reference maximum moves only when one of its own entries of this tile
         // exceeds it by more than kLazy, and then to the largest such entry: every row's
         // arithmetic is independent of the other rows of the block (and of the chunking).
-        auto needs = [&](const Ent& en) { return stage[en.sa] * sl2 > mrow[hh][en.row] + kLazy; };
-        bool lift = __ballot(needs(e0)) != 0ull;
-        for (int c0 = 64; c0 < nsel; c0 += 64) lift |= __ballot(needs(decode(c0 + lane, nsel))) != 0ull;
+        // Entries 0..63 keep their score and maximum in registers.
+        const float t0 = stage[e0.sa] * sl2;
+        float mo0 = mrow[hh][e0.row];
+        bool lift = __ballot(t0 > mo0 + kLazy) != 0ull;
+        for (int c0 = 64; c0 < nsel; c0 += 64) {
+          const Ent en = decode(c0 + lane, nsel);
+          lift |= __ballot(stage[en.sa] * sl2 > mrow[hh][en.row] + kLazy) != 0ull;
+        }
         if (lift) {
           if (lane < 32) mx[lane] = f2key(mrow[hh][lane]);
           lds_fence();
@@ -387,31 +466,32 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
               acc[hh][1][4 * g + i] *= alv[i];
             }
           }
+          mo0 = mrow[hh][e0.row];
         }
-        auto emit = [&](const Ent& en) { ptile[en.pa] = fexp2(stage[en.sa] * sl2 - mrow[hh][en.row]); };
-        emit(e0);
-        for (int c0 = 64; c0 < nsel; c0 += 64) emit(decode(c0 + lane, nsel));
+        auto emit = [&](int pa_, float t, float mo) {
+          const float pv = fexp2(t - mo);
+          const uint16_t hb = to_half_bits(E{}, pv);
+          phi[pa_] = hb;
+          plo[pa_] = to_half_bits(E{}, pv - from_half_bits(E{}, hb));  // exact difference
+        };
+        emit(e0.pa, t0, mo0);
+        for (int c0 = 64; c0 < nsel; c0 += 64) {
+          const Ent en = decode(c0 + lane, nsel);
+          emit(en.pa, stage[en.sa] * sl2, mrow[hh][en.row]);
+        }
         lds_fence();
-        // P enters the P·V product as hi + lo 16-bit parts (p - hi is exact in fp32), so the
-        // weights carry ~16 significant bits, as close to the fp32 p of the gather kernel as
-        // two products allow.
+        // P enters the P·V product as its hi and lo parts: two products, weights with ~16
+        // significant bits, close to the fp32 p of the gather kernel.
         uint4 pa[2], pl[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          const float4 x0 = *reinterpret_cast<const float4*>(&ptile[col * kPRow + ks * 16 + half * 8]);
-          const float4 x1 = *reinterpret_cast<const float4*>(&ptile[col * kPRow + ks * 16 + half * 8 + 4]);
-          lpart[hh] += ((x0.x + x0.y) + (x0.z + x0.w)) + ((x1.x + x1.y) + (x1.z + x1.w));
-          const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-          uint32_t hi[4], lo[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint16_t h0b = to_half_bits(E{}, x[2 * i]), h1b = to_half_bits(E{}, x[2 * i + 1]);
-            hi[i] = (uint32_t)h0b | ((uint32_t)h1b << 16);
-            lo[i] = pack_pair(E{}, x[2 * i] - from_half_bits(E{}, h0b), x[2 * i + 1] - from_half_bits(E{}, h1b));
-          }
-          pa[ks] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-          pl[ks] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+          pa[ks] = *reinterpret_cast<const uint4*>(&phi[col * kPRow + ks * 16 + half * 8]);
+          pl[ks] = *reinterpret_cast<const uint4*>(&plo[col * kPRow + ks * 16 + half * 8]);
         }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) lpart[hh] = sum8(E{}, pa[ks], lpart[hh]);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) lpart[hh] = sum8(E{}, pl[ks], lpart[hh]);
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
@@ -421,14 +501,28 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
             acc[hh][nb] = mma(E{}, pl[ks], vb, acc[hh][nb]);
           }
         // Clear the written P entries for the next use of the tile.
-        ptile[e0.pa] = 0.f;
-        for (int c0 = 64; c0 < nsel; c0 += 64) ptile[decode(c0 + lane, nsel).pa] = 0.f;
+        phi[e0.pa] = 0;
+        plo[e0.pa] = 0;
+        for (int c0 = 64; c0 < nsel; c0 += 64) {
+          const int pa_ = decode(c0 + lane, nsel).pa;
+          phi[pa_] = 0;
+          plo[pa_] = 0;
+        }
         lds_fence();
       }
     }
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next tile's loads of this wave landed
-    __syncthreads();                     // ... and every wave's; every wave is done with `buf`
-    buf ^= 1;
+    wraw = wnext;
+    // This wave's LDS writes of tile n + 1 are done; after the barrier every wave's are,
+    // and every wave is done with buffer n & 1 before it is refilled. No wait for the
+    // global loads in flight (a raw barrier, unlike __syncthreads).
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  for (int n = 0; n < ntiles; n += 2) {
+    tile(n, kra, vra);
+    if (n + 1 < ntiles) tile(n + 1, krb, vrb);
   }
   if (!active) return;
 
@@ -530,9 +624,15 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
   int* flags = reinterpret_cast<int*>(ws + L.flags);
   uint16_t* vt = reinterpret_cast<uint16_t*>(ws + L.vt);
 
-  hipLaunchKernelGGL(dense_mask_kernel, dim3(L.nqb, L.nchunk, (unsigned)B), dim3(256), 0, st, kv_pos, pos_stride_b,
-                     pos_stride_t, (int)T, (int)S, (int)K, L.nqb, L.nchunk, mask, flags);
-  GW_HIP_LAUNCH_CHECK("dense_mask_kernel launch");
+  {
+    const int vec = (K % 4 == 0 && pos_stride_t % 4 == 0 && pos_stride_b % 4 == 0 &&
+                     (reinterpret_cast<uintptr_t>(kv_pos) & 15) == 0)
+                        ? 1
+                        : 0;
+    hipLaunchKernelGGL(dense_mask_kernel, dim3(L.nqb, L.nchunk, (unsigned)B), dim3(256), 0, st, kv_pos, pos_stride_b,
+                       pos_stride_t, (int)T, (int)S, (int)K, L.nqb, L.nchunk, vec, mask, flags);
+    GW_HIP_LAUNCH_CHECK("dense_mask_kernel launch");
+  }
   hipLaunchKernelGGL(dense_vt_kernel, dim3(L.spad / 64, (unsigned)H, (unsigned)B), dim3(256), 0, st,
                      static_cast<const uint16_t*>(v), v_strides[0], v_strides[1], v_strides[2], (int)S, L.spad,
                      (int)H, vt);

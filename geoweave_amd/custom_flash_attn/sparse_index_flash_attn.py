@@ -96,7 +96,7 @@ def _check_inputs(q, k, v, kv_positions, bias, causal, layout):
 # when a query selects at least 1 / DENSE_MAX_RATIO of the keys, "dense" / "gather" force
 # one path (tests and measurements).
 FORWARD_PATH = "auto"
-DENSE_MAX_RATIO = 96
+DENSE_MAX_RATIO = 48
 
 
 def _use_dense(seqlen_k: int, num_kv: int, nheads: int, d: int) -> bool:
