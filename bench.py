@@ -12,9 +12,12 @@ config "Metric row": B = 1, S = 32 views x 1374 tokens (N = 43,968), 16 heads x 
 indexer 4 heads x 64, top-k 1024, bf16.
 
 Printed: ONE JSON line. ``value`` = indexer ms + attention-forward ms per layer (lower is
-better), ``roofline`` = the attention forward (the dominant kernel) against the HBM
-roofline on its algorithmic gathered K/V bytes, timed live with HIP events on the stream
-the kernel runs on, ``roofline_indexer`` = the indexer against the bf16 MFMA roofline,
+better), ``roofline`` = the attention forward (the dominant kernels) against the HBM
+roofline on the algorithmic bytes of the sparse attention (the gathered K/V rows), timed
+live with HIP events on the stream the kernels run on, ``roofline_dense_mfma`` = the same
+call against the bf16 MFMA roofline on the flops of its masked dense formulation (every
+(query, key) product: 4*B*T*S*H*D), ``roofline_indexer`` = the indexer against the bf16
+MFMA roofline,
 ``cpu_baseline`` = the fp32 CPU oracle (the restatement of the reference's torch backend)
 on a bounded sample of query rows of the same layer, scaled to the full layer.
 """
@@ -42,6 +45,13 @@ def attn_fwd_algorithmic_bytes(B, T, H, D, K, elt=2):
     """Gathered K and V rows (K per query, shared by the H heads) + q read + o write +
     int32 positions: B*T*K*H*D*2*elt + 2*B*T*H*D*elt + 4*B*T*K."""
     return B * T * K * H * D * 2 * elt + 2 * B * T * H * D * elt + 4 * B * T * K
+
+
+def attn_fwd_dense_flops(B, T, S, H, D):
+    """4 * B * T * S * H * D: the Q.K^T and P.V products over every (query, key) pair of the
+    masked dense formulation (the hi/lo split of P, which doubles the P.V instructions, is
+    not counted)."""
+    return 4 * B * T * S * H * D
 
 
 def indexer_algorithmic_flops(B, T, S, Hi, Di):
@@ -535,6 +545,9 @@ def main() -> int:
     ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer (projection + glue) timing")
     ap.add_argument("--no-c5", action="store_true", help="skip the C5 (full aggregator) timing")
     ap.add_argument("--no-sd", action="store_true", help="skip the approximate (source-downsample) top-k timing")
+    ap.add_argument("--attn-path", choices=("auto", "dense", "gather"), default="auto",
+                    help="attention forward without attn_sum: the masked dense pass, the gather kernel, "
+                         "or the automatic choice (dense when S <= 48 K)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run 3 plain device copies of 1 GiB (reference kernel for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE scaling)")
@@ -552,11 +565,13 @@ def main() -> int:
     from geoweave_amd.custom_flash_attn.sparse_index_flash_attn import (
         sparse_index_flash_attn_inference_func,
     )
+    from geoweave_amd.custom_flash_attn import sparse_index_flash_attn as sifa
     from geoweave_amd.custom_indexer import sparse_topk_indexer_inference_func
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU (MI355X)", file=sys.stderr)
         return 2
+    sifa.FORWARD_PATH = args.attn_path
     dev = torch.device("cuda", 0)
     props = torch.cuda.get_device_properties(dev)
 
@@ -609,8 +624,12 @@ def main() -> int:
     att_avg = statistics.mean(att_ms)
     idx_avg = statistics.mean(idx_ms)
     att_gbs = att_bytes / (att_avg * 1e-3) / 1e9
+    dense_flops = attn_fwd_dense_flops(B, T, T, H, D)
+    dense_tflops = dense_flops / (att_avg * 1e-3) / 1e12
     idx_tflops = idx_flops / (idx_avg * 1e-3) / 1e12
-    traffic = read_traffic_summary(REPO / "profiles" / f"sparse_attn_fwd_S{views}_pmc.md")
+    dense_used = sifa._use_dense(T, Kk, H, D)
+    prof_name = f"dense_attn_fwd_S{views}_pmc.md" if dense_used else f"sparse_attn_fwd_S{views}_pmc.md"
+    traffic = read_traffic_summary(REPO / "profiles" / prof_name)
 
     extra = {}
     if args.with_attn_sum:
@@ -647,8 +666,10 @@ def main() -> int:
         },
         "indexer_ms": round(idx_avg, 3),
         "attn_fwd_ms": round(att_avg, 3),
+        "attn_path": "dense" if dense_used else "gather",
         "roofline": {
-            "kernel": "sparse_attn_fwd_kernel",
+            "kernel": ("dense_attn_kernel (+ dense_mask_kernel, dense_vt_kernel: one attention call)"
+                       if dense_used else "sparse_attn_fwd_kernel"),
             "bound": "hbm",
             "achieved": round(att_gbs, 1),
             "peak": HBM_PEAK_GBS,
@@ -656,6 +677,15 @@ def main() -> int:
             "frac": round(att_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "algorithmic_bytes": att_bytes,
+        },
+        "roofline_dense_mfma": None if not dense_used else {
+            "kernel": "dense_attn_kernel (+ dense_mask_kernel, dense_vt_kernel: one attention call)",
+            "bound": "mfma",
+            "achieved": round(dense_tflops, 2),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(dense_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "dense_flops": dense_flops,
         },
         "roofline_indexer": {
             "kernels": "indexer_score_kernel<sample>+select<tau>+score<filter>+select<final>+fallback",

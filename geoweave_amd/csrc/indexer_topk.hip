@@ -883,7 +883,7 @@ int choose_nsplit(int64_t tiles, int64_t S, int slots, bool sample) {
   if (!sample) return 1;
   int best = 1;
   double best_eff = -1.0;
-  for (int ns = 1; ns <= kMaxSplit; ns <<= 1) {
+  for (int ns = 1; ns <= kMaxSplit; ++ns) {
     if (ns > 1 && S / (ns * (int64_t)kBN) < 8) break;
     const double waves = (double)(tiles * ns) / slots;
     const double eff = waves / ceil(waves);
