@@ -220,7 +220,7 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
 
 constexpr int kDW = 8;      // waves (32-query blocks) per workgroup, sharing each K/V tile
-constexpr int kPRow = 40;   // 16-bit elements per P-tile row (32 keys + padding: 80 bytes)
+constexpr int kPElems = 32 * 32 + 64;  // P tile (32 rows x 32 keys, 16-bit) + dummy slots
 
 // K tile: 32 keys x (2 heads x 64) bf16 = 32 rows of 256 bytes; the 16-byte chunk c of key
 // row kl sits at position c ^ (kl & 15). V^T tile: 128 rows (head, d) x 32 keys = 128 rows of
@@ -229,19 +229,18 @@ constexpr int kPRow = 40;   // 16-bit elements per P-tile row (32 keys + padding
 template <typename E>
 __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams p) {
   constexpr int HPW = kDHpw;
-  __shared__ __align__(16) uint8_t ktile[2][8192];
-  __shared__ __align__(16) uint8_t vtile[2][8192];
+  __shared__ __align__(16) uint8_t ktile[4][8192];  // ring of 4 tiles: tile t in buffer t % 4
+  __shared__ __align__(16) uint8_t vtile[4][8192];
   // Per wave: the S tile staged as float4 groups, lane-contiguous (element r of lane l at
   // ((r >> 2) * 64 + l) * 4 + (r & 3)); P as two 16-bit tiles hi and lo (p = hi + lo to
-  // ~16 significant bits) with padded rows; the compacted entry list. Lanes without an
-  // entry use dummy slots, so no per-entry step needs a branch: row 32 (m = +inf there, so
-  // p = 0), P slot kPRow * 32 + lane, list slot 1024 + lane.
+  // ~16 significant bits), rows of 64 bytes with XOR-swizzled 16-byte chunks; the compacted
+  // entry list. Lanes without an entry use dummy slots, so no per-entry step needs a branch:
+  // row 32 (m = +inf there, so p = 0), P slot 1024 + lane, list slot 1024 + lane.
   __shared__ __align__(16) float stage_all[kDW][16 * 64];
-  __shared__ __align__(16) uint16_t phi_all[kDW][kPRow * 32 + 64];
-  __shared__ __align__(16) uint16_t plo_all[kDW][kPRow * 32 + 64];
+  __shared__ __align__(16) uint16_t phi_all[kDW][kPElems];
+  __shared__ __align__(16) uint16_t plo_all[kDW][kPElems];
   __shared__ uint16_t elist_all[kDW][32 * 32 + 64];
   __shared__ __align__(16) float mrow_all[kDW][HPW][36];
-  __shared__ __align__(16) float lrow_all[kDW][HPW][36];
   __shared__ __align__(16) float arow_all[kDW][32];
   __shared__ uint32_t mx_all[kDW][33];
 
@@ -252,7 +251,6 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
   uint16_t* plo = plo_all[wave];
   uint16_t* elist = elist_all[wave];
   float (*mrow)[36] = mrow_all[wave];
-  float (*lrow)[36] = lrow_all[wave];
   float* arow = arow_all[wave];
   uint32_t* mx = mx_all[wave];
 
@@ -292,10 +290,9 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) {
       mrow[hh][lane] = lane < 32 ? -INFINITY : INFINITY;
-      lrow[hh][lane] = 0.f;
     }
   }
-  for (int i = lane; i < (kPRow * 32 + 64) / 8; i += 64) {
+  for (int i = lane; i < kPElems / 8; i += 64) {
     reinterpret_cast<uint4*>(phi)[i] = make_uint4(0, 0, 0, 0);
     reinterpret_cast<uint4*>(plo)[i] = make_uint4(0, 0, 0, 0);
   }
@@ -356,31 +353,36 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
     const int row = tile_row(r, ln >> 5);
     en.sa = en.ok ? ((r >> 2) * 64 + ln) * 4 + (r & 3) : 0;
     en.row = en.ok ? row : 32;
-    en.pa = en.ok ? row * kPRow + (ln & 31) : kPRow * 32 + lane;
+    // P tile rows of 64 bytes, 16-byte chunk c of row rr at c ^ ((rr >> 2) & 3).
+    en.pa = en.ok ? row * 32 + ((((ln & 31) >> 3) ^ ((row >> 2) & 3)) << 3) + (ln & 7) : 1024 + lane;
     return en;
   };
 
-  // Iteration n: tile n + 1 goes from registers to LDS buffer (n + 1) & 1 (last read in
-  // iteration n - 1), tile n + 3 is loaded into registers, tile n is computed from buffer
-  // n & 1; one barrier per tile. The wave's private LDS needs no barrier (one wave).
+  // Tiles are processed in pairs with one workgroup barrier per pair. Tile t lives in LDS
+  // buffer t % 4. While computing tile t a wave writes tile t + 2 from registers into buffer
+  // (t + 2) % 4 (last read in the previous pair, before the last barrier) and loads tile
+  // t + 4 into the freed registers; the barrier after each pair makes the next pair's tiles
+  // visible. Two register pairs alternate by tile (no register copies, which would wait for
+  // the loads). The wave's private LDS needs no barrier (one wave).
   const int ntiles = (p.S + 31) / 32;
-  // Tiles n + 1 and n + 2 are in flight in two register pairs that alternate by iteration
-  // (no register copies, which would wait for the loads).
+  const int last = (ntiles - 1) * 32;
   uint4 kra, vra, krb, vrb;
   {
     uint4 k0r, v0r;
     gload(0, k0r, v0r);
     lstore(0, k0r, v0r);
+    gload(min(32, last), k0r, v0r);
+    lstore(1, k0r, v0r);
   }
-  if (ntiles > 1) gload(32, kra, vra);
-  if (ntiles > 2) gload(64, krb, vrb);
+  gload(min(64, last), kra, vra);
+  gload(min(96, last), krb, vrb);
   uint32_t wraw = mask_raw(0);
   __syncthreads();
-  auto tile = [&](int n, uint4& kr, uint4& vr) {
+  auto tile = [&](int n, uint4& kr, uint4& vr, bool pair_end) {
     const int k0 = n * 32;
-    const int buf = n & 1;
-    lstore(buf ^ 1, kr, vr);                   // past the last tile: never read
-    gload(min(k0 + 96, (ntiles - 1) * 32), kr, vr);
+    const int buf = n & 3;
+    lstore((n + 2) & 3, kr, vr);                // past the last tile: never read
+    gload(min(k0 + 128, last), kr, vr);
     const uint32_t wnext = mask_raw(k0 + 32);  // past the last tile: unused
     const uint32_t w = (active && k0 + col < p.S) ? wraw : 0u;
     // This lane's rows 8g + 4*half + i (g, i < 4) are bits 8g + 4*half + i of w; bit r of
@@ -485,8 +487,9 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
         uint4 pa[2], pl[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          pa[ks] = *reinterpret_cast<const uint4*>(&phi[col * kPRow + ks * 16 + half * 8]);
-          pl[ks] = *reinterpret_cast<const uint4*>(&plo[col * kPRow + ks * 16 + half * 8]);
+          const int pofs = col * 32 + (((2 * ks + half) ^ ((col >> 2) & 3)) << 3);
+          pa[ks] = *reinterpret_cast<const uint4*>(&phi[pofs]);
+          pl[ks] = *reinterpret_cast<const uint4*>(&plo[pofs]);
         }
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) lpart[hh] = sum8(E{}, pa[ks], lpart[hh]);
@@ -512,22 +515,25 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
       }
     }
     wraw = wnext;
-    // This wave's LDS writes of tile n + 1 are done; after the barrier every wave's are,
-    // and every wave is done with buffer n & 1 before it is refilled. No wait for the
-    // global loads in flight (a raw barrier, unlike __syncthreads).
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
+    if (pair_end) {
+      // This wave's LDS writes of the next pair's tiles are done; after the barrier every
+      // wave's are, and every wave is done with this pair's buffers before they are refilled.
+      // No wait for the global loads in flight (a raw barrier, unlike __syncthreads).
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    }
   };
   for (int n = 0; n < ntiles; n += 2) {
-    tile(n, kra, vra);
-    if (n + 1 < ntiles) tile(n + 1, krb, vrb);
+    tile(n, kra, vra, false);
+    if (n + 1 < ntiles) tile(n + 1, krb, vrb, true);
   }
   if (!active) return;
 
   // o = O / l, lse = (m + log2 l) ln 2; rows without any selected key give o = 0, lse = -inf.
   // l of row r = the shares of lanes r and r + 32.
+  float (*lrow)[32] = reinterpret_cast<float (*)[32]>(stage);  // the staging area is free now
 #pragma unroll
   for (int hh = 0; hh < HPW; ++hh) {
     if (half == 1) lrow[hh][col] = lpart[hh];
