@@ -1,7 +1,7 @@
 // Sparse-index attention forward as a masked dense pass on the matrix cores (gfx950, D = 64).
 //
 // The reference forms softmax(q·k_s)·v_s over the keys s each query selected by gathering
-// their K and V rows (sparse_index_flash_attn.py:196-262). For 16 heads of 64 a gathered
+// their K and V rows (_fwd_kernel, sparse_index_flash_attn.py:129-259). For 16 heads of 64 a gathered
 // (query, key) pair moves 4 KiB; when a query selects a few per cent of all keys (1,024 of
 // 43,968 at 32 views) computing every (query, key) product on the matrix cores costs less
 // than gathering the selected ones. This file does that: per tile of 32 queries x 32 keys,
@@ -11,8 +11,10 @@
 //
 // The softmax only runs on the selected pairs. Per tile the selected (row, key) entries are
 // compacted into a list once, shared by the wave's two heads; for each head the S tile is
-// staged in LDS, the listed scores are read back, exponentiated, summed per row with LDS
-// atomics and scattered into a zeroed P tile that feeds the P·V product.
+// staged in LDS, the listed scores are read back and exponentiated, and each p is written
+// as hi + lo 16-bit parts (p - hi is exact in fp32) into zeroed P tiles that feed two P·V
+// products, so the weights keep ~16 significant bits. Row sums are taken from the same P
+// operands (v_dot2 with ones), in a fixed order.
 //
 // Online softmax with a lazy reference maximum: a row's reference m is raised only when an
 // entry exceeds it by more than kLazy in the exp2 domain; O and the row sum are then rescaled.
@@ -215,9 +217,6 @@ __device__ __forceinline__ uint32_t pack_pair(BF16 e, float lo, float hi) {
 __device__ __forceinline__ uint32_t pack_pair(FP16 e, float lo, float hi) {
   return (uint32_t)to_half_bits(e, lo) | ((uint32_t)to_half_bits(e, hi) << 16);
 }
-
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glb_void_t;
 
 constexpr int kDW = 8;      // waves (32-query blocks) per workgroup, sharing each K/V tile
 constexpr int kPElems = 32 * 32 + 64;  // P tile (32 rows x 32 keys, 16-bit) + dummy slots
