@@ -3,12 +3,13 @@ fp32 CPU oracle and the gather kernel.
 
 The dense pass computes every (query, key) product on the matrix cores and masks the keys a
 query did not select; o and lse must equal the sparse attention's. Tolerance: 2e-2 abs/rel for
-bf16/fp16 outputs (P enters the P·V product in the input dtype, as the gather kernel's fp32 p
-does not: both are within the bar), 1e-4 for lse. Cases: the layer's per-view shape in bf16
-and fp16, ragged -1 padding with T and S not multiples of 32 or 64, cross attention (T != S),
-empty rows, out-of-range and repeated positions (repeats go to the gather kernel inside the
-call), scores with a large dynamic range rising along the key order (the lazy maximum is raised
-and O rescaled on many tiles), bhtd strides, determinism, and a full-size layer on sampled rows.
+bf16/fp16 outputs (P enters the P·V product as hi + lo 16-bit parts, close to the gather
+kernel's fp32 p), 1e-4 for lse. Cases: the layer's per-view shape in bf16 and fp16, ragged -1
+padding with T and S not multiples of 32 or 64, cross attention (T != S), empty rows,
+out-of-range and repeated positions (repeats go to the gather kernel inside the call, also
+when the mask is built in several key chunks), scores with a large dynamic range rising along
+the key order (the lazy maximum is raised and O rescaled on many tiles), bhtd strides,
+determinism, and a full-size layer on sampled rows.
 """
 import contextlib
 
@@ -146,3 +147,21 @@ def test_full_size_sampled_rows(gpu_device, views):
     ro, _, rl = oatt.sparse_attention(q[:, rows], k, v, pos[:, rows])
     torch.testing.assert_close(o[:, rows], ro, **TOL)
     torch.testing.assert_close(lse[:, rows], rl, atol=1e-4, rtol=1e-4)
+
+
+def test_repeated_position_in_an_upper_key_chunk(gpu_device):
+    # S > 16,384: the mask is built in several key chunks; a repeat in the last chunk flags
+    # its block like one in the first, and the gather kernel computes that block.
+    T, S, H, K = 80, 40000, 2, 256
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn(1, T, H, 64, generator=g).bfloat16()
+    k = torch.randn(1, S, H, 64, generator=g).bfloat16()
+    v = torch.randn(1, S, H, 64, generator=g).bfloat16()
+    pos = _distinct_positions(1, T, S, K, seed=32)
+    pos[0, 40, 7] = 39999
+    pos[0, 40, 8] = 39999      # block 1 (rows 32..63): repeat in chunk 2
+    pos[0, 75, :5] = 20000     # block 2: five copies in chunk 1
+    o, lse = _run(q, k, v, pos)
+    ro, _, rl = oatt.sparse_attention(q, k, v, pos)
+    torch.testing.assert_close(o, ro, **TOL)
+    torch.testing.assert_close(lse, rl, atol=1e-4, rtol=1e-4)
