@@ -30,4 +30,4 @@ int hip_error(hipError_t err, const char* what) {
 
 extern "C" const char* gw_last_error(void) { return gw::g_last_error.c_str(); }
 
-extern "C" int gw_abi_version(void) { return 104; }
+extern "C" int gw_abi_version(void) { return 105; }

@@ -37,6 +37,7 @@
 #include "gw_attn.h"
 #include "gw_common.h"
 #include "gw_select.h"
+#include "gw_sort.h"
 
 namespace gw {
 namespace {
@@ -171,6 +172,11 @@ struct DenseParams {
   int64_t osb, ost, osh;
   int T, S, Spad, H, nqb, nchunk;
   float scale_log2;
+  // attn_sum (ATTN kernels only): the scaled score of every selected (query, key) and head,
+  // sws[((b * T + t) * K + slot) * H + h], slot = rank of the key among the query's
+  // selected keys in ascending key order.
+  float* sws;
+  int K;
 };
 
 // The attention runs one wave per workgroup. LDS operations of a wave are performed in
@@ -225,11 +231,19 @@ constexpr int kPElems = 32 * 32 + 64;  // P tile (32 rows x 32 keys, 16-bit) + d
 // row kl sits at position c ^ (kl & 15). V^T tile: 128 rows (head, d) x 32 keys = 128 rows of
 // 64 bytes; chunk c of row rr sits at c ^ ((rr >> 2) & 3). Both layouts make the MFMA operand
 // reads (32 consecutive rows at one chunk) touch distinct bank groups within 16 lanes.
-template <typename E>
+template <typename E, bool ATTN>
 __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams p) {
   constexpr int HPW = kDHpw;
-  __shared__ __align__(16) uint8_t ktile[4][8192];  // ring of 4 tiles: tile t in buffer t % 4
-  __shared__ __align__(16) uint8_t vtile[4][8192];
+  // Ring of kRing K/V tiles (tile t in buffer t % kRing), one barrier per kDist tiles. With
+  // attn_sum the per-wave slot arrays need the LDS of two ring buffers: two tiles, a barrier
+  // per tile.
+  constexpr int kRing = ATTN ? 2 : 4;
+  constexpr int kDist = kRing / 2;
+  __shared__ __align__(16) uint8_t ktile[kRing][8192];
+  __shared__ __align__(16) uint8_t vtile[kRing][8192];
+  // attn_sum: per wave, each listed entry's slot and the rows' running slot counts.
+  __shared__ uint16_t eslot_all[ATTN ? kDW : 1][ATTN ? 32 * 32 + 64 : 1];
+  __shared__ uint32_t rcnt_all[ATTN ? kDW : 1][ATTN ? 33 : 1];
   // Per wave: the S tile staged as float4 groups, lane-contiguous (element r of lane l at
   // ((r >> 2) * 64 + l) * 4 + (r & 3)); P as two 16-bit tiles hi and lo (p = hi + lo to
   // ~16 significant bits), rows of 64 bytes with XOR-swizzled 16-byte chunks; the compacted
@@ -252,6 +266,8 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
   float (*mrow)[36] = mrow_all[wave];
   float* arow = arow_all[wave];
   uint32_t* mx = mx_all[wave];
+  uint16_t* eslot = eslot_all[ATTN ? wave : 0];
+  uint32_t* rcnt = rcnt_all[ATTN ? wave : 0];
 
   const int nhg = p.H / HPW;
   const int hg = blockIdx.x % nhg;  // consecutive workgroups (different XCDs) take different heads
@@ -290,6 +306,7 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
     for (int hh = 0; hh < HPW; ++hh) {
       mrow[hh][lane] = lane < 32 ? -INFINITY : INFINITY;
     }
+    if constexpr (ATTN) rcnt[lane] = 0u;
   }
   for (int i = lane; i < kPElems / 8; i += 64) {
     reinterpret_cast<uint4*>(phi)[i] = make_uint4(0, 0, 0, 0);
@@ -357,31 +374,35 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
     return en;
   };
 
-  // Tiles are processed in pairs with one workgroup barrier per pair. Tile t lives in LDS
-  // buffer t % 4. While computing tile t a wave writes tile t + 2 from registers into buffer
-  // (t + 2) % 4 (last read in the previous pair, before the last barrier) and loads tile
-  // t + 4 into the freed registers; the barrier after each pair makes the next pair's tiles
-  // visible. Two register pairs alternate by tile (no register copies, which would wait for
-  // the loads). The wave's private LDS needs no barrier (one wave).
+  // Tile t lives in LDS buffer t % kRing. While computing tile t a wave writes tile
+  // t + kDist from registers into buffer (t + kDist) % kRing (last read before the last
+  // barrier) and loads tile t + 2 kDist into the freed registers; the barrier after every
+  // kDist tiles makes the next tiles visible. kDist register sets alternate by tile (no
+  // register copies, which would wait for the loads). The wave's private LDS needs no
+  // barrier (one wave).
   const int ntiles = (p.S + 31) / 32;
   const int last = (ntiles - 1) * 32;
+  // Staging registers: named variables (an array of them indexed through the tile calls
+  // would live in scratch memory).
   uint4 kra, vra, krb, vrb;
   {
     uint4 k0r, v0r;
     gload(0, k0r, v0r);
     lstore(0, k0r, v0r);
-    gload(min(32, last), k0r, v0r);
-    lstore(1, k0r, v0r);
+    if constexpr (kDist == 2) {
+      gload(min(32, last), k0r, v0r);
+      lstore(1, k0r, v0r);
+    }
   }
-  gload(min(64, last), kra, vra);
-  gload(min(96, last), krb, vrb);
+  gload(min(32 * kDist, last), kra, vra);
+  if constexpr (kDist == 2) gload(min(96, last), krb, vrb);
   uint32_t wraw = mask_raw(0);
   __syncthreads();
-  auto tile = [&](int n, uint4& kr, uint4& vr, bool pair_end) {
+  auto tile = [&](int n, uint4& kr, uint4& vr, bool sync_after) {
     const int k0 = n * 32;
-    const int buf = n & 3;
-    lstore((n + 2) & 3, kr, vr);                // past the last tile: never read
-    gload(min(k0 + 128, last), kr, vr);
+    const int buf = n & (kRing - 1);
+    lstore((n + kDist) & (kRing - 1), kr, vr);  // past the last tile: never read
+    gload(min(k0 + 64 * kDist, last), kr, vr);
     const uint32_t wnext = mask_raw(k0 + 32);  // past the last tile: unused
     const uint32_t w = (active && k0 + col < p.S) ? wraw : 0u;
     // This lane's rows 8g + 4*half + i (g, i < 4) are bits 8g + 4*half + i of w; bit r of
@@ -407,6 +428,15 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
       }
       lds_fence();
       const Ent e0 = decode(lane, nsel);  // entries 0..63; later chunks are decoded on the fly
+      if constexpr (ATTN) {
+        // Slots in ascending key order per row: the list is in key order and one atomic's
+        // lanes are served in lane order.
+        for (int c0 = 0; c0 < nsel; c0 += 64) {
+          const Ent en = c0 == 0 ? e0 : decode(c0 + lane, nsel);
+          if (en.ok) eslot[c0 + lane] = (uint16_t)atomicAdd(&rcnt[en.row], 1u);
+        }
+        lds_fence();
+      }
 
       // Both heads' score products first: head 1's MFMAs run while head 0's softmax does.
       f32x16 sacc[HPW];
@@ -480,6 +510,16 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
           const Ent en = decode(c0 + lane, nsel);
           emit(en.pa, stage[en.sa] * sl2, mrow[hh][en.row]);
         }
+        if constexpr (ATTN) {
+          auto keep = [&](const Ent& en, int i, float t) {
+            if (en.ok) p.sws[(((int64_t)b * p.T + q0 + en.row) * p.K + eslot[i]) * p.H + h0 + hh] = t;
+          };
+          keep(e0, lane, t0);
+          for (int c0 = 64; c0 < nsel; c0 += 64) {
+            const Ent en = decode(c0 + lane, nsel);
+            keep(en, c0 + lane, stage[en.sa] * sl2);
+          }
+        }
         lds_fence();
         // P enters the P·V product as its hi and lo parts: two products, weights with ~16
         // significant bits, close to the fp32 p of the gather kernel.
@@ -514,7 +554,7 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
       }
     }
     wraw = wnext;
-    if (pair_end) {
+    if (sync_after) {
       // This wave's LDS writes of the next pair's tiles are done; after the barrier every
       // wave's are, and every wave is done with this pair's buffers before they are refilled.
       // No wait for the global loads in flight (a raw barrier, unlike __syncthreads).
@@ -524,9 +564,13 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
       asm volatile("" ::: "memory");
     }
   };
-  for (int n = 0; n < ntiles; n += 2) {
-    tile(n, kra, vra, false);
-    if (n + 1 < ntiles) tile(n + 1, krb, vrb, true);
+  if constexpr (kDist == 2) {
+    for (int n = 0; n < ntiles; n += 2) {
+      tile(n, kra, vra, false);
+      if (n + 1 < ntiles) tile(n + 1, krb, vrb, true);
+    }
+  } else {
+    for (int n = 0; n < ntiles; ++n) tile(n, kra, vra, true);
   }
   if (!active) return;
 
@@ -565,12 +609,131 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// attn_sum from the slot-indexed scores: one wave per query row. The row's valid positions,
+// sorted ascending, are in slot order: slot i holds the i-th smallest selected key. So
+// attn_sum[t, j] = sum_h exp2(sws[t, i(j), h] - lse2[t, h]) with i(j) the rank of position j
+// (a wave bitonic sort of (position, j)); invalid positions give 0. With KL, the row's
+// indexer KL loss follows from the same registers (the per-row term of
+// sparse_indexer_kl_loss, indexer_kl_fused.py:8-155, as in the gather kernel's epilogue).
+// Rows of blocks flagged for a repeated position were computed by the gather kernel.
+// ---------------------------------------------------------------------------------------
+struct AttnSumParams {
+  const int32_t* pos;
+  int64_t psb, pst;
+  const float* sws;
+  const float* lse;  // natural log, [B, T, H]
+  const int* flags;
+  float* attn_sum;   // [B, T, K]
+  const void* logits;
+  int logits_dt;
+  int64_t lsb, lst;
+  float kl_eps;
+  float* row_loss;
+  int B, T, S, H, K, nqb, nchunk;
+};
+
+__device__ __forceinline__ float as_load(int dt, const void* base, int64_t i) {
+  if (dt == GW_DTYPE_FP32) return static_cast<const float*>(base)[i];
+  const uint32_t u = static_cast<const uint16_t*>(base)[i];
+  if (dt == GW_DTYPE_BF16) return __uint_as_float(u << 16);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)u);
+}
+
+__device__ __forceinline__ float as_wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+__device__ __forceinline__ float as_wave_max(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+  return x;
+}
+
+template <int R, bool KL>
+__global__ __launch_bounds__(256) void dense_attn_sum_kernel(const AttnSumParams p) {
+  __shared__ float lse2_s[4][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= (int64_t)p.B * p.T) return;  // whole wave; no barriers below
+  const int b = (int)(row / p.T), t = (int)(row - (int64_t)b * p.T);
+  {
+    const int* f = p.flags + ((int64_t)b * p.nqb + (t >> 5)) * p.nchunk;
+    bool flagged = false;
+    for (int c = 0; c < p.nchunk; ++c) flagged |= f[c] != 0;
+    if (flagged) return;
+  }
+  if (lane < p.H) lse2_s[wave][lane] = p.lse[row * p.H + lane] * kDLog2e;
+  const int32_t* prow = p.pos + b * p.psb + (int64_t)t * p.pst;
+  uint64_t key[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int j = r * 64 + lane;
+    const int32_t ps = j < p.K ? prow[j] : -1;
+    const bool ok = ps >= 0 && ps < p.S;
+    // invalid positions (and padding past K) sort last, after every valid key
+    key[r] = ((uint64_t)(ok ? (uint32_t)ps : 0xFFFFFFFFu) << 32) | (uint32_t)j;
+  }
+  wave_bitonic_sort<R>(key);
+  lds_fence();
+  const float* srow = p.sws + row * (int64_t)p.K * p.H;
+  float av[R], zv[R];
+  float sa = 0.f, mz = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * 64 + lane;  // slot = sorted rank
+    const int j = (int)(uint32_t)key[r];
+    const bool ok = (key[r] >> 32) != 0xFFFFFFFFull;
+    float sum = 0.f;
+    if (ok) {
+      const float* sp = srow + (int64_t)i * p.H;
+      for (int h = 0; h < p.H; ++h) {
+        const float l2 = lse2_s[wave][h];
+        if (l2 != -INFINITY) sum += fexp2(sp[h] - l2);
+      }
+    }
+    av[r] = sum;
+    zv[r] = -INFINITY;
+    if (j < p.K) {
+      p.attn_sum[row * p.K + j] = sum;
+      if constexpr (KL) {
+        zv[r] = as_load(p.logits_dt, p.logits, b * p.lsb + (int64_t)t * p.lst + j);
+        sa += sum;
+        mz = fmaxf(mz, zv[r]);
+      }
+    }
+  }
+  if constexpr (KL) {
+    sa = as_wave_sum(sa);
+    mz = as_wave_max(mz);
+    float se = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if ((int)(uint32_t)key[r] < p.K) se += expf(zv[r] - mz);
+    se = as_wave_sum(se);
+    const float lse = mz + logf(se);
+    const float denom = sa + p.kl_eps;
+    float acc = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if ((int)(uint32_t)key[r] < p.K) {
+        const float pj = av[r] / denom;
+        acc += pj * (logf(pj + p.kl_eps) - (zv[r] - lse));
+      }
+    }
+    acc = as_wave_sum(acc);
+    if (lane == 0) p.row_loss[row] = acc;
+  }
+}
+
 struct DenseLayout {
-  size_t mask, flags, vt, total;
+  size_t mask, flags, vt, sws, total;
   int nqb, nchunk, spad;
 };
 
-DenseLayout dense_layout(int64_t B, int64_t T, int64_t S, int64_t H) {
+DenseLayout dense_layout(int64_t B, int64_t T, int64_t S, int64_t H, int64_t K, bool attn) {
   DenseLayout L;
   L.nqb = (int)((T + 31) / 32);
   L.nchunk = (int)((S + kMaskChunk - 1) / kMaskChunk);
@@ -584,24 +747,51 @@ DenseLayout dense_layout(int64_t B, int64_t T, int64_t S, int64_t H) {
   o = up(o + (size_t)B * L.nqb * (size_t)L.nchunk * 4);
   L.vt = o;
   o = up(o + (size_t)B * (size_t)H * 64 * (size_t)L.spad * 2);
+  L.sws = o;
+  if (attn) o = up(o + (size_t)B * (size_t)T * (size_t)K * (size_t)H * 4);
   L.total = o;
   return L;
+}
+
+constexpr int kDenseAttnMaxK = 1024;  // attn_sum: a row's positions sorted in registers
+
+int pow2_at_least(int64_t x) {
+  int r = 1;
+  while (r < x) r <<= 1;
+  return r;
+}
+
+template <bool KL>
+int launch_attn_sum(const AttnSumParams& p, int rows, hipStream_t st) {
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  switch (pow2_at_least((p.K + 63) / 64)) {
+    case 1: hipLaunchKernelGGL((dense_attn_sum_kernel<1, KL>), grid, dim3(256), 0, st, p); break;
+    case 2: hipLaunchKernelGGL((dense_attn_sum_kernel<2, KL>), grid, dim3(256), 0, st, p); break;
+    case 4: hipLaunchKernelGGL((dense_attn_sum_kernel<4, KL>), grid, dim3(256), 0, st, p); break;
+    case 8: hipLaunchKernelGGL((dense_attn_sum_kernel<8, KL>), grid, dim3(256), 0, st, p); break;
+    default: hipLaunchKernelGGL((dense_attn_sum_kernel<16, KL>), grid, dim3(256), 0, st, p); break;
+  }
+  GW_HIP_LAUNCH_CHECK("dense_attn_sum_kernel launch");
+  return GW_OK;
 }
 
 }  // namespace
 }  // namespace gw
 
-extern "C" size_t gw_sparse_attn_fwd_dense_workspace_size(int64_t B, int64_t T, int64_t S, int64_t H, int64_t D) {
-  if (B <= 0 || T <= 0 || S <= 0 || H <= 0 || D != 64) return 0;
-  return gw::dense_layout(B, T, S, H).total;
+extern "C" size_t gw_sparse_attn_fwd_dense_workspace_size(int64_t B, int64_t T, int64_t S, int64_t H, int64_t D,
+                                                          int64_t K, int want_attn_sum) {
+  if (B <= 0 || T <= 0 || S <= 0 || H <= 0 || K <= 0 || D != 64) return 0;
+  return gw::dense_layout(B, T, S, H, K, want_attn_sum != 0).total;
 }
 
 extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t* q_strides, const void* k,
                                         const int64_t* k_strides, const void* v, const int64_t* v_strides,
                                         const int32_t* kv_pos, int64_t pos_stride_b, int64_t pos_stride_t,
-                                        void* o, const int64_t* o_strides, float* lse, int64_t B, int64_t T,
-                                        int64_t S, int64_t H, int64_t D, int64_t K, float softmax_scale,
-                                        void* workspace, size_t workspace_bytes, void* stream) {
+                                        void* o, const int64_t* o_strides, float* lse, float* attn_sum, int64_t B,
+                                        int64_t T, int64_t S, int64_t H, int64_t D, int64_t K, float softmax_scale,
+                                        const void* logits, int logits_dtype, int64_t logits_stride_b,
+                                        int64_t logits_stride_t, float eps, float* row_loss, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
   using namespace gw;
   clear_error();
   GW_CHECK_ARG(dtype == GW_DTYPE_BF16 || dtype == GW_DTYPE_FP16, "unsupported dtype code %d", dtype);
@@ -610,6 +800,11 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
   if (D != 64) return set_error(GW_ERR_UNSUPPORTED, "the dense forward needs head dim 64, got %lld", (long long)D);
   if (H % kDHpw != 0)
     return set_error(GW_ERR_UNSUPPORTED, "the dense forward needs an even head count, got %lld", (long long)H);
+  const bool want_attn = attn_sum != nullptr;
+  const bool want_kl = logits != nullptr;
+  if (want_attn && K > kDenseAttnMaxK)
+    return set_error(GW_ERR_UNSUPPORTED, "the dense forward computes attn_sum for K <= %d, got %lld", kDenseAttnMaxK,
+                     (long long)K);
   if (B == 0 || T == 0) return GW_OK;
   GW_CHECK_ARG(K >= 1 && S >= 1, "kv_positions must have at least one candidate and S >= 1");
   GW_CHECK_ARG(q && k && v && kv_pos && o, "null tensor pointer");
@@ -619,7 +814,15 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
     GW_CHECK_ARG(q_strides[i] % 8 == 0 && k_strides[i] % 8 == 0 && v_strides[i] % 8 == 0 && o_strides[i] % 8 == 0,
                  "b/t/h strides must be multiples of 8 elements");
   GW_CHECK_ARG(B <= 65535 && T < (1ll << 31) && S < (1ll << 30) && K < (1ll << 31), "size exceeds the grid range");
-  const DenseLayout L = dense_layout(B, T, S, H);
+  GW_CHECK_ARG(!want_kl || want_attn, "the fused KL loss needs attn_sum");
+  GW_CHECK_ARG(!want_attn || lse != nullptr, "attn_sum needs the lse output");
+  if (want_kl) {
+    GW_CHECK_ARG(row_loss != nullptr, "null row_loss pointer");
+    GW_CHECK_ARG(logits_dtype == GW_DTYPE_BF16 || logits_dtype == GW_DTYPE_FP16 || logits_dtype == GW_DTYPE_FP32,
+                 "unsupported logits dtype code %d", logits_dtype);
+    GW_CHECK_ARG(eps >= 0.f, "eps must be non-negative, got %g", (double)eps);
+  }
+  const DenseLayout L = dense_layout(B, T, S, H, K, want_attn);
   GW_CHECK_ARG((int64_t)L.nqb * (H / kDHpw) < (1ll << 31), "too many query blocks");
   GW_CHECK_ARG(workspace != nullptr && workspace_bytes >= L.total && aligned16(workspace),
                "the dense forward needs a 16-byte aligned %zu-byte workspace, got %zu", L.total, workspace_bytes);
@@ -628,6 +831,7 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
   uint32_t* mask = reinterpret_cast<uint32_t*>(ws + L.mask);
   int* flags = reinterpret_cast<int*>(ws + L.flags);
   uint16_t* vt = reinterpret_cast<uint16_t*>(ws + L.vt);
+  float* sws = want_attn ? reinterpret_cast<float*>(ws + L.sws) : nullptr;
 
   {
     const int vec = (K % 4 == 0 && pos_stride_t % 4 == 0 && pos_stride_b % 4 == 0 &&
@@ -661,13 +865,51 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
   p.nqb = L.nqb;
   p.nchunk = L.nchunk;
   p.scale_log2 = softmax_scale * kDLog2e;
+  p.sws = sws;
+  p.K = (int)K;
   const dim3 grid((unsigned)((L.nqb + kDW - 1) / kDW * (H / kDHpw)), (unsigned)B);
-  if (dtype == GW_DTYPE_BF16)
-    hipLaunchKernelGGL(dense_attn_kernel<BF16>, grid, dim3(kDW * 64), 0, st, p);
-  else
-    hipLaunchKernelGGL(dense_attn_kernel<FP16>, grid, dim3(kDW * 64), 0, st, p);
+  if (dtype == GW_DTYPE_BF16) {
+    if (want_attn)
+      hipLaunchKernelGGL((dense_attn_kernel<BF16, true>), grid, dim3(kDW * 64), 0, st, p);
+    else
+      hipLaunchKernelGGL((dense_attn_kernel<BF16, false>), grid, dim3(kDW * 64), 0, st, p);
+  } else {
+    if (want_attn)
+      hipLaunchKernelGGL((dense_attn_kernel<FP16, true>), grid, dim3(kDW * 64), 0, st, p);
+    else
+      hipLaunchKernelGGL((dense_attn_kernel<FP16, false>), grid, dim3(kDW * 64), 0, st, p);
+  }
   GW_HIP_LAUNCH_CHECK("dense_attn_kernel launch");
-  // Blocks with a repeated position: the gather kernel (it returns at once for the others).
+  if (want_attn) {
+    AttnSumParams ap;
+    ap.pos = kv_pos;
+    ap.psb = pos_stride_b;
+    ap.pst = pos_stride_t;
+    ap.sws = sws;
+    ap.lse = lse;
+    ap.flags = flags;
+    ap.attn_sum = attn_sum;
+    ap.logits = logits;
+    ap.logits_dt = logits_dtype;
+    ap.lsb = logits_stride_b;
+    ap.lst = logits_stride_t;
+    ap.kl_eps = eps;
+    ap.row_loss = row_loss;
+    ap.B = (int)B;
+    ap.T = (int)T;
+    ap.S = (int)S;
+    ap.H = (int)H;
+    ap.K = (int)K;
+    ap.nqb = L.nqb;
+    ap.nchunk = L.nchunk;
+    const int rows = (int)(B * T);
+    const int rc = want_kl ? launch_attn_sum<true>(ap, rows, st) : launch_attn_sum<false>(ap, rows, st);
+    if (rc != GW_OK) return rc;
+  }
+  // Blocks with a repeated position: the gather kernel (it returns at once for the others),
+  // with attn_sum and the KL loss when asked (its score workspace is the same region).
   return attn_fwd_flagged_blocks(dtype, q, q_strides, k, k_strides, v, v_strides, kv_pos, pos_stride_b, pos_stride_t,
-                                 o, o_strides, lse, B, T, S, H, D, K, softmax_scale, flags, L.nqb, L.nchunk, stream);
+                                 o, o_strides, lse, attn_sum, B, T, S, H, D, K, softmax_scale, logits, logits_dtype,
+                                 logits_stride_b, logits_stride_t, eps, row_loss, sws,
+                                 want_attn ? (size_t)B * T * K * H * 4 : 0, flags, L.nqb, L.nchunk, stream);
 }

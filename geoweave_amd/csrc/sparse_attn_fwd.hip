@@ -447,7 +447,6 @@ int attn_fwd_impl(int dtype, const void* q, const int64_t* q_strides, const void
   p.blk_flags = blk_flags;
   p.nqb = nqb;
   p.nchunk = nchunk;
-  GW_CHECK_ARG(blk_flags == nullptr || (!want_attn && kl == nullptr), "block flags need the plain forward");
   p.T = (int)T;
   p.S = (int)S;
   p.H = (int)H;
@@ -513,10 +512,13 @@ extern "C" int gw_sparse_attn_fwd_kl(int dtype, const void* q, const int64_t* q_
 int gw::attn_fwd_flagged_blocks(int dtype, const void* q, const int64_t* q_strides, const void* k,
                                 const int64_t* k_strides, const void* v, const int64_t* v_strides,
                                 const int32_t* kv_pos, int64_t pos_stride_b, int64_t pos_stride_t, void* o,
-                                const int64_t* o_strides, float* lse, int64_t B, int64_t T, int64_t S, int64_t H,
-                                int64_t D, int64_t K, float softmax_scale, const int* blk_flags, int nqb,
-                                int nchunk, void* stream) {
+                                const int64_t* o_strides, float* lse, float* attn_sum, int64_t B, int64_t T,
+                                int64_t S, int64_t H, int64_t D, int64_t K, float softmax_scale, const void* logits,
+                                int logits_dtype, int64_t logits_stride_b, int64_t logits_stride_t, float eps,
+                                float* row_loss, void* workspace, size_t workspace_bytes, const int* blk_flags,
+                                int nqb, int nchunk, void* stream) {
+  const gw::KlArgs kl{logits, logits_dtype, logits_stride_b, logits_stride_t, eps, row_loss};
   return gw::attn_fwd_impl(dtype, q, q_strides, k, k_strides, v, v_strides, kv_pos, pos_stride_b, pos_stride_t, o,
-                           o_strides, lse, nullptr, B, T, S, H, D, K, softmax_scale, nullptr, 0, nullptr, stream,
-                           blk_flags, nqb, nchunk);
+                           o_strides, lse, attn_sum, B, T, S, H, D, K, softmax_scale, workspace, workspace_bytes,
+                           logits != nullptr ? &kl : nullptr, stream, blk_flags, nqb, nchunk);
 }

@@ -92,11 +92,12 @@ def _check_inputs(q, k, v, kv_positions, bias, causal, layout):
     return batch, seqlen_q, seqlen_k, nheads, d
 
 
-# Forward without attn_sum: "auto" picks the masked dense pass (gw_sparse_attn_fwd_dense)
-# when a query selects at least 1 / DENSE_MAX_RATIO of the keys, "dense" / "gather" force
-# one path (tests and measurements).
+# Forward: "auto" picks the masked dense pass (gw_sparse_attn_fwd_dense) when a query
+# selects at least 1 / DENSE_MAX_RATIO of the keys (and, with attn_sum, K <=
+# DENSE_ATTN_SUM_MAX_K), "dense" / "gather" force one path (tests and measurements).
 FORWARD_PATH = "auto"
 DENSE_MAX_RATIO = 48
+DENSE_ATTN_SUM_MAX_K = 1024
 
 
 def _use_dense(seqlen_k: int, num_kv: int, nheads: int, d: int) -> bool:
@@ -142,13 +143,8 @@ def _flash_attn_forward(
     o = torch.empty(q.shape, device=q.device, dtype=q.dtype)
     lse = torch.empty((batch, seqlen_q, nheads), device=q.device, dtype=torch.float32)
     attn_sum = None
-    ws = None
-    ws_bytes = 0
     if return_attn:
         attn_sum = torch.empty((batch, seqlen_q, num_kv), device=q.device, dtype=torch.float32)
-        lib = _lib.load()
-        ws_bytes = int(lib.gw_sparse_attn_fwd_workspace_size(batch, seqlen_q, nheads, num_kv, 1))
-        ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
     if batch == 0 or seqlen_q == 0 or num_kv == 0:
         if attn_sum is not None:
             attn_sum.zero_()
@@ -167,20 +163,29 @@ def _flash_attn_forward(
         batch, seqlen_q, seqlen_k, nheads, d, num_kv,
         float(softmax_scale),
     )
-    if kl_logits is None and attn_sum is None and _use_dense(seqlen_k, num_kv, nheads, d):
-        dense_bytes = int(lib.gw_sparse_attn_fwd_dense_workspace_size(batch, seqlen_q, seqlen_k, nheads, d))
-        dws = torch.empty(max(dense_bytes, 1), device=q.device, dtype=torch.uint8)
-        rc = lib.gw_sparse_attn_fwd_dense(*common[:13], *common[14:], dws.data_ptr(), dense_bytes,
-                                          _lib.stream_handle(q.device))
-        _lib.check(rc, "gw_sparse_attn_fwd_dense")
-    elif kl_logits is None:
-        rc = lib.gw_sparse_attn_fwd(*common, _lib.ptr(ws), ws_bytes, _lib.stream_handle(q.device))
-        _lib.check(rc, "gw_sparse_attn_fwd")
+    stream = _lib.stream_handle(q.device)
+    if kl_logits is None:
+        kl_args = (None, 0, 0, 0, 0.0, None)
     else:
         code = _lib.GW_DTYPE_FP32 if kl_logits.dtype == torch.float32 else _lib.dtype_code(kl_logits.dtype)
-        rc = lib.gw_sparse_attn_fwd_kl(*common, kl_logits.data_ptr(), code, kl_logits.stride(0),
-                                       kl_logits.stride(1), float(kl_eps), kl_row_loss.data_ptr(),
-                                       _lib.ptr(ws), ws_bytes, _lib.stream_handle(q.device))
+        kl_args = (kl_logits.data_ptr(), code, kl_logits.stride(0), kl_logits.stride(1), float(kl_eps),
+                   kl_row_loss.data_ptr())
+    if _use_dense(seqlen_k, num_kv, nheads, d) and (attn_sum is None or num_kv <= DENSE_ATTN_SUM_MAX_K):
+        dense_bytes = int(lib.gw_sparse_attn_fwd_dense_workspace_size(batch, seqlen_q, seqlen_k, nheads, d, num_kv,
+                                                                      int(attn_sum is not None)))
+        dws = torch.empty(max(dense_bytes, 1), device=q.device, dtype=torch.uint8)
+        rc = lib.gw_sparse_attn_fwd_dense(*common, *kl_args, dws.data_ptr(), dense_bytes, stream)
+        _lib.check(rc, "gw_sparse_attn_fwd_dense")
+        return o, attn_sum, lse, softmax_scale
+    ws, ws_bytes = None, 0
+    if attn_sum is not None:
+        ws_bytes = int(lib.gw_sparse_attn_fwd_workspace_size(batch, seqlen_q, nheads, num_kv, 1))
+        ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
+    if kl_logits is None:
+        rc = lib.gw_sparse_attn_fwd(*common, _lib.ptr(ws), ws_bytes, stream)
+        _lib.check(rc, "gw_sparse_attn_fwd")
+    else:
+        rc = lib.gw_sparse_attn_fwd_kl(*common, *kl_args, _lib.ptr(ws), ws_bytes, stream)
         _lib.check(rc, "gw_sparse_attn_fwd_kl")
     return o, attn_sum, lse, softmax_scale
 

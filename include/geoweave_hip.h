@@ -338,30 +338,39 @@ int gw_source_downsample_expand(int dtype, const int32_t* coarse_idx, const void
                                 int64_t pad_window, int32_t* out, void* stream);
 
 /* ------------------------------------------------------------------------------------
- * Sparse-index attention forward as a masked dense pass (no attn_sum): the same result as
- * gw_sparse_attn_fwd without attn_sum (o and lse, up to fp32 summation order), computed by
- * matrix-core products over every (query, key) pair with the selection as a mask. Replaces
- * the same reference compute as gw_sparse_attn_fwd when no attn_sum is asked for
- * (_flash_attn_forward with return_attn = False + _fwd_kernel,
- * easyvolcap/utils/custom_flash_attn/sparse_index_flash_attn.py:2001-2233, :129-259, as
- * reached from sparse_index_flash_attn_inference_func :3138-3163); it pays off when a
- * query selects more than roughly 1 % of the keys.
- * Needs D = 64 and an even H; otherwise GW_ERR_UNSUPPORTED (use gw_sparse_attn_fwd).
+ * Sparse-index attention forward as a masked dense pass: the same results as
+ * gw_sparse_attn_fwd / gw_sparse_attn_fwd_kl (o, lse, attn_sum and the KL row losses, up to
+ * fp32 summation order), computed by matrix-core products over every (query, key) pair with
+ * the selection as a mask. Replaces the same reference compute (_flash_attn_forward +
+ * _fwd_kernel + _attn_sum_kernel, easyvolcap/utils/custom_flash_attn/sparse_index_flash_attn.py:
+ * 2001-2233, :129-259, :375-458, as reached from sparse_index_flash_attn_func :3286 and
+ * sparse_index_flash_attn_inference_func :3138-3163; the fused KL as in gw_sparse_attn_fwd_kl);
+ * it pays off when a query selects more than roughly 1 % of the keys.
+ * Needs D = 64 and an even H, and K <= 1024 when attn_sum is asked for; otherwise
+ * GW_ERR_UNSUPPORTED (use gw_sparse_attn_fwd / gw_sparse_attn_fwd_kl).
+ * attn_sum (nullable) and lse: as for gw_sparse_attn_fwd (lse is required with attn_sum).
+ * logits (nullable; needs attn_sum) ... row_loss: the fused KL loss, as for
+ * gw_sparse_attn_fwd_kl.
  * Queries that list a position twice are computed by the gather kernel inside this call
  * (the reference counts a repeated position twice).
- * Workspace: gw_sparse_attn_fwd_dense_workspace_size(B, T, S, H, D) bytes, 16-byte
- * aligned: the selection mask (B * ceil(T/32) * S * 4 bytes), per-block flags and a
- * transposed copy of V (B * H * 64 * round_up(S, 64) * 2 bytes).
+ * Workspace: gw_sparse_attn_fwd_dense_workspace_size(B, T, S, H, D, K, want_attn_sum) bytes,
+ * 16-byte aligned: the selection mask (B * ceil(T/32) * S * 4 bytes), per-block flags, a
+ * transposed copy of V (B * H * 64 * round_up(S, 64) * 2 bytes) and, with attn_sum, the
+ * selected scores (B * T * K * H * 4 bytes).
  * ------------------------------------------------------------------------------------ */
-size_t gw_sparse_attn_fwd_dense_workspace_size(int64_t B, int64_t T, int64_t S, int64_t H, int64_t D);
+size_t gw_sparse_attn_fwd_dense_workspace_size(int64_t B, int64_t T, int64_t S, int64_t H, int64_t D,
+                                               int64_t K, int want_attn_sum);
 int gw_sparse_attn_fwd_dense(int dtype,
                              const void* q, const int64_t* q_strides,
                              const void* k, const int64_t* k_strides,
                              const void* v, const int64_t* v_strides,
                              const int32_t* kv_pos, int64_t pos_stride_b, int64_t pos_stride_t,
-                             void* o, const int64_t* o_strides, float* lse,
+                             void* o, const int64_t* o_strides, float* lse, float* attn_sum,
                              int64_t B, int64_t T, int64_t S, int64_t H, int64_t D, int64_t K,
-                             float softmax_scale, void* workspace, size_t workspace_bytes,
+                             float softmax_scale,
+                             const void* logits, int logits_dtype, int64_t logits_stride_b,
+                             int64_t logits_stride_t, float eps, float* row_loss,
+                             void* workspace, size_t workspace_bytes,
                              void* stream);
 
 #ifdef __cplusplus

@@ -165,3 +165,72 @@ def test_repeated_position_in_an_upper_key_chunk(gpu_device):
     ro, _, rl = oatt.sparse_attention(q, k, v, pos)
     torch.testing.assert_close(o, ro, **TOL)
     torch.testing.assert_close(lse, rl, atol=1e-4, rtol=1e-4)
+
+
+def _run_attn(q, k, v, pos, scale=None, path="dense", layout="bthd", kl=None):
+    qd, kd, vd, pd = (x.cuda() for x in (q, k, v, pos))
+    if layout == "bhtd":
+        qd, kd, vd = (x.transpose(1, 2).contiguous() for x in (qd, kd, vd))
+    extra = {}
+    if kl is not None:
+        extra = dict(kl_logits=kl.cuda(), kl_eps=1e-6,
+                     kl_row_loss=torch.empty(q.shape[0] * q.shape[1], device="cuda", dtype=torch.float32))
+    with _path(path):
+        o, attn, lse, _ = sifa._flash_attn_forward(qd, kd, vd, pd, softmax_scale=scale, return_attn=True,
+                                                   q_layout=layout, **extra)
+    torch.cuda.synchronize()
+    if layout == "bhtd":
+        o = o.transpose(1, 2)
+    loss = extra["kl_row_loss"].cpu() if kl is not None else None
+    return o.float().cpu(), attn.cpu(), lse.cpu(), loss
+
+
+@pytest.mark.parametrize("B,T,S,H,K,inv", [(1, 1374, 1374, 16, 1024, 0.0), (2, 300, 300, 4, 77, 0.5),
+                                            (1, 257, 1000, 6, 200, 0.2), (1, 70, 70, 2, 64, 0.3)])
+def test_attn_sum_matches_oracle(gpu_device, B, T, S, H, K, inv):
+    # attn_sum from the slot-indexed scores and the sorted positions; o unchanged by it
+    g = torch.Generator().manual_seed(T + K)
+    q = torch.randn(B, T, H, 64, generator=g).bfloat16()
+    k = torch.randn(B, S, H, 64, generator=g).bfloat16()
+    v = torch.randn(B, S, H, 64, generator=g).bfloat16()
+    pos = workloads.random_positions(B, T, S, K, seed=T + 1, invalid_fraction=inv)
+    print(f"[dense attn_sum] B={B} T={T} S={S} H={H} K={K}", flush=True)
+    o, attn, lse, _ = _run_attn(q, k, v, pos, scale=0.125)
+    ro, ra, rl = oatt.sparse_attention(q, k, v, pos, 0.125)
+    torch.testing.assert_close(o, ro, **TOL)
+    torch.testing.assert_close(attn, ra, atol=1e-4, rtol=1e-3)
+    torch.testing.assert_close(lse, rl, atol=1e-4, rtol=1e-4)
+    o2, lse2 = _run(q, k, v, pos, scale=0.125)
+    assert torch.equal(o, o2) and torch.equal(lse, lse2), "attn_sum must not change o or lse"
+    # every valid row's attention mass over the heads sums to H
+    valid = ((pos >= 0) & (pos < S)).any(-1)
+    torch.testing.assert_close(attn.sum(-1)[valid], torch.full((int(valid.sum()),), float(H)), atol=2e-3, rtol=1e-4)
+
+
+def test_attn_sum_repeated_positions_and_bhtd(gpu_device):
+    q, k, v = workloads.attention_inputs(1, 1, torch.bfloat16, tokens=200, seed=19)
+    pos = workloads.random_positions(1, 200, 200, 13, seed=20)
+    pos[0, 0, :] = -1
+    pos[0, 70, :] = 7          # the gather kernel computes this block, attn_sum included
+    o, attn, lse, _ = _run_attn(q, k, v, pos)
+    ro, ra, rl = oatt.sparse_attention(q, k, v, pos)
+    torch.testing.assert_close(o, ro, **TOL)
+    torch.testing.assert_close(attn, ra, atol=1e-4, rtol=1e-3)
+    torch.testing.assert_close(attn[0, 70], torch.full((13,), 16 / 13), atol=1e-5, rtol=1e-5)
+    assert torch.all(attn[0, 0] == 0)
+    o2, attn2, lse2, _ = _run_attn(q, k, v, pos, layout="bhtd")
+    assert torch.equal(o, o2) and torch.equal(attn, attn2) and torch.equal(lse, lse2)
+
+
+def test_fused_kl_rows_match_the_gather_kernel(gpu_device):
+    B, T, H, K = 2, 700, 16, 256
+    q, k, v = workloads.attention_inputs(1, B, torch.bfloat16, tokens=T, seed=23)
+    pos = workloads.random_positions(B, T, T, K, seed=24, invalid_fraction=0.2)
+    pos[1, 100, :4] = 5        # one flagged block: the gather kernel's fused KL
+    z = torch.randn(B, T, K, generator=torch.Generator().manual_seed(25))
+    od, ad, ld, kd = _run_attn(q, k, v, pos, kl=z)
+    og, ag, lg, kg = _run_attn(q, k, v, pos, kl=z, path="gather")
+    torch.testing.assert_close(ad, ag, atol=1e-4, rtol=1e-3)
+    torch.testing.assert_close(kd, kg, atol=1e-5, rtol=1e-4)
+    _, ad2, _, _ = _run_attn(q, k, v, pos)
+    assert torch.equal(ad, ad2), "the fused KL must not change attn_sum"

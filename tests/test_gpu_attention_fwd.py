@@ -61,16 +61,16 @@ def test_one_view_layer_16_heads_topk_1024(gpu_device, dtype):
     q, k, v = workloads.attention_inputs(1, 1, dtype)
     n = q.shape[1]
     pos = workloads.random_positions(1, n, n, 1024, seed=11)
-    o, attn, lse = _run(q, k, v, pos)
+    old_path, sifa.FORWARD_PATH = sifa.FORWARD_PATH, "gather"
+    try:
+        o, attn, lse = _run(q, k, v, pos)
+        o2, none_attn, _ = _run(q, k, v, pos, return_attn=False)
+    finally:
+        sifa.FORWARD_PATH = old_path
     ro, ra, rl = oatt.sparse_attention(q, k, v, pos)
     torch.testing.assert_close(o, ro, **TOL)
     torch.testing.assert_close(attn, ra, **TOL)
     torch.testing.assert_close(lse, rl, atol=1e-4, rtol=1e-4)
-    old_path, sifa.FORWARD_PATH = sifa.FORWARD_PATH, "gather"
-    try:
-        o2, none_attn, _ = _run(q, k, v, pos, return_attn=False)
-    finally:
-        sifa.FORWARD_PATH = old_path
     assert none_attn is None
     assert torch.equal(o, o2), "attn_sum must not change the gather kernel's o"
 
