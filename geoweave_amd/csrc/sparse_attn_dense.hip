@@ -4,31 +4,35 @@
 // their K and V rows (_fwd_kernel, sparse_index_flash_attn.py:129-259). For 16 heads of 64 a gathered
 // (query, key) pair moves 4 KiB; when a query selects a few per cent of all keys (1,024 of
 // 43,968 at 32 views) computing every (query, key) product on the matrix cores costs less
-// than gathering the selected ones. This file does that: per tile of 32 queries x 32 keys,
-// S = Q·Kᵀ and O += P·V are v_mfma_f32_32x32x16 products, and the selection enters as a
-// mask — P is zero at every pair the query did not select, so O, the row sums and the lse are
-// those of the sparse attention, up to fp32 summation order.
+// than gathering the selected ones. This file does that: per 32 queries x 32 keys and head,
+// S^T = K Q^T and O^T += V^T P^T are v_mfma_f32_32x32x16 products, and the selection enters
+// as the initial accumulator of S^T (0 where the query selected the key, -inf elsewhere), so P
+// is zero at every pair the query did not select and O, the row sums and the lse are those
+// of the sparse attention, up to fp32 summation order and the fp16 rounding of P.
 //
-// The softmax only runs on the selected pairs. Per tile the selected (row, key) entries are
-// compacted into a list once, shared by the wave's two heads; for each head the S tile is
-// staged in LDS, the listed scores are read back and exponentiated, and each p is written
-// as hi + lo 16-bit parts (p - hi is exact in fp32) into zeroed P tiles that feed two P·V
-// products, so the weights keep ~16 significant bits. Row sums are taken from the same P
-// operands (v_dot2 with ones), in a fixed order.
+// Transposed products keep the softmax in registers: the S^T accumulator of a lane holds 16
+// keys of one query (lanes l and l ^ 32 share the query), so the row maximum is a reduction
+// within the lane and one v_permlane32_swap, and the exponentiated entries packed to fp16 are
+// already the lane's B operand of the P·V product (V^T stored with the keys in that operand
+// order). V enters in fp16 scaled per column by an exact power of two that fits its range.
+// P holds 11 significant bits (the reference's fp32 weights, rounded to nearest); the row
+// sums add the fp32 weights.
 //
-// Online softmax with a lazy reference maximum: a row's reference m is raised only when an
-// entry exceeds it by more than kLazy in the exp2 domain; O and the row sum are then rescaled.
-// Every p = exp2(t - m) lies in [0, 2^kLazy], so P fits bf16/fp16 without overflow, and the
+// Online softmax with a lazy reference maximum: the weights p = exp2(t - m) of a sub-tile are
+// formed with the query's current m, and m is raised (O and the row sum rescaled, the weights
+// formed again) only when a lane's weights sum to more than kSumCap — the sum bounds every
+// weight, so P fits fp16 without overflow and no per-tile maximum is needed otherwise. The
 // final o = O / l and lse = m + log2(l) do not depend on which m was used.
 //
 // Pieces (all on the caller's stream):
-//   dense_mask_kernel  — maskT[b][qb][key]: bit i set when query qb*32 + i selected the key
-//                        (LDS atomic OR per listed position, per chunk of keys). A position
-//                        listed twice for one query (the atomic returns the bit already set)
-//                        flags the block: the gather kernel then computes that block, since
-//                        the reference counts a repeated position twice.
-//   dense_vt_kernel    — V as [B][H][64][S_pad] (S_pad = S rounded up to 64, zero padded):
-//                        the P·V B operand is 8 consecutive keys of one column, one 16-byte load.
+//   dense_mask_kernel  — selection words per (32-key sub-tile, query) (LDS atomic OR per listed
+//                        position, per chunk of keys). A position listed twice for one query
+//                        (the atomic returns the bit already set) flags the query's 32-query
+//                        block: the gather kernel then computes that block, since the
+//                        reference counts a repeated position twice.
+//   dense_vmax_kernel  — largest |v| per (head, d) column, for the fp16 scaling of V.
+//   dense_vt_kernel    — V^T as [B][H][64][S_pad] fp16 (S_pad = S rounded up to 64, zero
+//                        padded), keys in operand order: one 16-byte load per operand chunk.
 //   dense_attn_kernel  — 8 waves per workgroup, one per 32-query block, all on the same 2
 //                        heads: each K and V^T tile is read from memory once per workgroup
 //                        and shared through LDS.
@@ -45,7 +49,7 @@ namespace {
 constexpr float kDLog2e = 1.4426950408889634f;
 constexpr float kDLn2 = 0.6931471805599453f;
 constexpr int kDHpw = 2;           // heads per wave
-constexpr float kLazy = 8.f;       // p <= 2^kLazy before a rescale
+constexpr float kSumCap = 32768.f;  // a lane's weights of one sub-tile sum to at most this
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -61,32 +65,44 @@ __device__ __forceinline__ f32x16 mma(FP16, uint4 a, uint4 b, f32x16 c) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Selection mask, key-major per 32-query block, built per (block, chunk of kMaskChunk keys)
-// with LDS atomics. The atomic returns the word as it was: a bit already set means the query
-// listed the key twice, and the block is flagged. Positions are read 8 rows at a time (16
-// bytes per lane when the table allows), so the loads of a group are in flight together.
+// Selection mask, query-major per 32-key sub-tile: word[b][j][t] has bit i set when query t
+// selected key 32 j + i (t < T_pad = nqb_pad * 32, j < S_pad / 32; zero words past S and T).
+// Built per (32-query block, chunk of kMaskChunk keys) with LDS atomics. The atomic returns
+// the word as it was: a bit already set means the query listed the key twice, and the block
+// is flagged. Positions are read 8 rows at a time (16 bytes per lane when the table allows),
+// so the loads of a group are in flight together. The first workgroup of each batch also
+// clears the per-column maxima of |V| that dense_vmax_kernel accumulates.
 // ---------------------------------------------------------------------------------------
-constexpr int kMaskChunk = 16384;  // keys per workgroup (64 KiB of LDS words)
+constexpr int kMaskChunk = 16384;  // keys per workgroup
 
 __global__ __launch_bounds__(256) void dense_mask_kernel(const int32_t* __restrict__ pos, int64_t psb, int64_t pst,
-                                                         int T, int S, int K, int nqb, int nchunk, int vec,
-                                                         uint32_t* __restrict__ mask, int* __restrict__ flags) {
-  __shared__ uint32_t words[kMaskChunk];
+                                                         int T, int S, int Spad, int K, int nqb, int tpad,
+                                                         int nchunk, int vec, int vmax_words,
+                                                         uint32_t* __restrict__ mask, int* __restrict__ flags,
+                                                         uint32_t* __restrict__ vmax) {
+  // [key / 32][query], rows padded to 33 words so that one query's atomics spread over banks
+  __shared__ uint32_t words[(kMaskChunk / 32) * 33];
   __shared__ int dup_any;
   const int qb = blockIdx.x, chunk = blockIdx.y, b = blockIdx.z;
   const int c0 = chunk * kMaskChunk;
   const int len = min(kMaskChunk, S - c0);
-  for (int i = threadIdx.x; i < len; i += 256) words[i] = 0u;
+  const int nkt = min(kMaskChunk, Spad - c0) >> 5;
+  for (int i = threadIdx.x; i < nkt * 33; i += 256) words[i] = 0u;
+  if (qb == 0 && chunk == 0)
+    for (int i = threadIdx.x; i < vmax_words; i += 256) vmax[(int64_t)b * vmax_words + i] = 0u;
   if (threadIdx.x == 0) dup_any = 0;
   __syncthreads();
   bool dup = false;
-  const int rows = min(32, T - qb * 32);
-  const int32_t* pblk = pos + b * psb + (int64_t)(qb * 32) * pst;
+  const int rows = min(32, T - qb * 32);  // <= 0 for the padding blocks
+  const int32_t* pblk = pos + b * psb + (int64_t)min(qb * 32, T - 1) * pst;
   // Positions outside [c0, c0 + len) (other chunks, negative padding, >= S) wrap to large
   // unsigned offsets and are skipped.
-  auto put = [&](int32_t sidx, uint32_t bit) {
+  auto put = [&](int32_t sidx, int i) {
     const uint32_t sl = (uint32_t)sidx - (uint32_t)c0;
-    if (sl < (uint32_t)len) dup |= (atomicOr(&words[sl], bit) & bit) != 0u;
+    if (sl < (uint32_t)len) {
+      const uint32_t bit = 1u << (sl & 31u);
+      dup |= (atomicOr(&words[(sl >> 5) * 33 + i], bit) & bit) != 0u;
+    }
   };
   if (vec) {
     // K % 4 == 0 and 16-byte aligned rows: one int4 per lane and row.
@@ -100,11 +116,10 @@ __global__ __launch_bounds__(256) void dense_mask_kernel(const int32_t* __restri
           v[u] = r0 + u < rows ? reinterpret_cast<const int4*>(pblk + (int64_t)(r0 + u) * pst)[j4] : make_int4(-1, -1, -1, -1);
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          const uint32_t bit = 1u << ((r0 + u) & 31);
-          put(v[u].x, bit);
-          put(v[u].y, bit);
-          put(v[u].z, bit);
-          put(v[u].w, bit);
+          put(v[u].x, r0 + u);
+          put(v[u].y, r0 + u);
+          put(v[u].z, r0 + u);
+          put(v[u].w, r0 + u);
         }
       }
     }
@@ -112,24 +127,100 @@ __global__ __launch_bounds__(256) void dense_mask_kernel(const int32_t* __restri
 #pragma unroll 1
     for (int i = 0; i < rows; ++i) {
       const int32_t* prow = pblk + (int64_t)i * pst;
-      for (int j = threadIdx.x; j < K; j += 256) put(prow[j], 1u << i);
+      for (int j = threadIdx.x; j < K; j += 256) put(prow[j], i);
     }
   }
   if (dup) dup_any = 1;
   __syncthreads();
-  uint32_t* out = mask + ((int64_t)b * nqb + qb) * S + c0;
-  for (int i = threadIdx.x; i < len; i += 256) out[i] = words[i];
-  if (threadIdx.x == 0) flags[((int64_t)b * nqb + qb) * nchunk + chunk] = dup_any;
+  uint32_t* out = mask + ((int64_t)b * (Spad >> 5) + (c0 >> 5)) * tpad + qb * 32;
+  for (int idx = threadIdx.x; idx < nkt * 32; idx += 256) {
+    const int kt = idx >> 5, i = idx & 31;
+    out[(int64_t)kt * tpad + i] = words[kt * 33 + i];
+  }
+  if (threadIdx.x == 0 && qb < nqb) flags[((int64_t)b * nqb + qb) * nchunk + chunk] = dup_any;
 }
 
 // ---------------------------------------------------------------------------------------
-// V transposed per head: vt[b][h][d][s], s < S_pad, zero past S.
+// V enters the P·V product in fp16, scaled per (head, d) column by a power of two 2^e that
+// puts the column's largest |v| in [2^14, 2^15): the scaling is exact, every scaled value
+// fits fp16, and values down to 2^-28 of the column's largest stay normal. o is scaled back
+// by 2^-e. dense_vmax_kernel takes the column maxima (as ordered bit patterns of
+// non-negative floats, atomic max); columns that are all zero or hold inf/nan keep e = 0.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ int vscale_exp(uint32_t bits) {
+  const float mx = __uint_as_float(bits);
+  if (!(mx > 0.f) || !(mx <= 3.4028234663852886e38f)) return 0;
+  int x;
+  frexpf(mx, &x);  // mx = f 2^x, f in [0.5, 1)
+  return min(15 - x, 126);
+}
+
+__device__ __forceinline__ float in_to_float(int in_fp16, uint32_t u) {
+  return in_fp16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)u) : __uint_as_float(u << 16);
+}
+
+constexpr int kVmaxKeys = 256;  // keys per workgroup of dense_vmax_kernel (one head)
+
+__global__ __launch_bounds__(256) void dense_vmax_kernel(const uint16_t* __restrict__ v, int64_t vsb, int64_t vss,
+                                                         int64_t vsh, int S, int H, int in_fp16,
+                                                         uint32_t* __restrict__ vmax) {
+  __shared__ float part[4][64];
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int dc = threadIdx.x & 7, kr = threadIdx.x >> 3;  // 16-byte chunk of the row, key
+  const int s0 = blockIdx.x * kVmaxKeys;
+  const uint16_t* src = v + b * vsb + h * vsh + dc * 8;
+  float mx[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) mx[i] = 0.f;
+  uint4 val[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int s = s0 + kr + 32 * u;
+    val[u] = s < S ? *reinterpret_cast<const uint4*>(src + (int64_t)s * vss) : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const uint32_t w[4] = {val[u].x, val[u].y, val[u].z, val[u].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mx[2 * i] = fmaxf(mx[2 * i], fabsf(in_to_float(in_fp16, w[i] & 0xFFFFu)));
+      mx[2 * i + 1] = fmaxf(mx[2 * i + 1], fabsf(in_to_float(in_fp16, w[i] >> 16)));
+    }
+  }
+  // lanes with the same chunk: xor 8, 16, 32; then the four waves
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+#pragma unroll
+    for (int off = 8; off < 64; off <<= 1) mx[i] = fmaxf(mx[i], __shfl_xor(mx[i], off));
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane < 8) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) part[wave][lane * 8 + i] = mx[i];
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const float m4 = fmaxf(fmaxf(part[0][threadIdx.x], part[1][threadIdx.x]), fmaxf(part[2][threadIdx.x], part[3][threadIdx.x]));
+    atomicMax(vmax + ((int64_t)b * H + h) * 64 + threadIdx.x, __float_as_uint(m4));
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// V^T per head in fp16 (scaled as above): vt[b][h][d][s'], s' < S_pad, zero past S. Within
+// every 16 keys, key s sits at s' = s with bits 2 and 3 exchanged: that is the order in which
+// a lane's S^T accumulator entries enter the P·V product as its B operand (entries r < 8 of
+// lane l are keys 8(r/4) + 4(l/32) + r%4, which the operand's k-chunk l/32 lists as k =
+// 8(l/32) + r), so each V^T operand chunk is 8 consecutive s', one 16-byte load.
 // ---------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void dense_vt_kernel(const uint16_t* __restrict__ v, int64_t vsb, int64_t vss,
-                                                       int64_t vsh, int S, int Spad, int H,
+                                                       int64_t vsh, int S, int Spad, int H, int in_fp16,
+                                                       const uint32_t* __restrict__ vmax,
                                                        uint16_t* __restrict__ vt) {
   __shared__ __align__(16) uint16_t tile[64][72];  // [d][key], rows of 144 bytes
+  __shared__ int es[64];
   const int s0 = blockIdx.x * 64, h = blockIdx.y, b = blockIdx.z;
+  if (threadIdx.x < 64) es[threadIdx.x] = vscale_exp(vmax[((int64_t)b * H + h) * 64 + threadIdx.x]);
+  __syncthreads();
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
     const int idx = threadIdx.x + it * 256;
@@ -140,8 +231,12 @@ __global__ __launch_bounds__(256) void dense_vt_kernel(const uint16_t* __restric
     const uint32_t w[4] = {val.x, val.y, val.z, val.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      tile[c * 8 + 2 * i][key] = (uint16_t)(w[i] & 0xFFFFu);
-      tile[c * 8 + 2 * i + 1][key] = (uint16_t)(w[i] >> 16);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int d = c * 8 + 2 * i + u;
+        const float f = ldexpf(in_to_float(in_fp16, u ? w[i] >> 16 : w[i] & 0xFFFFu), es[d]);
+        tile[d][key] = __builtin_bit_cast(uint16_t, (_Float16)f);
+      }
     }
   }
   __syncthreads();
@@ -149,28 +244,37 @@ __global__ __launch_bounds__(256) void dense_vt_kernel(const uint16_t* __restric
   for (int it = 0; it < 2; ++it) {
     const int idx = threadIdx.x + it * 256;
     const int d = idx >> 3, kc = idx & 7;
-    const uint4 val = *reinterpret_cast<const uint4*>(&tile[d][kc * 8]);
-    *reinterpret_cast<uint4*>(vt + (((int64_t)b * H + h) * 64 + d) * Spad + s0 + kc * 8) = val;
+    // s' = 8 kc + 0..7 holds keys 16 (kc/2) + 4 (kc%2) + {0..3, 8..11}
+    const int k0 = 16 * (kc >> 1) + 4 * (kc & 1);
+    const uint2 lo = *reinterpret_cast<const uint2*>(&tile[d][k0]);
+    const uint2 hi = *reinterpret_cast<const uint2*>(&tile[d][k0 + 8]);
+    *reinterpret_cast<uint4*>(vt + (((int64_t)b * H + h) * 64 + d) * Spad + s0 + kc * 8) =
+        make_uint4(lo.x, lo.y, hi.x, hi.y);
   }
 }
 
 // ---------------------------------------------------------------------------------------
-// The attention. Accumulator element r of lane l holds (row 8*(r/4) + 4*(l/32) + r%4,
-// column l%32) of a 32x32 tile; A operands hold row l%32, B operands column l%32, each with
-// the 8-element k-chunk (l/32) of a 16-wide step.
+// The attention, transposed: per sub-tile of 32 keys a wave forms S^T = K Q^T (32 keys x 32
+// queries), so accumulator entry r of lane l holds query l%32 and key 8(r/4) + 4(l/32) + r%4:
+// every entry of a lane belongs to one query, and lanes l and l ^ 32 share it. The
+// exponentiated entries, packed to fp16, are already the B operand of O^T += V^T P^T
+// (32 keys x 32 queries, two k-steps of 16) — P never leaves the registers. The selection
+// enters as the initial accumulator of S^T: 0 where the query selected the key, -inf
+// elsewhere, so p = exp2(-inf) = 0 there.
 // ---------------------------------------------------------------------------------------
 struct DenseParams {
   const uint16_t* q;
   const uint16_t* k;
   const uint16_t* vt;
   const uint32_t* mask;
+  const uint32_t* vmax;
   const int* flags;
   uint16_t* o;
   float* lse;
   int64_t qsb, qst, qsh;
   int64_t ksb, kss, ksh;
   int64_t osb, ost, osh;
-  int T, S, Spad, H, nqb, nchunk;
+  int T, S, Spad, H, nqb, tpad, nchunk;
   float scale_log2;
   // attn_sum (ATTN kernels only): the scaled score of every selected (query, key) and head,
   // sws[((b * T + t) * K + slot) * H + h], slot = rank of the key among the query's
@@ -179,432 +283,277 @@ struct DenseParams {
   int K;
 };
 
-// The attention runs one wave per workgroup. LDS operations of a wave are performed in
-// issue order, so another lane's LDS write is visible to a later LDS read of this wave once
-// the compiler keeps them in program order; no s_barrier and, unlike __syncthreads, no wait
-// for the global loads in flight.
 __device__ __forceinline__ void lds_fence() { asm volatile("" ::: "memory"); }
-
-// Inclusive prefix sum over the 64 lanes with DPP row shifts and row broadcasts.
-__device__ __forceinline__ int wave_scan_dpp(int x) {
-  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);  // row_shr:1
-  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);  // row_shr:2
-  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);  // row_shr:4
-  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);  // row_shr:8
-  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false); // row_bcast:15 -> rows 1, 3
-  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false); // row_bcast:31 -> rows 2, 3
-  return x;
-}
-
-__device__ __forceinline__ int tile_row(int r, int half) { return 8 * (r >> 2) + 4 * half + (r & 3); }
 
 __device__ __forceinline__ uint16_t to_half_bits(BF16, float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 __device__ __forceinline__ uint16_t to_half_bits(FP16, float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
-// Sum of the 8 16-bit values of v added to c, in a fixed order (exact products with 1.0).
-__device__ __forceinline__ float sum8(BF16 e, uint4 v, float c) {
-  constexpr uint32_t one2 = 0x3F803F80u;
-  c = dot2(e, v.x, one2, c);
-  c = dot2(e, v.y, one2, c);
-  c = dot2(e, v.z, one2, c);
-  return dot2(e, v.w, one2, c);
+
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_f16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, f16x2_v));  // v_cvt_pk_f16_f32
 }
-__device__ __forceinline__ float sum8(FP16 e, uint4 v, float c) {
-  constexpr uint32_t one2 = 0x3C003C00u;
-  c = dot2(e, v.x, one2, c);
-  c = dot2(e, v.y, one2, c);
-  c = dot2(e, v.z, one2, c);
-  return dot2(e, v.w, one2, c);
+// 0 where sel is all ones, neg where it is zero (v_bfi_b32: (sel & 0) | (~sel & neg)).
+__device__ __forceinline__ float select_bias(int sel, float neg) {
+  float r;
+  asm("v_bfi_b32 %0, %1, 0, %2" : "=v"(r) : "v"(sel), "v"(neg));
+  return r;
 }
-__device__ __forceinline__ float from_half_bits(BF16, uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
-__device__ __forceinline__ float from_half_bits(FP16, uint16_t x) { return (float)__builtin_bit_cast(_Float16, x); }
-__device__ __forceinline__ uint32_t pack_pair(BF16 e, float lo, float hi) {
-  return (uint32_t)to_half_bits(e, lo) | ((uint32_t)to_half_bits(e, hi) << 16);
+// Lanes l and l ^ 32 exchange (v_permlane32_swap); both get op(own, partner).
+__device__ __forceinline__ float pair_max(float x) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
 }
-__device__ __forceinline__ uint32_t pack_pair(FP16 e, float lo, float hi) {
-  return (uint32_t)to_half_bits(e, lo) | ((uint32_t)to_half_bits(e, hi) << 16);
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+}
+__device__ __forceinline__ uint32_t pair_or(uint32_t x) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return sw[0] | sw[1];
 }
 
-constexpr int kDW = 8;      // waves (32-query blocks) per workgroup, sharing each K/V tile
-constexpr int kPElems = 32 * 32 + 64;  // P tile (32 rows x 32 keys, 16-bit) + dummy slots
+constexpr int kDW = 8;  // waves (32-query blocks) per workgroup, sharing each K/V tile
 
-// K tile: 32 keys x (2 heads x 64) bf16 = 32 rows of 256 bytes; the 16-byte chunk c of key
-// row kl sits at position c ^ (kl & 15). V^T tile: 128 rows (head, d) x 32 keys = 128 rows of
-// 64 bytes; chunk c of row rr sits at c ^ ((rr >> 2) & 3). Both layouts make the MFMA operand
-// reads (32 consecutive rows at one chunk) touch distinct bank groups within 16 lanes.
+// LDS tiles of 64 keys: K as 128 rows (head, key) and V^T as 128 rows (head, d), 128 bytes
+// each; the 16-byte chunk c of row R sits at c ^ swz(R). Operand reads (consecutive rows, one
+// chunk) and tile stores (8 lanes per row) then touch distinct banks in every group of 8 and
+// of 16 lanes.
+__device__ __forceinline__ int swz(int R) { return (R & 7) ^ ((R >> 3) & 1); }
+
 template <typename E, bool ATTN>
 __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams p) {
   constexpr int HPW = kDHpw;
-  // Ring of kRing K/V tiles (tile t in buffer t % kRing), one barrier per kDist tiles. With
-  // attn_sum the per-wave slot arrays need the LDS of two ring buffers: two tiles, a barrier
-  // per tile.
-  constexpr int kRing = ATTN ? 2 : 4;
-  constexpr int kDist = kRing / 2;
-  __shared__ __align__(16) uint8_t ktile[kRing][8192];
-  __shared__ __align__(16) uint8_t vtile[kRing][8192];
-  // attn_sum: per wave, each listed entry's slot and the rows' running slot counts.
-  __shared__ uint16_t eslot_all[ATTN ? kDW : 1][ATTN ? 32 * 32 + 64 : 1];
-  __shared__ uint32_t rcnt_all[ATTN ? kDW : 1][ATTN ? 33 : 1];
-  // Per wave: the S tile staged as float4 groups, lane-contiguous (element r of lane l at
-  // ((r >> 2) * 64 + l) * 4 + (r & 3)); P as two 16-bit tiles hi and lo (p = hi + lo to
-  // ~16 significant bits), rows of 64 bytes with XOR-swizzled 16-byte chunks; the compacted
-  // entry list. Lanes without an entry use dummy slots, so no per-entry step needs a branch:
-  // row 32 (m = +inf there, so p = 0), P slot 1024 + lane, list slot 1024 + lane.
-  __shared__ __align__(16) float stage_all[kDW][16 * 64];
-  __shared__ __align__(16) uint16_t phi_all[kDW][kPElems];
-  __shared__ __align__(16) uint16_t plo_all[kDW][kPElems];
-  __shared__ uint16_t elist_all[kDW][32 * 32 + 64];
-  __shared__ __align__(16) float mrow_all[kDW][HPW][36];
-  __shared__ __align__(16) float arow_all[kDW][32];
-  __shared__ uint32_t mx_all[kDW][33];
+  __shared__ __align__(16) uint8_t ktile[2][HPW * 8192];
+  __shared__ __align__(16) uint8_t vtile[2][HPW * 8192];
+  __shared__ float vsc_s[HPW][64];
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  float* stage = stage_all[wave];
-  uint16_t* phi = phi_all[wave];
-  uint16_t* plo = plo_all[wave];
-  uint16_t* elist = elist_all[wave];
-  float (*mrow)[36] = mrow_all[wave];
-  float* arow = arow_all[wave];
-  uint32_t* mx = mx_all[wave];
-  uint16_t* eslot = eslot_all[ATTN ? wave : 0];
-  uint32_t* rcnt = rcnt_all[ATTN ? wave : 0];
-
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int nhg = p.H / HPW;
   const int hg = blockIdx.x % nhg;  // consecutive workgroups (different XCDs) take different heads
-  const int qb = (blockIdx.x / nhg) * kDW + wave;
+  const int qb = (blockIdx.x / nhg) * kDW + wave;  // < nqb_pad
   const int b = blockIdx.y;
-  bool active = qb < p.nqb;
-  if (active) {
-    // A block holding a repeated position is computed by the gather kernel.
-    const int* f = p.flags + ((int64_t)b * p.nqb + qb) * p.nchunk;
-    for (int c = 0; c < p.nchunk; ++c) active &= f[c] == 0;
-  }
   const int col = lane & 31, half = lane >> 5;
   const int q0 = qb * 32;
+  const int t = q0 + col;
   const int h0 = hg * HPW;
+  const float sl2 = p.scale_log2;
 
-  uint4 a[HPW][4];
+  if (tid < HPW * 64)
+    vsc_s[tid >> 6][tid & 63] = ldexpf(1.f, -vscale_exp(p.vmax[((int64_t)b * p.H + h0 + (tid >> 6)) * 64 + (tid & 63)]));
+
+  // Q^T operands (B of S^T = K Q^T): query t, dims 16 ks + 8 half + 0..7.
+  uint4 qa[HPW][4];
   {
-    const int t = q0 + col;
-    const bool ok = active && t < p.T;
+    const bool ok = t < p.T;
     const uint16_t* qr = p.q + b * p.qsb + (int64_t)(ok ? t : 0) * p.qst + half * 8;
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh)
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks)
-        a[hh][ks] = ok ? *reinterpret_cast<const uint4*>(qr + (h0 + hh) * p.qsh + ks * 16) : make_uint4(0, 0, 0, 0);
+        qa[hh][ks] = ok ? *reinterpret_cast<const uint4*>(qr + (h0 + hh) * p.qsh + ks * 16) : make_uint4(0, 0, 0, 0);
   }
   f32x16 acc[HPW][2];
 #pragma unroll
   for (int hh = 0; hh < HPW; ++hh)
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
+    for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[hh][nb][r] = 0.f;
-  if (lane < 33) {
+      for (int r = 0; r < 16; ++r) acc[hh][db][r] = 0.f;
+  // Lazy reference maximum per query (exp2 domain), the same in lanes l and l ^ 32; a finite
+  // start keeps t - m = -inf at unselected entries. Row sums: this lane's keys only.
+  float m[HPW], l[HPW];
+#pragma unroll
+  for (int hh = 0; hh < HPW; ++hh) {
+    m[hh] = -3.4028234663852886e38f;
+    l[hh] = 0.f;
+  }
+
+  // Tile staging: each thread moves one 16-byte chunk of K and of V^T per head and tile,
+  // loaded into registers a tile ahead of its LDS store.
+  const int srow = tid >> 3, sc = tid & 7;
+  const int soff = srow * 128 + ((sc ^ swz(srow)) << 4);
+  const uint16_t* ksrc = p.k + b * p.ksb + (int64_t)h0 * p.ksh + sc * 8;
+  const uint16_t* vsrc = p.vt + (((int64_t)b * p.H + h0) * 64 + srow) * p.Spad + sc * 8;
+  const int64_t vhead = (int64_t)64 * p.Spad;
+  auto gload = [&](int k0, uint4& k0r, uint4& k1r, uint4& v0r, uint4& v1r) {
+    const int64_t key = min(k0 + srow, p.S - 1);  // keys past S: any valid row (their P is 0)
+    k0r = *reinterpret_cast<const uint4*>(ksrc + key * p.kss);
+    k1r = *reinterpret_cast<const uint4*>(ksrc + key * p.kss + p.ksh);
+    v0r = *reinterpret_cast<const uint4*>(vsrc + k0);
+    v1r = *reinterpret_cast<const uint4*>(vsrc + vhead + k0);
+  };
+  auto lstore = [&](int bf, const uint4& k0r, const uint4& k1r, const uint4& v0r, const uint4& v1r) {
+    *reinterpret_cast<uint4*>(&ktile[bf][soff]) = k0r;
+    *reinterpret_cast<uint4*>(&ktile[bf][8192 + soff]) = k1r;
+    *reinterpret_cast<uint4*>(&vtile[bf][soff]) = v0r;
+    *reinterpret_cast<uint4*>(&vtile[bf][8192 + soff]) = v1r;
+  };
+  // Operand reads: K rows 32 st + col (chunk 2 ks + half), V^T rows 32 db + col (chunk
+  // 4 st + 2 ks + half); swz of these rows is swz(col).
+  const int fc = swz(col);
+  const int kbase = col * 128, vbase = col * 128;
+  auto koff = [&](int hh, int st, int ks) { return hh * 8192 + kbase + st * 4096 + (((2 * ks + half) ^ fc) << 4); };
+  auto voff = [&](int hh, int db, int st, int ks) {
+    return hh * 8192 + vbase + db * 4096 + (((4 * st + 2 * ks + half) ^ fc) << 4);
+  };
+  // Mask words of query t, one per 32-key sub-tile.
+  const int nsub = p.Spad >> 5;
+  const uint32_t* mcol = p.mask + (int64_t)b * nsub * p.tpad + t;
+  auto mword = [&](int j) { return mcol[(int64_t)min(j, nsub - 1) * p.tpad]; };
+
+  uint32_t rank_base = 0;  // attn_sum: selected keys of query t before the sub-tile
+  float* srow_ws = ATTN ? p.sws + ((int64_t)b * p.T + min(t, p.T - 1)) * p.K * p.H + h0 : nullptr;
+  const float ninf = -INFINITY;
+
+  // One 32-key sub-tile: S^T for both heads from the selection bias, the softmax in
+  // registers, O^T += V^T P^T.
+  auto sub = [&](const uint8_t* kt, const uint8_t* vt, int st, uint32_t w) {
+    // Entry r of this lane is bit 8(r/4) + r%4 of w >> 4 half.
+    const uint32_t own = w >> (4 * half);
+    f32x16 bias;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int sel = __builtin_amdgcn_sbfe((int)own, 8 * (r >> 2) + (r & 3), 1);  // 0 or -1
+      bias[r] = select_bias(sel, ninf);
+    }
+    f32x16 s[HPW];
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) {
-      mrow[hh][lane] = lane < 32 ? -INFINITY : INFINITY;
+      s[hh] = bias;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        s[hh] = mma(E{}, *reinterpret_cast<const uint4*>(kt + koff(hh, st, ks)), qa[hh][ks], s[hh]);
     }
-    if constexpr (ATTN) rcnt[lane] = 0u;
-  }
-  for (int i = lane; i < kPElems / 8; i += 64) {
-    reinterpret_cast<uint4*>(phi)[i] = make_uint4(0, 0, 0, 0);
-    reinterpret_cast<uint4*>(plo)[i] = make_uint4(0, 0, 0, 0);
-  }
-  // Row sums: this lane's share of row `col` (keys 8*half + 0..7 and 16 + 8*half + 0..7 of
-  // each tile, the keys of its P·V operand), summed in a fixed order from hi and lo.
-  float lpart[HPW];
+    if constexpr (ATTN) {
+      // Each selected entry's scaled scores, at the slot of its key's rank.
 #pragma unroll
-  for (int hh = 0; hh < HPW; ++hh) lpart[hh] = 0.f;
-
-  const uint32_t* mbase = p.mask + ((int64_t)b * p.nqb + (active ? qb : 0)) * p.S;
-  const float sl2 = p.scale_log2;
-
-  // Tile loads: per wave one 16-byte chunk per lane of K and one of V^T (1 KB each), loaded
-  // into registers two tiles ahead and written to LDS one tile ahead.
-  const int krow = 4 * wave + (lane >> 4);                 // key row of this lane's K chunk
-  const int kchunk = (lane & 15) ^ (krow & 15);            // global chunk it loads
-  const uint16_t* ksrc0 = p.k + b * p.ksb + (int64_t)(h0 + (kchunk >> 3)) * p.ksh + (kchunk & 7) * 8;
-  const int vrow = 16 * wave + (lane >> 2);                // (head, d) row of this lane's V chunk
-  const int vchunk = (lane & 3) ^ ((vrow >> 2) & 3);
-  const uint16_t* vsrc0 = p.vt + (((int64_t)b * p.H + h0 + (vrow >> 6)) * 64 + (vrow & 63)) * p.Spad + vchunk * 8;
-  auto gload = [&](int kb0, uint4& kr, uint4& vr) {
-    const int key = min(kb0 + krow, p.S - 1);  // keys past S: any valid row (their P is 0)
-    kr = *reinterpret_cast<const uint4*>(ksrc0 + (int64_t)key * p.kss);
-    vr = *reinterpret_cast<const uint4*>(vsrc0 + kb0);
-  };
-  auto lstore = [&](int bf, const uint4& kr, const uint4& vr) {
-    *reinterpret_cast<uint4*>(&ktile[bf][wave * 1024 + lane * 16]) = kr;
-    *reinterpret_cast<uint4*>(&vtile[bf][wave * 1024 + lane * 16]) = vr;
-  };
-  // Loads in the tile loop are unconditional (clamped addresses): with no control flow around
-  // them the compiler's memory waits count exactly the loads still needed.
-  // The raw word is loaded a tile ahead; its validity select waits until the word is used.
-  auto mask_raw = [&](int kb0) -> uint32_t { return mbase[min(kb0 + col, p.S - 1)]; };
-  // Operand read offsets (bytes) within a tile.
-  uint32_t koff[HPW][4], voff[HPW][2][2];
-#pragma unroll
-  for (int hh = 0; hh < HPW; ++hh) {
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) koff[hh][ks] = col * 256 + (((hh * 8 + 2 * ks + half) ^ (col & 15)) * 16);
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const int rr = hh * 64 + nb * 32 + col;
-        voff[hh][nb][ks] = rr * 64 + (((2 * ks + half) ^ ((rr >> 2) & 3)) * 16);
+      for (int r = 0; r < 16; ++r) {
+        const int kk = 8 * (r >> 2) + 4 * half + (r & 3);
+        if ((own >> (8 * (r >> 2) + (r & 3))) & 1u) {
+          const uint32_t slot = rank_base + __popc(w & ((1u << kk) - 1u));
+          *reinterpret_cast<float2*>(srow_ws + (int64_t)slot * p.H) = make_float2(s[0][r] * sl2, s[1][r] * sl2);
+        }
       }
-  }
-
-  struct Ent {
-    int sa, row, pa;
-    bool ok;
-  };
-  auto decode = [&](int i, int nsel) {
-    Ent en;
-    en.ok = i < nsel;
-    const int e = elist[en.ok ? i : 1024 + lane];
-    const int r = e >> 6, ln = e & 63;
-    const int row = tile_row(r, ln >> 5);
-    en.sa = en.ok ? ((r >> 2) * 64 + ln) * 4 + (r & 3) : 0;
-    en.row = en.ok ? row : 32;
-    // P tile rows of 64 bytes, 16-byte chunk c of row rr at c ^ ((rr >> 2) & 3).
-    en.pa = en.ok ? row * 32 + ((((ln & 31) >> 3) ^ ((row >> 2) & 3)) << 3) + (ln & 7) : 1024 + lane;
-    return en;
-  };
-
-  // Tile t lives in LDS buffer t % kRing. While computing tile t a wave writes tile
-  // t + kDist from registers into buffer (t + kDist) % kRing (last read before the last
-  // barrier) and loads tile t + 2 kDist into the freed registers; the barrier after every
-  // kDist tiles makes the next tiles visible. kDist register sets alternate by tile (no
-  // register copies, which would wait for the loads). The wave's private LDS needs no
-  // barrier (one wave).
-  const int ntiles = (p.S + 31) / 32;
-  const int last = (ntiles - 1) * 32;
-  // Staging registers: named variables (an array of them indexed through the tile calls
-  // would live in scratch memory).
-  uint4 kra, vra, krb, vrb;
-  {
-    uint4 k0r, v0r;
-    gload(0, k0r, v0r);
-    lstore(0, k0r, v0r);
-    if constexpr (kDist == 2) {
-      gload(min(32, last), k0r, v0r);
-      lstore(1, k0r, v0r);
+      rank_base += __popc(w);
     }
-  }
-  gload(min(32 * kDist, last), kra, vra);
-  if constexpr (kDist == 2) gload(min(96, last), krb, vrb);
-  uint32_t wraw = mask_raw(0);
-  __syncthreads();
-  auto tile = [&](int n, uint4& kr, uint4& vr, bool sync_after) {
-    const int k0 = n * 32;
-    const int buf = n & (kRing - 1);
-    lstore((n + kDist) & (kRing - 1), kr, vr);  // past the last tile: never read
-    gload(min(k0 + 64 * kDist, last), kr, vr);
-    const uint32_t wnext = mask_raw(k0 + 32);  // past the last tile: unused
-    const uint32_t w = (active && k0 + col < p.S) ? wraw : 0u;
-    // This lane's rows 8g + 4*half + i (g, i < 4) are bits 8g + 4*half + i of w; bit r of
-    // m16 is accumulator element r.
-    const uint32_t xw = w >> (4 * half);
-    const uint32_t m16 = (xw & 0xFu) | ((xw >> 4) & 0xF0u) | ((xw >> 8) & 0xF00u) | ((xw >> 12) & 0xF000u);
-    if (__ballot(m16 != 0u) != 0ull) {
-      const uint8_t* kt = ktile[buf];
-      const uint8_t* vt = vtile[buf];
-      // Compact the selected entries (lane order, then r): exclusive prefix of the counts.
-      const int cnt = __popc(m16);
-      const int incl = wave_scan_dpp(cnt);
-      const int nsel = __builtin_amdgcn_readlane(incl, 63);
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh) {
+      // Weights with the current reference maximum. Their sum bounds each weight: while no
+      // lane's sum exceeds kSumCap every p fits fp16, and the maximum stays where it is.
+      float pv[16];
+      float ls = 0.f;
       {
-        int at = incl - cnt;
-        uint32_t mm = m16;
-        while (__ballot(mm != 0u) != 0ull) {
-          const bool has = mm != 0u;
-          elist[has ? at : 1024 + lane] = (uint16_t)(((__ffs(mm) - 1) << 6) | lane);
-          at += has ? 1 : 0;
-          mm &= mm - 1u;
-        }
+        const float nm = -m[hh];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pv[r] = fexp2(fmaf(s[hh][r], sl2, nm));
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ls += pv[r];  // fixed order
       }
-      lds_fence();
-      const Ent e0 = decode(lane, nsel);  // entries 0..63; later chunks are decoded on the fly
-      if constexpr (ATTN) {
-        // Slots in ascending key order per row: the list is in key order and one atomic's
-        // lanes are served in lane order.
-        for (int c0 = 0; c0 < nsel; c0 += 64) {
-          const Ent en = c0 == 0 ? e0 : decode(c0 + lane, nsel);
-          if (en.ok) eslot[c0 + lane] = (uint16_t)atomicAdd(&rcnt[en.row], 1u);
-        }
-        lds_fence();
+      if (__builtin_amdgcn_ballot_w64(!(ls <= kSumCap)) != 0ull) {
+        // Some query of the wave has an entry above its maximum by more than log2(kSumCap /
+        // 16) (or its first selected entry): every query moves its maximum to the largest
+        // selected entry of this sub-tile if that is higher, rescales O and the row sum, and
+        // the weights are formed again.
+        float mx = s[hh][0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[hh][r]);
+        const float mn = fmaxf(m[hh], pair_max(mx) * sl2);  // unselected entries are -inf
+        const float alpha = fexp2(m[hh] - mn);
+        m[hh] = mn;
+        l[hh] *= alpha;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[hh][db][r] *= alpha;
+        const float nm = -mn;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pv[r] = fexp2(fmaf(s[hh][r], sl2, nm));
+        ls = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ls += pv[r];
       }
-
-      // Both heads' score products first: head 1's MFMAs run while head 0's softmax does.
-      f32x16 sacc[HPW];
+      // Row sums of the fp32 weights (as the gather kernel's): lse and the attn_sum
+      // normalisation do not see the fp16 rounding of the product's operand.
+      l[hh] += ls;
+      uint32_t pk[8];
 #pragma unroll
-      for (int hh = 0; hh < HPW; ++hh) {
-        sacc[hh] = f32x16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < 8; ++j) pk[j] = pack_f16(pv[2 * j], pv[2 * j + 1]);
+      const uint4 pb0 = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+      const uint4 pb1 = make_uint4(pk[4], pk[5], pk[6], pk[7]);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-          sacc[hh] = mma(E{}, a[hh][ks], *reinterpret_cast<const uint4*>(kt + koff[hh][ks]), sacc[hh]);
+      for (int db = 0; db < 2; ++db) {
+        acc[hh][db] = mma(FP16{}, *reinterpret_cast<const uint4*>(vt + voff(hh, db, st, 0)), pb0, acc[hh][db]);
+        acc[hh][db] = mma(FP16{}, *reinterpret_cast<const uint4*>(vt + voff(hh, db, st, 1)), pb1, acc[hh][db]);
       }
-#pragma unroll
-      for (int hh = 0; hh < HPW; ++hh) {
-        const f32x16 s = sacc[hh];
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<float4*>(&stage[(g * 64 + lane) * 4]) = make_float4(s[4 * g], s[4 * g + 1], s[4 * g + 2], s[4 * g + 3]);
-        lds_fence();
-
-        // A row's reference maximum moves only when one of its own entries of this tile
-        // exceeds it by more than kLazy, and then to the largest such entry: every row's
-        // arithmetic is independent of the other rows of the block (and of the chunking).
-        // Entries 0..63 keep their score and maximum in registers.
-        const float t0 = stage[e0.sa] * sl2;
-        float mo0 = mrow[hh][e0.row];
-        bool lift = __ballot(t0 > mo0 + kLazy) != 0ull;
-        for (int c0 = 64; c0 < nsel; c0 += 64) {
-          const Ent en = decode(c0 + lane, nsel);
-          lift |= __ballot(stage[en.sa] * sl2 > mrow[hh][en.row] + kLazy) != 0ull;
-        }
-        if (lift) {
-          if (lane < 32) mx[lane] = f2key(mrow[hh][lane]);
-          lds_fence();
-          for (int c0 = 0; c0 < nsel; c0 += 64) {
-            const Ent en = c0 == 0 ? e0 : decode(c0 + lane, nsel);
-            const float t = stage[en.sa] * sl2;
-            if (t > mrow[hh][en.row] + kLazy) atomicMax(&mx[en.row], f2key(t));
-          }
-          lds_fence();
-          if (lane < 32) {
-            const float mold = mrow[hh][lane];
-            const float mnew = key2f(mx[lane]);
-            float alpha = 1.f;
-            if (mnew > mold) {
-              alpha = fexp2(mold - mnew);
-              mrow[hh][lane] = mnew;
-            }
-            arow[lane] = alpha;
-          }
-          lds_fence();
-          lpart[hh] *= arow[col];
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const float4 al = *reinterpret_cast<const float4*>(&arow[8 * g + 4 * half]);
-            const float alv[4] = {al.x, al.y, al.z, al.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              acc[hh][0][4 * g + i] *= alv[i];
-              acc[hh][1][4 * g + i] *= alv[i];
-            }
-          }
-          mo0 = mrow[hh][e0.row];
-        }
-        auto emit = [&](int pa_, float t, float mo) {
-          const float pv = fexp2(t - mo);
-          const uint16_t hb = to_half_bits(E{}, pv);
-          phi[pa_] = hb;
-          plo[pa_] = to_half_bits(E{}, pv - from_half_bits(E{}, hb));  // exact difference
-        };
-        emit(e0.pa, t0, mo0);
-        for (int c0 = 64; c0 < nsel; c0 += 64) {
-          const Ent en = decode(c0 + lane, nsel);
-          emit(en.pa, stage[en.sa] * sl2, mrow[hh][en.row]);
-        }
-        if constexpr (ATTN) {
-          auto keep = [&](const Ent& en, int i, float t) {
-            if (en.ok) p.sws[(((int64_t)b * p.T + q0 + en.row) * p.K + eslot[i]) * p.H + h0 + hh] = t;
-          };
-          keep(e0, lane, t0);
-          for (int c0 = 64; c0 < nsel; c0 += 64) {
-            const Ent en = decode(c0 + lane, nsel);
-            keep(en, c0 + lane, stage[en.sa] * sl2);
-          }
-        }
-        lds_fence();
-        // P enters the P·V product as its hi and lo parts: two products, weights with ~16
-        // significant bits, close to the fp32 p of the gather kernel.
-        uint4 pa[2], pl[2];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const int pofs = col * 32 + (((2 * ks + half) ^ ((col >> 2) & 3)) << 3);
-          pa[ks] = *reinterpret_cast<const uint4*>(&phi[pofs]);
-          pl[ks] = *reinterpret_cast<const uint4*>(&plo[pofs]);
-        }
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) lpart[hh] = sum8(E{}, pa[ks], lpart[hh]);
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) lpart[hh] = sum8(E{}, pl[ks], lpart[hh]);
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
-            const uint4 vb = *reinterpret_cast<const uint4*>(vt + voff[hh][nb][ks]);
-            acc[hh][nb] = mma(E{}, pa[ks], vb, acc[hh][nb]);
-            acc[hh][nb] = mma(E{}, pl[ks], vb, acc[hh][nb]);
-          }
-        // Clear the written P entries for the next use of the tile.
-        phi[e0.pa] = 0;
-        plo[e0.pa] = 0;
-        for (int c0 = 64; c0 < nsel; c0 += 64) {
-          const int pa_ = decode(c0 + lane, nsel).pa;
-          phi[pa_] = 0;
-          plo[pa_] = 0;
-        }
-        lds_fence();
-      }
-    }
-    wraw = wnext;
-    if (sync_after) {
-      // This wave's LDS writes of the next pair's tiles are done; after the barrier every
-      // wave's are, and every wave is done with this pair's buffers before they are refilled.
-      // No wait for the global loads in flight (a raw barrier, unlike __syncthreads).
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
     }
   };
-  if constexpr (kDist == 2) {
-    for (int n = 0; n < ntiles; n += 2) {
-      tile(n, kra, vra, false);
-      if (n + 1 < ntiles) tile(n + 1, krb, vrb, true);
-    }
-  } else {
-    for (int n = 0; n < ntiles; ++n) tile(n, kra, vra, true);
-  }
-  if (!active) return;
 
-  // o = O / l, lse = (m + log2 l) ln 2; rows without any selected key give o = 0, lse = -inf.
-  // l of row r = the shares of lanes r and r + 32.
-  float (*lrow)[32] = reinterpret_cast<float (*)[32]>(stage);  // the staging area is free now
-#pragma unroll
-  for (int hh = 0; hh < HPW; ++hh) {
-    if (half == 1) lrow[hh][col] = lpart[hh];
-    lds_fence();
-    if (half == 0) lrow[hh][col] = lpart[hh] + lrow[hh][col];
-    lds_fence();
+  // Tile n (64 keys) lives in LDS buffer n % 2. While computing tile n a thread stores tile
+  // n + 1 from registers into the other buffer (last read before the previous barrier) and
+  // loads tile n + 2 into the freed registers; one barrier per tile.
+  const int ntiles = p.Spad >> 6;
+  const int last = (ntiles - 1) * 64;
+  uint4 r0, r1, r2, r3;
+  {
+    uint4 a0, a1, a2, a3;
+    gload(0, a0, a1, a2, a3);
+    lstore(0, a0, a1, a2, a3);
+  }
+  gload(min(64, last), r0, r1, r2, r3);
+  uint32_t w0 = mword(0), w1 = mword(1);
+  __syncthreads();
+#pragma unroll 1
+  for (int n = 0; n < ntiles; ++n) {
+    const int buf = n & 1;
+    // The next tile's mask words before the tile loads: waiting for them later does not wait
+    // for the tile loads.
+    const uint32_t wn0 = mword(2 * n + 2), wn1 = mword(2 * n + 3);
+    lstore(buf ^ 1, r0, r1, r2, r3);  // past the last tile: never read
+    gload(min((n + 2) * 64, last), r0, r1, r2, r3);
+    sub(ktile[buf], vtile[buf], 0, w0);
+    sub(ktile[buf], vtile[buf], 1, w1);
+    w0 = wn0;
+    w1 = wn1;
+    // This thread's LDS stores of the next tile are done; after the barrier every thread's
+    // are, and every wave is done with this tile's buffer before it is refilled. No wait for
+    // the global loads in flight (a raw barrier, unlike __syncthreads).
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+
+  // o = O / l scaled back by 2^-e per column, lse = (m + log2 l) ln 2; queries without any
+  // selected key give o = 0, lse = -inf. Blocks holding a repeated position are written by
+  // the gather kernel.
+  bool active = qb < p.nqb && t < p.T;
+  if (qb < p.nqb) {
+    const int* f = p.flags + ((int64_t)b * p.nqb + qb) * p.nchunk;
+    for (int c = 0; c < p.nchunk; ++c) active &= f[c] == 0;
   }
 #pragma unroll
   for (int hh = 0; hh < HPW; ++hh) {
-    const int h = h0 + hh;
+    const float lt = pair_sum(l[hh]);
+    if (active) {
+      const int h = h0 + hh;
+      const float inv = lt > 0.f ? __frcp_rn(lt) : 0.f;
+      uint16_t* orow = p.o + b * p.osb + (int64_t)t * p.ost + h * p.osh;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const float4 lv = *reinterpret_cast<const float4*>(&lrow[hh][8 * g + 4 * half]);
-      const float lvv[4] = {lv.x, lv.y, lv.z, lv.w};
+      for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = q0 + 8 * g + 4 * half + i;
-        if (t < p.T) {
-          const float inv = lvv[i] > 0.f ? __frcp_rn(lvv[i]) : 0.f;
-          uint16_t* orow = p.o + b * p.osb + (int64_t)t * p.ost + h * p.osh + col;
-          orow[0] = to_half_bits(E{}, acc[hh][0][4 * g + i] * inv);
-          orow[32] = to_half_bits(E{}, acc[hh][1][4 * g + i] * inv);
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = 32 * db + 8 * g + 4 * half;
+          uint16_t hv[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) hv[i] = to_half_bits(E{}, acc[hh][db][4 * g + i] * inv * vsc_s[hh][d0 + i]);
+          *reinterpret_cast<uint2*>(orow + d0) =
+              make_uint2((uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16));
         }
-      }
-    }
-    if (lane < 32 && q0 + lane < p.T && p.lse) {
-      const float l = lrow[hh][lane];
-      p.lse[((int64_t)b * p.T + q0 + lane) * p.H + h] = l > 0.f ? (mrow[hh][lane] + flog2(l)) * kDLn2 : -INFINITY;
+      if (half == 0 && p.lse)
+        p.lse[((int64_t)b * p.T + t) * p.H + h] = lt > 0.f ? (m[hh] + flog2(lt)) * kDLn2 : -INFINITY;
     }
   }
 }
@@ -729,22 +678,25 @@ __global__ __launch_bounds__(256) void dense_attn_sum_kernel(const AttnSumParams
 }
 
 struct DenseLayout {
-  size_t mask, flags, vt, sws, total;
-  int nqb, nchunk, spad;
+  size_t mask, flags, vmax, vt, sws, total;
+  int nqb, nqb_pad, nchunk, spad;
 };
 
 DenseLayout dense_layout(int64_t B, int64_t T, int64_t S, int64_t H, int64_t K, bool attn) {
   DenseLayout L;
   L.nqb = (int)((T + 31) / 32);
+  L.nqb_pad = (L.nqb + kDW - 1) / kDW * kDW;
   L.nchunk = (int)((S + kMaskChunk - 1) / kMaskChunk);
   if (L.nchunk < 1) L.nchunk = 1;
   L.spad = (int)((S + 63) / 64 * 64);
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
   size_t o = 0;
   L.mask = o;
-  o = up(o + (size_t)B * L.nqb * (size_t)S * 4);
+  o = up(o + (size_t)B * (size_t)(L.spad / 32) * (size_t)L.nqb_pad * 32 * 4);
   L.flags = o;
   o = up(o + (size_t)B * L.nqb * (size_t)L.nchunk * 4);
+  L.vmax = o;
+  o = up(o + (size_t)B * (size_t)H * 64 * 4);
   L.vt = o;
   o = up(o + (size_t)B * (size_t)H * 64 * (size_t)L.spad * 2);
   L.sws = o;
@@ -800,6 +752,9 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
   if (D != 64) return set_error(GW_ERR_UNSUPPORTED, "the dense forward needs head dim 64, got %lld", (long long)D);
   if (H % kDHpw != 0)
     return set_error(GW_ERR_UNSUPPORTED, "the dense forward needs an even head count, got %lld", (long long)H);
+  if (!(softmax_scale > 0.f) || !(softmax_scale < 3.4e38f))
+    return set_error(GW_ERR_UNSUPPORTED, "the dense forward needs a positive finite softmax scale, got %g",
+                     (double)softmax_scale);
   const bool want_attn = attn_sum != nullptr;
   const bool want_kl = logits != nullptr;
   if (want_attn && K > kDenseAttnMaxK)
@@ -823,14 +778,16 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
     GW_CHECK_ARG(eps >= 0.f, "eps must be non-negative, got %g", (double)eps);
   }
   const DenseLayout L = dense_layout(B, T, S, H, K, want_attn);
-  GW_CHECK_ARG((int64_t)L.nqb * (H / kDHpw) < (1ll << 31), "too many query blocks");
+  GW_CHECK_ARG((int64_t)L.nqb_pad * (H / kDHpw) < (1ll << 31), "too many query blocks");
   GW_CHECK_ARG(workspace != nullptr && workspace_bytes >= L.total && aligned16(workspace),
                "the dense forward needs a 16-byte aligned %zu-byte workspace, got %zu", L.total, workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   uint32_t* mask = reinterpret_cast<uint32_t*>(ws + L.mask);
   int* flags = reinterpret_cast<int*>(ws + L.flags);
+  uint32_t* vmax = reinterpret_cast<uint32_t*>(ws + L.vmax);
   uint16_t* vt = reinterpret_cast<uint16_t*>(ws + L.vt);
+  const int in_fp16 = dtype == GW_DTYPE_FP16 ? 1 : 0;
   float* sws = want_attn ? reinterpret_cast<float*>(ws + L.sws) : nullptr;
 
   {
@@ -838,13 +795,18 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
                      (reinterpret_cast<uintptr_t>(kv_pos) & 15) == 0)
                         ? 1
                         : 0;
-    hipLaunchKernelGGL(dense_mask_kernel, dim3(L.nqb, L.nchunk, (unsigned)B), dim3(256), 0, st, kv_pos, pos_stride_b,
-                       pos_stride_t, (int)T, (int)S, (int)K, L.nqb, L.nchunk, vec, mask, flags);
+    hipLaunchKernelGGL(dense_mask_kernel, dim3(L.nqb_pad, L.nchunk, (unsigned)B), dim3(256), 0, st, kv_pos,
+                       pos_stride_b, pos_stride_t, (int)T, (int)S, L.spad, (int)K, L.nqb, L.nqb_pad * 32, L.nchunk,
+                       vec, (int)(H * 64), mask, flags, vmax);
     GW_HIP_LAUNCH_CHECK("dense_mask_kernel launch");
   }
+  hipLaunchKernelGGL(dense_vmax_kernel, dim3((unsigned)((S + kVmaxKeys - 1) / kVmaxKeys), (unsigned)H, (unsigned)B),
+                     dim3(256), 0, st, static_cast<const uint16_t*>(v), v_strides[0], v_strides[1], v_strides[2], (int)S, (int)H,
+                     in_fp16, vmax);
+  GW_HIP_LAUNCH_CHECK("dense_vmax_kernel launch");
   hipLaunchKernelGGL(dense_vt_kernel, dim3(L.spad / 64, (unsigned)H, (unsigned)B), dim3(256), 0, st,
                      static_cast<const uint16_t*>(v), v_strides[0], v_strides[1], v_strides[2], (int)S, L.spad,
-                     (int)H, vt);
+                     (int)H, in_fp16, vmax, vt);
   GW_HIP_LAUNCH_CHECK("dense_vt_kernel launch");
 
   DenseParams p;
@@ -852,6 +814,7 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
   p.k = static_cast<const uint16_t*>(k);
   p.vt = vt;
   p.mask = mask;
+  p.vmax = vmax;
   p.flags = flags;
   p.o = static_cast<uint16_t*>(o);
   p.lse = lse;
@@ -863,11 +826,12 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
   p.Spad = L.spad;
   p.H = (int)H;
   p.nqb = L.nqb;
+  p.tpad = L.nqb_pad * 32;
   p.nchunk = L.nchunk;
   p.scale_log2 = softmax_scale * kDLog2e;
   p.sws = sws;
   p.K = (int)K;
-  const dim3 grid((unsigned)((L.nqb + kDW - 1) / kDW * (H / kDHpw)), (unsigned)B);
+  const dim3 grid((unsigned)(L.nqb_pad / kDW * (H / kDHpw)), (unsigned)B);
   if (dtype == GW_DTYPE_BF16) {
     if (want_attn)
       hipLaunchKernelGGL((dense_attn_kernel<BF16, true>), grid, dim3(kDW * 64), 0, st, p);

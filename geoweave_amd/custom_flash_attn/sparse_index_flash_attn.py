@@ -100,8 +100,8 @@ DENSE_MAX_RATIO = 48
 DENSE_ATTN_SUM_MAX_K = 1024
 
 
-def _use_dense(seqlen_k: int, num_kv: int, nheads: int, d: int) -> bool:
-    if FORWARD_PATH == "gather" or d != 64 or nheads % 2:
+def _use_dense(seqlen_k: int, num_kv: int, nheads: int, d: int, softmax_scale: float = 1.0) -> bool:
+    if FORWARD_PATH == "gather" or d != 64 or nheads % 2 or not 0.0 < softmax_scale < float("inf"):
         return False
     return FORWARD_PATH == "dense" or seqlen_k <= DENSE_MAX_RATIO * num_kv
 
@@ -170,7 +170,7 @@ def _flash_attn_forward(
         code = _lib.GW_DTYPE_FP32 if kl_logits.dtype == torch.float32 else _lib.dtype_code(kl_logits.dtype)
         kl_args = (kl_logits.data_ptr(), code, kl_logits.stride(0), kl_logits.stride(1), float(kl_eps),
                    kl_row_loss.data_ptr())
-    if _use_dense(seqlen_k, num_kv, nheads, d) and (attn_sum is None or num_kv <= DENSE_ATTN_SUM_MAX_K):
+    if _use_dense(seqlen_k, num_kv, nheads, d, softmax_scale) and (attn_sum is None or num_kv <= DENSE_ATTN_SUM_MAX_K):
         dense_bytes = int(lib.gw_sparse_attn_fwd_dense_workspace_size(batch, seqlen_q, seqlen_k, nheads, d, num_kv,
                                                                       int(attn_sum is not None)))
         dws = torch.empty(max(dense_bytes, 1), device=q.device, dtype=torch.uint8)

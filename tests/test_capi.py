@@ -151,20 +151,23 @@ def _dense_call(**over):
     lib = _lib.load()
     s = _lib.strides3(1024, 1024, 64)
     args = dict(dtype=0, q=16, k=16, v=16, pos=16, o=16, lse=16, attn=None, B=1, T=4, S=4, H=16, D=64, K=4,
-                logits=None, row_loss=None, ws=None, ws_bytes=0)
+                scale=0.125, logits=None, row_loss=None, ws=None, ws_bytes=0)
     args.update(over)
     return lib.gw_sparse_attn_fwd_dense(
         args["dtype"], args["q"], s, args["k"], s, args["v"], s, args["pos"], 16, 4,
         args["o"], s, args["lse"], args["attn"], args["B"], args["T"], args["S"], args["H"], args["D"],
-        args["K"], 0.125, args["logits"], 2, 4, 1, 1e-6, args["row_loss"], args["ws"], args["ws_bytes"], None)
+        args["K"], args["scale"], args["logits"], 2, 4, 1, 1e-6, args["row_loss"], args["ws"], args["ws_bytes"], None)
 
 
 def test_dense_fwd_workspace_and_argument_checks_without_gpu():
     lib = _lib.load()
-    # mask 1 block x 4 keys x 4 B -> 256; flags 4 B -> 512; V^T 16 heads x 64 x 64 keys x 2 B
-    assert lib.gw_sparse_attn_fwd_dense_workspace_size(1, 4, 4, 16, 64, 4, 0) == 512 + 16 * 64 * 64 * 2
+    # mask: 2 sub-tiles of 32 keys (S padded to 64) x 256 queries (1 block padded to 8) x 4 B
+    # = 2048; flags 4 B -> 2304; |V| column maxima 16 heads x 64 x 4 B -> 6400; V^T 16 heads
+    # x 64 x 64 keys x 2 B
+    base = 2304 + 16 * 64 * 4 + 16 * 64 * 64 * 2
+    assert lib.gw_sparse_attn_fwd_dense_workspace_size(1, 4, 4, 16, 64, 4, 0) == base
     # + the selected scores for attn_sum: T x K x H x 4 B
-    assert lib.gw_sparse_attn_fwd_dense_workspace_size(1, 4, 4, 16, 64, 4, 1) == 512 + 16 * 64 * 64 * 2 + 4 * 4 * 16 * 4
+    assert lib.gw_sparse_attn_fwd_dense_workspace_size(1, 4, 4, 16, 64, 4, 1) == base + 4 * 4 * 16 * 4
     assert lib.gw_sparse_attn_fwd_dense_workspace_size(1, 4, 4, 16, 128, 4, 0) == 0
     assert _dense_call(D=128) == 2
     assert b"head dim" in lib.gw_last_error()
@@ -172,6 +175,8 @@ def test_dense_fwd_workspace_and_argument_checks_without_gpu():
     assert b"even head count" in lib.gw_last_error()
     assert _dense_call(attn=16, K=2048) == 2
     assert b"K <= 1024" in lib.gw_last_error()
+    assert _dense_call(scale=-0.125) == 2 and _dense_call(scale=0.0) == 2
+    assert b"positive finite softmax scale" in lib.gw_last_error()
     assert _dense_call(dtype=7) == 1
     assert _dense_call() == 1
     assert b"workspace" in lib.gw_last_error()
