@@ -33,9 +33,10 @@
 //   dense_vmax_kernel  — largest |v| per (head, d) column, for the fp16 scaling of V.
 //   dense_vt_kernel    — V^T as [B][H][64][S_pad] fp16 (S_pad = S rounded up to 64, zero
 //                        padded), keys in operand order: one 16-byte load per operand chunk.
-//   dense_attn_kernel  — 8 waves per workgroup, one per 32-query block, all on the same 2
-//                        heads: each K and V^T tile is read from memory once per workgroup
-//                        and shared through LDS.
+//   dense_attn_kernel  — 8 waves per workgroup, each on two 32-query blocks, all on one
+//                        head: each K and V^T tile is read from memory once per workgroup
+//                        and shared through LDS, and each K and V^T operand read from LDS
+//                        feeds the products of both blocks.
 #include <math.h>
 
 #include "gw_attn.h"
@@ -48,7 +49,6 @@ namespace {
 
 constexpr float kDLog2e = 1.4426950408889634f;
 constexpr float kDLn2 = 0.6931471805599453f;
-constexpr int kDHpw = 2;           // heads per wave
 constexpr float kSumCap = 32768.f;  // a lane's weights of one sub-tile sum to at most this
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -308,14 +308,12 @@ __device__ __forceinline__ float pair_sum(float x) {
   const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
 }
-__device__ __forceinline__ uint32_t pair_or(uint32_t x) {
-  const auto sw = __builtin_amdgcn_permlane32_swap(x, x, false, false);
-  return sw[0] | sw[1];
-}
 
-constexpr int kDW = 8;  // waves (32-query blocks) per workgroup, sharing each K/V tile
+constexpr int kDW = 8;   // waves per workgroup, sharing each K/V tile
+constexpr int kQPW = 2;  // 32-query blocks per wave (one head): each K and V^T operand feeds two products
+constexpr int kQBW = kDW * kQPW;  // 32-query blocks per workgroup
 
-// LDS tiles of 64 keys: K as 128 rows (head, key) and V^T as 128 rows (head, d), 128 bytes
+// LDS tiles of 64 keys of one head: K as 64 rows (key) and V^T as 64 rows (d), 128 bytes
 // each; the 16-byte chunk c of row R sits at c ^ swz(R). Operand reads (consecutive rows, one
 // chunk) and tile stores (8 lanes per row) then touch distinct banks in every group of 8 and
 // of 16 lanes.
@@ -323,172 +321,175 @@ __device__ __forceinline__ int swz(int R) { return (R & 7) ^ ((R >> 3) & 1); }
 
 template <typename E, bool ATTN>
 __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams p) {
-  constexpr int HPW = kDHpw;
-  __shared__ __align__(16) uint8_t ktile[2][HPW * 8192];
-  __shared__ __align__(16) uint8_t vtile[2][HPW * 8192];
-  __shared__ float vsc_s[HPW][64];
+  __shared__ __align__(16) uint8_t ktile[2][8192];
+  __shared__ __align__(16) uint8_t vtile[2][8192];
+  __shared__ float vsc_s[64];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int nhg = p.H / HPW;
-  const int hg = blockIdx.x % nhg;  // consecutive workgroups (different XCDs) take different heads
-  const int qb = (blockIdx.x / nhg) * kDW + wave;  // < nqb_pad
+  const int h = blockIdx.x % p.H;  // consecutive workgroups (different XCDs) take different heads
+  const int qb0 = (blockIdx.x / p.H) * kQBW + wave * kQPW;  // this wave's blocks qb0, qb0 + 1 (< nqb_pad)
   const int b = blockIdx.y;
   const int col = lane & 31, half = lane >> 5;
-  const int q0 = qb * 32;
-  const int t = q0 + col;
-  const int h0 = hg * HPW;
   const float sl2 = p.scale_log2;
-
-  if (tid < HPW * 64)
-    vsc_s[tid >> 6][tid & 63] = ldexpf(1.f, -vscale_exp(p.vmax[((int64_t)b * p.H + h0 + (tid >> 6)) * 64 + (tid & 63)]));
-
-  // Q^T operands (B of S^T = K Q^T): query t, dims 16 ks + 8 half + 0..7.
-  uint4 qa[HPW][4];
-  {
-    const bool ok = t < p.T;
-    const uint16_t* qr = p.q + b * p.qsb + (int64_t)(ok ? t : 0) * p.qst + half * 8;
+  int tq[kQPW];  // this lane's query in each block
 #pragma unroll
-    for (int hh = 0; hh < HPW; ++hh)
+  for (int a = 0; a < kQPW; ++a) tq[a] = (qb0 + a) * 32 + col;
+
+  if (tid < 64) vsc_s[tid] = ldexpf(1.f, -vscale_exp(p.vmax[((int64_t)b * p.H + h) * 64 + tid]));
+
+  // Q^T operands (B of S^T = K Q^T): query tq[a], dims 16 ks + 8 half + 0..7.
+  uint4 qa[kQPW][4];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        qa[hh][ks] = ok ? *reinterpret_cast<const uint4*>(qr + (h0 + hh) * p.qsh + ks * 16) : make_uint4(0, 0, 0, 0);
+  for (int a = 0; a < kQPW; ++a) {
+    const bool ok = tq[a] < p.T;
+    const uint16_t* qr = p.q + b * p.qsb + (int64_t)(ok ? tq[a] : 0) * p.qst + h * p.qsh + half * 8;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      qa[a][ks] = ok ? *reinterpret_cast<const uint4*>(qr + ks * 16) : make_uint4(0, 0, 0, 0);
   }
-  f32x16 acc[HPW][2];
+  f32x16 acc[kQPW][2];
 #pragma unroll
-  for (int hh = 0; hh < HPW; ++hh)
+  for (int a = 0; a < kQPW; ++a)
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[hh][db][r] = 0.f;
+      for (int r = 0; r < 16; ++r) acc[a][db][r] = 0.f;
   // Lazy reference maximum per query (exp2 domain), the same in lanes l and l ^ 32; a finite
   // start keeps t - m = -inf at unselected entries. Row sums: this lane's keys only.
-  float m[HPW], l[HPW];
+  float m[kQPW], l[kQPW];
 #pragma unroll
-  for (int hh = 0; hh < HPW; ++hh) {
-    m[hh] = -3.4028234663852886e38f;
-    l[hh] = 0.f;
+  for (int a = 0; a < kQPW; ++a) {
+    m[a] = -3.4028234663852886e38f;
+    l[a] = 0.f;
   }
 
-  // Tile staging: each thread moves one 16-byte chunk of K and of V^T per head and tile,
-  // loaded into registers a tile ahead of its LDS store.
+  // Tile staging: each thread moves one 16-byte chunk of K and one of V^T per tile, loaded
+  // into registers a tile ahead of its LDS store.
   const int srow = tid >> 3, sc = tid & 7;
   const int soff = srow * 128 + ((sc ^ swz(srow)) << 4);
-  const uint16_t* ksrc = p.k + b * p.ksb + (int64_t)h0 * p.ksh + sc * 8;
-  const uint16_t* vsrc = p.vt + (((int64_t)b * p.H + h0) * 64 + srow) * p.Spad + sc * 8;
-  const int64_t vhead = (int64_t)64 * p.Spad;
-  auto gload = [&](int k0, uint4& k0r, uint4& k1r, uint4& v0r, uint4& v1r) {
+  const uint16_t* ksrc = p.k + b * p.ksb + (int64_t)h * p.ksh + sc * 8;
+  const uint16_t* vsrc = p.vt + (((int64_t)b * p.H + h) * 64 + srow) * p.Spad + sc * 8;
+  auto gload = [&](int k0, uint4& kr, uint4& vr) {
     const int64_t key = min(k0 + srow, p.S - 1);  // keys past S: any valid row (their P is 0)
-    k0r = *reinterpret_cast<const uint4*>(ksrc + key * p.kss);
-    k1r = *reinterpret_cast<const uint4*>(ksrc + key * p.kss + p.ksh);
-    v0r = *reinterpret_cast<const uint4*>(vsrc + k0);
-    v1r = *reinterpret_cast<const uint4*>(vsrc + vhead + k0);
+    kr = *reinterpret_cast<const uint4*>(ksrc + key * p.kss);
+    vr = *reinterpret_cast<const uint4*>(vsrc + k0);
   };
-  auto lstore = [&](int bf, const uint4& k0r, const uint4& k1r, const uint4& v0r, const uint4& v1r) {
-    *reinterpret_cast<uint4*>(&ktile[bf][soff]) = k0r;
-    *reinterpret_cast<uint4*>(&ktile[bf][8192 + soff]) = k1r;
-    *reinterpret_cast<uint4*>(&vtile[bf][soff]) = v0r;
-    *reinterpret_cast<uint4*>(&vtile[bf][8192 + soff]) = v1r;
+  auto lstore = [&](int bf, const uint4& kr, const uint4& vr) {
+    *reinterpret_cast<uint4*>(&ktile[bf][soff]) = kr;
+    *reinterpret_cast<uint4*>(&vtile[bf][soff]) = vr;
   };
   // Operand reads: K rows 32 st + col (chunk 2 ks + half), V^T rows 32 db + col (chunk
   // 4 st + 2 ks + half); swz of these rows is swz(col).
   const int fc = swz(col);
-  const int kbase = col * 128, vbase = col * 128;
-  auto koff = [&](int hh, int st, int ks) { return hh * 8192 + kbase + st * 4096 + (((2 * ks + half) ^ fc) << 4); };
-  auto voff = [&](int hh, int db, int st, int ks) {
-    return hh * 8192 + vbase + db * 4096 + (((4 * st + 2 * ks + half) ^ fc) << 4);
-  };
-  // Mask words of query t, one per 32-key sub-tile.
+  auto koff = [&](int st, int ks) { return col * 128 + st * 4096 + (((2 * ks + half) ^ fc) << 4); };
+  auto voff = [&](int db, int st, int ks) { return col * 128 + db * 4096 + (((4 * st + 2 * ks + half) ^ fc) << 4); };
+  // Mask words of the lane's queries, one per 32-key sub-tile.
   const int nsub = p.Spad >> 5;
-  const uint32_t* mcol = p.mask + (int64_t)b * nsub * p.tpad + t;
-  auto mword = [&](int j) { return mcol[(int64_t)min(j, nsub - 1) * p.tpad]; };
+  const uint32_t* mcol = p.mask + (int64_t)b * nsub * p.tpad + tq[0];  // block qb0 + 1: + 32
+  auto mword = [&](int j, int a) { return mcol[(int64_t)min(j, nsub - 1) * p.tpad + 32 * a]; };
 
-  uint32_t rank_base = 0;  // attn_sum: selected keys of query t before the sub-tile
-  float* srow_ws = ATTN ? p.sws + ((int64_t)b * p.T + min(t, p.T - 1)) * p.K * p.H + h0 : nullptr;
+  uint32_t rank_base[kQPW] = {0u, 0u};  // attn_sum: selected keys of the query before the sub-tile
+  float* srow_ws[kQPW];
+#pragma unroll
+  for (int a = 0; a < kQPW; ++a)
+    srow_ws[a] = ATTN ? p.sws + ((int64_t)b * p.T + min(tq[a], p.T - 1)) * p.K * p.H + h : nullptr;
   const float ninf = -INFINITY;
 
-  // One 32-key sub-tile: S^T for both heads from the selection bias, the softmax in
+  // One 32-key sub-tile: S^T for both blocks from the selection bias, the softmax in
   // registers, O^T += V^T P^T.
-  auto sub = [&](const uint8_t* kt, const uint8_t* vt, int st, uint32_t w) {
-    // Entry r of this lane is bit 8(r/4) + r%4 of w >> 4 half.
-    const uint32_t own = w >> (4 * half);
-    f32x16 bias;
+  auto sub = [&](const uint8_t* kt, const uint8_t* vt, int st, const uint32_t (&w)[kQPW]) {
+    f32x16 s[kQPW];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int sel = __builtin_amdgcn_sbfe((int)own, 8 * (r >> 2) + (r & 3), 1);  // 0 or -1
-      bias[r] = select_bias(sel, ninf);
-    }
-    f32x16 s[HPW];
-#pragma unroll
-    for (int hh = 0; hh < HPW; ++hh) {
-      s[hh] = bias;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        s[hh] = mma(E{}, *reinterpret_cast<const uint4*>(kt + koff(hh, st, ks)), qa[hh][ks], s[hh]);
-    }
-    if constexpr (ATTN) {
-      // Each selected entry's scaled scores, at the slot of its key's rank.
+    for (int a = 0; a < kQPW; ++a) {
+      // Entry r of this lane is bit 8(r/4) + r%4 of w >> 4 half.
+      const uint32_t own = w[a] >> (4 * half);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int kk = 8 * (r >> 2) + 4 * half + (r & 3);
-        if ((own >> (8 * (r >> 2) + (r & 3))) & 1u) {
-          const uint32_t slot = rank_base + __popc(w & ((1u << kk) - 1u));
-          *reinterpret_cast<float2*>(srow_ws + (int64_t)slot * p.H) = make_float2(s[0][r] * sl2, s[1][r] * sl2);
-        }
+        const int sel = __builtin_amdgcn_sbfe((int)own, 8 * (r >> 2) + (r & 3), 1);  // 0 or -1
+        s[a][r] = select_bias(sel, ninf);
       }
-      rank_base += __popc(w);
     }
 #pragma unroll
-    for (int hh = 0; hh < HPW; ++hh) {
-      // Weights with the current reference maximum. Their sum bounds each weight: while no
-      // lane's sum exceeds kSumCap every p fits fp16, and the maximum stays where it is.
-      float pv[16];
-      float ls = 0.f;
-      {
-        const float nm = -m[hh];
+    for (int ks = 0; ks < 4; ++ks) {
+      const uint4 ka = *reinterpret_cast<const uint4*>(kt + koff(st, ks));
 #pragma unroll
-        for (int r = 0; r < 16; ++r) pv[r] = fexp2(fmaf(s[hh][r], sl2, nm));
+      for (int a = 0; a < kQPW; ++a) s[a] = mma(E{}, ka, qa[a][ks], s[a]);
+    }
+    if constexpr (ATTN) {
+      // Each selected entry's scaled score, at the slot of its key's rank.
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ls += pv[r];  // fixed order
+      for (int a = 0; a < kQPW; ++a) {
+        const uint32_t own = w[a] >> (4 * half);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kk = 8 * (r >> 2) + 4 * half + (r & 3);
+          if ((own >> (8 * (r >> 2) + (r & 3))) & 1u) {
+            const uint32_t slot = rank_base[a] + __popc(w[a] & ((1u << kk) - 1u));
+            srow_ws[a][(int64_t)slot * p.H] = s[a][r] * sl2;
+          }
+        }
+        rank_base[a] += __popc(w[a]);
       }
-      if (__builtin_amdgcn_ballot_w64(!(ls <= kSumCap)) != 0ull) {
-        // Some query of the wave has an entry above its maximum by more than log2(kSumCap /
-        // 16) (or its first selected entry): every query moves its maximum to the largest
-        // selected entry of this sub-tile if that is higher, rescales O and the row sum, and
-        // the weights are formed again.
-        float mx = s[hh][0];
+    }
+    // Weights with the current reference maximum. Their sum bounds each weight: while no
+    // lane's sum exceeds kSumCap every p fits fp16, and the maximum stays where it is.
+    float pv[kQPW][16], ls[kQPW];
 #pragma unroll
-        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[hh][r]);
-        const float mn = fmaxf(m[hh], pair_max(mx) * sl2);  // unselected entries are -inf
-        const float alpha = fexp2(m[hh] - mn);
-        m[hh] = mn;
-        l[hh] *= alpha;
+    for (int a = 0; a < kQPW; ++a) {
+      const float nm = -m[a];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pv[a][r] = fexp2(fmaf(s[a][r], sl2, nm));
+      ls[a] = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ls[a] += pv[a][r];  // fixed order
+    }
+    if (__builtin_amdgcn_ballot_w64(!(ls[0] <= kSumCap) || !(ls[1] <= kSumCap)) != 0ull) {
+      // Some query of the wave has an entry above its maximum by more than log2(kSumCap /
+      // 16) (or its first selected entry): every query moves its maximum to the largest
+      // selected entry of this sub-tile if that is higher, rescales O and the row sum, and
+      // the weights are formed again.
+#pragma unroll
+      for (int a = 0; a < kQPW; ++a) {
+        float mx = s[a][0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[a][r]);
+        const float mn = fmaxf(m[a], pair_max(mx) * sl2);  // unselected entries are -inf
+        const float alpha = fexp2(m[a] - mn);
+        m[a] = mn;
+        l[a] *= alpha;
 #pragma unroll
         for (int db = 0; db < 2; ++db)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[hh][db][r] *= alpha;
+          for (int r = 0; r < 16; ++r) acc[a][db][r] *= alpha;
         const float nm = -mn;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) pv[r] = fexp2(fmaf(s[hh][r], sl2, nm));
-        ls = 0.f;
+        for (int r = 0; r < 16; ++r) pv[a][r] = fexp2(fmaf(s[a][r], sl2, nm));
+        ls[a] = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ls += pv[r];
-      }
-      // Row sums of the fp32 weights (as the gather kernel's): lse and the attn_sum
-      // normalisation do not see the fp16 rounding of the product's operand.
-      l[hh] += ls;
-      uint32_t pk[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) pk[j] = pack_f16(pv[2 * j], pv[2 * j + 1]);
-      const uint4 pb0 = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-      const uint4 pb1 = make_uint4(pk[4], pk[5], pk[6], pk[7]);
-#pragma unroll
-      for (int db = 0; db < 2; ++db) {
-        acc[hh][db] = mma(FP16{}, *reinterpret_cast<const uint4*>(vt + voff(hh, db, st, 0)), pb0, acc[hh][db]);
-        acc[hh][db] = mma(FP16{}, *reinterpret_cast<const uint4*>(vt + voff(hh, db, st, 1)), pb1, acc[hh][db]);
+        for (int r = 0; r < 16; ++r) ls[a] += pv[a][r];
       }
     }
+    uint4 pb[kQPW][2];
+#pragma unroll
+    for (int a = 0; a < kQPW; ++a) {
+      // Row sums of the fp32 weights (as the gather kernel's): lse and the attn_sum
+      // normalisation do not see the fp16 rounding of the product's operand.
+      l[a] += ls[a];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        pb[a][ks] = make_uint4(pack_f16(pv[a][8 * ks], pv[a][8 * ks + 1]), pack_f16(pv[a][8 * ks + 2], pv[a][8 * ks + 3]),
+                               pack_f16(pv[a][8 * ks + 4], pv[a][8 * ks + 5]), pack_f16(pv[a][8 * ks + 6], pv[a][8 * ks + 7]));
+    }
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const uint4 va = *reinterpret_cast<const uint4*>(vt + voff(db, st, ks));
+#pragma unroll
+        for (int a = 0; a < kQPW; ++a) acc[a][db] = mma(FP16{}, va, pb[a][ks], acc[a][db]);
+      }
   };
 
   // Tile n (64 keys) lives in LDS buffer n % 2. While computing tile n a thread stores tile
@@ -496,27 +497,31 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
   // loads tile n + 2 into the freed registers; one barrier per tile.
   const int ntiles = p.Spad >> 6;
   const int last = (ntiles - 1) * 64;
-  uint4 r0, r1, r2, r3;
+  uint4 kr, vr;
   {
-    uint4 a0, a1, a2, a3;
-    gload(0, a0, a1, a2, a3);
-    lstore(0, a0, a1, a2, a3);
+    uint4 k0r, v0r;
+    gload(0, k0r, v0r);
+    lstore(0, k0r, v0r);
   }
-  gload(min(64, last), r0, r1, r2, r3);
-  uint32_t w0 = mword(0), w1 = mword(1);
+  gload(min(64, last), kr, vr);
+  uint32_t w0[kQPW] = {mword(0, 0), mword(0, 1)}, w1[kQPW] = {mword(1, 0), mword(1, 1)};
   __syncthreads();
 #pragma unroll 1
   for (int n = 0; n < ntiles; ++n) {
     const int buf = n & 1;
-    // The next tile's mask words before the tile loads: waiting for them later does not wait
-    // for the tile loads.
-    const uint32_t wn0 = mword(2 * n + 2), wn1 = mword(2 * n + 3);
-    lstore(buf ^ 1, r0, r1, r2, r3);  // past the last tile: never read
-    gload(min((n + 2) * 64, last), r0, r1, r2, r3);
+    // The next tile's mask words before the tile loads: waiting for them later does not
+    // wait for the tile loads.
+    const uint32_t wn0[kQPW] = {mword(2 * n + 2, 0), mword(2 * n + 2, 1)};
+    const uint32_t wn1[kQPW] = {mword(2 * n + 3, 0), mword(2 * n + 3, 1)};
+    lstore(buf ^ 1, kr, vr);  // past the last tile: never read
+    gload(min((n + 2) * 64, last), kr, vr);
     sub(ktile[buf], vtile[buf], 0, w0);
     sub(ktile[buf], vtile[buf], 1, w1);
-    w0 = wn0;
-    w1 = wn1;
+#pragma unroll
+    for (int a = 0; a < kQPW; ++a) {
+      w0[a] = wn0[a];
+      w1[a] = wn1[a];
+    }
     // This thread's LDS stores of the next tile are done; after the barrier every thread's
     // are, and every wave is done with this tile's buffer before it is refilled. No wait for
     // the global loads in flight (a raw barrier, unlike __syncthreads).
@@ -529,16 +534,16 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
   // o = O / l scaled back by 2^-e per column, lse = (m + log2 l) ln 2; queries without any
   // selected key give o = 0, lse = -inf. Blocks holding a repeated position are written by
   // the gather kernel.
-  bool active = qb < p.nqb && t < p.T;
-  if (qb < p.nqb) {
-    const int* f = p.flags + ((int64_t)b * p.nqb + qb) * p.nchunk;
-    for (int c = 0; c < p.nchunk; ++c) active &= f[c] == 0;
-  }
 #pragma unroll
-  for (int hh = 0; hh < HPW; ++hh) {
-    const float lt = pair_sum(l[hh]);
+  for (int a = 0; a < kQPW; ++a) {
+    const int qb = qb0 + a, t = tq[a];
+    bool active = qb < p.nqb && t < p.T;
+    if (qb < p.nqb) {
+      const int* f = p.flags + ((int64_t)b * p.nqb + qb) * p.nchunk;
+      for (int c = 0; c < p.nchunk; ++c) active &= f[c] == 0;
+    }
+    const float lt = pair_sum(l[a]);
     if (active) {
-      const int h = h0 + hh;
       const float inv = lt > 0.f ? __frcp_rn(lt) : 0.f;
       uint16_t* orow = p.o + b * p.osb + (int64_t)t * p.ost + h * p.osh;
 #pragma unroll
@@ -548,12 +553,12 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
           const int d0 = 32 * db + 8 * g + 4 * half;
           uint16_t hv[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) hv[i] = to_half_bits(E{}, acc[hh][db][4 * g + i] * inv * vsc_s[hh][d0 + i]);
+          for (int i = 0; i < 4; ++i) hv[i] = to_half_bits(E{}, acc[a][db][4 * g + i] * inv * vsc_s[d0 + i]);
           *reinterpret_cast<uint2*>(orow + d0) =
               make_uint2((uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16));
         }
       if (half == 0 && p.lse)
-        p.lse[((int64_t)b * p.T + t) * p.H + h] = lt > 0.f ? (m[hh] + flog2(lt)) * kDLn2 : -INFINITY;
+        p.lse[((int64_t)b * p.T + t) * p.H + h] = lt > 0.f ? (m[a] + flog2(lt)) * kDLn2 : -INFINITY;
     }
   }
 }
@@ -685,7 +690,7 @@ struct DenseLayout {
 DenseLayout dense_layout(int64_t B, int64_t T, int64_t S, int64_t H, int64_t K, bool attn) {
   DenseLayout L;
   L.nqb = (int)((T + 31) / 32);
-  L.nqb_pad = (L.nqb + kDW - 1) / kDW * kDW;
+  L.nqb_pad = (L.nqb + kQBW - 1) / kQBW * kQBW;
   L.nchunk = (int)((S + kMaskChunk - 1) / kMaskChunk);
   if (L.nchunk < 1) L.nchunk = 1;
   L.spad = (int)((S + 63) / 64 * 64);
@@ -750,8 +755,6 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
   GW_CHECK_ARG(B >= 0 && T >= 0 && S >= 0 && H >= 1 && K >= 0, "invalid sizes B=%lld T=%lld S=%lld H=%lld K=%lld",
                (long long)B, (long long)T, (long long)S, (long long)H, (long long)K);
   if (D != 64) return set_error(GW_ERR_UNSUPPORTED, "the dense forward needs head dim 64, got %lld", (long long)D);
-  if (H % kDHpw != 0)
-    return set_error(GW_ERR_UNSUPPORTED, "the dense forward needs an even head count, got %lld", (long long)H);
   if (!(softmax_scale > 0.f) || !(softmax_scale < 3.4e38f))
     return set_error(GW_ERR_UNSUPPORTED, "the dense forward needs a positive finite softmax scale, got %g",
                      (double)softmax_scale);
@@ -778,7 +781,7 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
     GW_CHECK_ARG(eps >= 0.f, "eps must be non-negative, got %g", (double)eps);
   }
   const DenseLayout L = dense_layout(B, T, S, H, K, want_attn);
-  GW_CHECK_ARG((int64_t)L.nqb_pad * (H / kDHpw) < (1ll << 31), "too many query blocks");
+  GW_CHECK_ARG((int64_t)(L.nqb_pad / kQBW) * H < (1ll << 31), "too many query blocks");
   GW_CHECK_ARG(workspace != nullptr && workspace_bytes >= L.total && aligned16(workspace),
                "the dense forward needs a 16-byte aligned %zu-byte workspace, got %zu", L.total, workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -831,7 +834,7 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
   p.scale_log2 = softmax_scale * kDLog2e;
   p.sws = sws;
   p.K = (int)K;
-  const dim3 grid((unsigned)(L.nqb_pad / kDW * (H / kDHpw)), (unsigned)B);
+  const dim3 grid((unsigned)(L.nqb_pad / kQBW * H), (unsigned)B);
   if (dtype == GW_DTYPE_BF16) {
     if (want_attn)
       hipLaunchKernelGGL((dense_attn_kernel<BF16, true>), grid, dim3(kDW * 64), 0, st, p);

@@ -101,7 +101,7 @@ DENSE_ATTN_SUM_MAX_K = 1024
 
 
 def _use_dense(seqlen_k: int, num_kv: int, nheads: int, d: int, softmax_scale: float = 1.0) -> bool:
-    if FORWARD_PATH == "gather" or d != 64 or nheads % 2 or not 0.0 < softmax_scale < float("inf"):
+    if FORWARD_PATH == "gather" or d != 64 or not 0.0 < softmax_scale < float("inf"):
         return False
     return FORWARD_PATH == "dense" or seqlen_k <= DENSE_MAX_RATIO * num_kv
 
