@@ -33,7 +33,7 @@
 //   dense_vmax_kernel  — largest |v| per (head, d) column, for the fp16 scaling of V.
 //   dense_vt_kernel    — V^T as [B][H][64][S_pad] fp16 (S_pad = S rounded up to 64, zero
 //                        padded), keys in operand order: one 16-byte load per operand chunk.
-//   dense_attn_kernel  — 8 waves per workgroup, each on two 32-query blocks, all on one
+//   dense_attn_kernel  — 4 waves per workgroup, each on two 32-query blocks, all on one
 //                        head: each K and V^T tile is read from memory once per workgroup
 //                        and shared through LDS, and each K and V^T operand read from LDS
 //                        feeds the products of both blocks.
@@ -309,9 +309,12 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
 }
 
-constexpr int kDW = 8;   // waves per workgroup, sharing each K/V tile
+// Waves per workgroup, sharing each K/V tile. Two workgroups share a CU (two waves per SIMD
+// from different workgroups): one wave's barrier or memory wait is not the other's.
+constexpr int kDW = 4;
 constexpr int kQPW = 2;  // 32-query blocks per wave (one head): each K and V^T operand feeds two products
 constexpr int kQBW = kDW * kQPW;  // 32-query blocks per workgroup
+static_assert(kDW == 4, "the tile staging moves two K and two V^T rows of 64 per thread");
 
 // LDS tiles of 64 keys of one head: K as 64 rows (key) and V^T as 64 rows (d), 128 bytes
 // each; the 16-byte chunk c of row R sits at c ^ swz(R). Operand reads (consecutive rows, one
@@ -320,7 +323,7 @@ constexpr int kQBW = kDW * kQPW;  // 32-query blocks per workgroup
 __device__ __forceinline__ int swz(int R) { return (R & 7) ^ ((R >> 3) & 1); }
 
 template <typename E, bool ATTN>
-__global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams p) {
+__global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DenseParams p) {
   __shared__ __align__(16) uint8_t ktile[2][8192];
   __shared__ __align__(16) uint8_t vtile[2][8192];
   __shared__ float vsc_s[64];
@@ -365,20 +368,25 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
     l[a] = 0.f;
   }
 
-  // Tile staging: each thread moves one 16-byte chunk of K and one of V^T per tile, loaded
-  // into registers a tile ahead of its LDS store.
+  // Tile staging: each thread moves two 16-byte chunks of K and two of V^T per tile (rows
+  // srow and srow + 32), loaded into registers a tile ahead of their LDS store.
   const int srow = tid >> 3, sc = tid & 7;
-  const int soff = srow * 128 + ((sc ^ swz(srow)) << 4);
+  const int soff = srow * 128 + ((sc ^ swz(srow)) << 4);  // swz(srow + 32) = swz(srow)
   const uint16_t* ksrc = p.k + b * p.ksb + (int64_t)h * p.ksh + sc * 8;
   const uint16_t* vsrc = p.vt + (((int64_t)b * p.H + h) * 64 + srow) * p.Spad + sc * 8;
-  auto gload = [&](int k0, uint4& kr, uint4& vr) {
-    const int64_t key = min(k0 + srow, p.S - 1);  // keys past S: any valid row (their P is 0)
-    kr = *reinterpret_cast<const uint4*>(ksrc + key * p.kss);
-    vr = *reinterpret_cast<const uint4*>(vsrc + k0);
+  auto gload = [&](int k0, uint4& ka, uint4& kb, uint4& va, uint4& vb) {
+    const int64_t key = min(k0 + srow, p.S - 1);
+    const int64_t key2 = min(k0 + srow + 32, p.S - 1);
+    ka = *reinterpret_cast<const uint4*>(ksrc + key * p.kss);
+    kb = *reinterpret_cast<const uint4*>(ksrc + key2 * p.kss);
+    va = *reinterpret_cast<const uint4*>(vsrc + k0);
+    vb = *reinterpret_cast<const uint4*>(vsrc + (int64_t)32 * p.Spad + k0);
   };
-  auto lstore = [&](int bf, const uint4& kr, const uint4& vr) {
-    *reinterpret_cast<uint4*>(&ktile[bf][soff]) = kr;
-    *reinterpret_cast<uint4*>(&vtile[bf][soff]) = vr;
+  auto lstore = [&](int bf, const uint4& ka, const uint4& kb, const uint4& va, const uint4& vb) {
+    *reinterpret_cast<uint4*>(&ktile[bf][soff]) = ka;
+    *reinterpret_cast<uint4*>(&ktile[bf][soff + 4096]) = kb;
+    *reinterpret_cast<uint4*>(&vtile[bf][soff]) = va;
+    *reinterpret_cast<uint4*>(&vtile[bf][soff + 4096]) = vb;
   };
   // Operand reads: K rows 32 st + col (chunk 2 ks + half), V^T rows 32 db + col (chunk
   // 4 st + 2 ks + half); swz of these rows is swz(col).
@@ -497,13 +505,13 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
   // loads tile n + 2 into the freed registers; one barrier per tile.
   const int ntiles = p.Spad >> 6;
   const int last = (ntiles - 1) * 64;
-  uint4 kr, vr;
+  uint4 kra, krb, vra, vrb;
   {
-    uint4 k0r, v0r;
-    gload(0, k0r, v0r);
-    lstore(0, k0r, v0r);
+    uint4 a0, a1, a2, a3;
+    gload(0, a0, a1, a2, a3);
+    lstore(0, a0, a1, a2, a3);
   }
-  gload(min(64, last), kr, vr);
+  gload(min(64, last), kra, krb, vra, vrb);
   uint32_t w0[kQPW] = {mword(0, 0), mword(0, 1)}, w1[kQPW] = {mword(1, 0), mword(1, 1)};
   __syncthreads();
 #pragma unroll 1
@@ -513,8 +521,8 @@ __global__ __launch_bounds__(kDW * 64) void dense_attn_kernel(const DenseParams 
     // wait for the tile loads.
     const uint32_t wn0[kQPW] = {mword(2 * n + 2, 0), mword(2 * n + 2, 1)};
     const uint32_t wn1[kQPW] = {mword(2 * n + 3, 0), mword(2 * n + 3, 1)};
-    lstore(buf ^ 1, kr, vr);  // past the last tile: never read
-    gload(min((n + 2) * 64, last), kr, vr);
+    lstore(buf ^ 1, kra, krb, vra, vrb);  // past the last tile: never read
+    gload(min((n + 2) * 64, last), kra, krb, vra, vrb);
     sub(ktile[buf], vtile[buf], 0, w0);
     sub(ktile[buf], vtile[buf], 1, w1);
 #pragma unroll
