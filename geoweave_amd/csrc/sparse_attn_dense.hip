@@ -327,6 +327,9 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
   __shared__ __align__(16) uint8_t ktile[2][8192];
   __shared__ __align__(16) uint8_t vtile[2][8192];
   __shared__ float vsc_s[64];
+  // attn_sum: per lane a row of 16 scaled scores (rows of 20 floats: 16-byte stores of 8
+  // consecutive lanes touch distinct banks)
+  __shared__ __align__(16) float ascore[ATTN ? kDW : 1][ATTN ? 64 * 20 : 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -426,16 +429,26 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
       for (int a = 0; a < kQPW; ++a) s[a] = mma(E{}, ka, qa[a][ks], s[a]);
     }
     if constexpr (ATTN) {
-      // Each selected entry's scaled score, at the slot of its key's rank.
+      // Each selected entry's scaled score, at the slot of its key's rank. The lane's 16
+      // scores go to its LDS row, and a loop over the lane's selected entries (most lanes
+      // have none or one per sub-tile) reads each back and stores it.
+      float* st_l = &ascore[wave][lane * 20];
 #pragma unroll
       for (int a = 0; a < kQPW; ++a) {
         const uint32_t own = w[a] >> (4 * half);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kk = 8 * (r >> 2) + 4 * half + (r & 3);
-          if ((own >> (8 * (r >> 2) + (r & 3))) & 1u) {
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<float4*>(st_l + 4 * g) =
+              make_float4(s[a][4 * g] * sl2, s[a][4 * g + 1] * sl2, s[a][4 * g + 2] * sl2, s[a][4 * g + 3] * sl2);
+        // bit r = entry r (key 8(r/4) + 4 half + r%4)
+        uint32_t bits = (own & 0xFu) | ((own >> 4) & 0xF0u) | ((own >> 8) & 0xF00u) | ((own >> 12) & 0xF000u);
+        while (__builtin_amdgcn_ballot_w64(bits != 0u) != 0ull) {
+          if (bits != 0u) {
+            const int r = __builtin_ctz(bits);
+            const int kk = 8 * (r >> 2) + 4 * half + (r & 3);
             const uint32_t slot = rank_base[a] + __popc(w[a] & ((1u << kk) - 1u));
-            srow_ws[a][(int64_t)slot * p.H] = s[a][r] * sl2;
+            srow_ws[a][(int64_t)slot * p.H] = st_l[r];
+            bits &= bits - 1u;
           }
         }
         rank_base[a] += __popc(w[a]);
@@ -651,9 +664,22 @@ __global__ __launch_bounds__(256) void dense_attn_sum_kernel(const AttnSumParams
     float sum = 0.f;
     if (ok) {
       const float* sp = srow + (int64_t)i * p.H;
-      for (int h = 0; h < p.H; ++h) {
-        const float l2 = lse2_s[wave][h];
-        if (l2 != -INFINITY) sum += fexp2(sp[h] - l2);
+      if ((p.H & 3) == 0) {
+        // the slot's heads as 16-byte loads (rows of H floats, H % 4 == 0: 16-byte aligned)
+        for (int h = 0; h < p.H; h += 4) {
+          const float4 sv = *reinterpret_cast<const float4*>(sp + h);
+          const float svv[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const float l2 = lse2_s[wave][h + u];
+            if (l2 != -INFINITY) sum += fexp2(svv[u] - l2);
+          }
+        }
+      } else {
+        for (int h = 0; h < p.H; ++h) {
+          const float l2 = lse2_s[wave][h];
+          if (l2 != -INFINITY) sum += fexp2(sp[h] - l2);
+        }
       }
     }
     av[r] = sum;
@@ -768,6 +794,8 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
                      (double)softmax_scale);
   const bool want_attn = attn_sum != nullptr;
   const bool want_kl = logits != nullptr;
+  if (want_attn && H > 64)
+    return set_error(GW_ERR_UNSUPPORTED, "the dense forward computes attn_sum for H <= 64, got %lld", (long long)H);
   if (want_attn && K > kDenseAttnMaxK)
     return set_error(GW_ERR_UNSUPPORTED, "the dense forward computes attn_sum for K <= %d, got %lld", kDenseAttnMaxK,
                      (long long)K);
