@@ -194,6 +194,9 @@ def long_context_c3(steps: int = 5, warmup: int = 2, views: int = 64, topk: int 
     att_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
     B, T, H, D = q.shape
     att_bytes = attn_fwd_algorithmic_bytes(B, T, H, D, topk)
+    from geoweave_amd.custom_flash_attn import sparse_index_flash_attn as sifa
+
+    attn_path = "dense" if sifa._use_dense(T, topk, H, D, 0.125) else "gather"
 
     # The query-chunked stream (dsa_attention.py:1017-1283): same work, the indices and the
     # indexer workspace live per chunk of 16384 queries. Peak memory above the inputs.
@@ -229,6 +232,7 @@ def long_context_c3(steps: int = 5, warmup: int = 2, views: int = 64, topk: int 
         "value_ms": round(idx_ms + att_ms, 3),
         "indexer_ms": round(idx_ms, 3),
         "attn_fwd_ms": round(att_ms, 3),
+        "attn_path": attn_path,
         "attn_fwd_gbs": round(att_bytes / (att_ms * 1e-3) / 1e9, 1),
         "indexer_tflops": round(indexer_algorithmic_flops(B, T, T, qi.shape[2], qi.shape[3]) / (idx_ms * 1e-3) / 1e12, 2),
     }
@@ -547,7 +551,7 @@ def main() -> int:
     ap.add_argument("--no-sd", action="store_true", help="skip the approximate (source-downsample) top-k timing")
     ap.add_argument("--attn-path", choices=("auto", "dense", "gather"), default="auto",
                     help="attention forward without attn_sum: the masked dense pass, the gather kernel, "
-                         "or the automatic choice (dense when S <= 48 K)")
+                         "or the automatic choice (dense when S <= 96 K)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run 3 plain device copies of 1 GiB (reference kernel for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE scaling)")

@@ -94,9 +94,10 @@ def _check_inputs(q, k, v, kv_positions, bias, causal, layout):
 
 # Forward: "auto" picks the masked dense pass (gw_sparse_attn_fwd_dense) when a query
 # selects at least 1 / DENSE_MAX_RATIO of the keys (and, with attn_sum, K <=
-# DENSE_ATTN_SUM_MAX_K), "dense" / "gather" force one path (tests and measurements).
+# DENSE_ATTN_SUM_MAX_K), "dense" / "gather" force one path (tests and measurements). The
+# dense pass costs ~ T·S, the gather ~ T·K: on MI355X they break even near S = 117·K.
 FORWARD_PATH = "auto"
-DENSE_MAX_RATIO = 48
+DENSE_MAX_RATIO = 96
 DENSE_ATTN_SUM_MAX_K = 1024
 
 

@@ -346,17 +346,22 @@ int gw_source_downsample_expand(int dtype, const int32_t* coarse_idx, const void
  * 2001-2233, :129-259, :375-458, as reached from sparse_index_flash_attn_func :3286 and
  * sparse_index_flash_attn_inference_func :3138-3163; the fused KL as in gw_sparse_attn_fwd_kl);
  * it pays off when a query selects more than roughly 1 % of the keys.
- * Needs D = 64 and an even H, and K <= 1024 when attn_sum is asked for; otherwise
- * GW_ERR_UNSUPPORTED (use gw_sparse_attn_fwd / gw_sparse_attn_fwd_kl).
+ * Needs D = 64 and a positive softmax_scale, and K <= 1024 and H <= 64 when attn_sum is
+ * asked for; otherwise GW_ERR_UNSUPPORTED (use gw_sparse_attn_fwd / gw_sparse_attn_fwd_kl).
+ * The P·V product takes P in fp16 (the fp32 weights rounded to nearest, 11 significant bits)
+ * against V in fp16 scaled per (head, d) column by an exact power of two; row sums and lse
+ * come from the fp32 weights. K and V must be finite (an inf or nan in a row the query did
+ * not select reaches its products through the zero weight).
  * attn_sum (nullable) and lse: as for gw_sparse_attn_fwd (lse is required with attn_sum).
  * logits (nullable; needs attn_sum) ... row_loss: the fused KL loss, as for
  * gw_sparse_attn_fwd_kl.
  * Queries that list a position twice are computed by the gather kernel inside this call
  * (the reference counts a repeated position twice).
  * Workspace: gw_sparse_attn_fwd_dense_workspace_size(B, T, S, H, D, K, want_attn_sum) bytes,
- * 16-byte aligned: the selection mask (B * ceil(T/32) * S * 4 bytes), per-block flags, a
- * transposed copy of V (B * H * 64 * round_up(S, 64) * 2 bytes) and, with attn_sum, the
- * selected scores (B * T * K * H * 4 bytes).
+ * 16-byte aligned: the selection words (B * round_up(S, 64) / 32 * round_up(T, 256) * 4
+ * bytes), per-block flags, the |V| column maxima (B * H * 64 * 4 bytes), the scaled fp16
+ * V^T (B * H * 64 * round_up(S, 64) * 2 bytes) and, with attn_sum, the selected scores
+ * (B * T * K * H * 4 bytes).
  * ------------------------------------------------------------------------------------ */
 size_t gw_sparse_attn_fwd_dense_workspace_size(int64_t B, int64_t T, int64_t S, int64_t H, int64_t D,
                                                int64_t K, int want_attn_sum);
