@@ -3,8 +3,10 @@ fp32 CPU oracle and the gather kernel.
 
 The dense pass computes every (query, key) product on the matrix cores and masks the keys a
 query did not select; o and lse must equal the sparse attention's. Tolerance: 2e-2 abs/rel for
-bf16/fp16 outputs (P enters the P·V product as hi + lo 16-bit parts, close to the gather
-kernel's fp32 p), 1e-4 for lse. Cases: the layer's per-view shape in bf16 and fp16, ragged -1
+bf16/fp16 outputs (P enters the P·V product in fp16 against V scaled per column by a power of
+two; the row sums add the fp32 weights), 1e-4 for lse. Cases: V columns far outside the fp16
+range and far below it (the per-column scaling), odd head counts, a softmax scale other than
+1/8, the layer's per-view shape in bf16 and fp16, ragged -1
 padding with T and S not multiples of 32 or 64, cross attention (T != S), empty rows,
 out-of-range and repeated positions (repeats go to the gather kernel inside the call, also
 when the mask is built in several key chunks), scores with a large dynamic range rising along
@@ -234,3 +236,43 @@ def test_fused_kl_rows_match_the_gather_kernel(gpu_device):
     torch.testing.assert_close(kd, kg, atol=1e-5, rtol=1e-4)
     _, ad2, _, _ = _run_attn(q, k, v, pos)
     assert torch.equal(ad, ad2), "the fused KL must not change attn_sum"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_v_columns_outside_the_fp16_range(gpu_device, dtype):
+    # V enters the product in fp16 scaled per (head, column) by 2^e: columns with |v| up to
+    # 1e9 (bf16; 3e3 for fp16 inputs), down to 1e-9, and an all-zero column keep their
+    # relative precision.
+    B, T, S, H, K = 1, 200, 700, 2, 96
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(B, T, H, 64, generator=g).to(dtype)
+    k = torch.randn(B, S, H, 64, generator=g).to(dtype)
+    big = 1e9 if dtype == torch.bfloat16 else 3e3
+    col = torch.ones(64)
+    col[:16] = big
+    col[16:32] = 1e-9 if dtype == torch.bfloat16 else 1e-4
+    col[32] = 0.0
+    v = (torch.randn(B, S, H, 64, generator=g) * col).to(dtype)
+    pos = _distinct_positions(B, T, S, K, seed=5)
+    print(f"[dense V scaling] {dtype}", flush=True)
+    o, lse = _run(q, k, v, pos, scale=0.125)
+    ro, rl = oatt.sparse_attention(q, k, v, pos, 0.125)[0::2]
+    w = col.clamp_min(1e-30).view(1, 1, 1, 64)  # compare each column at its own scale
+    torch.testing.assert_close(o / w, ro.float() / w, **TOL)
+    assert torch.all(o[..., 32] == 0)
+    torch.testing.assert_close(lse, rl, atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("H", [1, 3])
+def test_odd_head_counts_and_scale(gpu_device, H):
+    B, T, S, K = 2, 150, 333, 40
+    g = torch.Generator().manual_seed(H)
+    q = torch.randn(B, T, H, 64, generator=g).bfloat16()
+    k = torch.randn(B, S, H, 64, generator=g).bfloat16()
+    v = torch.randn(B, S, H, 64, generator=g).bfloat16()
+    pos = _distinct_positions(B, T, S, K, seed=H + 3)
+    print(f"[dense odd heads] H={H}", flush=True)
+    o, lse = _run(q, k, v, pos, scale=0.3)
+    ro, rl = oatt.sparse_attention(q, k, v, pos, 0.3)[0::2]
+    torch.testing.assert_close(o, ro.float(), **TOL)
+    torch.testing.assert_close(lse, rl, atol=1e-4, rtol=1e-4)
