@@ -283,6 +283,8 @@ struct DenseParams {
   int K;
 };
 
+// Keeps the compiler from moving LDS accesses across this point; within one wave the LDS
+// performs them in issue order, so no barrier is needed between a wave's own write and read.
 __device__ __forceinline__ void lds_fence() { asm volatile("" ::: "memory"); }
 
 __device__ __forceinline__ uint16_t to_half_bits(BF16, float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
