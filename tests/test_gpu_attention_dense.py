@@ -135,7 +135,7 @@ def test_bhtd_matches_bthd_and_is_deterministic(gpu_device):
     assert torch.equal(o1, o3) and torch.equal(l1, l3)
 
 
-@pytest.mark.parametrize("views", [16])
+@pytest.mark.parametrize("views", [16, 64])  # 64 views: N = 87,936, the C3 shape
 def test_full_size_sampled_rows(gpu_device, views):
     q, k, v = workloads.attention_inputs(views, 1, torch.bfloat16)
     n = q.shape[1]
