@@ -83,7 +83,9 @@ __global__ __launch_bounds__(256) void dense_mask_kernel(const int32_t* __restri
   // [key / 32][query], rows padded to 33 words so that one query's atomics spread over banks
   __shared__ uint32_t words[(kMaskChunk / 32) * 33];
   __shared__ int dup_any;
-  const int qb = blockIdx.x, chunk = blockIdx.y, b = blockIdx.z;
+  // The chunks of one block are consecutive workgroups: they run together and share the
+  // block's positions through the caches.
+  const int chunk = blockIdx.x, qb = blockIdx.y, b = blockIdx.z;
   const int c0 = chunk * kMaskChunk;
   const int len = min(kMaskChunk, S - c0);
   const int nkt = min(kMaskChunk, Spad - c0) >> 5;
@@ -819,7 +821,7 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
     GW_CHECK_ARG(eps >= 0.f, "eps must be non-negative, got %g", (double)eps);
   }
   const DenseLayout L = dense_layout(B, T, S, H, K, want_attn);
-  GW_CHECK_ARG((int64_t)(L.nqb_pad / kQBW) * H < (1ll << 31), "too many query blocks");
+  GW_CHECK_ARG((int64_t)(L.nqb_pad / kQBW) * H < (1ll << 31) && L.nqb_pad <= 65535, "too many query blocks");
   GW_CHECK_ARG(workspace != nullptr && workspace_bytes >= L.total && aligned16(workspace),
                "the dense forward needs a 16-byte aligned %zu-byte workspace, got %zu", L.total, workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -836,7 +838,7 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
                      (reinterpret_cast<uintptr_t>(kv_pos) & 15) == 0)
                         ? 1
                         : 0;
-    hipLaunchKernelGGL(dense_mask_kernel, dim3(L.nqb_pad, L.nchunk, (unsigned)B), dim3(256), 0, st, kv_pos,
+    hipLaunchKernelGGL(dense_mask_kernel, dim3(L.nchunk, L.nqb_pad, (unsigned)B), dim3(256), 0, st, kv_pos,
                        pos_stride_b, pos_stride_t, (int)T, (int)S, L.spad, (int)K, L.nqb, L.nqb_pad * 32, L.nchunk,
                        vec, (int)(H * 64), mask, flags, vmax);
     GW_HIP_LAUNCH_CHECK("dense_mask_kernel launch");
