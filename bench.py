@@ -49,8 +49,7 @@ def attn_fwd_algorithmic_bytes(B, T, H, D, K, elt=2):
 
 def attn_fwd_dense_flops(B, T, S, H, D):
     """4 * B * T * S * H * D: the Q.K^T and P.V products over every (query, key) pair of the
-    masked dense formulation (the hi/lo split of P, which doubles the P.V instructions, is
-    not counted)."""
+    masked dense formulation (what the kernel executes: one MFMA flop per counted flop)."""
     return 4 * B * T * S * H * D
 
 
