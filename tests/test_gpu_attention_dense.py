@@ -276,3 +276,35 @@ def test_odd_head_counts_and_scale(gpu_device, H):
     ro, rl = oatt.sparse_attention(q, k, v, pos, 0.3)[0::2]
     torch.testing.assert_close(o, ro.float(), **TOL)
     torch.testing.assert_close(lse, rl, atol=1e-4, rtol=1e-4)
+
+
+def _random_shape(seed):
+    g = torch.Generator().manual_seed(1000 + seed)
+    r = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))
+    S = r(1, 2100)
+    return dict(B=r(1, 2), T=r(1, 700), S=S, H=r(1, 5), K=r(1, min(S, 300)),
+                inv=float(torch.rand(1, generator=g)) * 0.5,
+                dtype=torch.bfloat16 if seed % 2 == 0 else torch.float16, seed=seed)
+
+
+@pytest.mark.parametrize("case", [_random_shape(i) for i in range(12)],
+                         ids=lambda c: f"B{c['B']}T{c['T']}S{c['S']}H{c['H']}K{c['K']}")
+def test_random_shapes_against_the_oracle(gpu_device, case):
+    # Seeded random sizes (T, S not multiples of 32 or 64, S below one tile, small K, ragged
+    # -1 padding of distinct positions): o, lse and attn_sum at the stated bars.
+    B, T, S, H, K, dt = case["B"], case["T"], case["S"], case["H"], case["K"], case["dtype"]
+    g = torch.Generator().manual_seed(case["seed"])
+    q = torch.randn(B, T, H, 64, generator=g).to(dt)
+    k = torch.randn(B, S, H, 64, generator=g).to(dt)
+    v = torch.randn(B, S, H, 64, generator=g).to(dt)
+    pos = workloads.random_positions(B, T, S, K, seed=case["seed"], invalid_fraction=case["inv"])
+    print(f"[dense random] {case}", flush=True)
+    ro, ra, rl = oatt.sparse_attention(q, k, v, pos, 0.125)
+    o, lse = _run(q, k, v, pos, scale=0.125)
+    torch.testing.assert_close(o, ro.float(), **TOL)
+    torch.testing.assert_close(lse, rl, atol=1e-4, rtol=1e-4)
+    if K <= 1024:
+        o2, attn, lse2, _ = _run_attn(q, k, v, pos, scale=0.125)
+        torch.testing.assert_close(o2, ro.float(), **TOL)
+        torch.testing.assert_close(attn, ra, atol=1e-4, rtol=1e-3)
+        torch.testing.assert_close(lse2, rl, atol=1e-4, rtol=1e-4)
