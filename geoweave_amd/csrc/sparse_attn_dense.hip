@@ -278,9 +278,9 @@ struct DenseParams {
   int64_t osb, ost, osh;
   int T, S, Spad, H, nqb, tpad, nchunk;
   float scale_log2;
-  // attn_sum (ATTN kernels only): the scaled score of every selected (query, key) and head,
-  // sws[((b * T + t) * K + slot) * H + h], slot = rank of the key among the query's
-  // selected keys in ascending key order.
+  // attn_sum (ATTN kernels only): the score q.k (not yet scaled) of every selected (query,
+  // key) and head, sws[((b * T + t) * K + slot) * H + h], slot = rank of the key among the
+  // query's selected keys in ascending key order.
   float* sws;
   int K;
 };
@@ -331,7 +331,7 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
   __shared__ __align__(16) uint8_t ktile[2][8192];
   __shared__ __align__(16) uint8_t vtile[2][8192];
   __shared__ float vsc_s[64];
-  // attn_sum: per lane a row of 16 scaled scores (rows of 20 floats: 16-byte stores of 8
+  // attn_sum: per lane a row of 16 scores (rows of 20 floats: 16-byte stores of 8
   // consecutive lanes touch distinct banks)
   __shared__ __align__(16) float ascore[ATTN ? kDW : 1][ATTN ? 64 * 20 : 4];
 
@@ -433,8 +433,8 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
       for (int a = 0; a < kQPW; ++a) s[a] = mma(E{}, ka, qa[a][ks], s[a]);
     }
     if constexpr (ATTN) {
-      // Each selected entry's scaled score, at the slot of its key's rank. The lane's 16
-      // scores go to its LDS row, and a loop over the lane's selected entries (most lanes
+      // Each selected entry's score (unscaled: dense_attn_sum_kernel applies the scale), at
+      // the slot of its key's rank. The lane's 16 scores go to its LDS row, and a loop over the lane's selected entries (most lanes
       // have none or one per sub-tile) reads each back and stores it.
       float* st_l = &ascore[wave][lane * 20];
 #pragma unroll
@@ -442,8 +442,7 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
         const uint32_t own = w[a] >> (4 * half);
 #pragma unroll
         for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<float4*>(st_l + 4 * g) =
-              make_float4(s[a][4 * g] * sl2, s[a][4 * g + 1] * sl2, s[a][4 * g + 2] * sl2, s[a][4 * g + 3] * sl2);
+          *reinterpret_cast<float4*>(st_l + 4 * g) = make_float4(s[a][4 * g], s[a][4 * g + 1], s[a][4 * g + 2], s[a][4 * g + 3]);
         // bit r = entry r (key 8(r/4) + 4 half + r%4)
         uint32_t bits = (own & 0xFu) | ((own >> 4) & 0xF0u) | ((own >> 8) & 0xF00u) | ((own >> 12) & 0xF000u);
         while (__builtin_amdgcn_ballot_w64(bits != 0u) != 0ull) {
@@ -591,7 +590,7 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
 // ---------------------------------------------------------------------------------------
 // attn_sum from the slot-indexed scores: one wave per query row. The row's valid positions,
 // sorted ascending, are in slot order: slot i holds the i-th smallest selected key. So
-// attn_sum[t, j] = sum_h exp2(sws[t, i(j), h] - lse2[t, h]) with i(j) the rank of position j
+// attn_sum[t, j] = sum_h exp2(sws[t, i(j), h] * scale log2(e) - lse2[t, h]) with i(j) the rank of position j
 // (a wave bitonic sort of (position, j)); invalid positions give 0. With KL, the row's
 // indexer KL loss follows from the same registers (the per-row term of
 // sparse_indexer_kl_loss, indexer_kl_fused.py:8-155, as in the gather kernel's epilogue).
@@ -610,6 +609,7 @@ struct AttnSumParams {
   float kl_eps;
   float* row_loss;
   int B, T, S, H, K, nqb, nchunk;
+  float scale_log2;  // sws holds unscaled scores
 };
 
 __device__ __forceinline__ float as_load(int dt, const void* base, int64_t i) {
@@ -676,13 +676,13 @@ __global__ __launch_bounds__(256) void dense_attn_sum_kernel(const AttnSumParams
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             const float l2 = lse2_s[wave][h + u];
-            if (l2 != -INFINITY) sum += fexp2(svv[u] - l2);
+            if (l2 != -INFINITY) sum += fexp2(fmaf(svv[u], p.scale_log2, -l2));
           }
         }
       } else {
         for (int h = 0; h < p.H; ++h) {
           const float l2 = lse2_s[wave][h];
-          if (l2 != -INFINITY) sum += fexp2(sp[h] - l2);
+          if (l2 != -INFINITY) sum += fexp2(fmaf(sp[h], p.scale_log2, -l2));
         }
       }
     }
@@ -909,6 +909,7 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
     ap.K = (int)K;
     ap.nqb = L.nqb;
     ap.nchunk = L.nchunk;
+    ap.scale_log2 = p.scale_log2;
     const int rows = (int)(B * T);
     const int rc = want_kl ? launch_attn_sum<true>(ap, rows, st) : launch_attn_sum<false>(ap, rows, st);
     if (rc != GW_OK) return rc;
