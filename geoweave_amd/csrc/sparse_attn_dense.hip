@@ -457,29 +457,36 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
         rank_base[a] += __popc(w[a]);
       }
     }
-    // Weights with the current reference maximum. Their sum bounds each weight: while no
-    // lane's sum exceeds kSumCap every p fits fp16, and the maximum stays where it is.
-    float pv[kQPW][16], ls[kQPW];
+    // Per block: the weights, then its P·V products, so that the second block's exp2 (which
+    // co-executes with matrix products on this GPU, unlike fp32 VALU) overlaps the first
+    // block's products. The V^T operands are read once for both blocks.
+    uint4 va[2][2];
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) va[db][ks] = *reinterpret_cast<const uint4*>(vt + voff(db, st, ks));
 #pragma unroll
     for (int a = 0; a < kQPW; ++a) {
-      const float nm = -m[a];
+      // Weights with the current reference maximum. Their sum bounds each weight: while no
+      // lane's sum exceeds kSumCap every p fits fp16, and the maximum stays where it is.
+      float pv[16];
+      float ls = 0.f;
+      {
+        const float nm = -m[a];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) pv[a][r] = fexp2(fmaf(s[a][r], sl2, nm));
-      ls[a] = 0.f;
+        for (int r = 0; r < 16; ++r) pv[r] = fexp2(fmaf(s[a][r], sl2, nm));
 #pragma unroll
-      for (int r = 0; r < 16; ++r) ls[a] += pv[a][r];  // fixed order
-    }
-    if (__builtin_amdgcn_ballot_w64(!(ls[0] <= kSumCap) || !(ls[1] <= kSumCap)) != 0ull) {
-      // Some query of the wave has an entry above its maximum by more than log2(kSumCap /
-      // 16) (or its first selected entry): every query moves its maximum to the largest
-      // selected entry of this sub-tile if that is higher, rescales O and the row sum, and
-      // the weights are formed again.
-#pragma unroll
-      for (int a = 0; a < kQPW; ++a) {
+        for (int r = 0; r < 16; ++r) ls += pv[r];
+      }
+      if (__builtin_amdgcn_ballot_w64(!(ls <= kSumCap)) != 0ull) {
+        // Some query of the block has an entry above its maximum by more than log2(kSumCap /
+        // 16) (or its first selected entry): every query of the block moves its maximum to
+        // its largest selected entry of this sub-tile if that is higher, rescales O and the
+        // row sum, and the weights are formed again.
         float mx = s[a][0];
 #pragma unroll
         for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[a][r]);
-        const float mn = fmaxf(m[a], pair_max(mx) * sl2);  // unselected entries are -inf
+        const float mn = fmaxf(m[a], pair_max(mx) * sl2);
         const float alpha = fexp2(m[a] - mn);
         m[a] = mn;
         l[a] *= alpha;
@@ -489,31 +496,24 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
           for (int r = 0; r < 16; ++r) acc[a][db][r] *= alpha;
         const float nm = -mn;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) pv[a][r] = fexp2(fmaf(s[a][r], sl2, nm));
-        ls[a] = 0.f;
+        for (int r = 0; r < 16; ++r) pv[r] = fexp2(fmaf(s[a][r], sl2, nm));
+        ls = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ls[a] += pv[a][r];
+        for (int r = 0; r < 16; ++r) ls += pv[r];
       }
-    }
-    uint4 pb[kQPW][2];
-#pragma unroll
-    for (int a = 0; a < kQPW; ++a) {
       // Row sums of the fp32 weights (as the gather kernel's): lse and the attn_sum
       // normalisation do not see the fp16 rounding of the product's operand.
-      l[a] += ls[a];
+      l[a] += ls;
+      uint4 pb[2];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        pb[a][ks] = make_uint4(pack_f16(pv[a][8 * ks], pv[a][8 * ks + 1]), pack_f16(pv[a][8 * ks + 2], pv[a][8 * ks + 3]),
-                               pack_f16(pv[a][8 * ks + 4], pv[a][8 * ks + 5]), pack_f16(pv[a][8 * ks + 6], pv[a][8 * ks + 7]));
+        pb[ks] = make_uint4(pack_f16(pv[8 * ks], pv[8 * ks + 1]), pack_f16(pv[8 * ks + 2], pv[8 * ks + 3]),
+                            pack_f16(pv[8 * ks + 4], pv[8 * ks + 5]), pack_f16(pv[8 * ks + 6], pv[8 * ks + 7]));
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) acc[a][db] = mma(FP16{}, va[db][ks], pb[ks], acc[a][db]);
     }
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const uint4 va = *reinterpret_cast<const uint4*>(vt + voff(db, st, ks));
-#pragma unroll
-        for (int a = 0; a < kQPW; ++a) acc[a][db] = mma(FP16{}, va, pb[a][ks], acc[a][db]);
-      }
   };
 
   // Tile n (64 keys) lives in LDS buffer n % 2. While computing tile n a thread stores tile
