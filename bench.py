@@ -12,14 +12,16 @@ config "Metric row": B = 1, S = 32 views x 1374 tokens (N = 43,968), 16 heads x 
 indexer 4 heads x 64, top-k 1024, bf16.
 
 Printed: ONE JSON line. ``value`` = indexer ms + attention-forward ms per layer (lower is
-better), ``roofline`` = the attention forward (the dominant kernels) against the HBM
-roofline on the algorithmic bytes of the sparse attention (the gathered K/V rows), timed
-live with HIP events on the stream the kernels run on, ``roofline_dense_mfma`` = the same
-call against the bf16 MFMA roofline on the flops of its masked dense formulation (every
-(query, key) product: 4*B*T*S*H*D), ``roofline_indexer`` = the indexer against the bf16
-MFMA roofline,
-``cpu_baseline`` = the fp32 CPU oracle (the restatement of the reference's torch backend)
-on a bounded sample of query rows of the same layer, scaled to the full layer.
+better). ``roofline`` = the attention forward (the dominant call) against the roofline of
+what it executes, timed live with HIP events on the stream the kernels run on: for the
+masked dense pass the bf16 MFMA roofline on its flops (every (query, key) product,
+4*B*T*S*H*D), for the gather kernel the HBM roofline on the gathered K/V bytes.
+``attn_effective_gathered_bandwidth`` = the sparse formulation's gathered bytes over the
+same time (a rate, not a roofline, for the dense pass). ``roofline_indexer`` = the indexer
+against the bf16 MFMA roofline. ``cpu_baseline`` = the fp32 CPU oracle (the restatement of
+the reference's torch backend) on a fixed sample of query rows of the same layer (median of
+3 passes, scaled to the full layer), plus config C1 timed in full (median of 3 runs) beside
+the GPU's C1 time.
 """
 from __future__ import annotations
 
@@ -428,22 +430,9 @@ def aggregator_c5(steps: int = 2, warmup: int = 1, views: int = 32, topk: int = 
     from geoweave_amd import aggregator as agg
 
     dev = torch.device("cuda", 0)
-    torch.manual_seed(20261201)
     with torch.device(dev):
         m = agg.Aggregator(indexer_layers="9-19", topk=topk)
-    with torch.no_grad():
-        for name, p in m.named_parameters():
-            if p.dim() >= 2:
-                p.normal_(0.0, p[0].numel() ** -0.5)
-            elif name.endswith("gamma"):
-                p.fill_(0.1)
-            elif "norm" in name and name.endswith("weight"):
-                p.normal_(1.0, 0.1)
-            elif "w_proj" in name:
-                p.fill_(1.0)
-            else:
-                p.normal_(0.0, 0.02)
-    m = m.to(torch.bfloat16)
+    m = agg.random_init_(m, 20261201).to(torch.bfloat16)
     g = torch.Generator(device=dev).manual_seed(20261201 + views)
     images = torch.rand(1, views, 3, 518, 518, generator=g, device=dev)
     stream = torch.cuda.current_stream(dev)
@@ -488,48 +477,111 @@ def aggregator_c5(steps: int = 2, warmup: int = 1, views: int = 32, topk: int = 
     }
 
 
-def cpu_baseline(views: int, budget_s: float, rows_per_chunk: int = 128):
-    """Times the fp32 CPU oracle (indexer scores + top-k + sparse attention) on query
-    rows of the same layer until ``budget_s`` seconds have elapsed; scales to all rows."""
-    import torch
+def cpu_model() -> str:
+    """The host CPU's model name (``/proc/cpuinfo``), or the platform's fallback."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
-    from geoweave_amd import workloads
+
+def _oracle_layer(qi, ki, wi, q, k, v, rows, topk=1024):
+    """(indexer s, attention s) of the fp32 CPU oracle on the given query rows."""
     from oracle import attention as oatt
     from oracle import indexer as oidx
 
+    t0 = time.perf_counter()
+    idx, _ = oidx.indexer_topk(qi[:, rows], ki, wi, None, topk, 0.125)
+    t1 = time.perf_counter()
+    oatt.sparse_attention(q[:, rows], k, v, idx, 0.125)
+    t2 = time.perf_counter()
+    return t1 - t0, t2 - t1
+
+
+def cpu_baseline(views: int, sample_rows: int = 2048, runs: int = 3, c1_gpu_ms=None):
+    """The fp32 CPU oracle (the restatement of the reference's torch backend: indexer scores
+    + torch.topk + the gathered sparse attention) on the host cores.
+
+    * ``value``: the metric's workload (S = ``views``) on a fixed sample of ``sample_rows``
+      random query rows against all keys, median of ``runs`` passes after a warm-up pass,
+      scaled to all rows (per-row cost does not depend on which rows).
+    * ``c1_full``: config C1 (S = 4, N = 5,496) over every row, median of ``runs`` runs
+      after a warm-up run, the indexer and the attention timed separately, beside the GPU's
+      time for the same C1 step."""
+    import torch
+
+    from geoweave_amd import workloads
+
     torch.set_num_threads(os.cpu_count() or 1)
-    qi, ki, wi = workloads.indexer_inputs(views, 1, torch.bfloat16)
-    q, k, v = workloads.attention_inputs(views, 1, torch.bfloat16)
-    qi, ki, wi, q, k, v = (x.float() for x in (qi, ki, wi, q, k, v))
-    n = q.shape[1]
-    g = torch.Generator().manual_seed(0)
-    order = torch.randperm(n, generator=g)
-    done = 0
-    t_idx = t_att = 0.0
-    while done < n and (t_idx + t_att) < budget_s:
-        rows = order[done:done + rows_per_chunk]
-        t0 = time.perf_counter()
-        idx, _ = oidx.indexer_topk(qi[:, rows], ki, wi, None, 1024, 0.125)
-        t1 = time.perf_counter()
-        oatt.sparse_attention(q[:, rows], k, v, idx, 0.125)
-        t2 = time.perf_counter()
-        t_idx += t1 - t0
-        t_att += t2 - t1
-        done += rows.numel()
-    scale = n / done
-    total_ms = (t_idx + t_att) * scale * 1e3
+    lay = workloads.layer_inputs(views, 1, torch.bfloat16)
+    t = [x.float() for x in (lay.q_idx, lay.k_idx, lay.w_idx, lay.q, lay.k, lay.v)]
+    n = lay.tokens
+    rows = torch.randperm(n, generator=torch.Generator().manual_seed(0))[:sample_rows]
+    _oracle_layer(*t, rows)
+    passes = [_oracle_layer(*t, rows) for _ in range(runs)]
+    scale = n / rows.numel()
+    med = sorted(passes, key=sum)[len(passes) // 2]
+    del lay, t
+    c1 = workloads.layer_inputs(4, 1, torch.bfloat16)
+    t = [x.float() for x in (c1.q_idx, c1.k_idx, c1.w_idx, c1.q, c1.k, c1.v)]
+    all_rows = torch.arange(c1.tokens)
+    _oracle_layer(*t, all_rows)
+    c1_runs = [_oracle_layer(*t, all_rows) for _ in range(runs)]
+    c1_med = sorted(c1_runs, key=sum)[len(c1_runs) // 2]
+    c1_ms = sum(c1_med) * 1e3
     return {
-        "value": round(total_ms, 1),
+        "value": round(sum(med) * scale * 1e3, 1),
         "unit": "ms",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"fp32 CPU oracle (indexer scores + torch.topk + gathered sparse attention) on "
-                   f"{done} random query rows of the S={views} layer against all {n} keys, "
-                   f"{t_idx + t_att:.1f} s, scaled x{scale:.1f} to all rows"),
-        "indexer_ms": round(t_idx * scale * 1e3, 1),
-        "attn_fwd_ms": round(t_att * scale * 1e3, 1),
-        "cpu_model": platform.processor() or platform.machine(),
+        "sample": (f"fp32 CPU oracle (indexer scores + torch.topk + gathered sparse attention) on a fixed "
+                   f"sample of {rows.numel()} random query rows of the S={views} layer against all {n} keys, "
+                   f"median of {runs} passes after a warm-up ({sum(med):.1f} s), scaled x{scale:.2f} to all rows"),
+        "indexer_ms": round(med[0] * scale * 1e3, 1),
+        "attn_fwd_ms": round(med[1] * scale * 1e3, 1),
+        "cpu_model": cpu_model(),
+        "c1_full": {
+            "workload": f"C1: B=1, S=4 views (N={c1.tokens}), every query row, fp32, top-k 1024",
+            "runs_ms": [round(sum(r) * 1e3, 1) for r in c1_runs],
+            "median_ms": round(c1_ms, 1),
+            "indexer_ms": round(c1_med[0] * 1e3, 1),
+            "attn_fwd_ms": round(c1_med[1] * 1e3, 1),
+            "gpu_ms": c1_gpu_ms,
+            "cpu_over_gpu": None if not c1_gpu_ms else round(c1_ms / c1_gpu_ms, 1),
+        },
     }
+
+
+def gpu_step_ms(views: int, topk: int = 1024, steps: int = 10, warmup: int = 3) -> float:
+    """GPU time of one metric step (indexer top-k + inference attention) at S = ``views``
+    (HIP events on the launch stream, mean over ``steps``)."""
+    import torch
+
+    from geoweave_amd import workloads
+    from geoweave_amd.custom_flash_attn.sparse_index_flash_attn import sparse_index_flash_attn_inference_func
+    from geoweave_amd.custom_indexer import sparse_topk_indexer_inference_func
+
+    dev = torch.device("cuda", 0)
+    lay = workloads.layer_inputs(views, 1, torch.bfloat16)
+    qi, ki, wi, q, k, v = (x.to(dev) for x in (lay.q_idx, lay.k_idx, lay.w_idx, lay.q, lay.k, lay.v))
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        idx, _ = sparse_topk_indexer_inference_func(qi, ki, wi, qi.new_empty(0), topk, 0.125, 256, 0)
+        sparse_index_flash_attn_inference_func(q, k, v, idx, softmax_scale=0.125)
+
+    for _ in range(warmup):
+        step()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return round(e0.elapsed_time(e1) / steps, 3)
 
 
 def main() -> int:
@@ -539,7 +591,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--views", type=int, default=32)
     ap.add_argument("--topk", type=int, default=1024)
-    ap.add_argument("--cpu-budget-s", type=float, default=15.0)
+    ap.add_argument("--cpu-sample-rows", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--with-attn-sum", action="store_true",
                     help="also time the training forward that writes attn_sum")
@@ -670,9 +722,20 @@ def main() -> int:
         "indexer_ms": round(idx_avg, 3),
         "attn_fwd_ms": round(att_avg, 3),
         "attn_path": "dense" if dense_used else "gather",
-        "roofline": {
-            "kernel": ("dense_attn_kernel (+ dense_mask_kernel, dense_vt_kernel: one attention call)"
-                       if dense_used else "sparse_attn_fwd_kernel"),
+        # The roofline of what runs: the masked dense pass is bound by the matrix cores on
+        # the flops it executes; the gather kernel by HBM on the bytes it gathers.
+        "roofline": ({
+            "kernel": "dense_attn_kernel (one attention call: + dense_mask_kernel, dense_vmax_kernel, "
+                      "dense_vt_kernel)",
+            "bound": "mfma",
+            "achieved": round(dense_tflops, 2),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(dense_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": traffic,
+            "algorithmic_flops": dense_flops,
+        } if dense_used else {
+            "kernel": "sparse_attn_fwd_kernel",
             "bound": "hbm",
             "achieved": round(att_gbs, 1),
             "peak": HBM_PEAK_GBS,
@@ -680,15 +743,15 @@ def main() -> int:
             "frac": round(att_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "algorithmic_bytes": att_bytes,
-        },
-        "roofline_dense_mfma": None if not dense_used else {
-            "kernel": "dense_attn_kernel (+ dense_mask_kernel, dense_vt_kernel: one attention call)",
-            "bound": "mfma",
-            "achieved": round(dense_tflops, 2),
-            "peak": MFMA_BF16_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(dense_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-            "dense_flops": dense_flops,
+        }),
+        # The sparse formulation's bytes (the selected K/V rows the reference gathers) over
+        # the call's time: an effective rate of the whole attention, not a roofline of the
+        # dense pass (which does not move these bytes).
+        "attn_effective_gathered_bandwidth": {
+            "gathered_bytes": att_bytes,
+            "achieved": round(att_gbs, 1),
+            "unit": "GB/s",
+            "vs_hbm_peak": round(att_gbs / HBM_PEAK_GBS, 4),
         },
         "roofline_indexer": {
             "kernels": "indexer_score_kernel<sample>+select<tau>+score<filter>+select<final>+fallback",
@@ -734,7 +797,8 @@ def main() -> int:
     if not args.no_cpu_baseline:
         del lay
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(views, args.cpu_budget_s)
+        c1_gpu = gpu_step_ms(4, topk)
+        result["cpu_baseline"] = cpu_baseline(views, args.cpu_sample_rows, c1_gpu_ms=c1_gpu)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

@@ -44,11 +44,17 @@ def build(pos: torch.Tensor, src_len: int, cache: bool = True) -> Tuple[torch.Te
     lib = _lib.load()
     nbytes = int(lib.gw_kv_csr_size(bsz, tgt_len, src_len, num_kv))
     csr = torch.empty(nbytes, device=pos.device, dtype=torch.uint8)
+    # the sort's ping-pong buffers are transient: torch's caching allocator takes the block
+    # back when this tensor dies (after the queued kernels, on this stream), so only the
+    # table itself stays cached
+    ws_bytes = int(lib.gw_kv_csr_build_workspace_size(bsz, tgt_len, src_len, num_kv))
+    ws = torch.empty(ws_bytes, device=pos.device, dtype=torch.uint8)
     rc = lib.gw_kv_csr_build(
         pos.data_ptr(), pos.stride(0), pos.stride(1), bsz, tgt_len, src_len, num_kv,
-        csr.data_ptr(), nbytes, _lib.stream_handle(pos.device),
+        csr.data_ptr(), nbytes, ws.data_ptr(), ws_bytes, _lib.stream_handle(pos.device),
     )
     _lib.check(rc, "gw_kv_csr_build")
+    del ws
     if cache:
         with _lock:
             _cache.append((key, pos, csr))

@@ -41,7 +41,8 @@ _SIGNATURES = {
          ctypes.c_int, _p, _p, _p, _sz, _p],
     ),
     "gw_kv_csr_size": (_sz, [_i64, _i64, _i64, _i64]),
-    "gw_kv_csr_build": (ctypes.c_int, [_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _sz, _p]),
+    "gw_kv_csr_build_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
+    "gw_kv_csr_build": (ctypes.c_int, [_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _sz, _p, _sz, _p]),
     "gw_sparse_attn_bwd_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "gw_sparse_attn_bwd": (
         ctypes.c_int,

@@ -332,6 +332,27 @@ class Aggregator(nn.Module):
         return outputs, self.patch_start_idx
 
 
+def random_init_(model: Aggregator, seed: int = 20261201) -> Aggregator:
+    """Random-init the aggregator in place (no checkpoint exists offline): matrices and
+    convolution kernels ~ N(0, 1/fan_in), LayerScale gammas 0.1, LayerNorm gains
+    1 + N(0, 0.1), the indexer gate bias 1 (its reference init, ``indexer.py:63-68``), other
+    vectors ~ N(0, 0.02). Draws on the parameters' device."""
+    torch.manual_seed(seed)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if p.dim() >= 2:
+                p.normal_(0.0, p[0].numel() ** -0.5)
+            elif name.endswith("gamma"):
+                p.fill_(0.1)
+            elif "norm" in name and name.endswith("weight"):
+                p.normal_(1.0, 0.1)
+            elif "w_proj" in name:
+                p.fill_(1.0)
+            else:
+                p.normal_(0.0, 0.02)
+    return model
+
+
 class AggregatorGraph:
     """One HIP graph per input shape replaying the whole aggregator forward on static
     buffers (the reference's CUDA-graph "fullchain" path, ``dsa_attention.py:1600-1675``,

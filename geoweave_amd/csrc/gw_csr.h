@@ -11,10 +11,12 @@ namespace gw {
 // per-key reductions stay balanced when a few keys are chosen by many queries.
 constexpr int kCsrChunk = 2048;
 
+// The table (what the backward passes read) and, separately, the build's transient
+// workspace (the radix sort's key/value ping-pong buffers and digit counts).
 struct CsrLayout {
   int64_t nk = 0;  // keys = B * S
-  size_t header = 0, count = 0, off = 0, item_off = 0, part_off = 0, item_key = 0, entries = 0, scratch = 0,
-         hist = 0, raw = 0, total = 0;
+  size_t header = 0, count = 0, off = 0, item_off = 0, part_off = 0, item_key = 0, entries = 0, total = 0;
+  size_t scratch = 0, hist = 0, raw = 0, ws_total = 0;  // offsets into the build workspace
   int64_t max_items = 0;  // upper bound of header[0]
   int64_t max_parts = 0;  // upper bound of header[1]
 };

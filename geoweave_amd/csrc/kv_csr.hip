@@ -320,11 +320,13 @@ CsrLayout csr_layout(int64_t B, int64_t T, int64_t S, int64_t K) {
   L.max_items = (int64_t)nk + (int64_t)((ne + kCsrChunk - 1) / kCsrChunk);
   L.item_key = take((size_t)L.max_items * 4);
   L.entries = take(ne * 8);
+  L.total = o;
+  o = 0;
   L.scratch = take(ne * 16);
   const size_t tiles = (ne + kTile - 1) / kTile;
   L.hist = take((tiles + 1) * 64 * 4);  // [64][tiles] counts + [64] digit totals
   L.raw = take(tiles * 64 * 4);         // [64][tiles] counts
-  L.total = o;
+  L.ws_total = o;
   L.max_parts = 2 * (int64_t)((ne + kCsrChunk - 1) / kCsrChunk);
   return L;
 }
@@ -349,8 +351,14 @@ extern "C" size_t gw_kv_csr_size(int64_t B, int64_t T, int64_t S, int64_t K) {
   return gw::csr_layout(B, T, S, K).total;
 }
 
+extern "C" size_t gw_kv_csr_build_workspace_size(int64_t B, int64_t T, int64_t S, int64_t K) {
+  if (B <= 0 || T <= 0 || S <= 0 || K <= 0) return 256;
+  return gw::csr_layout(B, T, S, K).ws_total;
+}
+
 extern "C" int gw_kv_csr_build(const int32_t* pos, int64_t pos_stride_b, int64_t pos_stride_t, int64_t B,
-                               int64_t T, int64_t S, int64_t K, void* csr, size_t csr_bytes, void* stream) {
+                               int64_t T, int64_t S, int64_t K, void* csr, size_t csr_bytes, void* workspace,
+                               size_t workspace_bytes, void* stream) {
   using namespace gw;
   clear_error();
   GW_CHECK_ARG(B >= 0 && T >= 0 && S >= 0 && K >= 0, "invalid sizes B=%lld T=%lld S=%lld K=%lld", (long long)B,
@@ -370,7 +378,10 @@ extern "C" int gw_kv_csr_build(const int32_t* pos, int64_t pos_stride_b, int64_t
   GW_CHECK_ARG(B * S < (1ll << 30) && B * T * K < (1ll << 31) && T < (1ll << 31),
                "table too large for int32 CSR offsets");
   const CsrLayout L = csr_layout(B, T, S, K);
+  GW_CHECK_ARG(workspace != nullptr && aligned16(workspace) && workspace_bytes >= L.ws_total,
+               "the build needs a 16-byte aligned %zu-byte workspace, got %zu", L.ws_total, workspace_bytes);
   uint8_t* base = static_cast<uint8_t*>(csr);
+  uint8_t* wbase = static_cast<uint8_t*>(workspace);
   int* header = reinterpret_cast<int*>(base + L.header);
   int* count = reinterpret_cast<int*>(base + L.count);
   int* off = reinterpret_cast<int*>(base + L.off);
@@ -380,7 +391,7 @@ extern "C" int gw_kv_csr_build(const int32_t* pos, int64_t pos_stride_b, int64_t
   int2* entries = reinterpret_cast<int2*>(base + L.entries);
   const int nk = (int)L.nk;
   const uint32_t n = (uint32_t)(B * T * K);
-  uint32_t* keys_a = reinterpret_cast<uint32_t*>(base + L.scratch);
+  uint32_t* keys_a = reinterpret_cast<uint32_t*>(wbase + L.scratch);
   uint32_t* vals_a = keys_a + n;
   uint32_t* keys_b = vals_a + n;
   uint32_t* vals_b = keys_b + n;
@@ -396,8 +407,8 @@ extern "C" int gw_kv_csr_build(const int32_t* pos, int64_t pos_stride_b, int64_t
   rp.K = (int)K;
   rp.nk = nk;
   rp.entries = entries;
-  rp.hist = reinterpret_cast<uint32_t*>(base + L.hist);
-  rp.raw = reinterpret_cast<uint32_t*>(base + L.raw);
+  rp.hist = reinterpret_cast<uint32_t*>(wbase + L.hist);
+  rp.raw = reinterpret_cast<uint32_t*>(wbase + L.raw);
   rp.n = n;
   rp.tiles = (n + kTile - 1) / kTile;
   int passes = 0;

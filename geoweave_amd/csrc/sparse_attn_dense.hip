@@ -30,7 +30,12 @@
 //                        (the atomic returns the bit already set) flags the query's 32-query
 //                        block: the gather kernel then computes that block, since the
 //                        reference counts a repeated position twice.
-//   dense_vmax_kernel  — largest |v| per (head, d) column, for the fp16 scaling of V.
+//   dense_vmax_kernel  — largest |v| per (head, d) column, for the fp16 scaling of V; it also
+//                        flags a batch element whose K or V holds an inf or nan anywhere:
+//                        the dense products would carry it from rows a query did not select
+//                        (0 * inf, -inf + inf), so such a batch element is computed by the
+//                        gather kernel, which reads only the selected rows, as the reference
+//                        does.
 //   dense_vt_kernel    — V^T as [B][H][64][S_pad] fp16 (S_pad = S rounded up to 64, zero
 //                        padded), keys in operand order: one 16-byte load per operand chunk.
 //   dense_attn_kernel  — 4 waves per workgroup, each on two 32-query blocks, all on one
@@ -71,7 +76,7 @@ __device__ __forceinline__ f32x16 mma(FP16, uint4 a, uint4 b, f32x16 c) {
 // the word as it was: a bit already set means the query listed the key twice, and the block
 // is flagged. Positions are read 8 rows at a time (16 bytes per lane when the table allows),
 // so the loads of a group are in flight together. The first workgroup of each batch also
-// clears the per-column maxima of |V| that dense_vmax_kernel accumulates.
+// clears the per-column maxima of |V| and the non-finite flag that dense_vmax_kernel sets.
 // ---------------------------------------------------------------------------------------
 constexpr int kMaskChunk = 16384;  // keys per workgroup
 
@@ -79,7 +84,7 @@ __global__ __launch_bounds__(256) void dense_mask_kernel(const int32_t* __restri
                                                          int T, int S, int Spad, int K, int nqb, int tpad,
                                                          int nchunk, int vec, int vmax_words,
                                                          uint32_t* __restrict__ mask, int* __restrict__ flags,
-                                                         uint32_t* __restrict__ vmax) {
+                                                         uint32_t* __restrict__ vmax, int* __restrict__ bad) {
   // [key / 32][query], rows padded to 33 words so that one query's atomics spread over banks
   __shared__ uint32_t words[(kMaskChunk / 32) * 33];
   __shared__ int dup_any;
@@ -90,8 +95,10 @@ __global__ __launch_bounds__(256) void dense_mask_kernel(const int32_t* __restri
   const int len = min(kMaskChunk, S - c0);
   const int nkt = min(kMaskChunk, Spad - c0) >> 5;
   for (int i = threadIdx.x; i < nkt * 33; i += 256) words[i] = 0u;
-  if (qb == 0 && chunk == 0)
+  if (qb == 0 && chunk == 0) {
     for (int i = threadIdx.x; i < vmax_words; i += 256) vmax[(int64_t)b * vmax_words + i] = 0u;
+    if (threadIdx.x == 0) bad[b] = 0;
+  }
   if (threadIdx.x == 0) dup_any = 0;
   __syncthreads();
   bool dup = false;
@@ -148,6 +155,8 @@ __global__ __launch_bounds__(256) void dense_mask_kernel(const int32_t* __restri
 // fits fp16, and values down to 2^-28 of the column's largest stay normal. o is scaled back
 // by 2^-e. dense_vmax_kernel takes the column maxima (as ordered bit patterns of
 // non-negative floats, atomic max); columns that are all zero or hold inf/nan keep e = 0.
+// It reads the K rows of the same keys and head too, and sets bad[b] when any K or V value
+// of the batch element is an inf or a nan (exponent field all ones).
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ int vscale_exp(uint32_t bits) {
   const float mx = __uint_as_float(bits);
@@ -163,32 +172,45 @@ __device__ __forceinline__ float in_to_float(int in_fp16, uint32_t u) {
 
 constexpr int kVmaxKeys = 256;  // keys per workgroup of dense_vmax_kernel (one head)
 
+// Non-zero when either 16-bit half of w has its exponent field all ones (inf or nan).
+__device__ __forceinline__ uint32_t nonfinite2(uint32_t w, uint32_t e) {
+  return (uint32_t)((w & e) == e) | (uint32_t)(((w >> 16) & e) == e);
+}
+
 __global__ __launch_bounds__(256) void dense_vmax_kernel(const uint16_t* __restrict__ v, int64_t vsb, int64_t vss,
-                                                         int64_t vsh, int S, int H, int in_fp16,
-                                                         uint32_t* __restrict__ vmax) {
+                                                         int64_t vsh, const uint16_t* __restrict__ k, int64_t ksb,
+                                                         int64_t kss, int64_t ksh, int S, int H, int in_fp16,
+                                                         uint32_t* __restrict__ vmax, int* __restrict__ bad) {
   __shared__ float part[4][64];
   const int h = blockIdx.y, b = blockIdx.z;
   const int dc = threadIdx.x & 7, kr = threadIdx.x >> 3;  // 16-byte chunk of the row, key
   const int s0 = blockIdx.x * kVmaxKeys;
   const uint16_t* src = v + b * vsb + h * vsh + dc * 8;
+  const uint16_t* ksrc = k + b * ksb + h * ksh + dc * 8;
+  const uint32_t e = in_fp16 ? 0x7C00u : 0x7F80u;
   float mx[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) mx[i] = 0.f;
-  uint4 val[8];
+  uint4 val[8], kval[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const int s = s0 + kr + 32 * u;
     val[u] = s < S ? *reinterpret_cast<const uint4*>(src + (int64_t)s * vss) : make_uint4(0, 0, 0, 0);
+    kval[u] = s < S ? *reinterpret_cast<const uint4*>(ksrc + (int64_t)s * kss) : make_uint4(0, 0, 0, 0);
   }
+  uint32_t nf = 0u;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const uint32_t w[4] = {val[u].x, val[u].y, val[u].z, val[u].w};
+    const uint32_t kw[4] = {kval[u].x, kval[u].y, kval[u].z, kval[u].w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       mx[2 * i] = fmaxf(mx[2 * i], fabsf(in_to_float(in_fp16, w[i] & 0xFFFFu)));
       mx[2 * i + 1] = fmaxf(mx[2 * i + 1], fabsf(in_to_float(in_fp16, w[i] >> 16)));
+      nf |= nonfinite2(w[i], e) | nonfinite2(kw[i], e);
     }
   }
+  if (nf != 0u) bad[b] = 1;  // every writer stores the same value
   // lanes with the same chunk: xor 8, 16, 32; then the four waves
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -271,6 +293,7 @@ struct DenseParams {
   const uint32_t* mask;
   const uint32_t* vmax;
   const int* flags;
+  const int* bad;  // [B]: K or V of the batch element holds an inf or nan
   uint16_t* o;
   float* lse;
   int64_t qsb, qst, qsh;
@@ -556,12 +579,13 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
   }
 
   // o = O / l scaled back by 2^-e per column, lse = (m + log2 l) ln 2; queries without any
-  // selected key give o = 0, lse = -inf. Blocks holding a repeated position are written by
-  // the gather kernel.
+  // selected key give o = 0, lse = -inf. Blocks holding a repeated position, and batch
+  // elements with a non-finite K or V value, are written by the gather kernel.
+  const bool finite = p.bad[b] == 0;
 #pragma unroll
   for (int a = 0; a < kQPW; ++a) {
     const int qb = qb0 + a, t = tq[a];
-    bool active = qb < p.nqb && t < p.T;
+    bool active = finite && qb < p.nqb && t < p.T;
     if (qb < p.nqb) {
       const int* f = p.flags + ((int64_t)b * p.nqb + qb) * p.nchunk;
       for (int c = 0; c < p.nchunk; ++c) active &= f[c] == 0;
@@ -602,6 +626,7 @@ struct AttnSumParams {
   const float* sws;
   const float* lse;  // natural log, [B, T, H]
   const int* flags;
+  const int* bad;    // [B]
   float* attn_sum;   // [B, T, K]
   const void* logits;
   int logits_dt;
@@ -640,7 +665,7 @@ __global__ __launch_bounds__(256) void dense_attn_sum_kernel(const AttnSumParams
   const int b = (int)(row / p.T), t = (int)(row - (int64_t)b * p.T);
   {
     const int* f = p.flags + ((int64_t)b * p.nqb + (t >> 5)) * p.nchunk;
-    bool flagged = false;
+    bool flagged = p.bad[b] != 0;
     for (int c = 0; c < p.nchunk; ++c) flagged |= f[c] != 0;
     if (flagged) return;
   }
@@ -721,7 +746,7 @@ __global__ __launch_bounds__(256) void dense_attn_sum_kernel(const AttnSumParams
 }
 
 struct DenseLayout {
-  size_t mask, flags, vmax, vt, sws, total;
+  size_t mask, flags, bad, vmax, vt, sws, total;
   int nqb, nqb_pad, nchunk, spad;
 };
 
@@ -738,6 +763,8 @@ DenseLayout dense_layout(int64_t B, int64_t T, int64_t S, int64_t H, int64_t K, 
   o = up(o + (size_t)B * (size_t)(L.spad / 32) * (size_t)L.nqb_pad * 32 * 4);
   L.flags = o;
   o = up(o + (size_t)B * L.nqb * (size_t)L.nchunk * 4);
+  L.bad = o;
+  o = up(o + (size_t)B * 4);
   L.vmax = o;
   o = up(o + (size_t)B * (size_t)H * 64 * 4);
   L.vt = o;
@@ -828,6 +855,7 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   uint32_t* mask = reinterpret_cast<uint32_t*>(ws + L.mask);
   int* flags = reinterpret_cast<int*>(ws + L.flags);
+  int* bad = reinterpret_cast<int*>(ws + L.bad);
   uint32_t* vmax = reinterpret_cast<uint32_t*>(ws + L.vmax);
   uint16_t* vt = reinterpret_cast<uint16_t*>(ws + L.vt);
   const int in_fp16 = dtype == GW_DTYPE_FP16 ? 1 : 0;
@@ -840,12 +868,13 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
                         : 0;
     hipLaunchKernelGGL(dense_mask_kernel, dim3(L.nchunk, L.nqb_pad, (unsigned)B), dim3(256), 0, st, kv_pos,
                        pos_stride_b, pos_stride_t, (int)T, (int)S, L.spad, (int)K, L.nqb, L.nqb_pad * 32, L.nchunk,
-                       vec, (int)(H * 64), mask, flags, vmax);
+                       vec, (int)(H * 64), mask, flags, vmax, bad);
     GW_HIP_LAUNCH_CHECK("dense_mask_kernel launch");
   }
   hipLaunchKernelGGL(dense_vmax_kernel, dim3((unsigned)((S + kVmaxKeys - 1) / kVmaxKeys), (unsigned)H, (unsigned)B),
-                     dim3(256), 0, st, static_cast<const uint16_t*>(v), v_strides[0], v_strides[1], v_strides[2], (int)S, (int)H,
-                     in_fp16, vmax);
+                     dim3(256), 0, st, static_cast<const uint16_t*>(v), v_strides[0], v_strides[1], v_strides[2],
+                     static_cast<const uint16_t*>(k), k_strides[0], k_strides[1], k_strides[2], (int)S, (int)H,
+                     in_fp16, vmax, bad);
   GW_HIP_LAUNCH_CHECK("dense_vmax_kernel launch");
   hipLaunchKernelGGL(dense_vt_kernel, dim3(L.spad / 64, (unsigned)H, (unsigned)B), dim3(256), 0, st,
                      static_cast<const uint16_t*>(v), v_strides[0], v_strides[1], v_strides[2], (int)S, L.spad,
@@ -859,6 +888,7 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
   p.mask = mask;
   p.vmax = vmax;
   p.flags = flags;
+  p.bad = bad;
   p.o = static_cast<uint16_t*>(o);
   p.lse = lse;
   p.qsb = q_strides[0]; p.qst = q_strides[1]; p.qsh = q_strides[2];
@@ -895,6 +925,7 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
     ap.sws = sws;
     ap.lse = lse;
     ap.flags = flags;
+    ap.bad = bad;
     ap.attn_sum = attn_sum;
     ap.logits = logits;
     ap.logits_dt = logits_dtype;
@@ -914,10 +945,11 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
     const int rc = want_kl ? launch_attn_sum<true>(ap, rows, st) : launch_attn_sum<false>(ap, rows, st);
     if (rc != GW_OK) return rc;
   }
-  // Blocks with a repeated position: the gather kernel (it returns at once for the others),
-  // with attn_sum and the KL loss when asked (its score workspace is the same region).
+  // Blocks with a repeated position, and every block of a batch element with a non-finite
+  // K or V value: the gather kernel (it returns at once for the others), with attn_sum and
+  // the KL loss when asked (its score workspace is the same region).
   return attn_fwd_flagged_blocks(dtype, q, q_strides, k, k_strides, v, v_strides, kv_pos, pos_stride_b, pos_stride_t,
                                  o, o_strides, lse, attn_sum, B, T, S, H, D, K, softmax_scale, logits, logits_dtype,
                                  logits_stride_b, logits_stride_t, eps, row_loss, sws,
-                                 want_attn ? (size_t)B * T * K * H * 4 : 0, flags, L.nqb, L.nchunk, stream);
+                                 want_attn ? (size_t)B * T * K * H * 4 : 0, flags, bad, L.nqb, L.nchunk, stream);
 }

@@ -56,8 +56,10 @@ struct AttnFwdParams {
   int64_t lsb, lst;
   float kl_eps;
   float* row_loss;
-  // Optional: run only the 32-query blocks flagged here ([B][nqb][nchunk]).
+  // Optional: run only the 32-query blocks flagged here ([B][nqb][nchunk]), and every block
+  // of a batch element whose batch_flags[b] is non-zero (nullable).
   const int* blk_flags;
+  const int* batch_flags;
   int nqb, nchunk;
   int T, S, H, K;
   int NG;   // head groups (waves) per query
@@ -107,7 +109,7 @@ __global__ __launch_bounds__(256) void sparse_attn_fwd_kernel(const AttnFwdParam
     // uniform over the workgroup.
     const int qb = (int)((blockIdx.x * p.QPB) >> 5);
     const int* f = p.blk_flags + ((int64_t)blockIdx.y * p.nqb + qb) * p.nchunk;
-    bool run = false;
+    bool run = p.batch_flags != nullptr && p.batch_flags[blockIdx.y] != 0;
     for (int c = 0; c < p.nchunk; ++c) run |= f[c] != 0;
     if (!run) return;
   }
@@ -393,7 +395,7 @@ int attn_fwd_impl(int dtype, const void* q, const int64_t* q_strides, const void
                   int64_t pos_stride_t, void* o, const int64_t* o_strides, float* lse, float* attn_sum, int64_t B,
                   int64_t T, int64_t S, int64_t H, int64_t D, int64_t K, float softmax_scale, void* workspace,
                   size_t workspace_bytes, const KlArgs* kl, void* stream, const int* blk_flags = nullptr,
-                  int nqb = 0, int nchunk = 0) {
+                  const int* batch_flags = nullptr, int nqb = 0, int nchunk = 0) {
   GW_CHECK_ARG(dtype == GW_DTYPE_BF16 || dtype == GW_DTYPE_FP16, "unsupported dtype code %d", dtype);
   GW_CHECK_ARG(B >= 0 && T >= 0 && S >= 0 && H >= 1 && K >= 0,
                "invalid sizes B=%lld T=%lld S=%lld H=%lld K=%lld", (long long)B, (long long)T,
@@ -445,6 +447,7 @@ int attn_fwd_impl(int dtype, const void* q, const int64_t* q_strides, const void
   p.kl_eps = 0.f;
   p.row_loss = nullptr;
   p.blk_flags = blk_flags;
+  p.batch_flags = batch_flags;
   p.nqb = nqb;
   p.nchunk = nchunk;
   p.T = (int)T;
@@ -516,9 +519,9 @@ int gw::attn_fwd_flagged_blocks(int dtype, const void* q, const int64_t* q_strid
                                 int64_t S, int64_t H, int64_t D, int64_t K, float softmax_scale, const void* logits,
                                 int logits_dtype, int64_t logits_stride_b, int64_t logits_stride_t, float eps,
                                 float* row_loss, void* workspace, size_t workspace_bytes, const int* blk_flags,
-                                int nqb, int nchunk, void* stream) {
+                                const int* batch_flags, int nqb, int nchunk, void* stream) {
   const gw::KlArgs kl{logits, logits_dtype, logits_stride_b, logits_stride_t, eps, row_loss};
   return gw::attn_fwd_impl(dtype, q, q_strides, k, k_strides, v, v_strides, kv_pos, pos_stride_b, pos_stride_t, o,
                            o_strides, lse, attn_sum, B, T, S, H, D, K, softmax_scale, workspace, workspace_bytes,
-                           logits != nullptr ? &kl : nullptr, stream, blk_flags, nqb, nchunk);
+                           logits != nullptr ? &kl : nullptr, stream, blk_flags, batch_flags, nqb, nchunk);
 }

@@ -122,6 +122,28 @@ def random_positions(
     return pos.contiguous()
 
 
+def distinct_positions(batch: int, tgt_len: int, src_len: int, topk: int, seed: int,
+                       hub: Optional[int] = None) -> torch.Tensor:
+    """int32 ``[B, T, K]`` positions with no repeat inside a row, cheap at any size: row t
+    lists ``(off_t + j * step_t) mod S`` for j < K, with a random offset and a random step
+    coprime to S (so the K entries are distinct when K <= S). ``hub``: key listed in every
+    row that does not already list it (at j = 0), like a key the indexer picks for most
+    queries."""
+    import math
+
+    g = _gen(seed)
+    kk = min(topk, src_len)
+    cands = [s for s in range(1, min(src_len, 4096)) if math.gcd(s, src_len) == 1] or [1]
+    steps = torch.tensor(cands)[torch.randint(0, len(cands), (batch, tgt_len, 1), generator=g)]
+    off = torch.randint(0, src_len, (batch, tgt_len, 1), generator=g)
+    j = torch.arange(kk).view(1, 1, kk)
+    pos = (off + j * steps) % src_len
+    if hub is not None:
+        free = ~(pos == hub).any(-1)
+        pos[..., 0] = torch.where(free, torch.full_like(pos[..., 0], hub), pos[..., 0])
+    return pos.to(torch.int32).contiguous()
+
+
 def layer_inputs(views: int, batch: int = 1, dtype: torch.dtype = torch.bfloat16,
                  tokens: Optional[int] = None) -> LayerInputs:
     qi, ki, wi = indexer_inputs(views, batch, dtype, tokens)

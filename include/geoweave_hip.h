@@ -132,14 +132,20 @@ int gw_indexer_topk_fwd(int dtype, const void* q, const void* k, const void* w, 
  *
  * pos: int32, element (b,t,j) at b*pos_stride_b + t*pos_stride_t + j. Entries outside
  * [0, S) are skipped. csr: a caller-allocated buffer of gw_kv_csr_size(B,T,S,K) bytes,
- * 16-byte aligned, opaque; it stays valid until the buffer is reused. The entries of
- * each key are sorted by (t, j), so results computed from it are bitwise reproducible.
- * Work runs on `stream`; no host synchronisation.
+ * 16-byte aligned, opaque (per-key offsets and work items, and the (t, j) entries: about
+ * 8 bytes per table entry); it stays valid until the buffer is reused. workspace: the
+ * build's transient buffer of gw_kv_csr_build_workspace_size(B,T,S,K) bytes (the radix
+ * sort's ping-pong buffers, about 16 bytes per table entry), 16-byte aligned; it may be
+ * reused once the work queued on `stream` by this call has run. The entries of each key are
+ * sorted by (t, j), so results computed from the table are bitwise reproducible. Work runs
+ * on `stream`; no host synchronisation.
  */
 size_t gw_kv_csr_size(int64_t B, int64_t T, int64_t S, int64_t K);
+size_t gw_kv_csr_build_workspace_size(int64_t B, int64_t T, int64_t S, int64_t K);
 int gw_kv_csr_build(const int32_t* pos, int64_t pos_stride_b, int64_t pos_stride_t,
                     int64_t B, int64_t T, int64_t S, int64_t K,
-                    void* csr, size_t csr_bytes, void* stream);
+                    void* csr, size_t csr_bytes, void* workspace, size_t workspace_bytes,
+                    void* stream);
 
 /* ------------------------------------------------------------------------------------
  * Sparse-index attention, backward.
@@ -350,8 +356,9 @@ int gw_source_downsample_expand(int dtype, const int32_t* coarse_idx, const void
  * asked for; otherwise GW_ERR_UNSUPPORTED (use gw_sparse_attn_fwd / gw_sparse_attn_fwd_kl).
  * The P·V product takes P in fp16 (the fp32 weights rounded to nearest, 11 significant bits)
  * against V in fp16 scaled per (head, d) column by an exact power of two; row sums and lse
- * come from the fp32 weights. K and V must be finite (an inf or nan in a row the query did
- * not select reaches its products through the zero weight).
+ * come from the fp32 weights. A batch element whose K or V holds an inf or nan anywhere is
+ * computed by the gather kernel inside this call (the dense products would carry the value
+ * from rows a query did not select; the reference reads only the selected rows).
  * attn_sum (nullable) and lse: as for gw_sparse_attn_fwd (lse is required with attn_sum).
  * logits (nullable; needs attn_sum) ... row_loss: the fused KL loss, as for
  * gw_sparse_attn_fwd_kl.
@@ -359,7 +366,7 @@ int gw_source_downsample_expand(int dtype, const int32_t* coarse_idx, const void
  * (the reference counts a repeated position twice).
  * Workspace: gw_sparse_attn_fwd_dense_workspace_size(B, T, S, H, D, K, want_attn_sum) bytes,
  * 16-byte aligned: the selection words (B * round_up(S, 64) / 32 * round_up(T, 256) * 4
- * bytes), per-block flags, the |V| column maxima (B * H * 64 * 4 bytes), the scaled fp16
+ * bytes), per-block and per-batch-element flags, the |V| column maxima (B * H * 64 * 4 bytes), the scaled fp16
  * V^T (B * H * 64 * round_up(S, 64) * 2 bytes) and, with attn_sum, the selected scores
  * (B * T * K * H * 4 bytes).
  * ------------------------------------------------------------------------------------ */

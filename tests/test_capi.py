@@ -162,9 +162,10 @@ def _dense_call(**over):
 def test_dense_fwd_workspace_and_argument_checks_without_gpu():
     lib = _lib.load()
     # mask: 2 sub-tiles of 32 keys (S padded to 64) x 256 queries (1 block padded to the 8 of
-    # a workgroup) x 4 B = 2048; flags 4 B -> 2304; |V| column maxima 16 heads x 64 x 4 B ->
-    # 6400; V^T 16 heads x 64 x 64 keys x 2 B
-    base = 2304 + 16 * 64 * 4 + 16 * 64 * 64 * 2
+    # a workgroup) x 4 B = 2048; block flags 4 B -> 2304; non-finite flag per batch element
+    # 4 B -> 2560; |V| column maxima 16 heads x 64 x 4 B -> 6656; V^T 16 heads x 64 x 64 keys
+    # x 2 B
+    base = 2560 + 16 * 64 * 4 + 16 * 64 * 64 * 2
     assert lib.gw_sparse_attn_fwd_dense_workspace_size(1, 4, 4, 16, 64, 4, 0) == base
     # + the selected scores for attn_sum: T x K x H x 4 B
     assert lib.gw_sparse_attn_fwd_dense_workspace_size(1, 4, 4, 16, 64, 4, 1) == base + 4 * 4 * 16 * 4

@@ -308,3 +308,59 @@ def test_random_shapes_against_the_oracle(gpu_device, case):
         torch.testing.assert_close(o2, ro.float(), **TOL)
         torch.testing.assert_close(attn, ra, atol=1e-4, rtol=1e-3)
         torch.testing.assert_close(lse2, rl, atol=1e-4, rtol=1e-4)
+
+
+def _nonfinite_case(seed=41):
+    # Batch 0: inf / nan in K and V rows that no query selects (the reference never reads
+    # them). Batch 1: the same values in rows some queries do select.
+    B, T, S, H, K = 2, 100, 1000, 4, 32
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, H, 64, generator=g).bfloat16()
+    k = torch.randn(B, S, H, 64, generator=g).bfloat16()
+    v = torch.randn(B, S, H, 64, generator=g).bfloat16()
+    pos = _distinct_positions(B, T, S, K, seed=seed + 1)
+    unused = [sorted(set(range(S)) - set(pos[b].reshape(-1).tolist())) for b in range(B)]
+    assert len(unused[0]) >= 4, "the case needs keys that no query selects"
+    k[0, unused[0][0], 1, 5] = float("inf")
+    k[0, unused[0][1], 2, :] = float("nan")
+    v[0, unused[0][2], 0, 9] = float("-inf")
+    v[0, unused[0][3], 3, 0] = float("nan")
+    used = pos[1, 17, 3].item(), pos[1, 70, 9].item()
+    k[1, used[0], 1, 5] = float("inf")
+    v[1, used[1], 2, 7] = float("nan")
+    return q, k, v, pos
+
+
+def _assert_same_nonfinite(got, want, tol):
+    fin = torch.isfinite(want)
+    assert torch.equal(torch.isfinite(got), fin), "non-finite entries differ from the oracle"
+    torch.testing.assert_close(got[fin], want[fin], **tol)
+
+
+@pytest.mark.parametrize("with_attn", [False, True])
+def test_non_finite_k_v_take_the_gather_kernel(gpu_device, with_attn):
+    # An inf or nan in a K or V row that no query selected must not reach any output (the
+    # dense products would carry it through the -inf bias or the zero weight); the call
+    # computes such a batch element with the gather kernel, as the reference reads only the
+    # selected rows (sparse_index_flash_attn.py:205-216).
+    q, k, v, pos = _nonfinite_case()
+    print(f"[dense non-finite] with_attn={with_attn}", flush=True)
+    ro, ra, rl = oatt.sparse_attention(q, k, v, pos)
+    if with_attn:
+        o, attn, lse, _ = _run_attn(q, k, v, pos, path="auto")
+    else:
+        o, lse = _run(q, k, v, pos, path="auto")
+    assert torch.isfinite(o[0]).all() and torch.isfinite(lse[0]).all()
+    torch.testing.assert_close(o[0], ro[0], **TOL)
+    torch.testing.assert_close(lse[0], rl[0], atol=1e-4, rtol=1e-4)
+    assert not torch.isfinite(ro[1]).all(), "batch 1 plants values in selected rows"
+    _assert_same_nonfinite(o[1], ro[1], TOL)
+    _assert_same_nonfinite(lse[1].nan_to_num(posinf=float("nan")), rl[1].nan_to_num(posinf=float("nan")),
+                           dict(atol=1e-4, rtol=1e-4))
+    if with_attn:
+        torch.testing.assert_close(attn[0], ra[0], atol=1e-4, rtol=1e-3)
+        _assert_same_nonfinite(attn[1], ra[1], dict(atol=1e-4, rtol=1e-3))
+    # finite inputs of the same shape still take the dense pass and agree with these rows
+    k2, v2 = k.nan_to_num(nan=0.0, posinf=0.0, neginf=0.0), v.nan_to_num(nan=0.0, posinf=0.0, neginf=0.0)
+    o2, lse2 = _run(q, k2, v2, pos, path="dense")
+    torch.testing.assert_close(o2[0], o[0], **TOL)

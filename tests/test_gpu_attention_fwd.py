@@ -131,17 +131,45 @@ def test_inference_entry_and_stream(gpu_device):
     torch.testing.assert_close(o.float().cpu(), ro, **TOL)
 
 
+@pytest.mark.parametrize("path", ["auto", "gather"])
 @pytest.mark.parametrize("views", [16, 64])
-def test_full_size_sampled_rows(gpu_device, views):
+def test_full_size_sampled_rows(gpu_device, views, path):
     # Full layer size: exact comparison on a sample of query rows plus the
-    # size-independent invariant sum_j attn_sum[t, j] = H on every row.
+    # size-independent invariant sum_j attn_sum[t, j] = H on every row. Rows list distinct
+    # positions (as top-k does), so "auto" takes the masked dense pass with attn_sum; "gather"
+    # forces the gather kernel on the same inputs.
     q, k, v = workloads.attention_inputs(views, 1, torch.bfloat16)
     n = q.shape[1]
     g = torch.Generator().manual_seed(views)
-    pos = torch.randint(0, n, (1, n, 1024), generator=g, dtype=torch.int32)
-    o, attn, lse = _run(q, k, v, pos)
+    pos = workloads.distinct_positions(1, n, n, 1024, seed=views, hub=11)
+    print(f"[attn full size] views={views} path={path}", flush=True)
+    old = sifa.FORWARD_PATH
+    sifa.FORWARD_PATH = path
+    try:
+        o, attn, lse = _run(q, k, v, pos)
+    finally:
+        sifa.FORWARD_PATH = old
     torch.testing.assert_close(attn.sum(-1), torch.full((1, n), 16.0), atol=2e-3, rtol=1e-4)
     rows = torch.randperm(n, generator=g)[:128]
+    ro, ra, rl = oatt.sparse_attention(q[:, rows], k, v, pos[:, rows])
+    torch.testing.assert_close(o[:, rows], ro, **TOL)
+    torch.testing.assert_close(attn[:, rows], ra, **TOL)
+    torch.testing.assert_close(lse[:, rows], rl, atol=1e-4, rtol=1e-4)
+
+
+def test_full_size_repeated_positions_take_the_gather_kernel_per_block(gpu_device):
+    # Randomly drawn positions with repeats inside rows (every 32-query block then holds a
+    # repeat): the dense call hands each flagged block to the gather kernel, which counts a
+    # repeated position twice, as the reference does.
+    q, k, v = workloads.attention_inputs(16, 1, torch.bfloat16)
+    n = q.shape[1]
+    g = torch.Generator().manual_seed(161)
+    pos = workloads.distinct_positions(1, n, n, 1024, seed=161)
+    pos[0, 5000:5100] = torch.randint(0, n, (100, 1024), generator=g, dtype=torch.int32)
+    pos[0, 7000, :8] = 3
+    o, attn, lse = _run(q, k, v, pos)
+    rows = torch.cat([torch.arange(4990, 5110, 4), torch.tensor([7000, 7001, 7040]),
+                      torch.randperm(n, generator=g)[:32]])
     ro, ra, rl = oatt.sparse_attention(q[:, rows], k, v, pos[:, rows])
     torch.testing.assert_close(o[:, rows], ro, **TOL)
     torch.testing.assert_close(attn[:, rows], ra, **TOL)

@@ -153,10 +153,13 @@ def test_training_shape_sampled(gpu_device):
     q, k, v = workloads.attention_inputs(views, B, torch.bfloat16)
     n = q.shape[1]
     g = torch.Generator().manual_seed(views)
-    pos = torch.stack([torch.randint(0, n, (n, K), generator=g, dtype=torch.int32) for _ in range(B)])
+    # distinct positions per row (as top-k gives), with one key listed by every query, so
+    # the forward takes the masked dense pass and the CSR holds a key longer than a work item
+    pos = workloads.distinct_positions(B, n, n, K, seed=views, hub=12345)
+    pos[1, 100:140, 5] = pos[1, 100:140, 6]  # repeats in a few rows: those blocks gather
     do = torch.randn(B, n, 16, 64, generator=g).bfloat16()
     (dq, dk, dv), o, lse = _attn_grads(q, k, v, pos, do)
-    rows = torch.randperm(n, generator=g)[:96]
+    rows = torch.cat([torch.arange(100, 140, 8), torch.randperm(n, generator=g)[:96]])
     _, _, rlse = oatt.sparse_attention(q[:, rows], k, v, pos[:, rows])
     torch.testing.assert_close(lse[:, rows], rlse, atol=1e-4, rtol=1e-4)
     rq, _, _ = oatt.sparse_attention_bwd(q[:, rows], k, v, pos[:, rows], o[:, rows], lse[:, rows], do[:, rows])

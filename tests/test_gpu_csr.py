@@ -123,3 +123,24 @@ def test_csr_is_deterministic(gpu_device):
     for name, n in (("header", 2), ("off", 4001), ("item_off", 4001), ("part_off", 4001),
                     ("item_key", n_items), ("entries", 2 * 4000 * 128)):
         np.testing.assert_array_equal(_field(a, L[name], n), _field(b, L[name], n))
+
+
+def test_only_the_table_stays_allocated(gpu_device):
+    # The radix sort's ping-pong buffers (16 bytes per entry) are a transient workspace:
+    # after a C4-size build (B = 2, N = 32,976, K = 1,024) only the table stays allocated.
+    from geoweave_amd import _lib, workloads
+
+    B, n, K = 2, 32976, 1024
+    pos = workloads.distinct_positions(B, n, n, K, seed=3).cuda()
+    lib = _lib.load()
+    table = int(lib.gw_kv_csr_size(B, n, n, K))
+    scratch = int(lib.gw_kv_csr_build_workspace_size(B, n, n, K))
+    assert scratch >= 16 * B * n * K
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated()
+    csr, nbytes = _csr.build(pos, n, cache=False)
+    torch.cuda.synchronize()
+    kept = torch.cuda.memory_allocated() - before
+    assert nbytes == table and kept <= table + (2 << 20), f"{kept} bytes kept for a {table}-byte table"
+    print(f"[csr] table {table / 2**30:.2f} GiB kept, build workspace {scratch / 2**30:.2f} GiB released",
+          flush=True)
