@@ -232,7 +232,9 @@ __global__ __launch_bounds__(256) void sparse_attn_fwd_kernel(const AttnFwdParam
 #pragma unroll
       for (int i = 0; i < 8; ++i) of[i] = acc[i] * inv;
       *reinterpret_cast<uint4*>(p.o + b * p.osb + (int64_t)t * p.ost + h * p.osh + c * 8) = pack8<E>(of);
-      const float lse2 = l > 0.f ? m + flog2(l) : -INFINITY;
+      // l = 0: no valid entry (lse = -inf); a nan l (an inf or nan score of a selected
+      // key) gives a nan lse, as the reference's m + log(l) does
+      const float lse2 = l != 0.f ? m + flog2(l) : -INFINITY;
       if (c == 0) {
         if (p.lse) p.lse[((int64_t)b * p.T + t) * p.H + h] = lse2 * kLn2;
         if constexpr (ATTN) lse2_s[ql][h] = lse2;

@@ -65,8 +65,10 @@ def sparse_attention(
             s = s.masked_fill(~valid[:, None, :], float("-inf"))
             row_lse = torch.logsumexp(s, dim=-1)  # [Tc, H]
             p = torch.softmax(s, dim=-1)
+            # invalid entries (and so every entry of a row with none valid, whose softmax is
+            # nan) get 0; a nan from the scores themselves (an inf or nan in a selected
+            # K row) stays, as in the reference's softmax
             p = p.masked_fill(~valid[:, None, :], 0.0)
-            p = torch.nan_to_num(p, nan=0.0)  # rows with no valid entry
             o[b, t0:t1] = torch.einsum("thk,tkhd->thd", p, v_sel)
             attn_sum[b, t0:t1] = p.sum(dim=1)
             lse[b, t0:t1] = row_lse

@@ -524,3 +524,23 @@ def test_source_order_by_score_by_hand():
     c = torch.tensor([[[5, 3, 9, 1]]])
     s = torch.tensor([[[1.0, 2.0, 1.0, 2.0]]])
     assert osd.order_by_score(c, s).tolist() == [[[1, 3, 5, 9]]]
+
+
+def test_sparse_attention_non_finite_scores_follow_the_reference_softmax():
+    # An inf in a selected K row gives a +inf score: the reference's softmax
+    # (tests/sparse_index_flash_attn_tests.py:66, dsa_attention.py:4747) makes that (t, h)
+    # row nan; an all-invalid row is zeroed by the masked_fill. Pinned against the same ops
+    # written out on one row.
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(1, 3, 2, 4, generator=g)
+    k = torch.randn(1, 5, 2, 4, generator=g)
+    v = torch.randn(1, 5, 2, 4, generator=g)
+    q[0, 0, 1] = 1.0
+    k[0, 2, 1, 0] = float("inf")           # score of (t=0, h=1, key 2) is +inf
+    pos = torch.tensor([[[0, 2, 4], [1, 3, 4], [-1, -1, -1]]], dtype=torch.int32)
+    o, attn, lse = oatt.sparse_attention(q, k, v, pos, 0.5)
+    assert torch.isnan(o[0, 0, 1]).all() and torch.isfinite(o[0, 0, 0]).all()
+    assert lse[0, 0, 1] == float("inf") and torch.isfinite(o[0, 1]).all()
+    assert torch.equal(o[0, 2], torch.zeros(2, 4)) and torch.equal(attn[0, 2], torch.zeros(3))
+    s = (q[0, 1, 0] * k[0, [1, 3, 4], 0]).sum(-1) * 0.5
+    torch.testing.assert_close(o[0, 1, 0], torch.softmax(s, 0) @ v[0, [1, 3, 4], 0])
