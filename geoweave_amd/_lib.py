@@ -94,6 +94,13 @@ _SIGNATURES = {
          _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p, ctypes.c_int, _i64, _i64,
          ctypes.c_float, _p, _p, _sz, _p],
     ),
+    "gw_sparse_attn_fwd_dense_noalloc_capacity": (_sz, []),
+    "gw_sparse_attn_fwd_dense_noalloc": (
+        ctypes.c_int,
+        [ctypes.c_int, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64, _i64, _p, _i64p, _p, _p,
+         _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p, ctypes.c_int, _i64, _i64,
+         ctypes.c_float, _p, _p],
+    ),
 }
 
 _lock = threading.Lock()

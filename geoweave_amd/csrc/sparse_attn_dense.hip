@@ -44,6 +44,8 @@
 //                        feeds the products of both blocks.
 #include <math.h>
 
+#include <mutex>
+
 #include "gw_attn.h"
 #include "gw_common.h"
 #include "gw_select.h"
@@ -952,4 +954,61 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
                                  o, o_strides, lse, attn_sum, B, T, S, H, D, K, softmax_scale, logits, logits_dtype,
                                  logits_stride_b, logits_stride_t, eps, row_loss, sws,
                                  want_attn ? (size_t)B * T * K * H * 4 : 0, flags, bad, L.nqb, L.nchunk, stream);
+}
+
+// ---------------------------------------------------------------------------------------
+// Allocation-free variant: the workspace is a file-scope device array of a fixed size
+// (each GPU the library runs on holds its own copy until the process ends). Its device
+// address is looked up once per device (hipGetSymbolAddress with that device current) and
+// kept; host code never passes the array's name itself to a kernel. Every kernel of the call
+// clears what it needs before use (selection words, flags, column maxima), so the array's
+// contents from an earlier call do not matter; two calls that overlap on one GPU race on it.
+// ---------------------------------------------------------------------------------------
+namespace gw {
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+constexpr int kNoAllocMaxDevices = 64;
+
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+void* g_scratch_ptr[kNoAllocMaxDevices];
+hipError_t g_scratch_err[kNoAllocMaxDevices];
+std::once_flag g_scratch_once[kNoAllocMaxDevices];
+
+}  // namespace
+}  // namespace gw
+
+extern "C" size_t gw_sparse_attn_fwd_dense_noalloc_capacity(void) { return gw::kNoAllocScratchBytes; }
+
+extern "C" int gw_sparse_attn_fwd_dense_noalloc(int dtype, const void* q, const int64_t* q_strides, const void* k,
+                                                const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                                                const int32_t* kv_pos, int64_t pos_stride_b, int64_t pos_stride_t,
+                                                void* o, const int64_t* o_strides, float* lse, float* attn_sum,
+                                                int64_t B, int64_t T, int64_t S, int64_t H, int64_t D, int64_t K,
+                                                float softmax_scale, const void* logits, int logits_dtype,
+                                                int64_t logits_stride_b, int64_t logits_stride_t, float eps,
+                                                float* row_loss, void* stream) {
+  using namespace gw;
+  clear_error();
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_error(e, "hipGetDevice");
+  if (dev < 0 || dev >= kNoAllocMaxDevices)
+    return set_error(GW_ERR_UNSUPPORTED, "device %d is beyond the %d devices the allocation-free entry point serves",
+                     dev, kNoAllocMaxDevices);
+  std::call_once(g_scratch_once[dev], [dev] {
+    g_scratch_err[dev] = hipGetSymbolAddress(&g_scratch_ptr[dev], HIP_SYMBOL(scratch));
+  });
+  if (g_scratch_err[dev] != hipSuccess) return hip_error(g_scratch_err[dev], "hipGetSymbolAddress(scratch)");
+  const size_t need = gw_sparse_attn_fwd_dense_workspace_size(B, T, S, H, D, K, attn_sum != nullptr ? 1 : 0);
+  if (need > kNoAllocScratchBytes)
+    return set_error(GW_ERR_UNSUPPORTED,
+                     "this call needs %zu bytes of scratch; the allocation-free dense forward holds at most %zu "
+                     "(use gw_sparse_attn_fwd_dense with a workspace)",
+                     need, kNoAllocScratchBytes);
+  return gw_sparse_attn_fwd_dense(dtype, q, q_strides, k, k_strides, v, v_strides, kv_pos, pos_stride_b, pos_stride_t,
+                                  o, o_strides, lse, attn_sum, B, T, S, H, D, K, softmax_scale, logits, logits_dtype,
+                                  logits_stride_b, logits_stride_t, eps, row_loss, g_scratch_ptr[dev],
+                                  kNoAllocScratchBytes, stream);
 }

@@ -385,6 +385,32 @@ int gw_sparse_attn_fwd_dense(int dtype,
                              void* workspace, size_t workspace_bytes,
                              void* stream);
 
+/* ------------------------------------------------------------------------------------
+ * Allocation-free variant of gw_sparse_attn_fwd_dense. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Same arguments and results as
+ * gw_sparse_attn_fwd_dense without the workspace: the workspace is a file-scope device
+ * array of gw_sparse_attn_fwd_dense_noalloc_capacity() bytes (64 MiB) that each GPU the
+ * library runs on holds until the process ends. A call whose
+ * gw_sparse_attn_fwd_dense_workspace_size(...) exceeds it returns GW_ERR_UNSUPPORTED (for
+ * example the inference forward, no attn_sum, of 16 heads fits up to about 10 views of 1,374
+ * tokens). Works on the current device; the first call on a device looks up the array's
+ * address there. Calls that overlap on one GPU (other streams, other host threads) race on
+ * the array: serialise them. Calls no hipMalloc/hipFree or allocating library routine.
+ * ------------------------------------------------------------------------------------ */
+size_t gw_sparse_attn_fwd_dense_noalloc_capacity(void);
+int gw_sparse_attn_fwd_dense_noalloc(int dtype,
+                                     const void* q, const int64_t* q_strides,
+                                     const void* k, const int64_t* k_strides,
+                                     const void* v, const int64_t* v_strides,
+                                     const int32_t* kv_pos, int64_t pos_stride_b, int64_t pos_stride_t,
+                                     void* o, const int64_t* o_strides, float* lse, float* attn_sum,
+                                     int64_t B, int64_t T, int64_t S, int64_t H, int64_t D, int64_t K,
+                                     float softmax_scale,
+                                     const void* logits, int logits_dtype, int64_t logits_stride_b,
+                                     int64_t logits_stride_t, float eps, float* row_loss,
+                                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif
