@@ -29,24 +29,24 @@
 // is a candidate, so selecting among the candidates is exact. Ties at the k-th value are
 // broken deterministically (candidate order: split, then position in the list).
 //
-// MFMA layout (v_mfma_f32_32x32x16_{bf16,f16}): C[32 queries x 32 keys]; A = q rows
-// (stationary in VGPRs for the whole key sweep), B = key rows staged through LDS
-// (XOR-swizzled 16-byte chunks, conflict-free operand reads). Lane l owns key column l%32
-// and query rows 8*(r/4) + 4*(l/32) + r%4 of accumulator element r.
+// MFMA layout (v_mfma_f32_32x32x16_{bf16,f16}), transposed: per tile of 32 keys a wave
+// forms S^T[32 keys x 32 queries] = K Q^T with A = key rows staged through LDS (XOR-swizzled
+// 16-byte chunks, conflict-free operand reads) and B = its 32 query rows, stationary in
+// VGPRs for the whole key sweep. Lane l then holds query l%32 and keys 8*(r/4) + 4*(l/32) +
+// r%4 of the tile in accumulator element r: all 16 elements of a lane belong to one query.
 //
-// Candidate appends: about 2 % of scores pass tau, so most accumulator elements have a
-// passing lane somewhere in the wave and a store per element would issue a mostly empty
-// memory instruction per element. Instead each wave compacts its passing entries into an
-// LDS queue (a ballot and a lane count per element, one LDS write), and every 64 queued
-// entries are written out by one full store: each lane takes one entry, ranks it among
-// the lanes holding the same query row (ballots on the row bits) and writes it to that
-// row's list after the entries already written. Everything is in a fixed order, so the
-// lists are deterministic.
+// Candidate appends: about 4 % of the elements pass the threshold, so a memory instruction
+// per element would be mostly empty (and a wave issues one for most elements). Instead a
+// lane only compares each element against its query's threshold (a bit in a mask) and puts
+// its scores in an LDS staging row; once per stage of keys a short loop writes the marked
+// entries, every lane its lowest marked one per round, to its query's list (one list per
+// query and key split, shared by the query's two lanes). The lists come out in a fixed
+// order, the same on every run.
 //
 // Key splits: to fill the chip, the key range is divided over nsplit workgroups per
-// query tile. Split sp takes the 64-key stages sp, sp + nsplit, sp + 2*nsplit, ...; the
+// query tile. Split sp takes the key stages sp, sp + nsplit, sp + 2*nsplit, ...; the
 // interleave spreads any locality of a query's favourite keys (e.g. its own view) evenly
-// over the splits, so every list receives about (candidates / nsplit) entries.
+// over the splits, so every list receives about candidates / (2 nsplit) entries.
 #include <math.h>
 
 #include <mutex>
@@ -58,15 +58,16 @@ namespace gw {
 namespace {
 
 constexpr int kQW = 32;            // queries per wave
-constexpr int kBN = 64;            // keys per LDS stage (and split interleave granule)
 constexpr int kDI = 64;            // indexer head dim
-constexpr int kSubTotal = 8192;    // candidate slots per query over all key splits
+constexpr int kSubTotal = 8192;    // candidate slots per query over all lists
 constexpr int kMaxSplit = 8;
+constexpr int kMaxLists = kMaxSplit;
 constexpr int kMaxTopk = 2048;
 constexpr int kFallbackBlocks = 256;
-// Candidate layout: int2 {score bits, key} lists cand[(row * nsplit + split) * cap + i],
-// row = b * T + t, cap = kSubTotal / nsplit; counts[row * nsplit + split] = entries
-// appended (more than cap means the list overflowed).
+// Candidate layout: int2 {score bits, key} lists, one per row and key split: list l = split
+// of row r starts at cand[(r * nsplit + l) * cap], cap = kSubTotal / nsplit, and holds
+// counts[r * nsplit + l] entries (more than cap: the list overflowed; entries past cap were
+// not written).
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -138,11 +139,11 @@ struct ScoreParams {
   const uint16_t* mask;  // [B, T, S] or null
   const float* tau;      // [B*T] or null (-inf)
   float* samp;           // SAMPLE: [B*T, Ms]
-  int2* cand;            // FILTER: candidate lists, see kQueue
-  int* counts;           // FILTER: [B*T, nsplit] appends per list (may exceed cap)
+  int2* cand;            // FILTER: candidate lists (see kSubTotal)
+  int* counts;           // FILTER: [B*T, nsplit] entries per list (more than cap: overflowed)
   int T, S;
-  int nsplit, cap;
-  int nstages;           // 64-key stages of the sweep
+  int nsplit, cap;       // FILTER: key splits; valid entries per list
+  int nstages;           // key stages (ScoreShape::BN keys) of the sweep
   int Ms;
   int tau_mode;
   int force_wide;
@@ -162,24 +163,48 @@ __device__ __forceinline__ int sweep_key(int i, const ScoreParams& p) {
 // (kl & SWZ), SWZ = 15 for rows of >= 16 chunks (HI >= 2), else 7: the MFMA operand reads
 // (32 consecutive key rows at one logical chunk) then hit 16 distinct 16-byte bank groups
 // per 16 lanes (8 for HI = 1), one LDS pass per 256 bytes.
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glb_void_t;
+//
+// The loads are issued through inline asm, so the compiler does not see instructions that
+// write LDS behind its back: otherwise it cannot tell that a prefetch into one stage buffer
+// does not alias the operand reads of the other, and waits for the prefetch (vmcnt(0))
+// before the first read. The kernel waits for the loads itself (vmcnt(0) before the stage
+// barrier). M0 carries the wave's LDS destination and is restored after each load.
+__device__ __forceinline__ void lds_dma16(const void* src, const void* lds_dst) {
+  const uint32_t lds = (uint32_t)(uintptr_t)lds_dst;
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds))
+      : "memory");
+}
 
 // Workgroup shape of the score kernel: NW waves of 32 queries share every key tile (a
 // key tile read from L2 serves NW * 32 queries). HI <= 4 keeps its register file within
 // 256 per lane, so 8 waves (two per SIMD) fit one workgroup; HI = 8 needs 4.
 template <int HI>
 struct ScoreShape {
+  // keys per LDS stage (and split interleave granule): two 32-key tiles between barriers
+  // (one for HI = 8, whose key rows are 1 KB), so that two stage buffers and the score
+  // staging below fit the LDS.
+  static constexpr int BN = HI <= 4 ? 64 : 32;
   static constexpr int NW = HI <= 4 ? 8 : 4;
   static constexpr int BM = NW * kQW;        // queries per workgroup
   static constexpr int THREADS = NW * 64;
   static constexpr int MIN_WAVES_PER_EU = HI <= 4 ? 2 : 1;
-  // Per-wave LDS candidate queue (entries): written out when it holds FLUSH entries at a
-  // check after every 8 accumulator elements, so at most FLUSH - 1 + 8 * 64 < QUEUE are
-  // ever queued.
-  static constexpr int QUEUE = HI <= 4 ? 1024 : 640;
-  static constexpr int FLUSH = HI <= 4 ? 256 : 128;
 };
+
+// The products are transposed: per tile of 32 keys a wave forms S^T = K Q^T (A = key rows
+// from LDS, B = its 32 query rows, stationary in VGPRs), so lane l holds query l % 32 and
+// the 16 keys 8(r/4) + 4(l/32) + r%4 of the tile in accumulator element r: four groups of
+// four consecutive keys. Every element of a lane belongs to one query: its threshold is
+// one register, its gates are four broadcast LDS reads per head, and its candidates go to
+// its own list with no exchange between lanes. The two lanes of a query (l and l ^ 32)
+// hold disjoint keys and append to two lists of their own.
+constexpr int kStageRow = 36;  // two tiles of 16 scores per lane, padded
 
 template <typename E, int HI, bool SAMPLE, bool HAS_MASK>
 __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_PER_EU) void indexer_score_kernel(
@@ -189,18 +214,21 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
   constexpr int THREADS = ScoreShape<HI>::THREADS;
   constexpr int ROW_BYTES = HI * kDI * 2;
   constexpr int CHUNKS = ROW_BYTES / 16;              // 16-byte chunks per key row (>= 8)
-  constexpr int TILE_BYTES = kBN * ROW_BYTES;
+  constexpr int BN = ScoreShape<HI>::BN;
+  constexpr int TILE_BYTES = BN * ROW_BYTES;
   constexpr int LOADS = TILE_BYTES / (THREADS * 16);  // direct loads per thread per stage
-  constexpr int WVALS = kBN * HI;
+  constexpr int WVALS = BN * HI;
   constexpr int WLOADS = (WVALS + THREADS - 1) / THREADS;
   static_assert(LOADS * THREADS * 16 == TILE_BYTES, "key tile must split evenly over the threads");
 
-  __shared__ __attribute__((aligned(16))) uint8_t ktile[2][TILE_BYTES];
-  __shared__ float wtile[2][WVALS];
-  __shared__ __attribute__((aligned(16))) float tau_s[BM];
-  constexpr int QUEUE = ScoreShape<HI>::QUEUE;
-  __shared__ int2 cq[SAMPLE ? 1 : NW][SAMPLE ? 1 : QUEUE];  // FILTER: per-wave candidate queue
-  __shared__ int rcnt[SAMPLE ? 1 : NW][kQW];                 // FILTER: entries appended per row
+  // Two stage buffers (the next stage is loaded into one while the other is read).
+  __shared__ __attribute__((aligned(16))) uint8_t ktile0[TILE_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t ktile1[TILE_BYTES];
+  __shared__ __attribute__((aligned(16))) float wtile0[HI * BN];  // [head][key], gate * scale
+  __shared__ __attribute__((aligned(16))) float wtile1[HI * BN];
+  // FILTER: each wave's scores of the current stage, [lane][kStageRow floats]: element r of
+  // tile t at 16 t + r (rows padded by 4 floats against bank conflicts of the 16-byte stores).
+  __shared__ __attribute__((aligned(16))) float sstage[SAMPLE ? 1 : NW][SAMPLE ? 1 : 64 * kStageRow];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -213,38 +241,37 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
   const int nkeys = SAMPLE ? p.Ms : S;
   const int col = lane & 31;
   const int half = lane >> 5;
+  const int row = q0 + col;  // this lane's query
+  const bool row_ok = row < T;
+  const int64_t grow = (int64_t)b * T + (row_ok ? row : 0);
 
-  // A operands: this lane's query row (lane % 32), k-chunk (lane / 32) of each 16-wide step.
-  uint4 a[HI][4];
+  // B operands: this lane's query row, k-chunk (lane / 32) of each 16-wide step.
+  uint4 qop[HI][4];
   {
-    const int row = q0 + col;
-    const bool ok = row < T;
-    const uint16_t* qr = p.q + ((int64_t)b * T + (ok ? row : 0)) * (HI * kDI) + half * 8;
+    const uint16_t* qr = p.q + grow * (HI * kDI) + half * 8;
 #pragma unroll
     for (int h = 0; h < HI; ++h)
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks)
-        a[h][ks] = ok ? *reinterpret_cast<const uint4*>(qr + h * kDI + ks * 16) : make_uint4(0, 0, 0, 0);
+        qop[h][ks] = row_ok ? *reinterpret_cast<const uint4*>(qr + h * kDI + ks * 16) : make_uint4(0, 0, 0, 0);
   }
+  // Threshold of this lane's query (rows past T never pass).
+  float tau_l = INFINITY;
+  if (row_ok) {
+    if (p.tau_mode == kTauPlusInf) tau_l = INFINITY;
+    else if (p.tau_mode == kTauMinusInf || p.tau == nullptr) tau_l = -INFINITY;
+    else tau_l = p.tau[grow];
+  }
+  // FILTER: the list of this lane's query for this split is list grow * nsplit + split,
+  // kSubTotal / nsplit slots long; the two lanes of a query (l and l ^ 32) append to it in
+  // step, so both keep the same byte cursor woff. The wave's 32 rows have consecutive list
+  // blocks, so a list is addressed as a byte offset (< 2 MB) from the wave's first list.
+  const int stride = SAMPLE ? 0 : kSubTotal / nsplit;
+  int2* const lbase = SAMPLE ? nullptr : p.cand + (((int64_t)b * T + q0) * nsplit + split) * stride;
+  const uint32_t wstart = (uint32_t)(col * nsplit * stride) * 8u;
+  const uint32_t wend = wstart + (uint32_t)p.cap * 8u;  // first byte past the list's slots
+  uint32_t woff = wstart;
 
-  // Per-row thresholds of this wave's 32 rows (rows past T never pass).
-  if (lane < kQW) {
-    const int row = q0 + lane;
-    float tv = INFINITY;
-    if (row < T) {
-      if (p.tau_mode == kTauPlusInf) tv = INFINITY;
-      else if (p.tau_mode == kTauMinusInf || p.tau == nullptr) tv = -INFINITY;
-      else tv = p.tau[(int64_t)b * T + row];
-    }
-    tau_s[wave * kQW + lane] = tv;
-  }
-  // FILTER: list of query row q0 + rr at cand + (((b * T + q0 + rr) * nsplit + split) * cap.
-  const int64_t list0 = ((int64_t)b * T + q0) * nsplit + split;
-  const uint32_t half_tag = (uint32_t)(4 * half) << 24;  // row bits of this lane's half
-  uint32_t qn = 0;                                       // queued entries (wave-uniform)
-  if constexpr (!SAMPLE) {
-    if (lane < kQW) rcnt[wave][lane] = 0;
-  }
   // Loader geometry: load i of this thread fills LDS bytes [(i*NW + wave)*1024 + 16*lane, +16),
   // which hold physical chunk lane % CHUNKS of key row kl0 + i*RPI; its source is logical
   // chunk (lane % CHUNKS) ^ (row & SWZ). kl0 < RPI and RPI is a power of two, so
@@ -275,15 +302,15 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
   // or 0 (SAMPLE: not stored).
   constexpr uint32_t kNoGate = 0xFFFFFFFFu;
   uint32_t wraw[WLOADS];
-  auto gload = [&](int kb, int buf) {
-    const int live = min(kBN, nkeys - kb);
-    if (!SAMPLE && live == kBN) {
+  auto gload = [&](int kb, uint8_t* ktile) {
+    const int live = min(BN, nkeys - kb);
+    if (!SAMPLE && live == BN) {
       // Full stage of consecutive keys: uniform base + lane offset + i * NW KB.
       const char* kbase = reinterpret_cast<const char*>(p.k + ((int64_t)b * S + kb) * (HI * kDI));
 #pragma unroll
       for (int i = 0; i < LOADS; ++i) {
         const char* src = kbase + i * (NW * 1024) + voff(i);
-        __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(&ktile[buf][(i * NW + wave) * 1024]), 16, 0, 0);
+        lds_dma16(src, &ktile[(i * NW + wave) * 1024]);
       }
     } else {
       // Sample keys or the last stage: rows past the end re-read the last valid key.
@@ -293,7 +320,7 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
         const int key = sweep_key<SAMPLE>(kb + kl, p);
         const int lc = lc0 ^ ((i * RPI) & SWZ);
         const uint16_t* src = p.k + ((int64_t)b * S + key) * (HI * kDI) + lc * 8;
-        __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(&ktile[buf][(i * NW + wave) * 1024]), 16, 0, 0);
+        lds_dma16(src, &ktile[(i * NW + wave) * 1024]);
       }
     }
 #pragma unroll
@@ -308,184 +335,182 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
       wraw[i] = wv;
     }
   };
-  auto wstore = [&](int buf) {
+  auto wstore = [&](float* wtile) {
 #pragma unroll
     for (int i = 0; i < WLOADS; ++i) {
-      if (tid + THREADS * i < WVALS) {
+      const int c = tid + THREADS * i;
+      if (c < WVALS) {
         const float wv = wraw[i] == kNoGate ? (SAMPLE ? 0.f : __builtin_nanf(""))
                                             : to_f32(E{}, (uint16_t)wraw[i]) * p.scale;
-        wtile[buf][tid + THREADS * i] = wv;
+        wtile[(c % HI) * BN + c / HI] = wv;
       }
     }
   };
 
   int st = split;
   if (st < p.nstages) {
-    gload(st * kBN, 0);
-    wstore(0);
+    gload(st * BN, ktile0);
+    wstore(wtile0);
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct LDS loads have landed
   __syncthreads();
 
-  // Appends of one 32-key tile (FILTER). The second tile of a stage is appended one
-  // iteration late, after the stage-end vmcnt(0) + barrier: vmcnt counts stores as well
-  // as the direct LDS loads it waits for, so every store issued before that wait is
-  // followed by at least one tile of MFMA work rather than waited on at once.
-  float tau_r[16];  // thresholds of this lane's 16 rows (filled after the first barrier)
-  // Writes the queued entries to their rows' lists: all of them (`all`) or every full
-  // chunk of 64, moving the rest (< 64) to the front; qn is wave-uniform. Queue entries
-  // are {score bits, key | row << 24}. A row's next slot comes from an LDS atomic on the
-  // wave's own row counters: one instruction's lanes and successive instructions are
-  // served in order, so the lists come out the same on every run. Up to four chunks go
-  // per round, their LDS reads and atomics issued back to back.
-  auto flush = [&](bool all) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const uint32_t full = all ? qn : (qn & ~63u);
-    for (uint32_t h = 0; h < full; h += 256) {
-      int2 e[4];
-      int slot[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const uint32_t i = h + 64 * c + lane;
-        e[c] = i < full ? cq[wave][i] : make_int2(0, -1);
-      }
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        slot[c] = e[c].y != -1 ? atomicAdd(&rcnt[wave][((uint32_t)e[c].y >> 24) & 31u], 1) : p.cap;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        if (slot[c] < p.cap) {
-          const uint32_t rr = ((uint32_t)e[c].y >> 24) & 31u;
-          p.cand[(list0 + (int64_t)rr * nsplit) * p.cap + slot[c]] = make_int2(e[c].x, e[c].y & 0xFFFFFF);
-        }
-      }
-    }
-    const uint32_t rem = qn - full;
-    if (rem > 0 && full > 0) {
-      int2 mv = make_int2(0, 0);
-      if ((uint32_t)lane < rem) mv = cq[wave][full + lane];
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if ((uint32_t)lane < rem) cq[wave][lane] = mv;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    qn = rem;
-  };
-  // Queues the passing entries of a tile: a ballot, a count of the passing lanes below,
-  // one LDS write; the queue is written out once it holds FLUSH entries (checked after
-  // every 8 elements).
-  auto append = [&](const float (&sv)[16], int key) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const bool pass = sv[r] >= tau_r[r];  // NaN (key past the end) never passes
-      const uint64_t m = __ballot(pass);
-      const uint32_t addr = (uint32_t)(uintptr_t)&cq[wave][0] + 8u * (qn + lanes_below_u(m));
-      const uint32_t kt = (uint32_t)key | (half_tag + ((uint32_t)(8 * (r / 4) + (r % 4)) << 24));
-      // The LDS write runs with exec = the passing lanes, set and restored inside one asm
-      // statement, so there is no branch around it (a branch per accumulator element splits
-      // the epilogue into small blocks). The compiler does not count this write in its
-      // lgkmcnt waits; LDS operations of a wave complete in issue order, so an extra
-      // operation can only make those waits stricter, never release one early.
-      uint64_t saved;
-      asm volatile(
-          "s_and_saveexec_b64 %0, %1\n\t"
-          "ds_write_b64 %2, %3\n\t"
-          "s_or_b64 exec, exec, %0"
-          : "=&s"(saved)
-          : "s"(m), "v"(addr), "v"(make_uint2(__float_as_uint(sv[r]), kt))
-          : "memory", "scc");
-      qn += (uint32_t)__popcll(m);
-      if ((r & 7) == 7 && qn >= (uint32_t)ScoreShape<HI>::FLUSH) flush(false);
-    }
-  };
-  // Scores of the tile of 32 keys at kb + nb*32 (+ mask); SAMPLE stores them directly.
-  auto tile_scores = [&](float (&s)[16], int kb, int nb, int buf) {
-    const int kl = nb * 32 + col;
-    const uint8_t* tile = &ktile[buf][nb * 32 * ROW_BYTES];
+  // Scores of this lane's 16 keys of the tile at kb + nb*32 (+ mask); SAMPLE stores them.
+  // Key of element r: k4 + 8(r/4) + r%4 with k4 = kb + nb*32 + 4*half.
+  auto tile_scores = [&](float (&s)[16], int kb, int nb, const uint8_t* ktile, const float* wtile) {
+    const uint8_t* tile = &ktile[nb * 32 * ROW_BYTES];
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.f;
-#pragma unroll
-    for (int h = 0; h < HI; ++h) {
+    // Head h's products are issued before head h - 1's gate epilogue, and the scheduler may
+    // not hoist them further: two accumulators live at a time, not HI.
+    auto products = [&](int h) {
       f32x16 acc = f32x16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const uint4 bop = *reinterpret_cast<const uint4*>(tile + ((h & 1) ? rd_odd[ks] : rd_even[ks]) + h * 128);
-        acc = mfma32(E{}, a[h][ks], bop, acc);
+        const uint4 kop = *reinterpret_cast<const uint4*>(tile + ((h & 1) ? rd_odd[ks] : rd_even[ks]) + h * 128);
+        acc = mfma32(E{}, kop, qop[h][ks], acc);
       }
-      const float wv = wtile[buf][kl * HI + h];
+      return acc;
+    };
+    auto gate = [&](int h, const f32x16& acc) {
+      const float* wg = &wtile[h * BN + nb * 32 + 4 * half];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = fmaf(wv, relu_bits(acc[r]), s[r]);
+      for (int g = 0; g < 4; ++g) {
+        const float4 w4 = *reinterpret_cast<const float4*>(wg + 8 * g);
+        s[4 * g + 0] = fmaf(w4.x, relu_bits(acc[4 * g + 0]), s[4 * g + 0]);
+        s[4 * g + 1] = fmaf(w4.y, relu_bits(acc[4 * g + 1]), s[4 * g + 1]);
+        s[4 * g + 2] = fmaf(w4.z, relu_bits(acc[4 * g + 2]), s[4 * g + 2]);
+        s[4 * g + 3] = fmaf(w4.w, relu_bits(acc[4 * g + 3]), s[4 * g + 3]);
+      }
+    };
+    f32x16 acc_prev = products(0);
+#pragma unroll
+    for (int h = 1; h < HI; ++h) {
+      const f32x16 acc = products(h);
+      gate(h - 1, acc_prev);
+      __builtin_amdgcn_sched_barrier(0);
+      acc_prev = acc;
     }
-    const int kidx = kb + kl;
-    const bool kvalid = kidx < nkeys;
-    const int key = sweep_key<SAMPLE>(kidx, p);
+    gate(HI - 1, acc_prev);
+    const int k4 = kb + nb * 32 + 4 * half;
     if constexpr (HAS_MASK) {
+      if (row_ok) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = q0 + 8 * (r / 4) + 4 * half + (r % 4);
-        if (kvalid && row < T) s[r] += to_f32(E{}, p.mask[((int64_t)b * T + row) * S + key]);
+        for (int r = 0; r < 16; ++r) {
+          const int kidx = k4 + 8 * (r >> 2) + (r & 3);
+          if (kidx < nkeys) s[r] += to_f32(E{}, p.mask[grow * S + sweep_key<SAMPLE>(kidx, p)]);
+        }
       }
     }
     if constexpr (SAMPLE) {
-      if (kvalid) {
+      if (row_ok) {
+        float* dst = p.samp + grow * p.Ms;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = q0 + 8 * (r / 4) + 4 * half + (r % 4);
-          if (row < T) p.samp[((int64_t)b * T + row) * p.Ms + kidx] = s[r];
+        for (int g = 0; g < 4; ++g) {
+          const int kidx = k4 + 8 * g;
+          if (kidx + 3 < nkeys) {
+            *reinterpret_cast<float4*>(dst + kidx) = make_float4(s[4 * g], s[4 * g + 1], s[4 * g + 2], s[4 * g + 3]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (kidx + i < nkeys) dst[kidx + i] = s[4 * g + i];
+          }
         }
       }
     }
   };
-  static_assert(kBN == 64, "two 32-key tiles per stage");
-
-  if constexpr (!SAMPLE) {
+  // FILTER candidates. Per element the lane only compares: bit (16 t + r) of pmask marks
+  // element r of tile t of the stage, whose score the lane has put in its staging row.
+  // After the stage barrier one loop writes the stage's candidates: each round every lane
+  // takes its lowest marked element (iterations: the most any lane holds, about 4 where a
+  // lane holds 1.2 on average), so a stage issues a few mostly full stores instead of 16
+  // mostly empty ones per tile. The two lanes of a query write adjacent slots in a round.
+  constexpr int NT = BN / 32;  // tiles per stage
+  static_assert(NT * 16 + 4 <= kStageRow, "staging row too short");
+  float* const stg = &sstage[wave][lane * kStageRow];
+  uint32_t pmask = 0;  // marked elements of the pending stage
+  int kb_pend = 0;     // its first key + 4 half (this lane's key base)
+  char* const lbytes = reinterpret_cast<char*>(lbase);
+  auto mark = [&](const float (&sv)[16], int t) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const float4 t4 = *reinterpret_cast<const float4*>(&tau_s[wave * kQW + 8 * g + 4 * half]);
-      tau_r[4 * g + 0] = t4.x;
-      tau_r[4 * g + 1] = t4.y;
-      tau_r[4 * g + 2] = t4.z;
-      tau_r[4 * g + 3] = t4.w;
+    for (int g = 0; g < 4; ++g)
+      *reinterpret_cast<float4*>(stg + 16 * t + 4 * g) = make_float4(sv[4 * g], sv[4 * g + 1], sv[4 * g + 2], sv[4 * g + 3]);
+    uint32_t tb = 0;
+#pragma unroll
+    for (int r = 15; r >= 0; --r) tb = tb * 2u + (sv[r] >= tau_l ? 1u : 0u);  // NaN never passes
+    pmask |= tb << (16 * t);
+  };
+  // Element idx = 16 t + r of the stage holds key 32 t + 8 (r / 4) + r % 4 + 4 half past the
+  // stage's first key: idx + (idx & ~3) + 4 half. Two entries per round, so that their LDS
+  // reads share one wait.
+  auto flush = [&]() {
+    uint32_t mm = pmask;
+    pmask = 0;
+    while (__ballot(mm != 0u) != 0ull) {
+      uint32_t idx[2], has[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        has[u] = mm != 0u ? 1u : 0u;
+        idx[u] = has[u] ? (uint32_t)__builtin_ctz(mm) : 0u;
+        mm &= mm - 1u;
+      }
+      float sv[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) sv[u] = stg[idx[u]];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(has[u], has[u], false, false);
+        const uint32_t other = sw[0] ^ sw[1] ^ has[u];  // the partner lane's flag
+        const uint32_t pos = woff + ((half && other) ? 8u : 0u);
+        if (has[u] && pos < wend)
+          *reinterpret_cast<int2*>(lbytes + pos) =
+              make_int2(__float_as_int(sv[u]), kb_pend + (int)(idx[u] + (idx[u] & ~3u)));
+        woff += 8u * (has[u] + other);
+      }
     }
-  }
-  float sp[16];      // FILTER: scores of the pending tile
-  int key_prev = -1; // uniform >= 0: key column base of the pending tile (+ col per lane)
-  int buf = 0;
-  for (; st < p.nstages; st += nsplit) {
-    const int kb = st * kBN;
+  };
+
+  // One stage on buffer (kt, wt), prefetching the next stage into (kn, wn).
+  auto stage = [&](const uint8_t* kt, const float* wt, uint8_t* kn, float* wn) {
+    const int kb = st * BN;
     const bool more = st + nsplit < p.nstages;
-    if (more) gload((st + nsplit) * kBN, buf ^ 1);
-    if constexpr (!SAMPLE) {
-      if (key_prev >= 0) append(sp, key_prev + col);
+    if (more) gload((st + nsplit) * BN, kn);
+    // The previous stage's candidates are written here, after its stage-end vmcnt(0) +
+    // barrier: vmcnt counts stores as well as the direct LDS loads it waits for, so the
+    // stores are followed by a stage of MFMA work before that wait.
+    if constexpr (!SAMPLE) flush();
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      float s0[16];
+      tile_scores(s0, kb, t, kt, wt);
+      if constexpr (!SAMPLE) mark(s0, t);
     }
-    float s0[16];
-    tile_scores(s0, kb, 0, buf);
-    if constexpr (!SAMPLE) append(s0, kb + col);
-    tile_scores(sp, kb, 1, buf);
-    key_prev = kb + 32;
+    kb_pend = kb + 4 * half;
 
     // Keep the gate conversion (which waits for this stage's loads) after the tile work.
     __builtin_amdgcn_sched_barrier(0);
-    if (more) wstore(buf ^ 1);
+    if (more) wstore(wn);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): next stage's direct LDS loads have landed
     __syncthreads();
-    buf ^= 1;
+    st += nsplit;
+  };
+  uint8_t* kt = ktile0;
+  uint8_t* kn = ktile1;
+  float* wt = wtile0;
+  float* wn = wtile1;
+  while (st < p.nstages) {
+    stage(kt, wt, kn, wn);
+    uint8_t* const kx = kt;
+    kt = kn;
+    kn = kx;
+    float* const wx = wt;
+    wt = wn;
+    wn = wx;
   }
   if constexpr (!SAMPLE) {
-    if (key_prev >= 0) append(sp, key_prev + col);
-  }
-
-  if constexpr (!SAMPLE) {
-    flush(true);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (lane < kQW && q0 + lane < T) p.counts[list0 + (int64_t)lane * nsplit] = rcnt[wave][lane];
+    flush();
+    // entries of the list (both lanes hold the same count); above cap: overflowed
+    if (row_ok && half == 0) p.counts[grow * nsplit + split] = (int)((woff - wstart) >> 3);
   }
 }
 
@@ -540,7 +565,7 @@ constexpr int kSelRegs = 48;
 struct SelectParams {
   const int2* cand;
   const int* counts;
-  int nsplit, cap;
+  int nlist, cap, stride;
   int32_t* out_idx;
   uint16_t* out_scores;
   int Kk;
@@ -557,37 +582,37 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-// Row lists as one sequence: off[s] = entries of the lists before split s (uniform);
-// entry e sits at cand + (row * nsplit + s) * cap + (e - off[s]) for the split s holding it.
+// Row lists as one sequence: off[l] = entries of the lists before list l (uniform);
+// entry e sits at cand + (row * nlist + l) * stride + (e - off[l]) for the list l holding it.
 struct RowLists {
-  int64_t base;  // (row * nsplit) * cap
-  int off[kMaxSplit + 1];
-  int nsplit, cap;
+  int64_t base;  // row * nlist * stride
+  int off[kMaxLists + 1];
+  int nlist, stride;
   __device__ __forceinline__ int64_t at(int e) const {
     int64_t a = base + e;
 #pragma unroll
-    for (int s2 = 1; s2 < kMaxSplit; ++s2)
-      if (s2 < nsplit && e >= off[s2]) a += cap - (off[s2] - off[s2 - 1]);
+    for (int s2 = 1; s2 < kMaxLists; ++s2)
+      if (s2 < nlist && e >= off[s2]) a += stride - (off[s2] - off[s2 - 1]);
     return a;
   }
 };
 
 __device__ __forceinline__ bool row_lists(const SelectParams& p, int64_t row, RowLists& rl) {
-  rl.base = row * p.nsplit * (int64_t)p.cap;
-  rl.nsplit = p.nsplit;
-  rl.cap = p.cap;
+  rl.base = row * p.nlist * (int64_t)p.stride;
+  rl.nlist = p.nlist;
+  rl.stride = p.stride;
   bool bad = false;
   int acc = 0;
 #pragma unroll
-  for (int s2 = 0; s2 < kMaxSplit; ++s2) {
+  for (int s2 = 0; s2 < kMaxLists; ++s2) {
     rl.off[s2] = acc;
-    if (s2 < p.nsplit) {
-      const int c = p.counts[row * p.nsplit + s2];
+    if (s2 < p.nlist) {
+      const int c = p.counts[row * p.nlist + s2];
       bad |= c > p.cap;
       acc += min(c, p.cap);
     }
   }
-  rl.off[kMaxSplit] = acc;
+  rl.off[kMaxLists] = acc;
   return bad;
 }
 
@@ -599,7 +624,7 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
   if (row >= p.rows) return;
   RowLists rl;
   const bool bad = row_lists(p, row, rl);
-  const int total = rl.off[kMaxSplit];
+  const int total = rl.off[kMaxLists];
   if (bad || total < p.Kk) {
     // The candidates may miss part of the top-k: exact brute force.
     if (lane == 0) p.fb_list[atomicAdd(p.fb_count, 1)] = (int)row;
@@ -709,9 +734,9 @@ __global__ __launch_bounds__(256) void indexer_select_wide_kernel(const SelectPa
     const int64_t row = p.wide_list[item];
     RowLists rl;
     row_lists(p, row, rl);
-    const int total = rl.off[kMaxSplit];
-    for (int s2 = 0; s2 < p.nsplit; ++s2) {
-      const int2* src = p.cand + rl.base + (int64_t)s2 * p.cap;
+    const int total = rl.off[kMaxLists];
+    for (int s2 = 0; s2 < p.nlist; ++s2) {
+      const int2* src = p.cand + rl.base + (int64_t)s2 * p.stride;
       const int o = rl.off[s2], n = rl.off[s2 + 1] - o;
       for (int i = tid; i < n; i += kSelThreads) {
         const int2 e = src[i];
@@ -840,7 +865,7 @@ Plan make_layout(int64_t B, int64_t T, int64_t S, int64_t topk) {
   size_t off = 0;
   pl.off_tau = off;      off = align_up(off + rows * 4, 256);
   pl.off_samp = off;     off = align_up(off + (pl.sample ? rows * (size_t)pl.Ms * 4 : 0), 256);
-  pl.off_counts = off;   off = align_up(off + rows * kMaxSplit * 4, 256);
+  pl.off_counts = off;   off = align_up(off + rows * kMaxLists * 4, 256);
   pl.off_cand = off;     off = align_up(off + rows * (size_t)kSubTotal * 8, 256);
   pl.off_fb = off;       off = align_up(off + 64, 256);
   pl.off_fblist = off;   off = align_up(off + rows * 4, 256);
@@ -879,12 +904,12 @@ int filter_slots(const void* kernel, int threads) {
 
 // Picks the key split count: the fraction of the last wave of workgroups that is busy,
 // highest first, fewer splits on ties; each split keeps >= 8 stages of 64 keys.
-int choose_nsplit(int64_t tiles, int64_t S, int slots, bool sample) {
+int choose_nsplit(int64_t tiles, int64_t S, int slots, bool sample, int bn) {
   if (!sample) return 1;
   int best = 1;
   double best_eff = -1.0;
   for (int ns = 1; ns <= kMaxSplit; ++ns) {
-    if (ns > 1 && S / (ns * (int64_t)kBN) < 8) break;
+    if (ns > 1 && S / (ns * (int64_t)bn) < 8) break;
     const double waves = (double)(tiles * ns) / slots;
     const double eff = waves / ceil(waves);
     if (eff > best_eff + 1e-9) {
@@ -903,11 +928,13 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   GW_HIP_LAUNCH_CHECK("set_int_kernel");
   constexpr int BM = ScoreShape<HI>::BM;
   constexpr int THREADS = ScoreShape<HI>::THREADS;
+  constexpr int BN = ScoreShape<HI>::BN;
   const int64_t tiles = (base.T + BM - 1) / BM;
   const int64_t rows = B * (int64_t)base.T;
   pl.nsplit = choose_nsplit(tiles * B, base.S, filter_slots((const void*)indexer_score_kernel<E, HI, false, HAS_MASK>, THREADS),
-                            pl.sample);
-  pl.cap = kSubTotal / pl.nsplit;
+                            pl.sample, BN);
+  const int stride = kSubTotal / pl.nsplit;
+  pl.cap = stride;
   float* tau = reinterpret_cast<float*>(ws + pl.off_tau);
   if (pl.sample) {
     ScoreParams sp = base;
@@ -916,7 +943,7 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
     sp.tau = nullptr;
     sp.tau_mode = kTauArray;
     sp.nsplit = 1;
-    sp.nstages = (pl.Ms + kBN - 1) / kBN;
+    sp.nstages = (pl.Ms + BN - 1) / BN;
     hipLaunchKernelGGL((indexer_score_kernel<E, HI, true, HAS_MASK>), dim3((unsigned)tiles, 1, (unsigned)B), dim3(THREADS),
                        0, st, sp);
     GW_HIP_LAUNCH_CHECK("indexer_score_kernel<sample>");
@@ -933,15 +960,16 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   fp.counts = reinterpret_cast<int*>(ws + pl.off_counts);
   fp.nsplit = pl.nsplit;
   fp.cap = pl.cap;
-  fp.nstages = (base.S + kBN - 1) / kBN;
+  fp.nstages = (base.S + BN - 1) / BN;
   hipLaunchKernelGGL((indexer_score_kernel<E, HI, false, HAS_MASK>),
                      dim3((unsigned)tiles, (unsigned)pl.nsplit, (unsigned)B), dim3(THREADS), 0, st, fp);
   GW_HIP_LAUNCH_CHECK("indexer_score_kernel<filter>");
   SelectParams fs{};
   fs.cand = fp.cand;
   fs.counts = fp.counts;
-  fs.nsplit = pl.nsplit;
+  fs.nlist = pl.nsplit;
   fs.cap = pl.cap;
+  fs.stride = stride;
   fs.out_idx = out_idx;
   fs.out_scores = static_cast<uint16_t*>(out_scores);
   fs.Kk = pl.Kk;
