@@ -40,6 +40,11 @@ _SIGNATURES = {
         [ctypes.c_int, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,
          ctypes.c_int, _p, _p, _p, _sz, _p],
     ),
+    "gw_indexer_topk_fwd_view_bias": (
+        ctypes.c_int,
+        [ctypes.c_int, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+         ctypes.c_float, ctypes.c_int, _p, _p, _p, _sz, _p],
+    ),
     "gw_kv_csr_size": (_sz, [_i64, _i64, _i64, _i64]),
     "gw_kv_csr_build_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
     "gw_kv_csr_build": (ctypes.c_int, [_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _sz, _p, _sz, _p]),
@@ -55,6 +60,9 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.c_int, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
          ctypes.c_float, _p, _sz, _p, _sz, _p],
+    ),
+    "gw_indexer_view_bias_bwd_rows": (
+        ctypes.c_int, [ctypes.c_int, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p],
     ),
     "gw_indexer_kl_fwd": (ctypes.c_int, [ctypes.c_int, _p, _p, _i64, _i64, ctypes.c_float, _p, _p]),
     "gw_indexer_kl_bwd": (

@@ -176,13 +176,13 @@ class Block(nn.Module):
     ``attn`` is dense or sparse."""
 
     def __init__(self, dim: int, num_heads: int, mlp_ratio: float, qk_norm: bool, rope_base: Optional[float],
-                 sparse: bool = False, topk: int = 1024, init_values: float = 0.01):
+                 sparse: bool = False, topk: int = 1024, init_values: float = 0.01, score_dtype=None):
         super().__init__()
         self.norm1 = nn.LayerNorm(dim)
         self.sparse = sparse
         if sparse:
             self.attn = dsa_layer.SparseGlobalAttention(dim, num_heads, qk_norm=qk_norm, rope_base=rope_base,
-                                                        topk=topk)
+                                                        topk=topk, score_dtype=score_dtype)
         else:
             self.attn = DenseAttention(dim, num_heads, qk_norm, rope_base)
         self.ls1 = LayerScale(dim, init_values)
@@ -262,8 +262,10 @@ class Aggregator(nn.Module):
                  num_register_tokens: int = 4, qk_norm: bool = True, rope_freq: float = 100.0,
                  indexer_layers="9-19", reuse_topk_groups=None, topk: int = 1024, patch_depth: int = 24,
                  img_size: int = 518, patch_size: int = 14, source_downsample_factor: int = 1,
-                 source_downsample_options: Optional[Dict] = None):
+                 source_downsample_options: Optional[Dict] = None, score_dtype=None):
         super().__init__()
+        # score_dtype: the sparse layers' indexer and attention dtype (the reference preset's
+        # indexer_cfg "score_dtype", geoweave/configs/vggt.json:35); None = the activations'.
         # Approximate coarse selection in the sparse layers (off at factor 1, the reference
         # default; dsa_attention.py:122-132): the per-forward layout is filled in below.
         self.source_downsample_factor = int(source_downsample_factor)
@@ -283,7 +285,8 @@ class Aggregator(nn.Module):
                                            and l in self.sparse_layers and s in self.sparse_layers}
         self.frame_blocks = nn.ModuleList(Block(dim, num_heads, mlp_ratio, qk_norm, rope) for _ in range(depth))
         self.global_blocks = nn.ModuleList(
-            Block(dim, num_heads, mlp_ratio, qk_norm, rope, sparse=i in self.sparse_layers, topk=topk)
+            Block(dim, num_heads, mlp_ratio, qk_norm, rope, sparse=i in self.sparse_layers, topk=topk,
+                  score_dtype=score_dtype)
             for i in range(depth))
         self.register_buffer("_resnet_mean", torch.tensor(_RESNET_MEAN).view(1, 1, 3, 1, 1), persistent=False)
         self.register_buffer("_resnet_std", torch.tensor(_RESNET_STD).view(1, 1, 3, 1, 1), persistent=False)

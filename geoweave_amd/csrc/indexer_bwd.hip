@@ -302,3 +302,80 @@ extern "C" int gw_indexer_topk_bwd(int dtype, const void* q, const void* k, cons
   if (dtype == GW_DTYPE_BF16) return dispatch_idx_bwd<BF16>((int)Hi, p, (int)B, L.max_items, st);
   return dispatch_idx_bwd<FP16>((int)Hi, p, (int)B, L.max_items, st);
 }
+
+// ---------------------------------------------------------------------------------------
+// Soft view-bias gradient, per query row (reference _scatter_view_bias_grad,
+// sparse_topk_indexer.py:898-932: grad_view_bias[b, q_view[t], s_view[idx[b,t,j]]] +=
+// grad_scores[b,t,j] in fp32). This pass writes the row sums over key views,
+// part[b, t, v] = sum_{j : s_view[idx[b,t,j]] == v} grad[b,t,j]; the host groups the rows
+// by query view (a one-hot product). One wave per row: lane l adds entries l, l + 64, ...
+// into its own LDS histogram, then bin v sums the 64 histograms in lane order — a fixed
+// order, no atomics. Positions outside [0, S) contribute nothing.
+namespace gw {
+namespace {
+
+constexpr int kViewChunk = 128;  // key-view bins per pass (a 32 KB LDS histogram set)
+
+// View ids are clamped into the table (the host checks their range).
+__device__ __forceinline__ int clamp_bin(int v, int n) { return v < 0 ? 0 : (v >= n ? n - 1 : v); }
+
+template <typename E>
+__global__ __launch_bounds__(64) void view_bias_rows_kernel(const int32_t* __restrict__ idx,
+                                                            const uint16_t* __restrict__ grad,
+                                                            const int32_t* __restrict__ sview, int T, int S,
+                                                            int K, int Vs, float* __restrict__ part) {
+  __shared__ float hist[64 * kViewChunk];  // [lane][bin of the current chunk]
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;  // b * T + t
+  const int b = (int)(row / T);
+  float* mine = hist + lane * kViewChunk;
+  const int32_t* ir = idx + row * K;
+  const uint16_t* gr = grad + row * K;
+  const int32_t* sv = sview + (int64_t)b * S;
+  for (int v0 = 0; v0 < Vs; v0 += kViewChunk) {
+    const int nb = min(kViewChunk, Vs - v0);
+    for (int v = 0; v < nb; ++v) mine[v] = 0.f;
+    for (int j = lane; j < K; j += 64) {
+      const int s = ir[j];
+      if (s >= 0 && s < S) {
+        const int v = clamp_bin(sv[s], Vs) - v0;
+        if (v >= 0 && v < nb) mine[v] += to_f32(E{}, gr[j]);
+      }
+    }
+    __syncthreads();
+    for (int v = lane; v < nb; v += 64) {
+      float acc = 0.f;
+      for (int l = 0; l < 64; ++l) acc += hist[l * kViewChunk + v];
+      part[row * Vs + v0 + v] = acc;
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace
+}  // namespace gw
+
+extern "C" int gw_indexer_view_bias_bwd_rows(int dtype, const int32_t* topk_indices, const void* grad_scores,
+                                             const int32_t* s_view_ids, int64_t B, int64_t T, int64_t S,
+                                             int64_t K, int64_t Vs, float* row_grad, void* stream) {
+  using namespace gw;
+  clear_error();
+  GW_CHECK_ARG(dtype == GW_DTYPE_BF16 || dtype == GW_DTYPE_FP16, "unsupported dtype code %d", dtype);
+  GW_CHECK_ARG(B >= 0 && T >= 0 && S >= 1 && K >= 0, "invalid sizes B=%lld T=%lld S=%lld K=%lld", (long long)B,
+               (long long)T, (long long)S, (long long)K);
+  GW_CHECK_ARG(Vs >= 1 && Vs < (1ll << 20), "invalid key view count %lld", (long long)Vs);
+  if (B * T == 0) return GW_OK;
+  GW_CHECK_ARG(topk_indices && grad_scores && s_view_ids && row_grad, "null tensor pointer");
+  GW_CHECK_ARG(B * T < (1ll << 31) && S < (1ll << 31) && K < (1ll << 31), "size exceeds the int32 range");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == GW_DTYPE_BF16)
+    hipLaunchKernelGGL(view_bias_rows_kernel<BF16>, dim3((unsigned)(B * T)), dim3(64), 0, st, topk_indices,
+                       static_cast<const uint16_t*>(grad_scores), s_view_ids, (int)T, (int)S, (int)K, (int)Vs,
+                       row_grad);
+  else
+    hipLaunchKernelGGL(view_bias_rows_kernel<FP16>, dim3((unsigned)(B * T)), dim3(64), 0, st, topk_indices,
+                       static_cast<const uint16_t*>(grad_scores), s_view_ids, (int)T, (int)S, (int)K, (int)Vs,
+                       row_grad);
+  GW_HIP_LAUNCH_CHECK("view_bias_rows_kernel");
+  return GW_OK;
+}

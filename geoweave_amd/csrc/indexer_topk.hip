@@ -2,6 +2,7 @@
 // matrix in memory.
 //
 //   score[b,t,s] = sum_h w[b,s,h] * relu(scale * <q[b,t,h], k[b,s,h]>)  (+ mask[b,t,s])
+//                  (+ view_bias[b, q_view[b,t], s_view[b,s]])
 //
 // (reference easyvolcap/official_vggt/layers/indexer.py:430-466 and
 // easyvolcap/utils/custom_indexer/sparse_topk_indexer.py:935-951). scale > 0 lets the
@@ -132,11 +133,24 @@ __device__ __forceinline__ uint32_t lanes_below_u(uint64_t m) {
 
 enum TauMode { kTauArray = 0, kTauPlusInf = 1, kTauMinusInf = 2 };
 
+// Additive score terms (template flags): the dense mask [B, T, S] and the soft view bias, a
+// [B, Vq, Vs] table indexed by the query's and the key's view ids (reference
+// sparse_topk_indexer.py:935-951: (score + mask) + view_bias, in that order). View ids are
+// clamped into the table, so bad ids cannot read outside it; the host checks their range.
+constexpr int kBiasMask = 1;
+constexpr int kBiasView = 2;
+
+__device__ __forceinline__ int clamp_view(int v, int n) { return v < 0 ? 0 : (v >= n ? n - 1 : v); }
+
 struct ScoreParams {
   const uint16_t* q;     // [B, T, HI, 64]
   const uint16_t* k;     // [B, S, HI, 64]
   const uint16_t* w;     // [B, S, HI]
   const uint16_t* mask;  // [B, T, S] or null
+  const uint16_t* vbias;  // kBiasView: [B, Vq, Vs]
+  const int* qview;       // kBiasView: [B, T]
+  const int* sview;       // kBiasView: [B, S]
+  int Vq, Vs;
   const float* tau;      // [B*T] or null (-inf)
   float* samp;           // SAMPLE: [B*T, Ms]
   int2* cand;            // FILTER: candidate lists (see kSubTotal)
@@ -206,7 +220,7 @@ struct ScoreShape {
 // hold disjoint keys and append to two lists of their own.
 constexpr int kStageRow = 36;  // two tiles of 16 scores per lane, padded
 
-template <typename E, int HI, bool SAMPLE, bool HAS_MASK>
+template <typename E, int HI, bool SAMPLE, int BIAS>
 __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_PER_EU) void indexer_score_kernel(
     const ScoreParams p) {
   constexpr int NW = ScoreShape<HI>::NW;
@@ -244,6 +258,10 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
   const int row = q0 + col;  // this lane's query
   const bool row_ok = row < T;
   const int64_t grow = (int64_t)b * T + (row_ok ? row : 0);
+  // kBiasView: the view-bias table row of this lane's query.
+  const uint16_t* vrow = nullptr;
+  if constexpr ((BIAS & kBiasView) != 0)
+    vrow = p.vbias + ((int64_t)b * p.Vq + clamp_view(p.qview[grow], p.Vq)) * p.Vs;
 
   // B operands: this lane's query row, k-chunk (lane / 32) of each 16-wide step.
   uint4 qop[HI][4];
@@ -393,12 +411,22 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
     }
     gate(HI - 1, acc_prev);
     const int k4 = kb + nb * 32 + 4 * half;
-    if constexpr (HAS_MASK) {
+    if constexpr ((BIAS & kBiasMask) != 0) {
       if (row_ok) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int kidx = k4 + 8 * (r >> 2) + (r & 3);
           if (kidx < nkeys) s[r] += to_f32(E{}, p.mask[grow * S + sweep_key<SAMPLE>(kidx, p)]);
+        }
+      }
+    }
+    if constexpr ((BIAS & kBiasView) != 0) {
+      if (row_ok) {
+        const int* sv = p.sview + (int64_t)b * S;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kidx = k4 + 8 * (r >> 2) + (r & 3);
+          if (kidx < nkeys) s[r] += to_f32(E{}, vrow[clamp_view(sv[sweep_key<SAMPLE>(kidx, p)], p.Vs)]);
         }
       }
     }
@@ -770,6 +798,10 @@ struct FallbackParams {
   const uint16_t* k;
   const uint16_t* w;
   const uint16_t* mask;
+  const uint16_t* vbias;
+  const int* qview;
+  const int* sview;
+  int Vq, Vs;
   const int* fb_count;
   const int* fb_list;
   float* scratch;  // [gridDim.x, S]
@@ -779,7 +811,7 @@ struct FallbackParams {
   float scale;
 };
 
-template <typename E, int HI, bool HAS_MASK>
+template <typename E, int HI, int BIAS>
 __global__ __launch_bounds__(256) void indexer_fallback_kernel(const FallbackParams p) {
   __shared__ __attribute__((aligned(16))) uint32_t qs[HI * kDI / 2];
   __shared__ SelectShared sh;
@@ -810,7 +842,10 @@ __global__ __launch_bounds__(256) void indexer_fallback_kernel(const FallbackPar
         const float wv = to_f32(E{}, p.w[((int64_t)b * p.S + j) * HI + h]) * p.scale;
         s = fmaf(wv, relu_bits(z), s);
       }
-      if constexpr (HAS_MASK) s += to_f32(E{}, p.mask[(int64_t)row * p.S + j]);
+      if constexpr ((BIAS & kBiasMask) != 0) s += to_f32(E{}, p.mask[(int64_t)row * p.S + j]);
+      if constexpr ((BIAS & kBiasView) != 0)
+        s += to_f32(E{}, p.vbias[((int64_t)b * p.Vq + clamp_view(p.qview[row], p.Vq)) * p.Vs +
+                                 clamp_view(p.sview[(int64_t)b * p.S + j], p.Vs)]);
       sc[j] = s;
     }
     __threadfence_block();
@@ -920,7 +955,7 @@ int choose_nsplit(int64_t tiles, int64_t S, int slots, bool sample, int bn) {
   return best;
 }
 
-template <typename E, int HI, bool HAS_MASK>
+template <typename E, int HI, int BIAS>
 int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, void* out_scores,
               uint8_t* ws, hipStream_t st) {
   int* fb_count = reinterpret_cast<int*>(ws + pl.off_fb);  // [0] brute force, [1] wide select
@@ -931,7 +966,7 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   constexpr int BN = ScoreShape<HI>::BN;
   const int64_t tiles = (base.T + BM - 1) / BM;
   const int64_t rows = B * (int64_t)base.T;
-  pl.nsplit = choose_nsplit(tiles * B, base.S, filter_slots((const void*)indexer_score_kernel<E, HI, false, HAS_MASK>, THREADS),
+  pl.nsplit = choose_nsplit(tiles * B, base.S, filter_slots((const void*)indexer_score_kernel<E, HI, false, BIAS>, THREADS),
                             pl.sample, BN);
   const int stride = kSubTotal / pl.nsplit;
   pl.cap = stride;
@@ -944,7 +979,7 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
     sp.tau_mode = kTauArray;
     sp.nsplit = 1;
     sp.nstages = (pl.Ms + BN - 1) / BN;
-    hipLaunchKernelGGL((indexer_score_kernel<E, HI, true, HAS_MASK>), dim3((unsigned)tiles, 1, (unsigned)B), dim3(THREADS),
+    hipLaunchKernelGGL((indexer_score_kernel<E, HI, true, BIAS>), dim3((unsigned)tiles, 1, (unsigned)B), dim3(THREADS),
                        0, st, sp);
     GW_HIP_LAUNCH_CHECK("indexer_score_kernel<sample>");
     const dim3 tgrid((unsigned)((rows + 3) / 4));
@@ -961,7 +996,7 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   fp.nsplit = pl.nsplit;
   fp.cap = pl.cap;
   fp.nstages = (base.S + BN - 1) / BN;
-  hipLaunchKernelGGL((indexer_score_kernel<E, HI, false, HAS_MASK>),
+  hipLaunchKernelGGL((indexer_score_kernel<E, HI, false, BIAS>),
                      dim3((unsigned)tiles, (unsigned)pl.nsplit, (unsigned)B), dim3(THREADS), 0, st, fp);
   GW_HIP_LAUNCH_CHECK("indexer_score_kernel<filter>");
   SelectParams fs{};
@@ -989,6 +1024,11 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   bp.k = base.k;
   bp.w = base.w;
   bp.mask = base.mask;
+  bp.vbias = base.vbias;
+  bp.qview = base.qview;
+  bp.sview = base.sview;
+  bp.Vq = base.Vq;
+  bp.Vs = base.Vs;
   bp.fb_count = fb_count;
   bp.fb_list = fs.fb_list;
   bp.scratch = reinterpret_cast<float*>(ws + pl.off_scratch);
@@ -998,19 +1038,19 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   bp.S = base.S;
   bp.Kk = pl.Kk;
   bp.scale = base.scale;
-  hipLaunchKernelGGL((indexer_fallback_kernel<E, HI, HAS_MASK>), dim3(kFallbackBlocks), dim3(256), 0, st, bp);
+  hipLaunchKernelGGL((indexer_fallback_kernel<E, HI, BIAS>), dim3(kFallbackBlocks), dim3(256), 0, st, bp);
   GW_HIP_LAUNCH_CHECK("indexer_fallback_kernel");
   return GW_OK;
 }
 
-template <typename E, bool HAS_MASK>
+template <typename E, int BIAS>
 int dispatch_hi(int hi, const ScoreParams& base, const Plan& pl, int64_t B, int32_t* out_idx,
                 void* out_scores, uint8_t* ws, hipStream_t st) {
   switch (hi) {
-    case 1: return run_typed<E, 1, HAS_MASK>(base, pl, B, out_idx, out_scores, ws, st);
-    case 2: return run_typed<E, 2, HAS_MASK>(base, pl, B, out_idx, out_scores, ws, st);
-    case 4: return run_typed<E, 4, HAS_MASK>(base, pl, B, out_idx, out_scores, ws, st);
-    default: return run_typed<E, 8, HAS_MASK>(base, pl, B, out_idx, out_scores, ws, st);
+    case 1: return run_typed<E, 1, BIAS>(base, pl, B, out_idx, out_scores, ws, st);
+    case 2: return run_typed<E, 2, BIAS>(base, pl, B, out_idx, out_scores, ws, st);
+    case 4: return run_typed<E, 4, BIAS>(base, pl, B, out_idx, out_scores, ws, st);
+    default: return run_typed<E, 8, BIAS>(base, pl, B, out_idx, out_scores, ws, st);
   }
 }
 
@@ -1022,13 +1062,14 @@ extern "C" size_t gw_indexer_topk_workspace_size(int64_t B, int64_t T, int64_t S
   return gw::make_layout(B, T, S, topk).total;
 }
 
-extern "C" int gw_indexer_topk_fwd(int dtype, const void* q, const void* k, const void* w,
-                                   const void* mask, int64_t B, int64_t T, int64_t S, int64_t Hi,
-                                   int64_t Di, int64_t topk, float softmax_scale, int flags,
-                                   int32_t* out_indices, void* out_scores, void* workspace,
-                                   size_t workspace_bytes, void* stream) {
-  using namespace gw;
-  clear_error();
+namespace gw {
+namespace {
+
+int indexer_topk_impl(int dtype, const void* q, const void* k, const void* w, const void* mask,
+                      const void* view_bias, const int32_t* q_view_ids, const int32_t* s_view_ids, int64_t Vq,
+                      int64_t Vs, int64_t B, int64_t T, int64_t S, int64_t Hi, int64_t Di, int64_t topk,
+                      float softmax_scale, int flags, int32_t* out_indices, void* out_scores, void* workspace,
+                      size_t workspace_bytes, void* stream) {
   GW_CHECK_ARG(dtype == GW_DTYPE_BF16 || dtype == GW_DTYPE_FP16, "unsupported dtype code %d", dtype);
   GW_CHECK_ARG(B >= 0 && T >= 0 && S >= 0 && topk >= 1, "invalid sizes B=%lld T=%lld S=%lld topk=%lld",
                (long long)B, (long long)T, (long long)S, (long long)topk);
@@ -1037,6 +1078,11 @@ extern "C" int gw_indexer_topk_fwd(int dtype, const void* q, const void* k, cons
                      (long long)Hi, (long long)Di);
   GW_CHECK_ARG(softmax_scale > 0.f, "softmax_scale must be positive, got %g", (double)softmax_scale);
   GW_CHECK_ARG((flags & ~7) == 0 && (flags & 3) != 3, "invalid flags %d", flags);
+  const bool has_view = view_bias != nullptr;
+  if (has_view)
+    GW_CHECK_ARG(q_view_ids && s_view_ids && Vq >= 1 && Vs >= 1 && Vq * Vs < (1ll << 30),
+                 "view bias needs q/s view ids and a [B, Vq, Vs] table (Vq=%lld Vs=%lld)", (long long)Vq,
+                 (long long)Vs);
   if (B == 0 || T == 0) return GW_OK;
   GW_CHECK_ARG(S >= 1, "empty key set");
   const int64_t Kk = topk < S ? topk : S;
@@ -1058,6 +1104,11 @@ extern "C" int gw_indexer_topk_fwd(int dtype, const void* q, const void* k, cons
   base.k = static_cast<const uint16_t*>(k);
   base.w = static_cast<const uint16_t*>(w);
   base.mask = static_cast<const uint16_t*>(mask);
+  base.vbias = static_cast<const uint16_t*>(view_bias);
+  base.qview = q_view_ids;
+  base.sview = s_view_ids;
+  base.Vq = (int)Vq;
+  base.Vs = (int)Vs;
   base.T = (int)T;
   base.S = (int)S;
   base.scale = softmax_scale;
@@ -1067,10 +1118,47 @@ extern "C" int gw_indexer_topk_fwd(int dtype, const void* q, const void* k, cons
   base.force_wide = (flags & GW_TOPK_FLAG_FORCE_WIDE) ? 1 : 0;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool has_mask = mask != nullptr;
-  if (dtype == GW_DTYPE_BF16)
-    return has_mask ? dispatch_hi<BF16, true>((int)Hi, base, pl, B, out_indices, out_scores, ws, st)
-                    : dispatch_hi<BF16, false>((int)Hi, base, pl, B, out_indices, out_scores, ws, st);
-  return has_mask ? dispatch_hi<FP16, true>((int)Hi, base, pl, B, out_indices, out_scores, ws, st)
-                  : dispatch_hi<FP16, false>((int)Hi, base, pl, B, out_indices, out_scores, ws, st);
+  const int bias = (mask != nullptr ? kBiasMask : 0) | (has_view ? kBiasView : 0);
+  const int hi = (int)Hi;
+  if (dtype == GW_DTYPE_BF16) {
+    switch (bias) {
+      case 0: return dispatch_hi<BF16, 0>(hi, base, pl, B, out_indices, out_scores, ws, st);
+      case kBiasMask: return dispatch_hi<BF16, kBiasMask>(hi, base, pl, B, out_indices, out_scores, ws, st);
+      case kBiasView: return dispatch_hi<BF16, kBiasView>(hi, base, pl, B, out_indices, out_scores, ws, st);
+      default: return dispatch_hi<BF16, kBiasMask | kBiasView>(hi, base, pl, B, out_indices, out_scores, ws, st);
+    }
+  }
+  switch (bias) {
+    case 0: return dispatch_hi<FP16, 0>(hi, base, pl, B, out_indices, out_scores, ws, st);
+    case kBiasMask: return dispatch_hi<FP16, kBiasMask>(hi, base, pl, B, out_indices, out_scores, ws, st);
+    case kBiasView: return dispatch_hi<FP16, kBiasView>(hi, base, pl, B, out_indices, out_scores, ws, st);
+    default: return dispatch_hi<FP16, kBiasMask | kBiasView>(hi, base, pl, B, out_indices, out_scores, ws, st);
+  }
+}
+
+}  // namespace
+}  // namespace gw
+
+extern "C" int gw_indexer_topk_fwd(int dtype, const void* q, const void* k, const void* w,
+                                   const void* mask, int64_t B, int64_t T, int64_t S, int64_t Hi,
+                                   int64_t Di, int64_t topk, float softmax_scale, int flags,
+                                   int32_t* out_indices, void* out_scores, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  gw::clear_error();
+  return gw::indexer_topk_impl(dtype, q, k, w, mask, nullptr, nullptr, nullptr, 0, 0, B, T, S, Hi, Di, topk,
+                               softmax_scale, flags, out_indices, out_scores, workspace, workspace_bytes, stream);
+}
+
+extern "C" int gw_indexer_topk_fwd_view_bias(int dtype, const void* q, const void* k, const void* w,
+                                             const void* mask, const void* view_bias, const int32_t* q_view_ids,
+                                             const int32_t* s_view_ids, int64_t Vq, int64_t Vs, int64_t B,
+                                             int64_t T, int64_t S, int64_t Hi, int64_t Di, int64_t topk,
+                                             float softmax_scale, int flags, int32_t* out_indices,
+                                             void* out_scores, void* workspace, size_t workspace_bytes,
+                                             void* stream) {
+  gw::clear_error();
+  GW_CHECK_ARG(view_bias != nullptr, "null view-bias table");
+  return gw::indexer_topk_impl(dtype, q, k, w, mask, view_bias, q_view_ids, s_view_ids, Vq, Vs, B, T, S, Hi, Di,
+                               topk, softmax_scale, flags, out_indices, out_scores, workspace, workspace_bytes,
+                               stream);
 }

@@ -15,7 +15,14 @@ the reference package leaves it ``None`` (``custom_indexer/__init__.py:7``).
 Inputs: q ``[B,T,Hi,Di]``, k ``[B,S,Hi,Di]``, w ``[B,S,Hi]`` in one 16-bit float dtype on
 the GPU; mask: ``None``, an empty tensor, or an additive ``[B,T,S]`` (broadcast from
 ``[T,S]``/``[1,T,S]``). Supported: ``Di = 64``, ``Hi in {1,2,4,8}``, ``K <= 2048``.
-``view_bias_data`` (the soft view-bias training kernel) is not implemented.
+
+``view_bias_data`` (the soft view-bias training kernel, reference ``:2108-2186``): a dict
+with ``q_view_ids`` ``[B,T]``/``[T]``, ``s_view_ids`` ``[B,S]``/``[S]`` and ``view_bias``
+``[B,Vq,Vs]``/``[Vq,Vs]``; every score gets ``view_bias[b, q_view_ids[b,t],
+s_view_ids[b,s]]`` added after the mask, inside the HIP top-k (``gw_indexer_topk_fwd_view_bias``),
+and ``view_bias`` receives the gradient of the selected scores (``gw_indexer_view_bias_bwd_rows``
+and a one-hot product over query views). A dict missing any of the three keys counts as
+no view bias, as in the reference (``:635-636``).
 """
 from __future__ import annotations
 
@@ -26,7 +33,8 @@ import torch
 
 from .. import _lib
 
-__all__ = ["sparse_topk_indexer_func", "sparse_topk_indexer_inference_func", "SparseTopkIndexerFunc"]
+__all__ = ["sparse_topk_indexer_func", "sparse_topk_indexer_inference_func", "SparseTopkIndexerFunc",
+           "SparseTopkIndexerViewBiasFunc"]
 
 FLAG_TAU_PLUS_INF = 1
 FLAG_TAU_MINUS_INF = 2
@@ -62,6 +70,50 @@ def _check(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor):
         raise NotImplementedError(f"indexer heads x dim {n_heads} x {head_dim} not built (1/2/4/8 x 64)")
 
 
+def _normalize_view_bias_data(view_bias_data: Optional[dict], bsz: int, tgt_len: int, src_len: int,
+                              device, dtype) -> Optional[dict]:
+    """The reference's shape rules (``sparse_topk_indexer.py:621-659``): 1-D id vectors and a
+    2-D table gain a batch dimension, a batch of one is broadcast to ``bsz``; ids become
+    int64 and the table takes q's dtype. Missing keys: None (no view bias)."""
+    if view_bias_data is None:
+        return None
+    q_ids = view_bias_data.get("q_view_ids", None)
+    s_ids = view_bias_data.get("s_view_ids", None)
+    table = view_bias_data.get("view_bias", None)
+    if q_ids is None or s_ids is None or table is None:
+        return None
+    q_ids = q_ids.unsqueeze(0) if q_ids.dim() == 1 else q_ids
+    s_ids = s_ids.unsqueeze(0) if s_ids.dim() == 1 else s_ids
+    table = table.unsqueeze(0) if table.dim() == 2 else table
+    if q_ids.size(0) == 1 and bsz > 1:
+        q_ids = q_ids.expand(bsz, -1)
+    if s_ids.size(0) == 1 and bsz > 1:
+        s_ids = s_ids.expand(bsz, -1)
+    if table.size(0) == 1 and bsz > 1:
+        table = table.expand(bsz, -1, -1)
+    if tuple(q_ids.shape) != (bsz, tgt_len):
+        raise ValueError(f"q_view_ids shape {tuple(q_ids.shape)} mismatches ({bsz}, {tgt_len})")
+    if tuple(s_ids.shape) != (bsz, src_len):
+        raise ValueError(f"s_view_ids shape {tuple(s_ids.shape)} mismatches ({bsz}, {src_len})")
+    if table.dim() != 3 or int(table.shape[0]) != int(bsz):
+        raise ValueError(f"view_bias shape {tuple(table.shape)} mismatches batch {bsz}")
+    return dict(q_view_ids=q_ids.to(device=device, dtype=torch.long),
+                s_view_ids=s_ids.to(device=device, dtype=torch.long),
+                view_bias=table.to(device=device, dtype=dtype))
+
+
+def _view_ids_int32(q_view_ids: torch.Tensor, s_view_ids: torch.Tensor, n_q_views: int, n_s_views: int):
+    """int32 contiguous ids, checked against the table (an out-of-range id is an indexing
+    error in the reference's gather, ``indexer.py:519``; the kernels clamp, this raises)."""
+    qv = q_view_ids.to(torch.int32).contiguous()
+    sv = s_view_ids.to(torch.int32).contiguous()
+    lo_q, hi_q, lo_s, hi_s = torch.stack([qv.min(), qv.max(), sv.min(), sv.max()]).tolist()
+    if lo_q < 0 or hi_q >= n_q_views or lo_s < 0 or hi_s >= n_s_views:
+        raise IndexError(f"view ids out of range: q in [{lo_q}, {hi_q}] for {n_q_views} query views, "
+                         f"s in [{lo_s}, {hi_s}] for {n_s_views} key views")
+    return qv, sv
+
+
 def indexer_topk_forward(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -70,8 +122,11 @@ def indexer_topk_forward(
     topk: int,
     softmax_scale: Optional[float],
     flags: int = 0,
+    view_bias: Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Launches gw_indexer_topk_fwd on the current stream; returns (indices, scores)."""
+    """Launches gw_indexer_topk_fwd (gw_indexer_topk_fwd_view_bias when ``view_bias`` =
+    (q_view_ids int32 [B,T], s_view_ids int32 [B,S], table [B,Vq,Vs] in q's dtype), all
+    contiguous) on the current stream; returns (indices, scores)."""
     _check(q, k, w)
     q = q.contiguous()
     k = k.contiguous()
@@ -93,6 +148,16 @@ def indexer_topk_forward(
     lib = _lib.load()
     ws_bytes = int(lib.gw_indexer_topk_workspace_size(bsz, tgt_len, src_len, kk))
     ws = torch.empty(max(ws_bytes, 16), device=q.device, dtype=torch.uint8)
+    if view_bias is not None:
+        qv, sv, table = view_bias
+        rc = lib.gw_indexer_topk_fwd_view_bias(
+            _lib.dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), w.data_ptr(), _lib.ptr(mask),
+            table.data_ptr(), qv.data_ptr(), sv.data_ptr(), int(table.shape[1]), int(table.shape[2]),
+            bsz, tgt_len, src_len, n_heads, head_dim, kk, float(softmax_scale), int(flags),
+            idx.data_ptr(), scores.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_handle(q.device),
+        )
+        _lib.check(rc, "gw_indexer_topk_fwd_view_bias")
+        return idx, scores
     rc = lib.gw_indexer_topk_fwd(
         _lib.dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), w.data_ptr(), _lib.ptr(mask),
         bsz, tgt_len, src_len, n_heads, head_dim, kk, float(softmax_scale), int(flags),
@@ -136,6 +201,67 @@ class SparseTopkIndexerFunc(torch.autograd.Function):
         return dq, dk, dw, None, None, None, None, None
 
 
+def view_bias_backward(topk_indices: torch.Tensor, grad_scores: torch.Tensor, q_view_ids: torch.Tensor,
+                       s_view_ids: torch.Tensor, shape, dtype) -> torch.Tensor:
+    """grad of view_bias ``[B, Vq, Vs]`` from the selected scores' gradient (reference
+    ``_scatter_view_bias_grad``, ``sparse_topk_indexer.py:898-932``): fp32 sums, cast to the
+    table's dtype. Row sums over key views on the GPU (``gw_indexer_view_bias_bwd_rows``,
+    fixed order), then per batch the one-hot matrix of query views times the row sums."""
+    bsz, tgt_len, kk = topk_indices.shape
+    _, n_q, n_s = shape
+    src_len = int(s_view_ids.shape[1])
+    rows = torch.empty((bsz, tgt_len, n_s), device=grad_scores.device, dtype=torch.float32)
+    if bsz * tgt_len > 0:
+        g = grad_scores.to(topk_indices.device).contiguous()
+        if g.dtype not in (torch.float16, torch.bfloat16):
+            raise TypeError(f"grad_scores must be bfloat16 or float16, got {g.dtype}")
+        rc = _lib.load().gw_indexer_view_bias_bwd_rows(
+            _lib.dtype_code(g.dtype), topk_indices.contiguous().data_ptr(), g.data_ptr(), s_view_ids.data_ptr(),
+            bsz, tgt_len, src_len, kk, n_s, rows.data_ptr(), _lib.stream_handle(g.device))
+        _lib.check(rc, "gw_indexer_view_bias_bwd_rows")
+    onehot = torch.nn.functional.one_hot(q_view_ids.long(), n_q).to(torch.float32)  # [B, T, Vq]
+    grad = torch.bmm(onehot.transpose(1, 2).contiguous(), rows)  # [B, Vq, Vs]
+    return grad.to(dtype)
+
+
+class SparseTopkIndexerViewBiasFunc(torch.autograd.Function):
+    """Autograd wrapper with the soft view bias (reference ``sparse_topk_indexer.py:
+    2108-2186``): gradients for q, k, w (as ``SparseTopkIndexerFunc``) and for the table."""
+
+    @staticmethod
+    def forward(ctx, q, k, w, mask, q_view_ids, s_view_ids, view_bias, topk, softmax_scale, block_k, merge_blocks):
+        q = q.contiguous()
+        k = k.contiguous()
+        w = w.contiguous()
+        if softmax_scale is None:
+            softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+        table = view_bias.contiguous()
+        qv, sv = _view_ids_int32(q_view_ids, s_view_ids, int(table.shape[1]), int(table.shape[2]))
+        with torch.no_grad():
+            topk_indices, topk_scores = indexer_topk_forward(q, k, w, mask, topk, softmax_scale,
+                                                             view_bias=(qv, sv, table))
+        ctx.save_for_backward(q, k, w, topk_indices, qv, sv)
+        ctx.softmax_scale = float(softmax_scale)
+        ctx.view_bias_shape = tuple(int(x) for x in view_bias.shape)
+        ctx.view_bias_dtype = view_bias.dtype
+        ctx.mark_non_differentiable(topk_indices)
+        return topk_indices, topk_scores
+
+    @staticmethod
+    def backward(ctx, grad_indices, grad_scores):
+        q, k, w, topk_indices, qv, sv = ctx.saved_tensors
+        if grad_scores is None:
+            return (None,) * 11
+        if grad_scores.stride(-1) != 1:
+            grad_scores = grad_scores.contiguous()
+        dq, dk, dw = indexer_topk_backward(q, k, w, topk_indices, grad_scores, ctx.softmax_scale)
+        grad_view_bias = None
+        if ctx.needs_input_grad[6]:
+            grad_view_bias = view_bias_backward(topk_indices, grad_scores, qv, sv, ctx.view_bias_shape,
+                                                ctx.view_bias_dtype)
+        return dq, dk, dw, None, None, None, grad_view_bias, None, None, None, None
+
+
 def sparse_topk_indexer_func(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -148,10 +274,18 @@ def sparse_topk_indexer_func(
     view_bias_data: Optional[dict] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Drop-in for the reference ``sparse_topk_indexer_func`` (``:2188-2253``)."""
-    if view_bias_data is not None:
-        raise NotImplementedError("view_bias_data (soft view-bias kernel) is not supported by the HIP indexer")
     if mask is not None and mask.numel() == 0:
         mask = None
+    if view_bias_data is not None:
+        _check(q, k, w)
+        norm = _normalize_view_bias_data(view_bias_data, int(q.shape[0]), int(q.shape[1]), int(k.shape[1]),
+                                         q.device, q.dtype)
+        if norm is not None:
+            if softmax_scale is None:
+                softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+            return SparseTopkIndexerViewBiasFunc.apply(q, k, w, mask, norm["q_view_ids"], norm["s_view_ids"],
+                                                       norm["view_bias"], topk, float(softmax_scale), block_k,
+                                                       int(merge_blocks))
     return SparseTopkIndexerFunc.apply(q, k, w, mask, topk, softmax_scale, block_k, merge_blocks)
 
 

@@ -16,8 +16,13 @@ reference's parameter names (``qkv``, ``q_norm``, ``k_norm``, ``proj``,
    place from ``y`` through strides.
 3. ``gw_indexer_topk_fwd`` (top-k), ``gw_sparse_attn_fwd`` (attention), then ``proj``.
 
-The layer runs in one 16-bit dtype (bf16 by default); the glue's LayerNorm and RoPE are
-fp32 math on the 16-bit projection with one rounding at the end.
+The layer runs in the activations' 16-bit dtype (bf16 by default); the glue's LayerNorm
+and RoPE are fp32 math on the 16-bit projection with one rounding at the end. With
+``score_dtype`` set (the reference preset's ``"score_dtype": "float16"`` under bf16
+activations, ``geoweave/configs/vggt.json:35``), the attention q/k/v and the indexer q/k/w
+are cast to it after the glue and the indexer and attention run in it; their output is cast
+back to the activations' dtype before ``proj`` (``dsa_attention.py:4943-4948,5473``,
+``:617-620``).
 """
 from __future__ import annotations
 
@@ -37,7 +42,33 @@ from .custom_indexer.sparse_topk_indexer import sparse_topk_indexer_func, sparse
 from . import source_downsample as sdown
 
 __all__ = ["GlueLayout", "rope2d_tables", "dsa_glue_forward", "sparse_attention_streaming",
-           "LightningIndexerProjections", "SparseGlobalAttention"]
+           "LightningIndexerProjections", "SparseGlobalAttention", "parse_score_dtype"]
+
+
+def parse_score_dtype(value) -> Optional[torch.dtype]:
+    """The reference's dtype spelling (``DSAAttention._parse_dtype``,
+    ``dsa_attention.py:503-518``): a torch dtype, or "fp16"/"float16"/"half"/"f16",
+    "bf16"/"bfloat16", "fp32"/"float32"/"f32"; None, "", "none" and (as in the reference)
+    any other string mean "the activations' dtype". fp32 is refused: the HIP kernels
+    compute on 16-bit inputs."""
+    if value is None:
+        return None
+    if isinstance(value, str):
+        text = value.strip().lower()
+        if text in ("", "none"):
+            return None
+        table = {"fp16": torch.float16, "float16": torch.float16, "half": torch.float16, "f16": torch.float16,
+                 "bf16": torch.bfloat16, "bfloat16": torch.bfloat16,
+                 "fp32": torch.float32, "float32": torch.float32, "f32": torch.float32}
+        if text not in table:
+            return None
+        value = table[text]
+    if not isinstance(value, torch.dtype):
+        raise TypeError(f"score_dtype must be a torch dtype or a string, not {type(value).__name__}")
+    if value not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"score_dtype {value} is not supported: the indexer and attention kernels take "
+                        "bfloat16 or float16")
+    return value
 
 
 class GlueLayout:
@@ -265,9 +296,10 @@ class SparseGlobalAttention(nn.Module):
 
     def __init__(self, dim: int = 1024, num_heads: int = 16, qkv_bias: bool = True, proj_bias: bool = True,
                  qk_norm: bool = True, rope_base: Optional[float] = 100.0, indexer_heads: int = 4,
-                 indexer_dim: int = 64, topk: int = 1024):
+                 indexer_dim: int = 64, topk: int = 1024, score_dtype=None):
         super().__init__()
         self.dim = dim
+        self.score_dtype = parse_score_dtype(score_dtype)
         self.num_heads = num_heads
         self.head_dim = dim // num_heads
         self.scale = self.head_dim ** -0.5
@@ -280,6 +312,12 @@ class SparseGlobalAttention(nn.Module):
         self.topk = topk
         self.layout = GlueLayout(num_heads, self.head_dim, indexer_heads, indexer_dim)
         self._fused = None
+
+    def _to_score_dtype(self, x_dtype: torch.dtype, *tensors):
+        sd = self.score_dtype
+        if sd is None or sd == x_dtype:
+            return tensors
+        return tuple(None if t is None else t.to(sd) for t in tensors)
 
     def fused_projection(self, dtype: torch.dtype):
         """(W [ldy, dim], b [ldy]) in ``dtype``: ``[qkv | q_proj | k_proj | w_proj]`` plus zero
@@ -327,10 +365,11 @@ class SparseGlobalAttention(nn.Module):
             y, self.layout, _ln_params(self.q_norm), _ln_params(self.k_norm), _ln_params(self.indexer.k_norm),
             self.q_norm.eps if isinstance(self.q_norm, nn.LayerNorm) else 1e-5,
             pos if self.rope_base else None, self.rope_base or 100.0, rope_len)
+        q, k, v, iq, ik, iw = self._to_score_dtype(x.dtype, q, k, v, iq, ik, iw)
         kk = min(int(topk or self.topk), N)
         if query_chunk is not None and 0 < int(query_chunk) < N and topk_indices is None:
             o = sparse_attention_streaming(q, k, v, iq, ik, iw, kk, int(query_chunk), float(self.indexer.scale),
-                                           self.scale, source_downsample)
+                                           self.scale, source_downsample).to(x.dtype)
             out = F.linear(o.reshape(B, N, self.dim), self.proj.weight.to(x.dtype),
                            None if self.proj.bias is None else self.proj.bias.to(x.dtype))
             return (out, None) if return_topk else out
@@ -348,6 +387,7 @@ class SparseGlobalAttention(nn.Module):
                 idx, _ = sparse_topk_indexer_inference_func(iq, ik, iw, iq.new_empty(0), kk,
                                                             float(self.indexer.scale), 256, 0)
         o, _ = sparse_index_flash_attn_inference_func(q, k, v, idx, softmax_scale=self.scale)
+        o = o.to(x.dtype)
         out = F.linear(o.reshape(B, N, self.dim), self.proj.weight.to(x.dtype),
                        None if self.proj.bias is None else self.proj.bias.to(x.dtype))
         return (out, idx) if return_topk else out
@@ -385,9 +425,11 @@ class SparseGlobalAttention(nn.Module):
         q, k, iq, ik, iw = GlueFunction.apply(y, *ln(self.q_norm), *ln(self.k_norm), *ln(self.indexer.k_norm), lay, eps,
                                               pos32, cos, sin, n_rope)
         v = y[..., lay.v_off:lay.v_off + lay.H * 64].view(B, N, lay.H, 64)
+        q, k, v, iq, ik, iw = self._to_score_dtype(x.dtype, q, k, v, iq, ik, iw)
         kk = min(int(topk or self.topk), N)
         idx, scores = sparse_topk_indexer_func(iq, ik, iw, iq.new_empty(0), kk, float(self.indexer.scale), 256, 0)
         o, attn = sparse_index_flash_attn_func(q, k, v, idx, None, False, self.scale)
+        o = o.to(x.dtype)
         out = F.linear(o.reshape(B, N, self.dim), self.proj.weight.to(x.dtype),
                        None if self.proj.bias is None else self.proj.bias.to(x.dtype))
         return out, attn, scores, idx

@@ -120,6 +120,24 @@ int gw_indexer_topk_fwd(int dtype, const void* q, const void* k, const void* w, 
                         void* workspace, size_t workspace_bytes,
                         void* stream);
 
+/* The same top-k with the soft view bias added to every score (replaces
+ * SparseTopkIndexerViewBiasFunc.forward, easyvolcap/utils/custom_indexer/
+ * sparse_topk_indexer.py:2108-2157, whose _blockwise_topk_scores adds the term after the
+ * mask, :935-951; the bias itself is indexer.py:509-519):
+ *   score[b,t,s] = ... (+ mask[b,t,s]) + view_bias[b, q_view_ids[b,t], s_view_ids[b,s]]
+ * view_bias: [B, Vq, Vs] contiguous, in q's dtype; q_view_ids [B, T] and s_view_ids [B, S]
+ * int32, in [0, Vq) and [0, Vs) (ids outside are clamped into the table). Other arguments
+ * and the workspace as gw_indexer_topk_fwd.
+ */
+int gw_indexer_topk_fwd_view_bias(int dtype, const void* q, const void* k, const void* w, const void* mask,
+                                  const void* view_bias, const int32_t* q_view_ids,
+                                  const int32_t* s_view_ids, int64_t Vq, int64_t Vs,
+                                  int64_t B, int64_t T, int64_t S, int64_t Hi, int64_t Di, int64_t topk,
+                                  float softmax_scale, int flags,
+                                  int32_t* out_indices, void* out_scores,
+                                  void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
 /* ------------------------------------------------------------------------------------
  * Key-major (CSR) transpose of a [B, T, K] position table, shared by both backward
  * passes below (the attention's kv_positions and the indexer's topk_indices are the
@@ -207,6 +225,19 @@ int gw_indexer_topk_bwd(int dtype, const void* q, const void* k, const void* w,
                         const void* csr, size_t csr_bytes,
                         void* workspace, size_t workspace_bytes,
                         void* stream);
+
+/* Soft view-bias gradient, per query row: the first half of _scatter_view_bias_grad
+ * (easyvolcap/utils/custom_indexer/sparse_topk_indexer.py:898-932, called from
+ * SparseTopkIndexerViewBiasFunc.backward, :2159-2186). row_grad[b,t,v] (fp32 [B, T, Vs]) =
+ * sum of grad_scores[b,t,j] over the j whose key s = topk_indices[b,t,j] has
+ * s_view_ids[b,s] == v, summed in a fixed order (no atomics); positions outside [0, S) add
+ * nothing. grad_view_bias[b, vq, v] is then the sum of row_grad[b,t,v] over the rows with
+ * q_view_ids[b,t] == vq (the host's one-hot product). grad_scores: [B, T, K] in the 16-bit
+ * dtype; s_view_ids: [B, S] int32.
+ */
+int gw_indexer_view_bias_bwd_rows(int dtype, const int32_t* topk_indices, const void* grad_scores,
+                                  const int32_t* s_view_ids, int64_t B, int64_t T, int64_t S, int64_t K,
+                                  int64_t Vs, float* row_grad, void* stream);
 
 /* ------------------------------------------------------------------------------------
  * Indexer KL training loss, forward and backward.

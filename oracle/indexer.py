@@ -23,8 +23,10 @@ def indexer_scores(
     softmax_scale: Optional[float] = None,
     key_chunk: int = 4096,
     query_chunk: int = 2048,
+    view_bias: Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = None,
 ) -> torch.Tensor:
-    """score[b,t,s] = sum_h w[b,s,h] * relu(scale * <q[b,t,h], k[b,s,h]>) (+ mask[b,t,s]).
+    """score[b,t,s] = sum_h w[b,s,h] * relu(scale * <q[b,t,h], k[b,s,h]>) (+ mask[b,t,s])
+    (+ view_bias[b, q_view[b,t], s_view[b,s]]).
 
     Restates ``LightningIndexer._compute_scores`` / ``_compute_score_chunk``
     (reference ``easyvolcap/official_vggt/layers/indexer.py:383-466``) with every head in
@@ -33,7 +35,9 @@ def indexer_scores(
     additive mask (``indexer.py:412-415``). Everything is fp32 (the torch backend's
     ``score_dtype='float32'``, ``geoweave/inference.py:58``). Chunking over keys is the
     reference's own ``score_key_chunk_size`` loop; chunking over queries leaves per-row
-    arithmetic unchanged.
+    arithmetic unchanged. ``view_bias`` = (q_view_ids [B,T], s_view_ids [B,S], table
+    [B,Vq,Vs]): the soft view-bias term, added after the mask (``_compute_score_chunk``,
+    ``indexer.py:460-465``; ``sparse_topk_indexer.py:935-951``).
     """
     q = q.float()
     k = k.float()
@@ -54,7 +58,35 @@ def indexer_scores(
             out[:, t0:t1, s0:s1] = hs.sum(dim=2, dtype=torch.float32)
     if mask is not None and mask.numel() > 0:
         out = out + mask.float()
+    if view_bias is not None:
+        out = out + view_bias_term(*view_bias)
     return out
+
+
+def view_bias_term(q_view_ids: torch.Tensor, s_view_ids: torch.Tensor, table: torch.Tensor) -> torch.Tensor:
+    """fp32 ``[B,T,S]``: ``table[b, q_view_ids[b,t], s_view_ids[b,s]]`` (reference
+    ``LightningIndexer._compute_view_bias_chunk``, ``indexer.py:509-519``, over the whole key
+    range; ids ``[B,T]``/``[B,S]``, table ``[B,Vq,Vs]``)."""
+    qv = q_view_ids.long()
+    sv = s_view_ids.long()
+    tab = table.float()
+    bidx = torch.arange(tab.shape[0]).view(-1, 1, 1)
+    return tab[bidx, qv.unsqueeze(-1), sv.unsqueeze(1)]
+
+
+def view_bias_grad(indices: torch.Tensor, grad_scores: torch.Tensor, q_view_ids: torch.Tensor,
+                   s_view_ids: torch.Tensor, table_shape) -> torch.Tensor:
+    """fp32 gradient of the table from the selected scores' gradient: for every selected
+    (b, t, j), ``grad[b, q_view[b,t], s_view[b, indices[b,t,j]]] += grad_scores[b,t,j]``.
+    Restates ``_scatter_view_bias_grad`` (reference ``sparse_topk_indexer.py:898-932``: flat
+    index ``b*Vq*Vs + q_view*Vs + s_view``, fp32 ``scatter_add_``)."""
+    bsz, n_q, n_s = table_shape
+    idx = indices.long()
+    sv_sel = torch.gather(s_view_ids.long(), 1, idx.reshape(bsz, -1)).view_as(idx)  # [B,T,K]
+    lin = (torch.arange(bsz).view(-1, 1, 1) * (n_q * n_s) + q_view_ids.long().unsqueeze(-1) * n_s + sv_sel)
+    out = torch.zeros(bsz * n_q * n_s, dtype=torch.float32)
+    out.scatter_add_(0, lin.reshape(-1), grad_scores.float().reshape(-1))
+    return out.view(bsz, n_q, n_s)
 
 
 def indexer_topk(
@@ -65,6 +97,7 @@ def indexer_topk(
     topk: int,
     softmax_scale: Optional[float] = None,
     query_chunk: int = 1024,
+    view_bias: Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """(indices int32 [B,T,K], scores fp32 [B,T,K]) of the K largest scores per row.
 
@@ -81,7 +114,8 @@ def indexer_topk(
     for t0 in range(0, tgt_len, query_chunk):
         t1 = min(t0 + query_chunk, tgt_len)
         m = None if mask is None or mask.numel() == 0 else mask[:, t0:t1]
-        sc = indexer_scores(q[:, t0:t1], k, w, m, softmax_scale)
+        vb = None if view_bias is None else (view_bias[0][:, t0:t1], view_bias[1], view_bias[2])
+        sc = indexer_scores(q[:, t0:t1], k, w, m, softmax_scale, view_bias=vb)
         v, i = sc.topk(kk, dim=-1, sorted=False)
         idx[:, t0:t1] = i.to(torch.int32)
         val[:, t0:t1] = v

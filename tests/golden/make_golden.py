@@ -8,6 +8,11 @@ fixtures can pin the oracle:
   ``tests/indexer_projected_tests.py:130-187`` (q = [[1,0],[0,1]],
   k = [[1,0],[0.2,0.8],[0,1],[0.8,0.2]], w = 1, top-2, scale = 1/sqrt(2)) with the view
   bias removed; plus a 2-head case with signed w and an additive mask (-inf entries).
+* indexer_view_bias_kat.json - the reference's view-bias cases of
+  ``tests/indexer_projected_tests.py``: the top-2 case of :130-187 with its view bias, the
+  all-tie top-1 case of :64-128 (q = k = 0, so the bias alone ranks the keys) and the
+  gradient case of :189-243 with the table gradient of sum(topk_scores) counted by hand
+  from its (unambiguous) top-2 sets; plus a 2-head case with a mask and 3 x 2 views.
 * attn_fixture.json - sparse attention with the reference's hard-coded top-k index
   fixture ``[[0,2,5],[1,4,3],[0,3,5],[2,4,1]]`` (``tests/dsa_objective_value_gate_tests.py:370-374``)
   and a ragged row with -1 padding (``tests/sparse_index_flash_attn_tests.py:37-44``):
@@ -67,6 +72,47 @@ def make_indexer_kat():
     sc2 = indexer_scores_bf(q2, k2, w2, 0.5, mask)
     cases.append(dict(name="two_heads_signed_w_mask", q=q2, k=k2, w=w2, mask=mask, topk=3, scale=0.5,
                       scores=sc2, expected_sets=[topk_set(r, 3) for r in sc2]))
+    return cases
+
+
+def make_view_bias_kat():
+    def case(name, q, k, w, qv, sv, table, topk, scale, mask=None, grad=False):
+        sc = indexer_scores_bf(q, k, w, scale, mask)
+        sc = [[sc[t][s] + table[qv[t]][sv[s]] for s in range(len(k))] for t in range(len(q))]
+        c = dict(name=name, q=q, k=k, w=w, mask=mask, q_view_ids=[qv], s_view_ids=[sv], view_bias=[table],
+                 topk=topk, scale=scale, scores=sc)
+        if grad:
+            # d sum(topk_scores) / d table: one per selected (t, s), at (q_view[t], s_view[s])
+            g = [[0.0] * len(table[0]) for _ in table]
+            for t, row in enumerate(sc):
+                for s in topk_set(row, topk):
+                    g[qv[t]][sv[s]] += 1.0
+            c["table_grad_of_sum"] = [g]
+        return c
+
+    cases = []
+    scale = 1.0 / math.sqrt(2.0)
+    cases.append(case("reference_view_bias_top2",
+                      [[[1.0, 0.0]], [[0.0, 1.0]]],
+                      [[[1.0, 0.0]], [[0.2, 0.8]], [[0.0, 1.0]], [[0.8, 0.2]]],
+                      [[1.0]] * 4, [0, 1], [0, 0, 1, 1], [[0.0, 4.0], [3.0, 0.0]], 2, scale))
+    cases.append(case("reference_view_bias_ties_top1",
+                      [[[0.0] * 4], [[0.0] * 4]], [[[0.0] * 4]] * 4, [[1.0]] * 4,
+                      [0, 1], [0, 0, 1, 1], [[0.0, 5.0], [7.0, 0.0]], 1, 0.5))
+    cases.append(case("reference_view_bias_gradient",
+                      [[[1.0, 0.0]], [[0.0, 1.0]]],
+                      [[[1.0, 0.0]], [[0.0, 1.0]], [[0.7, 0.3]], [[0.3, 0.7]]],
+                      [[1.0]] * 4, [0, 1], [0, 0, 1, 1], [[0.0, 2.0], [1.5, 0.0]], 2, scale, grad=True))
+    rng = random.Random(20261202)
+    T, S, H, D = 4, 9, 2, 3
+    q2 = [[[rng.choice([-1.0, -0.5, 0.5, 1.0, 2.0]) for _ in range(D)] for _ in range(H)] for _ in range(T)]
+    k2 = [[[rng.choice([-1.0, 0.25, 0.5, 1.5]) for _ in range(D)] for _ in range(H)] for _ in range(S)]
+    w2 = [[rng.choice([-0.5, 0.75, 1.0, 1.25]) for _ in range(H)] for _ in range(S)]
+    mask = [[(-math.inf if (t + 2 * s) % 7 == 0 else 0.25 * ((t + s) % 3)) for s in range(S)] for t in range(T)]
+    qv = [0, 2, 1, 2]
+    sv = [1, 0, 0, 1, 1, 0, 1, 0, 1]
+    table = [[0.5, -1.0], [2.0, 0.0], [-0.75, 1.5]]
+    cases.append(case("two_heads_mask_three_by_two_views", q2, k2, w2, qv, sv, table, 3, 0.5, mask, grad=True))
     return cases
 
 
@@ -131,8 +177,9 @@ def make_attention_fixture():
 
 def main():
     (HERE / "indexer_kat.json").write_text(json.dumps(make_indexer_kat(), indent=1) + "\n")
+    (HERE / "indexer_view_bias_kat.json").write_text(json.dumps(make_view_bias_kat(), indent=1) + "\n")
     (HERE / "attn_fixture.json").write_text(json.dumps(make_attention_fixture(), indent=1) + "\n")
-    print("wrote", HERE / "indexer_kat.json", HERE / "attn_fixture.json")
+    print("wrote", HERE / "indexer_kat.json", HERE / "indexer_view_bias_kat.json", HERE / "attn_fixture.json")
 
 
 if __name__ == "__main__":

@@ -144,8 +144,123 @@ def test_dropin_entry_points(gpu_device):
     i2, s2 = sti.sparse_topk_indexer_inference_func(qd, kd, wd, qd.new_empty(0), 1024, 0.125, 256, 0,
                                                      outer_query_chunk=0, return_scores=True)
     assert torch.equal(i1, i2) and torch.equal(s1, s2)
-    with pytest.raises(NotImplementedError):
-        sti.sparse_topk_indexer_func(qd, kd, wd, None, 16, 0.125, 256, 0, view_bias_data={})
+    # a view-bias dict without its three keys is no view bias (reference :635-636)
+    i3, s3 = sti.sparse_topk_indexer_func(qd, kd, wd, None, 1024, 0.125, 256, 0, view_bias_data={})
+    assert torch.equal(i1, i3) and torch.equal(s1, s3)
+
+
+def _pad64(x):
+    return torch.nn.functional.pad(x, (0, 64 - x.shape[-1]))
+
+
+@pytest.mark.parametrize("case", json.loads((GOLDEN / "indexer_view_bias_kat.json").read_text()),
+                         ids=lambda c: c["name"])
+def test_view_bias_golden_kat(gpu_device, case):
+    # The reference's view-bias cases (tests/indexer_projected_tests.py:64-243), q/k
+    # zero-padded to Di = 64, through the drop-in with view_bias_data: index sets against the
+    # fp64 fixture scores (tie-aware), and d sum(topk_scores) / d view_bias counted by hand.
+    dev = "cuda"
+    q = _pad64(torch.tensor(case["q"]).unsqueeze(0)).bfloat16().to(dev).requires_grad_()
+    k = _pad64(torch.tensor(case["k"]).unsqueeze(0)).bfloat16().to(dev).requires_grad_()
+    w = torch.tensor(case["w"]).unsqueeze(0).bfloat16().to(dev).requires_grad_()
+    mask = None if case["mask"] is None else torch.tensor(case["mask"]).unsqueeze(0).bfloat16().to(dev)
+    table = torch.tensor(case["view_bias"], device=dev, requires_grad=True)  # fp32 [1, Vq, Vs]
+    vbd = dict(q_view_ids=torch.tensor(case["q_view_ids"], device=dev),
+               s_view_ids=torch.tensor(case["s_view_ids"], device=dev), view_bias=table)
+    idx, sc = sti.sparse_topk_indexer_func(q, k, w, mask, case["topk"], case["scale"], 256, 0, view_bias_data=vbd)
+    ref = torch.tensor(case["scores"], dtype=torch.float32)
+    rep = check_topk_rows(ref, idx[0].cpu(), case["topk"])
+    assert rep.ok, rep
+    torch.testing.assert_close(sc[0].float().cpu(), ref.gather(1, idx[0].long().cpu()), atol=2e-2, rtol=2e-2)
+    if "table_grad_of_sum" in case:
+        sc.float().sum().backward()
+        assert table.grad.dtype == torch.float32
+        torch.testing.assert_close(table.grad.cpu(), torch.tensor(case["table_grad_of_sum"]), atol=0, rtol=0)
+
+
+def _views(n, per_view):
+    return (torch.arange(n) // per_view).to(torch.int64)
+
+
+@pytest.mark.parametrize("with_mask", [False, True])
+def test_view_bias_layer_inputs(gpu_device, with_mask):
+    # S = 4 views of 1374 tokens (B = 1) or 2 x 1000-token batch elements with a mask; a
+    # table of N(0, 2) entries moves many selections across views.
+    if with_mask:
+        q, k, w = workloads.indexer_inputs(1, 2, torch.bfloat16, tokens=2000)
+        per = 500
+    else:
+        q, k, w = workloads.indexer_inputs(4, 1, torch.bfloat16)
+        per = 1374
+    B, N = q.shape[:2]
+    g = torch.Generator().manual_seed(21)
+    nv = (N + per - 1) // per
+    table = (2 * torch.randn(B, nv, nv, generator=g)).bfloat16()
+    qv = _views(N, per).expand(B, N).contiguous()
+    sv = _views(N, per).flip(0).expand(B, N).contiguous()  # key views in another order
+    mask = None
+    if with_mask:
+        mask = torch.randn(B, N, N, generator=g)
+        mask[torch.rand(B, N, N, generator=g) < 0.1] = float("-inf")
+        mask = mask.bfloat16()
+    topk = 512
+    dev = "cuda"
+    qv32, sv32 = qv.to(torch.int32).to(dev), sv.to(torch.int32).to(dev)
+    idx, sc = sti.indexer_topk_forward(q.to(dev), k.to(dev), w.to(dev), None if mask is None else mask.to(dev),
+                                       topk, 0.125, view_bias=(qv32, sv32, table.to(dev)))
+    idx, sc = idx.cpu(), sc.cpu()
+    for b in range(B):
+        ref = oidx.indexer_scores(q[b:b + 1], k[b:b + 1], w[b:b + 1], None if mask is None else mask[b:b + 1].float(),
+                                  0.125, view_bias=(qv[b:b + 1], sv[b:b + 1], table[b:b + 1]))[0]
+        rep = check_topk_rows(ref, idx[b], topk)
+        assert rep.ok, f"batch {b}: {rep}"
+        torch.testing.assert_close(sc[b].float(), ref.gather(1, idx[b].long()), atol=2e-2, rtol=2e-2)
+    # the bias changed the selection (a test of the term, not of the plain top-k again)
+    plain, _ = _gpu_topk(q, k, w, topk, mask=mask)
+    assert not torch.equal(plain.sort(-1).values, idx.sort(-1).values)
+
+
+@pytest.mark.parametrize("flags", [sti.FLAG_TAU_PLUS_INF, sti.FLAG_FORCE_WIDE])
+def test_view_bias_forced_fallback_paths(gpu_device, flags):
+    # the brute-force path (every query) and the LDS select path include the bias too
+    q, k, w = workloads.indexer_inputs(4, 1, torch.bfloat16)
+    q = q[:, :768].contiguous()
+    N = k.shape[1]
+    g = torch.Generator().manual_seed(22)
+    table = (3 * torch.randn(1, 2, 4, generator=g)).bfloat16()
+    qv = (torch.arange(768) % 2).view(1, -1)
+    sv = _views(N, 1374).view(1, -1)
+    dev = "cuda"
+    idx, sc = sti.indexer_topk_forward(q.to(dev), k.to(dev), w.to(dev), None, 1024, 0.125, flags,
+                                       view_bias=(qv.to(torch.int32).to(dev), sv.to(torch.int32).to(dev),
+                                                  table.to(dev)))
+    ref = oidx.indexer_scores(q, k, w, None, 0.125, view_bias=(qv, sv, table))[0]
+    rep = check_topk_rows(ref, idx[0].cpu(), 1024)
+    assert rep.ok, rep
+    torch.testing.assert_close(sc[0].float().cpu(), ref.gather(1, idx[0].long().cpu()), atol=2e-2, rtol=2e-2)
+
+
+def test_view_bias_gradients(gpu_device):
+    # A learnable [Vq, Vs] table broadcast over B = 2 (the soft view-bias training path):
+    # its gradient against the oracle's scatter (fp32 sums over the GPU's own selection,
+    # summed over the batch as the broadcast does); dq/dk/dw equal the plain backward's on
+    # the same selection (the bias does not enter them).
+    q, k, w = workloads.indexer_inputs(1, 2, torch.bfloat16, tokens=1500)
+    B, N = q.shape[:2]
+    dev = "cuda"
+    g = torch.Generator().manual_seed(23)
+    table = torch.randn(3, 5, generator=g).to(dev).requires_grad_()
+    qv = (torch.arange(N) * 3 // N).to(dev)
+    sv = (torch.arange(N) % 5).to(dev)
+    qd, kd, wd = (x.to(dev).requires_grad_() for x in (q, k, w))
+    idx, sc = sti.sparse_topk_indexer_func(qd, kd, wd, None, 256, 0.125, 256, 0,
+                                           view_bias_data=dict(q_view_ids=qv, s_view_ids=sv, view_bias=table))
+    gs = torch.randn(sc.shape, generator=g).bfloat16()
+    (sc.float() * gs.float().to(dev)).sum().backward()
+    want = oidx.view_bias_grad(idx.cpu(), gs, qv.cpu().expand(B, N), sv.cpu().expand(B, N), (B, 3, 5)).sum(0)
+    torch.testing.assert_close(table.grad.cpu(), want, atol=2e-2, rtol=1e-2)
+    dq, dk, dw = sti.indexer_topk_backward(q.to(dev), k.to(dev), w.to(dev), idx, gs.to(dev), 0.125)
+    assert torch.equal(qd.grad, dq) and torch.equal(kd.grad, dk) and torch.equal(wd.grad, dw)
 
 
 @pytest.mark.parametrize("views", [16])

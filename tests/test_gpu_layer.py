@@ -123,6 +123,50 @@ def test_sparse_global_attention_layer_stage_by_stage(gpu_device):
     torch.testing.assert_close(out.float().cpu(), ref, **TOL)
 
 
+def test_score_dtype_float16_layer_at_s4(gpu_device, monkeypatch):
+    # The reference preset's precision mode (geoweave/configs/vggt.json:35, "score_dtype":
+    # "float16" under bf16 activations; dsa_attention.py:4943-4948, :617-620): after the glue
+    # the attention q/k/v and the indexer q/k/w are cast to fp16, top-k and attention run in
+    # fp16, and the output returns to bf16 before proj. C1's shape: S = 4 views of 1374
+    # tokens, 16 heads of 64, top-k 1024.
+    B, N, dim, K = 1, 4 * 1374, 1024, 1024
+    m = _layer(dim, seed=11)
+    m.topk = K
+    m.score_dtype = dsa_layer.parse_score_dtype("float16")
+    m = m.cuda()
+    seen = []
+    real = dsa_layer.sparse_index_flash_attn_inference_func
+
+    def spy(q, k, v, idx, **kw):
+        seen.append((q.dtype, k.dtype, v.dtype))
+        return real(q, k, v, idx, **kw)
+
+    monkeypatch.setattr(dsa_layer, "sparse_index_flash_attn_inference_func", spy)
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(B, N, dim, generator=g).bfloat16()
+    pos = torch.randint(0, 38, (B, N, 2), generator=g)
+    out, idx = m(x.cuda(), pos.cuda(), return_topk=True)
+    torch.cuda.synchronize()
+    assert seen == [(torch.float16,) * 3]
+    assert out.dtype == torch.bfloat16
+
+    w, b = m.fused_projection(torch.bfloat16)
+    y = F.linear(x.cuda(), w, b)
+    norms = [(t.weight.detach().cuda(), t.bias.detach().cuda()) for t in (m.q_norm, m.k_norm, m.indexer.k_norm)]
+    glue = dsa_layer.dsa_glue_forward(y, m.layout, *norms, 1e-5, pos.cuda())
+    gq, gk, gv, giq, gik, giw = [t.to(torch.float16).cpu() for t in glue]
+    # indices: exact top-1024 of the oracle scores over the fp16 indexer q/k/w
+    ref_scores = oidx.indexer_scores(giq, gik, giw, None, 0.125)[0]
+    rep = check_topk_rows(ref_scores, idx[0].cpu(), K)
+    assert rep.ok, rep
+    # attention over those indices on the fp16 q/k/v, o rounded to fp16 then bf16, proj
+    o, _, _ = oatt.sparse_attention(gq, gk, gv, idx.cpu(), 0.125)
+    o = o.to(torch.float16).to(torch.bfloat16).float()
+    ref = F.linear(o.reshape(B, N, dim), m.proj.weight.detach().bfloat16().float().cpu(),
+                   m.proj.bias.detach().bfloat16().float().cpu())
+    torch.testing.assert_close(out.float().cpu(), ref, **TOL)
+
+
 def test_query_chunked_stream_equals_the_whole_layer(gpu_device):
     # The query-chunked sparse stream (dsa_attention.py:1017-1283) selects and attends per
     # chunk of queries; rows are independent, so the output equals the unchunked layer's
@@ -177,16 +221,19 @@ def test_glue_backward_matches_autograd_of_the_oracle(gpu_device, with_ln, with_
                 assert err < 2e-3, (key, err)
 
 
-def test_layer_training_gradients_match_the_fp32_pipeline(gpu_device):
+@pytest.mark.parametrize("score_dtype", [None, "float16"])
+def test_layer_training_gradients_match_the_fp32_pipeline(gpu_device, score_dtype):
     # forward_train + KL loss through every HIP backward (glue, indexer, attention, KL) vs
     # autograd of the fp32 CPU pipeline on the same bf16 inputs/weights and the GPU's own
-    # top-k indices. Bar: per-tensor relative error (norm) within 2e-2.
+    # top-k indices. Bar: per-tensor relative error (norm) within 2e-2. With score_dtype
+    # "float16" the indexer and attention run on fp16 casts of the glue's bf16 outputs and
+    # their gradients return through the casts.
     from geoweave_amd.custom_indexer import sparse_indexer_kl_loss
     from oracle import kl_loss as okl
 
     B, N, dim, K = 1, 600, 256, 64
     torch.manual_seed(3)
-    m = dsa_layer.SparseGlobalAttention(dim=dim, num_heads=4, topk=K)
+    m = dsa_layer.SparseGlobalAttention(dim=dim, num_heads=4, topk=K, score_dtype=score_dtype)
     with torch.no_grad():
         for name, p in m.named_parameters():
             p.copy_(torch.randn_like(p) * (dim ** -0.5 if p.dim() == 2 else 0.1))
@@ -203,6 +250,8 @@ def test_layer_training_gradients_match_the_fp32_pipeline(gpu_device):
 
     xd = x.cuda().requires_grad_()
     out, attn, scores, idx = m.forward_train(xd, pos.cuda())
+    assert scores.dtype == (torch.float16 if score_dtype else torch.bfloat16)
+    assert out.dtype == torch.bfloat16
     p = attn.to(torch.bfloat16)
     p = p / (p.sum(-1, keepdim=True) + 1e-6)
     loss = (out.float() * G.cuda()).sum() + sparse_indexer_kl_loss(p, scores, 1e-6)

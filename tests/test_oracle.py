@@ -39,6 +39,47 @@ def test_indexer_scores_and_topk_match_golden(case):
     torch.testing.assert_close(val, sc.gather(-1, idx.long()))
 
 
+def _view_bias_case(case):
+    q = _t(case["q"]).unsqueeze(0)
+    k = _t(case["k"]).unsqueeze(0)
+    w = _t(case["w"]).unsqueeze(0)
+    mask = None if case["mask"] is None else _t(case["mask"]).unsqueeze(0)
+    vb = (torch.tensor(case["q_view_ids"]), torch.tensor(case["s_view_ids"]), _t(case["view_bias"]))
+    return q, k, w, mask, vb
+
+
+@pytest.mark.parametrize("case", json.loads((GOLDEN / "indexer_view_bias_kat.json").read_text()),
+                         ids=lambda c: c["name"])
+def test_indexer_view_bias_matches_golden(case):
+    # fp64 loops of the reference's view-bias cases (tests/indexer_projected_tests.py:64-243)
+    q, k, w, mask, vb = _view_bias_case(case)
+    sc = oidx.indexer_scores(q, k, w, mask, case["scale"], view_bias=vb)
+    torch.testing.assert_close(sc[0], _t(case["scores"]), atol=1e-6, rtol=1e-6)
+    idx, val = oidx.indexer_topk(q, k, w, mask, case["topk"], case["scale"], view_bias=vb)
+    rep = check_topk_rows(_t(case["scores"]), idx[0], case["topk"])
+    assert rep.ok, rep
+    if "table_grad_of_sum" in case:
+        g = oidx.view_bias_grad(idx, torch.ones(idx.shape), vb[0], vb[1], vb[2].shape)
+        torch.testing.assert_close(g, _t(case["table_grad_of_sum"]), atol=0, rtol=0)
+
+
+def test_view_bias_grad_equals_autograd_of_the_gathered_term():
+    # the scatter restatement against autograd of table[b, q_view, s_view[idx]] (an
+    # independent route: index-gather backward)
+    g = torch.Generator().manual_seed(5)
+    B, T, S, K, Vq, Vs = 2, 13, 17, 5, 3, 4
+    qv = torch.randint(0, Vq, (B, T), generator=g)
+    sv = torch.randint(0, Vs, (B, S), generator=g)
+    idx = torch.stack([torch.stack([torch.randperm(S, generator=g)[:K] for _ in range(T)]) for _ in range(B)])
+    table = torch.randn(B, Vq, Vs, generator=g, requires_grad=True)
+    gs = torch.randn(B, T, K, generator=g)
+    term = oidx.view_bias_term(qv, sv, table)  # [B, T, S]
+    (term.gather(-1, idx) * gs).sum().backward()
+    torch.testing.assert_close(oidx.view_bias_grad(idx, gs, qv, sv, table.shape), table.grad)
+    # a transposed lookup (s view as row) would fail this: Vq != Vs and ids differ
+    assert oidx.view_bias_term(qv, sv, table.detach())[0, 0, 0] == table[0, qv[0, 0], sv[0, 0]]
+
+
 def test_indexer_scores_closed_form_single_head_unit_gate():
     # Hi = 1, w = 1  =>  score = relu(scale * q k^T)
     g = torch.Generator().manual_seed(0)
