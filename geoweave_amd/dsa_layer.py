@@ -42,7 +42,28 @@ from .custom_indexer.sparse_topk_indexer import sparse_topk_indexer_func, sparse
 from . import source_downsample as sdown
 
 __all__ = ["GlueLayout", "rope2d_tables", "dsa_glue_forward", "sparse_attention_streaming",
-           "LightningIndexerProjections", "SparseGlobalAttention", "parse_score_dtype"]
+           "LightningIndexerProjections", "SparseGlobalAttention", "parse_score_dtype", "rope_base_from_pos_type",
+           "pi3_global_attention", "grid_positions"]
+
+
+def rope_base_from_pos_type(pos_type: str) -> Optional[float]:
+    """Pi3's ``pos_type`` (``pi3_training.py:163-167``): "rope<freq>" (e.g. "rope100") gives
+    the rotary base ``freq``; any other type has no rotary embedding (None)."""
+    if isinstance(pos_type, str) and pos_type.startswith("rope"):
+        return float(pos_type[len("rope"):])
+    return None
+
+
+def grid_positions(batch_views: int, grid_h: int, grid_w: int, n_special: int = 5, device=None) -> torch.Tensor:
+    """int32 ``[batch_views, n_special + grid_h * grid_w, 2]`` token positions shared by VGGT
+    and Pi3 (``aggregator.py:521-526``; Pi3 ``pi3_training.py:818-827``): ``n_special``
+    camera/register tokens at (0, 0), then the (y, x) patch grid plus one, row-major. For a
+    global-attention layer over S views, reshape to ``[B, S * tokens, 2]``."""
+    ys = torch.arange(grid_h, device=device).repeat_interleave(grid_w)
+    xs = torch.arange(grid_w, device=device).repeat(grid_h)
+    grid = torch.stack([ys, xs], dim=-1) + 1
+    special = torch.zeros(n_special, 2, dtype=grid.dtype, device=device)
+    return torch.cat([special, grid], 0).to(torch.int32).expand(batch_views, -1, -1).contiguous()
 
 
 def parse_score_dtype(value) -> Optional[torch.dtype]:
@@ -433,3 +454,16 @@ class SparseGlobalAttention(nn.Module):
         out = F.linear(o.reshape(B, N, self.dim), self.proj.weight.to(x.dtype),
                        None if self.proj.bias is None else self.proj.bias.to(x.dtype))
         return out, attn, scores, idx
+
+
+def pi3_global_attention(dim: int = 1024, num_heads: int = 16, pos_type: str = "rope100", topk: int = 1024,
+                         indexer_heads: int = 4, indexer_dim: int = 64, score_dtype="float16") -> SparseGlobalAttention:
+    """The sparse global attention of Pi3's DSA decoder blocks (``DSABlockRope``,
+    ``aidi/third_party/pi3_training/pi3/models/layers/block.py:345-447``, built by
+    ``pi3_training.py:245-275`` for the layers of ``indexer_layers``, 9-17 in
+    ``geoweave/configs/pi3.json``): qkv bias on, per-head q/k LayerNorm, Pi3's ``RoPE2D`` with
+    the base of ``pos_type`` (the same rotation as VGGT's: frequencies base^(-2i/32) per
+    32-dim half, y then x), indexer 4 x 64 with top-k 1024, and the preset's fp16 scores."""
+    return SparseGlobalAttention(dim, num_heads, qkv_bias=True, proj_bias=True, qk_norm=True,
+                                 rope_base=rope_base_from_pos_type(pos_type), indexer_heads=indexer_heads,
+                                 indexer_dim=indexer_dim, topk=topk, score_dtype=score_dtype)

@@ -7,7 +7,10 @@ Reference: ``DSAAttention._project_qkv_and_indexer_fused``
 (``easyvolcap/official_vggt/layers/dsa_attention.py:583-625``), the q/k glue of
 ``DSAAttention.forward`` (``:4928-4948``), ``LightningIndexer.project``
 (``easyvolcap/official_vggt/layers/indexer.py:302-328``) and
-``RotaryPositionEmbedding2D`` (``easyvolcap/official_vggt/layers/rope.py:62-200``).
+``RotaryPositionEmbedding2D`` (``easyvolcap/official_vggt/layers/rope.py:62-200``); Pi3's
+``RoPE2D`` (``aidi/third_party/pi3_training/pi3/models/layers/pos_embed.py:112-160``, the
+torch module the reference runs: its compiled ``cuRoPE2D`` is not part of the checkout) and
+Pi3's token positions (``pi3_training.py:818-827``, ``pos_embed.py:161-173``).
 """
 from __future__ import annotations
 
@@ -48,6 +51,44 @@ def rope2d(tokens: torch.Tensor, positions: torch.Tensor, base: float = 100.0) -
     return torch.cat((vert, horiz), dim=-1)
 
 
+def rope2d_pi3(tokens: torch.Tensor, positions: torch.Tensor, freq: float = 100.0) -> torch.Tensor:
+    """Pi3's ``RoPE2D.forward`` (``pos_embed.py:112-160``) in fp32: D = dim/2 features per
+    axis, ``inv_freq = 1 / freq^(arange(0, D, 2)/D)``, ``freqs = cat(t x inv_freq, t x
+    inv_freq)``, the first half of the features rotated with ``positions[..., 0]`` (y) and
+    the second with ``positions[..., 1]`` (x), each by ``x cos + rotate_half(x) sin`` with
+    ``rotate_half(x) = cat(-x2, x1)``. tokens ``[B, H, N, dim]``, positions ``[B, N, 2]``."""
+    D = tokens.shape[-1] // 2
+    n_pos = int(positions.max()) + 1
+    inv_freq = 1.0 / (freq ** (torch.arange(0, D, 2).float() / D))
+    t = torch.arange(n_pos, dtype=inv_freq.dtype)
+    freqs = torch.einsum("i,j->ij", t, inv_freq)
+    freqs = torch.cat((freqs, freqs), dim=-1)
+    cos, sin = freqs.cos(), freqs.sin()
+
+    def rotate_half(x):
+        return torch.cat((-x[..., x.shape[-1] // 2:], x[..., :x.shape[-1] // 2]), dim=-1)
+
+    def apply_1d(x, p):
+        c = F.embedding(p, cos)[:, None, :, :]
+        s_ = F.embedding(p, sin)[:, None, :, :]
+        return x * c + rotate_half(x) * s_
+
+    y, x = tokens.float().chunk(2, dim=-1)
+    return torch.cat((apply_1d(y, positions[:, :, 0].long()), apply_1d(x, positions[:, :, 1].long())), dim=-1)
+
+
+def pi3_positions(batch_views: int, grid_h: int, grid_w: int, n_special: int = 5) -> torch.Tensor:
+    """int64 ``[batch_views, n_special + grid_h * grid_w, 2]``: Pi3's decoder positions
+    (``pi3_training.py:818-827``): the (y, x) patch grid of ``PositionGetter``
+    (``pos_embed.py:161-173``, row-major ``cartesian_prod(y, x)``) plus one, after
+    ``n_special`` register tokens at (0, 0)."""
+    ys = torch.arange(grid_h).repeat_interleave(grid_w)
+    xs = torch.arange(grid_w).repeat(grid_h)
+    grid = torch.stack([ys, xs], dim=-1) + 1
+    special = torch.zeros(n_special, 2, dtype=grid.dtype)
+    return torch.cat([special, grid], dim=0).expand(batch_views, -1, -1).clone()
+
+
 def fused_projection_glue(
     x: torch.Tensor,
     weight: torch.Tensor,
@@ -58,6 +99,7 @@ def fused_projection_glue(
     ln_eps: float = 1e-5,
     rope_base: float = 100.0,
     y: Optional[torch.Tensor] = None,
+    rope=None,
 ):
     """(q, k, v, idx_q, idx_k, idx_w) in fp32, q/k/v ``[B, N, H, D]``, idx_q/idx_k
     ``[B, N, Hi, Di]``, idx_w ``[B, N, Hi]``.
@@ -66,7 +108,8 @@ def fused_projection_glue(
     (``dsa_attention.py:590-600``; pass ``y`` to start from a given projection). q/k:
     ``q_norm``/``k_norm`` LayerNorm over the head dim, then rope (``:4935-4940``); indexer
     k: ``k_norm`` then rope, indexer q: rope (``:606-618``). ``norms`` maps 'q', 'k',
-    'idx_k' to (weight, bias) or None (identity).
+    'idx_k' to (weight, bias) or None (identity). ``rope``: the rotation ``(tokens [B, H, N,
+    D], pos, base) -> tokens`` (default ``rope2d``, VGGT's; ``rope2d_pi3`` for Pi3's).
     """
     H, D, Hi, Di = dims["H"], dims["D"], dims["Hi"], dims["Di"]
     if y is None:
@@ -89,6 +132,7 @@ def fused_projection_glue(
 
     q, k, ik = ln(q, "q"), ln(k, "k"), ln(ik, "idx_k")
     if pos is not None:
-        rp = lambda t: rope2d(t.permute(0, 2, 1, 3), pos, rope_base).permute(0, 2, 1, 3)
+        rot = rope2d if rope is None else rope
+        rp = lambda t: rot(t.permute(0, 2, 1, 3), pos, rope_base).permute(0, 2, 1, 3)
         q, k, iq, ik = rp(q), rp(k), rp(iq), rp(ik)
     return q, k, v, iq, ik, iw

@@ -167,6 +167,50 @@ def test_score_dtype_float16_layer_at_s4(gpu_device, monkeypatch):
     torch.testing.assert_close(out.float().cpu(), ref, **TOL)
 
 
+def test_pi3_global_attention_layer(gpu_device):
+    # Pi3's DSA decoder attention (block.py:345-447 via pi3_training.py:245-275): qkv bias,
+    # q/k LayerNorm, Pi3's RoPE2D (pos_embed.py:112-160) at base 100 over Pi3's positions
+    # (5 register tokens at (0, 0), the 37 x 37 grid + 1), fp16 scores; 2 views in one
+    # global layer. Stage by stage against the oracle with Pi3's rotation.
+    S, P, dim, K = 2, 1374, 1024, 1024
+    torch.manual_seed(31)
+    m = dsa_layer.pi3_global_attention(dim=dim, topk=K)
+    with torch.no_grad():
+        for prm in m.parameters():
+            prm.copy_(torch.randn_like(prm) * (0.03 if prm.dim() > 1 else 0.5))
+        for norm in (m.q_norm, m.k_norm, m.indexer.k_norm):
+            norm.weight.add_(1.0)
+        m.indexer.w_proj.bias.fill_(1.0)
+    m = m.cuda()
+    g = torch.Generator().manual_seed(32)
+    x = torch.randn(1, S * P, dim, generator=g).bfloat16()
+    pos = dsa_layer.grid_positions(S, 37, 37).reshape(1, S * P, 2)
+    assert torch.equal(pos.long(), olg.pi3_positions(S, 37, 37).reshape(1, S * P, 2))
+    out, idx = m(x.cuda(), pos.cuda(), return_topk=True)
+    torch.cuda.synchronize()
+
+    w, b = m.fused_projection(torch.bfloat16)
+    y = F.linear(x.cuda(), w, b)
+    norms = {"q": (m.q_norm.weight.detach().float().cpu(), m.q_norm.bias.detach().float().cpu()),
+             "k": (m.k_norm.weight.detach().float().cpu(), m.k_norm.bias.detach().float().cpu()),
+             "idx_k": (m.indexer.k_norm.weight.detach().float().cpu(), m.indexer.k_norm.bias.detach().float().cpu())}
+    glue = dsa_layer.dsa_glue_forward(y, m.layout, *[tuple(t.cuda() for t in norms[key]) for key in ("q", "k", "idx_k")],
+                                      1e-5, pos.cuda())
+    want = olg.fused_projection_glue(None, None, None, dict(H=16, D=64, Hi=4, Di=64), norms, pos.long(),
+                                     y=y[..., :m.layout.width].float().cpu(), rope=olg.rope2d_pi3)
+    for a, bb in zip(glue, want):
+        torch.testing.assert_close(a.float().cpu(), bb, **TOL)
+    gq, gk, gv, giq, gik, giw = [t.to(torch.float16).cpu() for t in glue]
+    ref_scores = oidx.indexer_scores(giq, gik, giw, None, 0.125)[0]
+    rep = check_topk_rows(ref_scores, idx[0].cpu(), K)
+    assert rep.ok, rep
+    o, _, _ = oatt.sparse_attention(gq, gk, gv, idx.cpu(), 0.125)
+    o = o.to(torch.float16).to(torch.bfloat16).float()
+    ref = F.linear(o.reshape(1, S * P, dim), m.proj.weight.detach().bfloat16().float().cpu(),
+                   m.proj.bias.detach().bfloat16().float().cpu())
+    torch.testing.assert_close(out.float().cpu(), ref, **TOL)
+
+
 def test_query_chunked_stream_equals_the_whole_layer(gpu_device):
     # The query-chunked sparse stream (dsa_attention.py:1017-1283) selects and attends per
     # chunk of queries; rows are independent, so the output equals the unchunked layer's

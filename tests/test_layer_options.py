@@ -29,3 +29,21 @@ def test_layer_keeps_the_score_dtype():
     m = dsa_layer.SparseGlobalAttention(dim=128, num_heads=2, topk=8, score_dtype="float16")
     assert m.score_dtype == torch.float16
     assert dsa_layer.SparseGlobalAttention(dim=128, num_heads=2, topk=8).score_dtype is None
+
+
+def test_pi3_settings():
+    # pi3_training.py:163-167 (pos_type), :253-263 (qkv_bias, qk_norm), pi3.json (score_dtype)
+    assert dsa_layer.rope_base_from_pos_type("rope100") == 100.0
+    assert dsa_layer.rope_base_from_pos_type("rope37.5") == 37.5
+    assert dsa_layer.rope_base_from_pos_type("none") is None
+    m = dsa_layer.pi3_global_attention(dim=256, num_heads=4, topk=64)
+    assert m.qkv.bias is not None and isinstance(m.q_norm, torch.nn.LayerNorm)
+    assert m.rope_base == 100.0 and m.score_dtype == torch.float16
+
+
+def test_grid_positions_match_the_oracle_restatement():
+    from oracle import layer_glue as olg
+
+    got = dsa_layer.grid_positions(3, 37, 37)
+    want = olg.pi3_positions(3, 37, 37)
+    assert got.dtype == torch.int32 and torch.equal(got.long(), want)

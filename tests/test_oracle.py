@@ -425,6 +425,26 @@ def test_rope2d_oracle_identity_relative_position_and_brute_force():
     assert abs(float(s1) - float(s2)) < 1e-4
 
 
+def test_pi3_rope2d_is_the_same_rotation_and_positions_match_the_grid():
+    # Pi3's RoPE2D (pos_embed.py:112-160) against the brute-force-pinned VGGT rotation:
+    # same frequencies (freq^(-2i/32) per 32-dim half), same halves (y then x), same
+    # rotate_half pairing (i, i + 16) -- so one glue kernel serves both models. A slip in
+    # either restatement (half order, pairing, frequency exponent) breaks the equality.
+    from oracle import layer_glue as olg
+
+    g = torch.Generator().manual_seed(22)
+    t = torch.randn(2, 3, 50, 64, generator=g)
+    pos = torch.randint(0, 38, (2, 50, 2), generator=g)
+    torch.testing.assert_close(olg.rope2d_pi3(t, pos, 100.0), olg.rope2d(t, pos, 100.0), rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(olg.rope2d_pi3(t, pos, 37.0), olg.rope2d(t, pos, 37.0), rtol=1e-6, atol=1e-6)
+    # positions: 5 register tokens at (0, 0), then the (y, x) grid + 1 in row-major order
+    p = olg.pi3_positions(2, 3, 4)
+    assert p.shape == (2, 17, 2)
+    assert p[0, :5].abs().sum() == 0
+    assert p[0, 5].tolist() == [1, 1] and p[0, 6].tolist() == [1, 2] and p[0, 9].tolist() == [2, 1]
+    assert p[1, -1].tolist() == [3, 4]
+
+
 def test_layer_glue_oracle_matches_the_unfused_reference_order():
     # The fused projection (dsa_attention.py:583-625) equals the unfused path: qkv linear
     # -> reshape(B, N, 3, H, D) (:229-233), q_norm/k_norm, rope (:4935-4940); indexer
