@@ -80,8 +80,12 @@ def train_step_c4(steps: int = 5, warmup: int = 2, views: int = 24, batch: int =
     attn_sum, the indexer KL loss on the layer's normalised attention mass
     (dsa_attention.py:5395-5411: attn cast to q's dtype, p = attn / (sum + eps),
     sparse_indexer_kl_loss(p, topk_scores)), and the backward of o (a random dO) and of
-    the KL loss (KL backward, CSR build, attention dq/dkv, indexer dq/dkw). Times each
-    phase with HIP events on the launch stream."""
+    the KL loss. As in the reference presets (detach_input, vggt.json:17,
+    dsa_attention.py:4694-4695) the loss sees the attention mass detached: it trains the
+    indexer (KL backward, indexer dq/dkw over the CSR) and the attention gets the gradient
+    of o alone (the masked dense backward). ``kl_into_attention`` times the same step with
+    the mass not detached (the KL gradient also flows into q, k, v: the CSR backward with
+    dattn). Times each phase with HIP events on the launch stream."""
     import torch
 
     from geoweave_amd import _csr, workloads
@@ -98,7 +102,7 @@ def train_step_c4(steps: int = 5, warmup: int = 2, views: int = 24, batch: int =
     stream = torch.cuda.current_stream(dev)
     eps = 1e-6
 
-    def one(ev=None, fused=False):
+    def one(ev=None, fused=False, detach=True):
         for x in (qi, ki, wi, q, k, v):
             x.grad = None
         _csr.clear_cache()
@@ -107,7 +111,7 @@ def train_step_c4(steps: int = 5, warmup: int = 2, views: int = 24, batch: int =
         idx, sc = sparse_topk_indexer_func(qi, ki, wi, None, topk, 0.125, 256, 0)
         if fused:
             # KL on the attention mass computed in the attention epilogue (one launch)
-            o, attn, kl = sparse_attention_kl_loss(q, k, v, idx, sc, eps, 0.125)
+            o, attn, kl = sparse_attention_kl_loss(q, k, v, idx, sc, eps, 0.125, detach_input=detach)
             if ev:
                 ev[1].record(stream)
                 ev[2].record(stream)
@@ -115,7 +119,7 @@ def train_step_c4(steps: int = 5, warmup: int = 2, views: int = 24, batch: int =
             o, attn = sparse_index_flash_attn_func(q, k, v, idx, None, False, 0.125)
             if ev:
                 ev[1].record(stream)
-            p = attn.to(q.dtype)
+            p = (attn.detach() if detach else attn).to(q.dtype)
             p = p / (p.sum(dim=-1, keepdim=True) + eps)
             kl = sparse_indexer_kl_loss(p, sc, eps)
             if ev:
@@ -124,22 +128,24 @@ def train_step_c4(steps: int = 5, warmup: int = 2, views: int = 24, batch: int =
         if ev:
             ev[3].record(stream)
 
-    def timed(fused):
+    def timed(fused, detach=True):
         for _ in range(warmup):
-            one(fused=fused)
+            one(fused=fused, detach=detach)
         torch.cuda.synchronize()
         evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
         for i in range(steps):
-            one(evs[i], fused)
+            one(evs[i], fused, detach)
         torch.cuda.synchronize()
         return [statistics.mean(e[j].elapsed_time(e[j + 1]) for e in evs) for j in range(3)]
 
     fwd, kl_ms, bwd = timed(False)
     f_fwd, _, f_bwd = timed(True)
+    n_fwd, n_kl, n_bwd = timed(False, detach=False)
     gather = batch * T * topk * H * D * 2 * 2
     return {
         "workload": f"C4 training step: B={batch}, S={views} views (N={T}), H={H}, D={D}, top-k {topk}, bf16, "
-                    "indexer + attention forward (attn_sum on), indexer KL loss, backward through autograd",
+                    "indexer + attention forward (attn_sum on), indexer KL loss on the detached attention mass "
+                    "(the reference presets' detach_input), backward through autograd",
         "fwd_ms": round(fwd, 3),
         "kl_loss_fwd_ms": round(kl_ms, 3),
         "bwd_ms": round(bwd, 3),
@@ -151,8 +157,17 @@ def train_step_c4(steps: int = 5, warmup: int = 2, views: int = 24, batch: int =
             "bwd_ms": round(f_bwd, 3),
             "step_ms": round(f_fwd + f_bwd, 3),
         },
+        "kl_into_attention": {
+            "note": "same step with the attention mass not detached: the KL gradient also flows into q, k, v "
+                    "(attention backward with dattn: the CSR path)",
+            "fwd_ms": round(n_fwd, 3),
+            "kl_loss_fwd_ms": round(n_kl, 3),
+            "bwd_ms": round(n_bwd, 3),
+            "step_ms": round(n_fwd + n_kl + n_bwd, 3),
+        },
         "attn_gathered_bytes_fwd": gather,
         "attn_gathered_bytes_bwd": 2 * gather,
+        "attn_dense_bwd_flops": 10 * batch * T * T * H * D,
     }
 
 
@@ -343,8 +358,9 @@ def layer_train_c4(steps: int = 3, warmup: int = 1, views: int = 24, batch: int 
     """The whole layer trained at the C4 shape (B=2, S=24 views, N=32,976), random-init
     weights, bf16: ``SparseGlobalAttention.forward_train`` (fused projection, glue, indexer
     top-k with scores, attention with attn_sum, output projection), the indexer KL loss on
-    the normalised attention mass, and the backward through every stage (GEMMs, glue,
-    attention, indexer, KL). HIP events on the launch stream."""
+    the normalised attention mass (detached, as the reference presets' detach_input), and the
+    backward through every stage (GEMMs, glue, attention, indexer, KL). HIP events on the
+    launch stream."""
     import torch
 
     from geoweave_amd import dsa_layer, workloads
@@ -365,7 +381,7 @@ def layer_train_c4(steps: int = 3, warmup: int = 1, views: int = 24, batch: int 
         x.grad = None
         rec(0)
         out, attn, scores, _ = m.forward_train(x, pos, rope_len=rope_len)
-        p = attn.to(torch.bfloat16)
+        p = attn.detach().to(torch.bfloat16)
         p = p / (p.sum(-1, keepdim=True) + 1e-6)
         kl = sparse_indexer_kl_loss(p, scores, 1e-6)
         rec(1)
@@ -383,7 +399,8 @@ def layer_train_c4(steps: int = 3, warmup: int = 1, views: int = 24, batch: int 
     bwd = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
     return {
         "workload": f"whole-layer training step: B={batch}, S={views} views (N={x.shape[1]}), dim 1024, 16 heads, "
-                    f"indexer 4x64, top-k {topk}, bf16, random-init weights, output-gradient + indexer KL loss",
+                    f"indexer 4x64, top-k {topk}, bf16, random-init weights, output-gradient + indexer KL loss on the "
+                    "detached attention mass",
         "fwd_ms": round(fwd, 3),
         "bwd_ms": round(bwd, 3),
         "step_ms": round(fwd + bwd, 3),

@@ -109,6 +109,13 @@ _SIGNATURES = {
          _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p, ctypes.c_int, _i64, _i64,
          ctypes.c_float, _p, _p],
     ),
+    "gw_sparse_attn_bwd_dense_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
+    "gw_sparse_attn_bwd_dense": (
+        ctypes.c_int,
+        [ctypes.c_int, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64, _i64, _p, _i64p, _p, _i64p,
+         _p, _p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64, _i64,
+         ctypes.c_float, _p, _p, _sz, _p],
+    ),
 }
 
 _lock = threading.Lock()

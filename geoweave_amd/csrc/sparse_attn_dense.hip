@@ -48,108 +48,14 @@
 
 #include "gw_attn.h"
 #include "gw_common.h"
+#include "gw_dense.h"
 #include "gw_select.h"
 #include "gw_sort.h"
 
 namespace gw {
 namespace {
 
-constexpr float kDLog2e = 1.4426950408889634f;
-constexpr float kDLn2 = 0.6931471805599453f;
 constexpr float kSumCap = 32768.f;  // a lane's weights of one sub-tile sum to at most this
-
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ f32x16 mma(BF16, uint4 a, uint4 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-}
-__device__ __forceinline__ f32x16 mma(FP16, uint4 a, uint4 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
-                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
-}
-
-// ---------------------------------------------------------------------------------------
-// Selection mask, query-major per 32-key sub-tile: word[b][j][t] has bit i set when query t
-// selected key 32 j + i (t < T_pad = nqb_pad * 32, j < S_pad / 32; zero words past S and T).
-// Built per (32-query block, chunk of kMaskChunk keys) with LDS atomics. The atomic returns
-// the word as it was: a bit already set means the query listed the key twice, and the block
-// is flagged. Positions are read 8 rows at a time (16 bytes per lane when the table allows),
-// so the loads of a group are in flight together. The first workgroup of each batch also
-// clears the per-column maxima of |V| and the non-finite flag that dense_vmax_kernel sets.
-// ---------------------------------------------------------------------------------------
-constexpr int kMaskChunk = 16384;  // keys per workgroup
-
-__global__ __launch_bounds__(256) void dense_mask_kernel(const int32_t* __restrict__ pos, int64_t psb, int64_t pst,
-                                                         int T, int S, int Spad, int K, int nqb, int tpad,
-                                                         int nchunk, int vec, int vmax_words,
-                                                         uint32_t* __restrict__ mask, int* __restrict__ flags,
-                                                         uint32_t* __restrict__ vmax, int* __restrict__ bad) {
-  // [key / 32][query], rows padded to 33 words so that one query's atomics spread over banks
-  __shared__ uint32_t words[(kMaskChunk / 32) * 33];
-  __shared__ int dup_any;
-  // The chunks of one block are consecutive workgroups: they run together and share the
-  // block's positions through the caches.
-  const int chunk = blockIdx.x, qb = blockIdx.y, b = blockIdx.z;
-  const int c0 = chunk * kMaskChunk;
-  const int len = min(kMaskChunk, S - c0);
-  const int nkt = min(kMaskChunk, Spad - c0) >> 5;
-  for (int i = threadIdx.x; i < nkt * 33; i += 256) words[i] = 0u;
-  if (qb == 0 && chunk == 0) {
-    for (int i = threadIdx.x; i < vmax_words; i += 256) vmax[(int64_t)b * vmax_words + i] = 0u;
-    if (threadIdx.x == 0) bad[b] = 0;
-  }
-  if (threadIdx.x == 0) dup_any = 0;
-  __syncthreads();
-  bool dup = false;
-  const int rows = min(32, T - qb * 32);  // <= 0 for the padding blocks
-  const int32_t* pblk = pos + b * psb + (int64_t)min(qb * 32, T - 1) * pst;
-  // Positions outside [c0, c0 + len) (other chunks, negative padding, >= S) wrap to large
-  // unsigned offsets and are skipped.
-  auto put = [&](int32_t sidx, int i) {
-    const uint32_t sl = (uint32_t)sidx - (uint32_t)c0;
-    if (sl < (uint32_t)len) {
-      const uint32_t bit = 1u << (sl & 31u);
-      dup |= (atomicOr(&words[(sl >> 5) * 33 + i], bit) & bit) != 0u;
-    }
-  };
-  if (vec) {
-    // K % 4 == 0 and 16-byte aligned rows: one int4 per lane and row.
-    const int n4 = K >> 2;
-    for (int j4 = threadIdx.x; j4 < n4; j4 += 256) {
-#pragma unroll 1
-      for (int r0 = 0; r0 < rows; r0 += 8) {
-        int4 v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-          v[u] = r0 + u < rows ? reinterpret_cast<const int4*>(pblk + (int64_t)(r0 + u) * pst)[j4] : make_int4(-1, -1, -1, -1);
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          put(v[u].x, r0 + u);
-          put(v[u].y, r0 + u);
-          put(v[u].z, r0 + u);
-          put(v[u].w, r0 + u);
-        }
-      }
-    }
-  } else {
-#pragma unroll 1
-    for (int i = 0; i < rows; ++i) {
-      const int32_t* prow = pblk + (int64_t)i * pst;
-      for (int j = threadIdx.x; j < K; j += 256) put(prow[j], i);
-    }
-  }
-  if (dup) dup_any = 1;
-  __syncthreads();
-  uint32_t* out = mask + ((int64_t)b * (Spad >> 5) + (c0 >> 5)) * tpad + qb * 32;
-  for (int idx = threadIdx.x; idx < nkt * 32; idx += 256) {
-    const int kt = idx >> 5, i = idx & 31;
-    out[(int64_t)kt * tpad + i] = words[kt * 33 + i];
-  }
-  if (threadIdx.x == 0 && qb < nqb) flags[((int64_t)b * nqb + qb) * nchunk + chunk] = dup_any;
-}
 
 // ---------------------------------------------------------------------------------------
 // V enters the P·V product in fp16, scaled per (head, d) column by a power of two 2^e that
@@ -168,16 +74,7 @@ __device__ __forceinline__ int vscale_exp(uint32_t bits) {
   return min(15 - x, 126);
 }
 
-__device__ __forceinline__ float in_to_float(int in_fp16, uint32_t u) {
-  return in_fp16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)u) : __uint_as_float(u << 16);
-}
-
 constexpr int kVmaxKeys = 256;  // keys per workgroup of dense_vmax_kernel (one head)
-
-// Non-zero when either 16-bit half of w has its exponent field all ones (inf or nan).
-__device__ __forceinline__ uint32_t nonfinite2(uint32_t w, uint32_t e) {
-  return (uint32_t)((w & e) == e) | (uint32_t)(((w >> 16) & e) == e);
-}
 
 __global__ __launch_bounds__(256) void dense_vmax_kernel(const uint16_t* __restrict__ v, int64_t vsb, int64_t vss,
                                                          int64_t vsh, const uint16_t* __restrict__ k, int64_t ksb,
@@ -310,46 +207,12 @@ struct DenseParams {
   int K;
 };
 
-// Keeps the compiler from moving LDS accesses across this point; within one wave the LDS
-// performs them in issue order, so no barrier is needed between a wave's own write and read.
-__device__ __forceinline__ void lds_fence() { asm volatile("" ::: "memory"); }
-
-__device__ __forceinline__ uint16_t to_half_bits(BF16, float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
-__device__ __forceinline__ uint16_t to_half_bits(FP16, float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
-
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2_v __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t pack_f16(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, f16x2_v));  // v_cvt_pk_f16_f32
-}
-// 0 where sel is all ones, neg where it is zero (v_bfi_b32: (sel & 0) | (~sel & neg)).
-__device__ __forceinline__ float select_bias(int sel, float neg) {
-  float r;
-  asm("v_bfi_b32 %0, %1, 0, %2" : "=v"(r) : "v"(sel), "v"(neg));
-  return r;
-}
-// Lanes l and l ^ 32 exchange (v_permlane32_swap); both get op(own, partner).
-__device__ __forceinline__ float pair_max(float x) {
-  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-}
-__device__ __forceinline__ float pair_sum(float x) {
-  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-}
-
 // Waves per workgroup, sharing each K/V tile. Two workgroups share a CU (two waves per SIMD
 // from different workgroups): one wave's barrier or memory wait is not the other's.
 constexpr int kDW = 4;
 constexpr int kQPW = 2;  // 32-query blocks per wave (one head): each K and V^T operand feeds two products
 constexpr int kQBW = kDW * kQPW;  // 32-query blocks per workgroup
 static_assert(kDW == 4, "the tile staging moves two K and two V^T rows of 64 per thread");
-
-// LDS tiles of 64 keys of one head: K as 64 rows (key) and V^T as 64 rows (d), 128 bytes
-// each; the 16-byte chunk c of row R sits at c ^ swz(R). Operand reads (consecutive rows, one
-// chunk) and tile stores (8 lanes per row) then touch distinct banks in every group of 8 and
-// of 16 lanes.
-__device__ __forceinline__ int swz(int R) { return (R & 7) ^ ((R >> 3) & 1); }
 
 template <typename E, bool ATTN>
 __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DenseParams p) {
@@ -870,7 +733,7 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
                         : 0;
     hipLaunchKernelGGL(dense_mask_kernel, dim3(L.nchunk, L.nqb_pad, (unsigned)B), dim3(256), 0, st, kv_pos,
                        pos_stride_b, pos_stride_t, (int)T, (int)S, L.spad, (int)K, L.nqb, L.nqb_pad * 32, L.nchunk,
-                       vec, (int)(H * 64), mask, flags, vmax, bad);
+                       vec, (int)(H * 64), mask, flags, vmax, bad, nullptr, nullptr);
     GW_HIP_LAUNCH_CHECK("dense_mask_kernel launch");
   }
   hipLaunchKernelGGL(dense_vmax_kernel, dim3((unsigned)((S + kVmaxKeys - 1) / kVmaxKeys), (unsigned)H, (unsigned)B),

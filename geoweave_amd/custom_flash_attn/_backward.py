@@ -1,16 +1,32 @@
-"""Backward of sparse-index attention through ``gw_sparse_attn_bwd`` (gfx950).
+"""Backward of sparse-index attention (gfx950).
 
 Reference: ``SparseIndexFlashAttnFunc.backward`` and ``_sparse_index_flash_attn_backward``
 (``easyvolcap/utils/custom_flash_attn/sparse_index_flash_attn.py:3240-3283,2442-2846``):
 ``dattn_sum`` is cast to q's dtype (``:3244-3245``), gradients are accumulated in fp32 and
-returned in the input dtype (``:3247-3282``). Here dK/dV come from a key-major reduction
-over the CSR of ``kv_positions`` instead of fp32 atomics, so they are reproducible.
+returned in the input dtype (``:3247-3282``). Two implementations, neither with float
+atomics, so gradients are reproducible:
+
+* ``gw_sparse_attn_bwd_dense``: masked dense passes on the matrix cores, for D = 64 without
+  an attn_sum gradient (the reference presets detach the attention mass before the indexer
+  loss, ``easyvolcap/official_vggt/layers/dsa_attention.py:4694-4695``) when a query selects
+  at least 1 / ``DENSE_MAX_RATIO`` of the keys. A batch element with a position listed twice
+  in a row or a non-finite input is reported back by the kernels and the call is redone by
+  the CSR path.
+* ``gw_sparse_attn_bwd``: gathers over the selected rows, with dK/dV from a key-major
+  reduction over the CSR of ``kv_positions``.
 """
 from __future__ import annotations
 
 import torch
 
 from .. import _csr, _lib
+
+# "auto": the dense passes when they apply (see above), else the CSR path; "dense" forces
+# the dense passes whenever they can run at all, "csr" the CSR path (tests, measurements).
+BACKWARD_PATH = "auto"
+DENSE_MAX_RATIO = 96
+# The path the last call took ("dense" or "csr"), for tests.
+last_path = None
 
 
 def _strides(x: torch.Tensor, layout: str):
@@ -49,8 +65,39 @@ def sparse_attn_backward(do, q, k, v, kv_positions, o, lse, dattn_sum, softmax_s
         dattn_sum = dattn_sum.to(q.dtype).contiguous()
     if kv_positions.stride(-1) != 1:
         kv_positions = kv_positions.contiguous()
-    csr, csr_bytes = _csr.build(kv_positions, seqlen_k)
     lib = _lib.load()
+    global last_path
+    dense_ok = (d == 64 and dattn_sum is None and 0.0 < float(softmax_scale) < float("inf")
+                and BACKWARD_PATH != "csr")
+    if dense_ok and (BACKWARD_PATH == "dense" or seqlen_k <= DENSE_MAX_RATIO * num_kv):
+        ws_bytes = int(lib.gw_sparse_attn_bwd_dense_workspace_size(batch, seqlen_q, seqlen_k, nheads, d, num_kv))
+        ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
+        route = torch.empty(batch, device=q.device, dtype=torch.int32)
+        rc = lib.gw_sparse_attn_bwd_dense(
+            _lib.dtype_code(q.dtype),
+            q.data_ptr(), _lib.strides3(*_strides(q, q_layout)),
+            k.data_ptr(), _lib.strides3(*_strides(k, q_layout)),
+            v.data_ptr(), _lib.strides3(*_strides(v, q_layout)),
+            kv_positions.data_ptr(), kv_positions.stride(0), kv_positions.stride(1),
+            o.data_ptr(), _lib.strides3(*_strides(o, q_layout)),
+            do.data_ptr(), _lib.strides3(*_strides(do, q_layout)),
+            lse.data_ptr(),
+            dq.data_ptr(), _lib.strides3(*_strides(dq, q_layout)),
+            dk.data_ptr(), _lib.strides3(*_strides(dk, q_layout)),
+            dv.data_ptr(), _lib.strides3(*_strides(dv, q_layout)),
+            batch, seqlen_q, seqlen_k, nheads, d, num_kv, float(softmax_scale),
+            route.data_ptr(), ws.data_ptr(), ws_bytes,
+            _lib.stream_handle(q.device),
+        )
+        _lib.check(rc, "gw_sparse_attn_bwd_dense")
+        del ws
+        # Reading the flags waits for the passes; a flagged batch element (a repeated position
+        # or a non-finite input) is rare, and then the whole call is redone by the CSR path.
+        if not bool(route.any()):
+            last_path = "dense"
+            return dq, dk, dv
+    last_path = "csr"
+    csr, csr_bytes = _csr.build(kv_positions, seqlen_k)
     ws_bytes = int(lib.gw_sparse_attn_bwd_workspace_size(batch, seqlen_q, seqlen_k, nheads, d, num_kv))
     ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
     rc = lib.gw_sparse_attn_bwd(

@@ -202,6 +202,10 @@ class SparseIndexFlashAttnFunc(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, kv_positions, bias=None, causal=False, softmax_scale=None):
+        # An output that takes no part in the loss (attn_sum detached before the indexer loss,
+        # as the reference presets do) brings None instead of zeros: the backward then skips
+        # the attn_sum term, which zeros would contribute nothing to.
+        ctx.set_materialize_grads(False)
         if kv_positions.stride(-1) != 1:
             kv_positions = kv_positions.contiguous()
         o, attn_sum, lse, ctx.softmax_scale = _flash_attn_forward(
@@ -225,6 +229,10 @@ class SparseIndexFlashAttnBhtdFunc(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, kv_positions, bias=None, causal=False, softmax_scale=None):
+        # An output that takes no part in the loss (attn_sum detached before the indexer loss,
+        # as the reference presets do) brings None instead of zeros: the backward then skips
+        # the attn_sum term, which zeros would contribute nothing to.
+        ctx.set_materialize_grads(False)
         if kv_positions.stride(-1) != 1:
             kv_positions = kv_positions.contiguous()
         o, attn_sum, lse, ctx.softmax_scale = _flash_attn_forward(

@@ -112,6 +112,8 @@ class _AttnWithKLRows(torch.autograd.Function):
     def forward(ctx, q, k, v, kv_positions, logits, eps, softmax_scale):
         from ..custom_flash_attn.sparse_index_flash_attn import _flash_attn_forward
 
+        # attn_sum without a gradient (the loss on a detached mass) brings None, not zeros
+        ctx.set_materialize_grads(False)
         if kv_positions.stride(-1) != 1:
             kv_positions = kv_positions.contiguous()
         if logits.stride(-1) != 1:
@@ -151,17 +153,22 @@ class _KLFromRowLosses(torch.autograd.Function):
     def backward(ctx, grad_out):
         a, z = ctx.saved_tensors
         d_attn, d_logits = kl_loss_backward(a, z, grad_out, ctx.eps)
-        return d_attn, d_logits.to(ctx.logits_dtype), None, None
+        return (d_attn if ctx.needs_input_grad[0] else None), d_logits.to(ctx.logits_dtype), None, None
 
 
-def sparse_attention_kl_loss(q, k, v, kv_positions, logits, eps: float = 1e-6, softmax_scale=None):
+def sparse_attention_kl_loss(q, k, v, kv_positions, logits, eps: float = 1e-6, softmax_scale=None,
+                             detach_input: bool = False):
     """``(o, attn_sum, loss)``: ``sparse_index_flash_attn_func(q, k, v, kv_positions)``
     followed by ``sparse_indexer_kl_loss(attn_sum, logits, eps)`` (reference
     ``dsa_attention.py:5395-5411`` with the attention mass as p), with the loss's forward
     fused into the attention's attn_sum epilogue: attn_sum is not read back for the loss.
     Same values and gradients as the two calls (the fused sums run in another order);
-    ``logits`` is the indexer's ``topk_scores`` aligned with ``kv_positions``."""
+    ``logits`` is the indexer's ``topk_scores`` aligned with ``kv_positions``.
+    ``detach_input``: the loss sees the attention mass detached (the reference's indexer
+    option of that name, on in its presets, ``dsa_attention.py:4694-4695``), so the loss
+    trains the indexer only and brings no gradient into q, k, v."""
     if logits.shape != kv_positions.shape:
         raise ValueError(f"logits {tuple(logits.shape)} must match kv_positions {tuple(kv_positions.shape)}")
     o, attn_sum, row_loss = _AttnWithKLRows.apply(q, k, v, kv_positions, logits, float(eps), softmax_scale)
-    return o, attn_sum, _KLFromRowLosses.apply(attn_sum, logits, row_loss, float(eps))
+    p = attn_sum.detach() if detach_input else attn_sum
+    return o, attn_sum, _KLFromRowLosses.apply(p, logits, row_loss, float(eps))

@@ -442,6 +442,48 @@ int gw_sparse_attn_fwd_dense_noalloc(int dtype,
                                      int64_t logits_stride_t, float eps, float* row_loss,
                                      void* stream);
 
+/* ------------------------------------------------------------------------------------
+ * Sparse-index attention backward as masked dense passes: the same gradients as
+ * gw_sparse_attn_bwd without an attn_sum gradient (dq, dk, dv up to fp32 summation order and
+ * the rounding of P and dS to the input type for their matrix products), computed on the
+ * matrix cores over every (query, key) pair with the selection as a mask. Replaces the same
+ * reference compute as gw_sparse_attn_bwd (_sparse_index_flash_attn_backward ->
+ * _bwd_preprocess_do_o_dot + _bwd_sparse_index_kernel,
+ * easyvolcap/utils/custom_flash_attn/sparse_index_flash_attn.py:2442-2846, :534-576,
+ * :579-743, behind SparseIndexFlashAttnFunc.backward :3240-3283) for the case the reference
+ * presets train with: the attention mass is detached before the indexer loss (detach_input,
+ * easyvolcap/official_vggt/layers/dsa_attention.py:4694-4695), so dattn_sum is absent or zero.
+ * It pays off when a query selects more than roughly 1 % of the keys.
+ * Needs D = 64 and a positive softmax_scale; otherwise GW_ERR_UNSUPPORTED.
+ * Arguments as for gw_sparse_attn_bwd (no dattn_sum, no CSR). route: device int array of B
+ * entries, written by this call: route[b] = 1 for a batch element it left untouched
+ * (dq/dk/dv of that element not written) because a row lists a position twice (the reference
+ * counts it twice) or q, k, v, dO, o or lse hold a non-finite value (the dense products would
+ * carry it from rows a query did not select); compute such elements with gw_sparse_attn_bwd.
+ * Every element of dq/dk/dv of the other batch elements is written.
+ * Workspace: gw_sparse_attn_bwd_dense_workspace_size(B, T, S, H, D, K) bytes, 16-byte aligned
+ * (selection words query- and key-major, 2 * B * round_up(S, 128) / 32 * round_up(T, 256) * 4
+ * bytes; q^T, dO^T and k^T copies, B * H * 64 * (2 round_up(T, 256) + round_up(S, 128)) * 2
+ * bytes; per-row lse and delta, B * H * round_up(T, 256) * 8 bytes).
+ * ------------------------------------------------------------------------------------ */
+size_t gw_sparse_attn_bwd_dense_workspace_size(int64_t B, int64_t T, int64_t S, int64_t H, int64_t D,
+                                               int64_t K);
+int gw_sparse_attn_bwd_dense(int dtype,
+                             const void* q, const int64_t* q_strides,
+                             const void* k, const int64_t* k_strides,
+                             const void* v, const int64_t* v_strides,
+                             const int32_t* kv_pos, int64_t pos_stride_b, int64_t pos_stride_t,
+                             const void* o, const int64_t* o_strides,
+                             const void* dout, const int64_t* do_strides,
+                             const float* lse,
+                             void* dq, const int64_t* dq_strides,
+                             void* dk, const int64_t* dk_strides,
+                             void* dv, const int64_t* dv_strides,
+                             int64_t B, int64_t T, int64_t S, int64_t H, int64_t D, int64_t K,
+                             float softmax_scale, int* route,
+                             void* workspace, size_t workspace_bytes,
+                             void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -207,6 +207,36 @@ def test_fused_kl_gradients_equal_the_two_calls(gpu_device):
         assert torch.equal(a, b)
 
 
+def test_fused_kl_detached_mass_equals_the_two_calls(gpu_device):
+    # The reference presets' training (detach_input): the loss sees the attention mass
+    # detached, so q, k, v get the gradient of o alone (the masked dense backward) and the
+    # logits the KL gradient.
+    from geoweave_amd.custom_flash_attn import _backward
+    from geoweave_amd.custom_flash_attn import sparse_index_flash_attn as sifa
+
+    from geoweave_amd import workloads
+
+    q, k, v, _, z = _attn_inputs(1, 400, 600, 16, 256, seed=15, invalid=False)
+    pos = workloads.distinct_positions(1, 400, 600, 256, seed=15).cuda()  # as top-k gives
+    do = torch.randn(q.shape, generator=torch.Generator().manual_seed(16)).bfloat16().cuda()
+    grads = []
+    for fused in (True, False):
+        qd, kd, vd, zd = (x.detach().clone().requires_grad_() for x in (q, k, v, z))
+        if fused:
+            o, attn, loss = klf.sparse_attention_kl_loss(qd, kd, vd, pos, zd, 1e-6, 0.125, detach_input=True)
+        else:
+            o, attn = sifa.sparse_index_flash_attn_func(qd, kd, vd, pos, None, False, 0.125)
+            loss = sparse_indexer_kl_loss(attn.detach(), zd, 1e-6)
+        ((o.float() * do.float()).sum() + 3.0 * loss).backward()
+        assert _backward.last_path == "dense"
+        grads.append((float(loss.detach()), qd.grad, kd.grad, vd.grad, zd.grad))
+    torch.cuda.synchronize()
+    (l1, *g1), (l2, *g2) = grads
+    assert abs(l1 - l2) <= 1e-5 * abs(l2) + 1e-7
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+
+
 def test_fused_kl_limits(gpu_device):
     from geoweave_amd.custom_flash_attn.sparse_index_flash_attn import _flash_attn_forward
 
