@@ -201,7 +201,8 @@ struct DenseParams {
   int T, S, Spad, H, nqb, tpad, nchunk;
   float scale_log2;
   // attn_sum (ATTN kernels only): the score q.k (not yet scaled) of every selected (query,
-  // key) and head, sws[((b * T + t) * K + slot) * H + h], slot = rank of the key among the
+  // key) and head, sws[((b * H + h) * T + t) * K + slot] (head-major: one workgroup, which
+  // holds one head, fills whole cache lines of a row), slot = rank of the key among the
   // query's selected keys in ascending key order.
   float* sws;
   int K;
@@ -297,7 +298,7 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
   float* srow_ws[kQPW];
 #pragma unroll
   for (int a = 0; a < kQPW; ++a)
-    srow_ws[a] = ATTN ? p.sws + ((int64_t)b * p.T + min(tq[a], p.T - 1)) * p.K * p.H + h : nullptr;
+    srow_ws[a] = ATTN ? p.sws + (((int64_t)b * p.H + h) * p.T + min(tq[a], p.T - 1)) * p.K : nullptr;
   const float ninf = -INFINITY;
 
   // One 32-key sub-tile: S^T for both blocks from the selection bias, the softmax in
@@ -322,8 +323,9 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
     }
     if constexpr (ATTN) {
       // Each selected entry's score (unscaled: dense_attn_sum_kernel applies the scale), at
-      // the slot of its key's rank. The lane's 16 scores go to its LDS row, and a loop over the lane's selected entries (most lanes
-      // have none or one per sub-tile) reads each back and stores it.
+      // the slot of its key's rank. The lane's 16 scores go to its LDS row, and a loop over the
+      // lane's selected entries (most lanes have none or one per sub-tile) reads each back and
+      // stores it.
       float* st_l = &ascore[wave][lane * 20];
 #pragma unroll
       for (int a = 0; a < kQPW; ++a) {
@@ -338,7 +340,7 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
             const int r = __builtin_ctz(bits);
             const int kk = 8 * (r >> 2) + 4 * half + (r & 3);
             const uint32_t slot = rank_base[a] + __popc(w[a] & ((1u << kk) - 1u));
-            srow_ws[a][(int64_t)slot * p.H] = st_l[r];
+            srow_ws[a][slot] = st_l[r];
             bits &= bits - 1u;
           }
         }
@@ -479,7 +481,7 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
 // ---------------------------------------------------------------------------------------
 // attn_sum from the slot-indexed scores: one wave per query row. The row's valid positions,
 // sorted ascending, are in slot order: slot i holds the i-th smallest selected key. So
-// attn_sum[t, j] = sum_h exp2(sws[t, i(j), h] * scale log2(e) - lse2[t, h]) with i(j) the rank of position j
+// attn_sum[t, j] = sum_h exp2(sws[h][t][i(j)] * scale log2(e) - lse2[t, h]) with i(j) the rank of position j
 // (a wave bitonic sort of (position, j)); invalid positions give 0. With KL, the row's
 // indexer KL loss follows from the same registers (the per-row term of
 // sparse_indexer_kl_loss, indexer_kl_fused.py:8-155, as in the gather kernel's epilogue).
@@ -523,6 +525,7 @@ __device__ __forceinline__ float as_wave_max(float x) {
 template <int R, bool KL>
 __global__ __launch_bounds__(256) void dense_attn_sum_kernel(const AttnSumParams p) {
   __shared__ float lse2_s[4][64];
+  __shared__ __align__(16) float slot_sum[4][R * 64 + 4];  // per wave: the row's per-slot head sums
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
@@ -547,7 +550,38 @@ __global__ __launch_bounds__(256) void dense_attn_sum_kernel(const AttnSumParams
   }
   wave_bitonic_sort<R>(key);
   lds_fence();
-  const float* srow = p.sws + row * (int64_t)p.K * p.H;
+  // Per-slot sums over the heads, in slot order: head h's scores of this row are the K floats
+  // at srow + h * hstride (head-major workspace), read four slots per lane and load; the
+  // sums go through the wave's LDS row to the lanes that hold each slot's position.
+  const float* srow = p.sws + ((int64_t)b * p.H * p.T + t) * p.K;
+  const int64_t hstride = (int64_t)p.T * p.K;
+  int nvalid = 0;  // valid positions sort first: slots [0, nvalid) are in use
+#pragma unroll
+  for (int r = 0; r < R; ++r) nvalid += __popcll(__builtin_amdgcn_ballot_w64((key[r] >> 32) != 0xFFFFFFFFull));
+  float* ssum = &slot_sum[wave][0];
+  const bool vec = (p.K & 3) == 0;  // head rows 16-byte aligned
+  for (int i0 = 4 * lane; i0 < nvalid; i0 += 256) {
+    float a4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int h = 0; h < p.H; ++h) {
+      const float l2 = lse2_s[wave][h];
+      if (l2 == -INFINITY) continue;  // a row without valid keys (the same for every head)
+      const float* sp = srow + h * hstride + i0;
+      float v[4];
+      if (vec) {
+        const float4 f = *reinterpret_cast<const float4*>(sp);  // i0 + 3 < K when K % 4 == 0
+        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = i0 + u < p.K ? sp[u] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) a4[u] += fexp2(fmaf(v[u], p.scale_log2, -l2));
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) ssum[i0 + u] = a4[u];
+  }
+  lds_fence();
   float av[R], zv[R];
   float sa = 0.f, mz = -INFINITY;
 #pragma unroll
@@ -555,27 +589,7 @@ __global__ __launch_bounds__(256) void dense_attn_sum_kernel(const AttnSumParams
     const int i = r * 64 + lane;  // slot = sorted rank
     const int j = (int)(uint32_t)key[r];
     const bool ok = (key[r] >> 32) != 0xFFFFFFFFull;
-    float sum = 0.f;
-    if (ok) {
-      const float* sp = srow + (int64_t)i * p.H;
-      if ((p.H & 3) == 0) {
-        // the slot's heads as 16-byte loads (rows of H floats, H % 4 == 0: 16-byte aligned)
-        for (int h = 0; h < p.H; h += 4) {
-          const float4 sv = *reinterpret_cast<const float4*>(sp + h);
-          const float svv[4] = {sv.x, sv.y, sv.z, sv.w};
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const float l2 = lse2_s[wave][h + u];
-            if (l2 != -INFINITY) sum += fexp2(fmaf(svv[u], p.scale_log2, -l2));
-          }
-        }
-      } else {
-        for (int h = 0; h < p.H; ++h) {
-          const float l2 = lse2_s[wave][h];
-          if (l2 != -INFINITY) sum += fexp2(fmaf(sp[h], p.scale_log2, -l2));
-        }
-      }
-    }
+    const float sum = ok ? ssum[i] : 0.f;
     av[r] = sum;
     zv[r] = -INFINITY;
     if (j < p.K) {
