@@ -9,7 +9,8 @@
 // scale move onto the gate: w*relu(scale*z) = (scale*w)*relu(z).
 //
 // Pipeline (all on the caller's stream, no host synchronisation):
-//  K0 score_kernel<SAMPLE>: MFMA scores of every query against Ms strided sample keys.
+//  K0 score_kernel<SAMPLE>: MFMA scores of every query against Ms strided sample keys
+//                           (split over workgroups like K1).
 //  K0b tau_kernel:          one wave per query: a threshold tau whose rank among the
 //                           sample scores lies in [r, r + 8], r chosen so that at least
 //                           topk keys of the whole row score >= tau with very high
@@ -131,6 +132,80 @@ __device__ __forceinline__ uint32_t lanes_below_u(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
+// Bisection for a threshold key over per-lane key slots, wave-wide. Invariant: cnt_lo =
+// count(key >= lo) >= need > cnt_hi = count(key >= hi); each step counts the keys >= mid.
+// Returns the final lo: hi = lo + 1, or the first lo whose count is <= need + slack.
+// Only the keys in [lo, hi) can change a count, so once at most kCompactKeys of them are
+// left they are copied (ballot-ordered) into the wave's LDS buffer and the remaining steps
+// count those, one or a few per lane, plus cnt_hi, instead of every slot. The sequence of
+// mid values and counts, and so the result, is the bisection's over all slots.
+constexpr int kCompactKeys = 256;
+
+template <int S>
+__device__ __forceinline__ uint32_t wave_bisect_keys(const uint32_t (&kv)[S], int nslot, uint64_t lo, uint64_t hi,
+                                                     int cnt_lo, int cnt_hi, int need, int slack, uint32_t* buf) {
+  while (hi - lo > 1 && cnt_lo - cnt_hi > kCompactKeys) {
+    const uint32_t mid = (uint32_t)(lo + ((hi - lo) >> 1));
+    uint32_t cc = 0;
+#pragma unroll
+    for (int m0 = 0; m0 < S; m0 += 8) {
+      if (m0 < nslot) {
+#pragma unroll
+        for (int m = m0; m < m0 + 8 && m < S; ++m) cc += kv[m] >= mid;
+      }
+    }
+    const int c = (int)wave_sum_u(cc);
+    if (c >= need) {
+      lo = mid;
+      cnt_lo = c;
+      if (c <= need + slack) return (uint32_t)lo;
+    } else {
+      hi = mid;
+      cnt_hi = c;
+    }
+  }
+  if (hi - lo <= 1) return (uint32_t)lo;
+  // Copy the keys in [lo, hi) (cnt_lo - cnt_hi of them) into buf, slot by slot.
+  const uint32_t lo32 = (uint32_t)lo, span = (uint32_t)(hi - lo);
+  int base = 0;
+#pragma unroll
+  for (int m0 = 0; m0 < S; m0 += 8) {
+    if (m0 < nslot) {
+#pragma unroll
+      for (int m = m0; m < m0 + 8 && m < S; ++m) {
+        const bool in = kv[m] - lo32 < span;
+        const uint64_t bm = __ballot(in);
+        const int at = base + (int)lanes_below_u(bm);
+        if (in && at < kCompactKeys) buf[at] = kv[m];  // the bound holds by the invariant
+        base += __popcll(bm);
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int lane = threadIdx.x & 63;
+  constexpr int CS = kCompactKeys / 64;
+  uint32_t cv[CS];
+#pragma unroll
+  for (int j = 0; j < CS; ++j) cv[j] = j * 64 + lane < base ? buf[j * 64 + lane] : 0u;  // 0 < every mid
+  // Every copied key is below the hi of the copy, whose count cnt_hi stays the base.
+  while (hi - lo > 1) {
+    const uint32_t mid = (uint32_t)(lo + ((hi - lo) >> 1));
+    uint32_t cc = 0;
+#pragma unroll
+    for (int j = 0; j < CS; ++j) cc += cv[j] >= mid;
+    const int c = cnt_hi + (int)wave_sum_u(cc);
+    if (c >= need) {
+      lo = mid;
+      if (c <= need + slack) break;
+    } else {
+      hi = mid;
+    }
+  }
+  return (uint32_t)lo;
+}
+
 enum TauMode { kTauArray = 0, kTauPlusInf = 1, kTauMinusInf = 2 };
 
 // Additive score terms (template flags): the dense mask [B, T, S] and the soft view bias, a
@@ -248,8 +323,9 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int b = blockIdx.z;
-  const int split = SAMPLE ? 0 : (int)blockIdx.y;
-  const int nsplit = SAMPLE ? 1 : p.nsplit;
+  // Key splits: split sp sweeps stages sp, sp + nsplit, ... (SAMPLE: of the sample keys).
+  const int split = (int)blockIdx.y;
+  const int nsplit = p.nsplit;
   const int q0 = blockIdx.x * BM + wave * kQW;
   const int T = p.T, S = p.S;
   const int nkeys = SAMPLE ? p.Ms : S;
@@ -548,9 +624,10 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
 template <int MPL>
 __global__ __launch_bounds__(256) void indexer_tau_kernel(const float* samp, int Ms, int rank, int slack,
                                                           float* tau, int64_t rows) {
+  __shared__ uint32_t cbuf[4][kCompactKeys];
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  if (row >= rows) return;  // whole wave; no barriers below
   const float* src = samp + row * Ms;
   uint32_t kv[MPL];
   uint32_t lmin = 0xFFFFFFFFu, lmax = 0u;
@@ -561,22 +638,10 @@ __global__ __launch_bounds__(256) void indexer_tau_kernel(const float* samp, int
     lmax = max(lmax, kv[m]);
   }
   // Invariant: count(key >= lo) >= rank and count(key >= hi) < rank.
-  uint64_t lo = wave_min_u(lmin);
-  uint64_t hi = (uint64_t)wave_max_u(lmax) + 1;
-  while (hi - lo > 1) {
-    const uint32_t mid = (uint32_t)(lo + ((hi - lo) >> 1));
-    uint32_t c = 0;
-#pragma unroll
-    for (int m = 0; m < MPL; ++m) c += kv[m] >= mid;
-    c = wave_sum_u(c);
-    if ((int)c < rank) {
-      hi = mid;
-    } else {
-      lo = mid;
-      if ((int)c <= rank + slack) break;
-    }
-  }
-  if (lane == 0) tau[row] = key2f((uint32_t)lo);
+  const uint64_t lo = wave_min_u(lmin);
+  const uint64_t hi = (uint64_t)wave_max_u(lmax) + 1;
+  const uint32_t t = wave_bisect_keys<MPL>(kv, MPL, lo, hi, 64 * MPL, 0, rank, slack, cbuf[threadIdx.x >> 6]);
+  if (lane == 0) tau[row] = key2f(t);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -646,6 +711,7 @@ __device__ __forceinline__ bool row_lists(const SelectParams& p, int64_t row, Ro
 
 template <typename E>
 __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams p) {
+  __shared__ uint32_t cbuf[4][kCompactKeys];
   constexpr int KS = kSelRegs;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -681,34 +747,17 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
       }
     }
   }
-  // Key range of the live slots: empty slots hold 0, which kv - 1 wraps to the maximum.
+  // Key range of the live slots: empty slots hold 0, which kv - 1 wraps to the maximum (the
+  // + 1 comes after the wave minimum, so a lane without live slots does not wrap back to 0).
+  // Candidates passed a >= comparison and are never NaN, so no live key is 0.
 #pragma unroll
   for (int m = 0; m < KS; ++m) {
     lmin = min(lmin, kv[m] - 1u);
     lmax = max(lmax, kv[m]);
   }
-  lmin += 1u;
-  // Bisection on the key value: count(key >= lo) >= Kk > count(key >= hi).
-  uint64_t lo = wave_min_u(lmin), hi = (uint64_t)wave_max_u(lmax) + 1;
-  while (hi - lo > 1) {
-    const uint32_t mid = (uint32_t)(lo + ((hi - lo) >> 1));
-    uint32_t cc = 0;
-#pragma unroll
-    for (int m0 = 0; m0 < KS; m0 += 8) {
-      if (m0 < nch) {
-#pragma unroll
-        for (int m = m0; m < m0 + 8; ++m) cc += kv[m] >= mid;
-      }
-    }
-    const int n = (int)wave_sum_u(cc);
-    if (n >= p.Kk) {
-      lo = mid;
-      if (n == p.Kk) break;
-    } else {
-      hi = mid;
-    }
-  }
-  const uint32_t thr = (uint32_t)lo;
+  // Bisection on the key value: count(key >= lo) = total >= Kk > count(key >= hi) = 0.
+  const uint64_t lo = (uint64_t)wave_min_u(lmin) + 1, hi = (uint64_t)wave_max_u(lmax) + 1;
+  const uint32_t thr = wave_bisect_keys<KS>(kv, nch, lo, hi, total, 0, p.Kk, 0, cbuf[threadIdx.x >> 6]);
   // Elements > thr are all selected; of those == thr, the first (Kk - count(> thr)) in
   // candidate order (split, position). Output positions come from wave ballots, so each
   // write goes to base + (selected lanes below this one).
@@ -977,10 +1026,13 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
     sp.Ms = pl.Ms;
     sp.tau = nullptr;
     sp.tau_mode = kTauArray;
-    sp.nsplit = 1;
+    // The sample keys split over workgroups too: one workgroup per query tile would leave
+    // most of the chip idle.
+    sp.nsplit = choose_nsplit(tiles * B, pl.Ms, filter_slots((const void*)indexer_score_kernel<E, HI, true, BIAS>, THREADS),
+                              true, BN);
     sp.nstages = (pl.Ms + BN - 1) / BN;
-    hipLaunchKernelGGL((indexer_score_kernel<E, HI, true, BIAS>), dim3((unsigned)tiles, 1, (unsigned)B), dim3(THREADS),
-                       0, st, sp);
+    hipLaunchKernelGGL((indexer_score_kernel<E, HI, true, BIAS>),
+                       dim3((unsigned)tiles, (unsigned)sp.nsplit, (unsigned)B), dim3(THREADS), 0, st, sp);
     GW_HIP_LAUNCH_CHECK("indexer_score_kernel<sample>");
     const dim3 tgrid((unsigned)((rows + 3) / 4));
     if (pl.Ms == 4096)
