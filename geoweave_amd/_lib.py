@@ -89,11 +89,26 @@ _SIGNATURES = {
     ),
     "gw_source_downsample_pool": (
         ctypes.c_int,
-        [ctypes.c_int, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p, _p, _p],
+        [ctypes.c_int, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, ctypes.c_int, _p, _p, _p],
     ),
     "gw_source_downsample_expand": (
         ctypes.c_int,
-        [ctypes.c_int, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, ctypes.c_int, _i64, _i64, _p, _p],
+        [ctypes.c_int, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, ctypes.c_int, _i64, _i64,
+         _p, _i64, _p, _p],
+    ),
+    "gw_source_downsample_rerank": (
+        ctypes.c_int,
+        [ctypes.c_int, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
+         ctypes.c_float, _p, _p, _p],
+    ),
+    "gw_source_downsample_subcell_top1": (
+        ctypes.c_int,
+        [ctypes.c_int, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _i64,
+         _i64, _p, _i64, _i64, ctypes.c_float, _p, _p, _p],
+    ),
+    "gw_source_downsample_static_pack4": (
+        ctypes.c_int,
+        [ctypes.c_int, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _p, _p],
     ),
     "gw_sparse_attn_fwd_dense_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int]),
     "gw_sparse_attn_fwd_dense": (

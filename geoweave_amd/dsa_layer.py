@@ -224,7 +224,7 @@ def sparse_attention_streaming(q, k, v, idx_q, idx_k, idx_w, topk: int, query_ch
         idx = None
         if prepared is not None:
             idx = sdown.select_topk(idx_q[:, s0:s1], idx_k, idx_w, topk, indexer_scale, source_downsample,
-                                    prepared=prepared)
+                                    prepared=prepared, q_offset=s0)
         if idx is None:
             idx, _ = sparse_topk_indexer_inference_func(idx_q[:, s0:s1], idx_k, idx_w, empty, topk, indexer_scale,
                                                         256, 0)

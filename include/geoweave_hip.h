@@ -342,9 +342,10 @@ int gw_sparse_attn_fwd_kl(int dtype,
 /* ------------------------------------------------------------------------------------
  * Source-downsample coarse selector (inference only, off unless requested): the device
  * steps around an indexer top-k over pooled source rows. Replaces the torch pooling of
- * DSAAttention._prepare_source_downsample_projected and the torch expansion of
- * _expand_source_downsample_chunk (easyvolcap/official_vggt/layers/dsa_attention.py:
- * 3386-3542 and :4079-4128; "legacy" strategy, :4187-4217).
+ * DSAAttention._prepare_source_downsample_projected, the torch expansion of
+ * _expand_source_downsample_chunk and the torch selection of the other strategies
+ * (easyvolcap/official_vggt/layers/dsa_attention.py:3386-3542, :4079-4186, :3554-4078;
+ * dispatch :4187-4260).
  *
  * source_to_fine: int32 [L, M], the fine tokens (< S) each source row covers, -1 past
  * the row's count (built on the host from the view/grid layout, :3069-3259).
@@ -352,27 +353,69 @@ int gw_sparse_attn_fwd_kl(int dtype,
  * gw_source_downsample_pool: source_k [B, L, Hi, Di] and source_w [B, L, Hi] (dtype,
  *   contiguous) = the mean of each row's fine rows of k [B, S, Hi, Di] and w [B, S, Hi]
  *   (contiguous): fp32 sum in listed order / count, rounded once (F.avg_pool2d over a cell,
- *   or the mean of its representative points; special and edge rows are copies).
- *   Supported: Hi <= 8, Hi * Di a multiple of 8.
- * gw_source_downsample_expand: out int32 [B, T, target] (contiguous) from the chosen
+ *   or the mean of its representative points; special and edge rows are copies). With
+ *   round_sum != 0 the sum is rounded to the dtype before the division, as the reference's
+ *   query mean does (gathered.sum(dim=2) / denom, :3976-3983). w and source_w may both be
+ *   null (queries have no gate). Supported: Hi <= 8, Hi * Di a multiple of 8.
+ * gw_source_downsample_expand: out int32 [B, T_out, target] (contiguous) from the chosen
  *   source rows coarse_idx [B, T, Kc] (element (b,t,c) at b*idx_stride_b + t*idx_stride_t
  *   + c) taken in their given order or, when coarse_scores (dtype, same layout) is given,
  *   by score descending and row index ascending on ties (the reference's order is that of
  *   an unsorted torch.topk, i.e. unspecified; Kc <= 4096 then): round_robin != 0 lists the
- *   m-th token of every
- *   chosen row for m = 0, 1, ... (full cells), else row by row; invalid slots are skipped
- *   and the list is cut to target; a query with fewer valid tokens repeats its last
- *   min(count, pad_window) tokens cyclically, or gets -1 everywhere if it has none.
+ *   m-th token of every chosen row for m = 0, 1, ... (full cells), else row by row;
+ *   invalid slots are skipped and the list is cut to target; a query with fewer valid
+ *   tokens repeats its last min(count, pad_window) tokens cyclically, or gets -1
+ *   everywhere if it has none. The table of batch element b starts at source_to_fine +
+ *   b * table_stride_b (0: one table; the per-batch tables of subcell_static_pack4,
+ *   _expand_source_downsample_chunk_batched :4129-4186). row_map (int32 [T_out], or null
+ *   for T_out = T) makes output row t read chosen row row_map[t]: the broadcast of a
+ *   coarse query's selection to its fine queries (qk_sym_x2_broadcast, :3999-4017).
  *   Supported: target <= 4096.
+ * gw_source_downsample_rerank (exact_rerank, _select_source_downsample_exact_rerank
+ *   :3599-3635 with _score_source_downsample_candidates :3554-3597): for every query q
+ *   [B, T, Hi, Di] the fine tokens of its chosen rows (row-major over (chosen row, slot))
+ *   are scored against k [B, S, Hi, Di] / w [B, S, Hi] with the indexer formula in fp32,
+ *   and out int32 [B, T, target] receives the top target of them (ties in candidate order;
+ *   tokens > kth first, then those equal to it). A query with fewer valid candidates than
+ *   target sets *fail (a device int the caller clears; its out row is then unspecified):
+ *   the reference then retries the chunk with a larger coarse budget. Supported: Hi <= 8,
+ *   Di a multiple of 8, Hi * Di <= 1024, Kc * M <= 8192.
+ * gw_source_downsample_subcell_top1 (_select_source_downsample_subcell_top1 :3629-3812):
+ *   chosen rows (coarse_idx + coarse_scores, expanded by score descending) that are
+ *   special/edge rows (< first_cell_row) give their token; the rest of the target,
+ *   ceil((target - singles) / W) sub-cells at most (and at most those of the chosen
+ *   cells), goes to the best-scoring sub-cells of the chosen cells, scored against the
+ *   pooled sub-cell keys sub_k [B, C * G, Hi, Di] / sub_w [B, C * G, Hi] (cell c = row
+ *   first_cell_row + c; subcell_to_fine int32 [C * G, W] their tokens). out [B, T,
+ *   target]: the singles in order, then the kept sub-cells' tokens in (cell order,
+ *   sub-cell) order, cut to target; *fail as above. Supported: Kc <= 2048, Kc * G <= 8192.
+ * gw_source_downsample_static_pack4 (subcell_static_pack4 table, :3521-3542): table int32
+ *   [B, L, W]: rows below first_cell_row keep their token (source_to_fine[r, 0]); cell c
+ *   lists the tokens of its sub-cell with the largest head-mean of sub_w [B, C * G, Hi]
+ *   (fp32 sum times 1 / Hi, rounded to the dtype; the first on ties).
  */
 int gw_source_downsample_pool(int dtype, const void* k, const void* w, int64_t B, int64_t S, int64_t Hi,
-                              int64_t Di, const int32_t* source_to_fine, int64_t L, int64_t M,
+                              int64_t Di, const int32_t* source_to_fine, int64_t L, int64_t M, int round_sum,
                               void* source_k, void* source_w, void* stream);
 int gw_source_downsample_expand(int dtype, const int32_t* coarse_idx, const void* coarse_scores,
                                 int64_t idx_stride_b, int64_t idx_stride_t,
                                 int64_t B, int64_t T, int64_t Kc, const int32_t* source_to_fine,
-                                int64_t L, int64_t M, int round_robin, int64_t target,
-                                int64_t pad_window, int32_t* out, void* stream);
+                                int64_t table_stride_b, int64_t L, int64_t M, int round_robin, int64_t target,
+                                int64_t pad_window, const int32_t* row_map, int64_t T_out, int32_t* out,
+                                void* stream);
+int gw_source_downsample_rerank(int dtype, const void* q, const void* k, const void* w, int64_t B, int64_t T,
+                                int64_t S, int64_t Hi, int64_t Di, const int32_t* coarse_idx, int64_t idx_stride_b,
+                                int64_t idx_stride_t, int64_t Kc, const int32_t* source_to_fine, int64_t L,
+                                int64_t M, int64_t target, float scale, int32_t* out, int* fail, void* stream);
+int gw_source_downsample_subcell_top1(int dtype, const void* q, const void* sub_k, const void* sub_w, int64_t B,
+                                      int64_t T, int64_t C, int64_t G, int64_t Hi, int64_t Di,
+                                      const int32_t* coarse_idx, const void* coarse_scores, int64_t idx_stride_b,
+                                      int64_t idx_stride_t, int64_t Kc, const int32_t* source_to_fine, int64_t L,
+                                      int64_t M, int64_t first_cell_row, const int32_t* subcell_to_fine, int64_t W,
+                                      int64_t target, float scale, int32_t* out, int* fail, void* stream);
+int gw_source_downsample_static_pack4(int dtype, const void* sub_w, int64_t B, int64_t C, int64_t G, int64_t Hi,
+                                      const int32_t* source_to_fine, int64_t L, int64_t M, int64_t first_cell_row,
+                                      const int32_t* subcell_to_fine, int64_t W, int32_t* table, void* stream);
 
 /* ------------------------------------------------------------------------------------
  * Sparse-index attention forward as a masked dense pass: the same results as

@@ -34,7 +34,8 @@ def _inputs(tpv, views, seed, dtype=torch.bfloat16, B=1):
 def test_pooled_sources_bit_exact(gpu_device, tpv, views, psi, factor, rep, dtype):
     q, k, w = _inputs(tpv, views, 11, dtype, B=2)
     cfg = sd.SourceDownsample(tpv, views, psi, factor=factor, representative_points=rep)
-    layout, table, sk, sw = sd.prepare(k.cuda(), w.cuda(), cfg)
+    prep = sd.prepare(k.cuda(), w.cuda(), cfg)
+    layout, table, sk, sw = prep.layout, prep.table, prep.source_k, prep.source_w
     lay = osd.source_layout(tpv, views, psi, factor, representative_points=rep)
     assert np.array_equal(layout.source_to_fine, lay["source_to_fine"])
     rk, rw = osd.pool_sources(k, w, lay)
@@ -66,7 +67,8 @@ def test_select_matches_oracle(gpu_device):
     q, k, w = _inputs(tpv, views, 21)
     cfg = sd.SourceDownsample(tpv, views, psi, factor=2)
     qd, kd, wd = q.cuda(), k.cuda(), w.cuda()
-    layout, table, sk, sw = sd.prepare(kd, wd, cfg)
+    prep = sd.prepare(kd, wd, cfg)
+    layout, table, sk, sw = prep.layout, prep.table, prep.source_k, prep.source_w
     lay = osd.source_layout(tpv, views, psi, 2)
     kc = sd.coarse_budget(layout, topk, cfg)
     assert kc == osd.coarse_topk(lay, topk)
