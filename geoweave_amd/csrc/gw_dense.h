@@ -108,8 +108,12 @@ __device__ __forceinline__ uint32_t lane_bit_transpose32(uint32_t x, int lane) {
 // is flagged (flags[b][qb][chunk]; dup_b[b] = 1 too when dup_b is given). Positions are read
 // 8 rows at a time (16 bytes per lane when the table allows), so the loads of a group are in
 // flight together. With maskT, the same bits key-major as well: maskT[b][qb][s] has bit i set
-// when query 32 qb + i selected key s (s < S_pad). The first workgroup of each batch element
-// clears vmax_words words of vmax and bad[b] (for the forward's dense_vmax_kernel), when given.
+// when query 32 qb + i selected key s (s < S_pad). With bias_order the query-major words are
+// stored for the plain forward's bias instead: key 8 g + 4 h + j (g, j < 4, h < 2) at bit
+// 8 j + 7 - g - 4 h, and inverted (a set bit = not selected), so that shifting the word left
+// by g + 4 h puts the keys of accumulator group g of lane half h at the sign bits of the four
+// bytes. The first workgroup of each batch element clears vmax_words words of vmax and bad[b]
+// (for the forward's dense_vmax_kernel), when given.
 // ---------------------------------------------------------------------------------------
 constexpr int kMaskChunk = 16384;  // keys per workgroup
 
@@ -118,7 +122,8 @@ __global__ __launch_bounds__(256) void dense_mask_kernel(const int32_t* __restri
                                                          int nchunk, int vec, int vmax_words,
                                                          uint32_t* __restrict__ mask, int* __restrict__ flags,
                                                          uint32_t* __restrict__ vmax, int* __restrict__ bad,
-                                                         uint32_t* __restrict__ maskT, int* __restrict__ dup_b) {
+                                                         uint32_t* __restrict__ maskT, int* __restrict__ dup_b,
+                                                         int bias_order) {
   // [key / 32][query], rows padded to 33 words so that one query's atomics spread over banks
   __shared__ uint32_t words[(kMaskChunk / 32) * 33];
   __shared__ int dup_any;
@@ -143,7 +148,8 @@ __global__ __launch_bounds__(256) void dense_mask_kernel(const int32_t* __restri
   auto put = [&](int32_t sidx, int i) {
     const uint32_t sl = (uint32_t)sidx - (uint32_t)c0;
     if (sl < (uint32_t)len) {
-      const uint32_t bit = 1u << (sl & 31u);
+      const uint32_t kk = sl & 31u;
+      const uint32_t bit = 1u << (bias_order ? 8u * (kk & 3u) + 7u - (kk >> 3) - 4u * ((kk >> 2) & 1u) : kk);
       dup |= (atomicOr(&words[(sl >> 5) * 33 + i], bit) & bit) != 0u;
     }
   };
@@ -178,7 +184,8 @@ __global__ __launch_bounds__(256) void dense_mask_kernel(const int32_t* __restri
   uint32_t* out = mask + ((int64_t)b * (Spad >> 5) + (c0 >> 5)) * tpad + qb * 32;
   for (int idx = threadIdx.x; idx < nkt * 32; idx += 256) {
     const int kt = idx >> 5, i = idx & 31;
-    out[(int64_t)kt * tpad + i] = words[kt * 33 + i];
+    const uint32_t wv = words[kt * 33 + i];
+    out[(int64_t)kt * tpad + i] = bias_order ? ~wv : wv;
   }
   if (maskT != nullptr) {
     // Two sub-tiles per wave at a time, one per half-wave: lane i reads query i's word and

@@ -307,12 +307,25 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
     f32x16 s[kQPW];
 #pragma unroll
     for (int a = 0; a < kQPW; ++a) {
-      // Entry r of this lane is bit 8(r/4) + r%4 of w >> 4 half.
-      const uint32_t own = w[a] >> (4 * half);
+      if constexpr (ATTN) {
+        // Entry r of this lane is bit 8(r/4) + r%4 of w >> 4 half.
+        const uint32_t own = w[a] >> (4 * half);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int sel = __builtin_amdgcn_sbfe((int)own, 8 * (r >> 2) + (r & 3), 1);  // 0 or -1
-        s[a][r] = select_bias(sel, ninf);
+        for (int r = 0; r < 16; ++r) {
+          const int sel = __builtin_amdgcn_sbfe((int)own, 8 * (r >> 2) + (r & 3), 1);  // 0 or -1
+          s[a][r] = select_bias(sel, ninf);
+        }
+      } else {
+        // Bias-order words: entry 4 g + j of this lane is the sign bit of byte j of w << (g + 4
+        // half), set when the key is not selected; a sign-extended byte select masks -inf
+        // (one instruction per entry).
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint32_t sh = w[a] << (g + 4 * half);
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            s[a][4 * g + j] = __uint_as_float((uint32_t)(int32_t)(int8_t)(sh >> (8 * j)) & 0xFF800000u);
+        }
       }
     }
 #pragma unroll
@@ -747,7 +760,7 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
                         : 0;
     hipLaunchKernelGGL(dense_mask_kernel, dim3(L.nchunk, L.nqb_pad, (unsigned)B), dim3(256), 0, st, kv_pos,
                        pos_stride_b, pos_stride_t, (int)T, (int)S, L.spad, (int)K, L.nqb, L.nqb_pad * 32, L.nchunk,
-                       vec, (int)(H * 64), mask, flags, vmax, bad, nullptr, nullptr);
+                       vec, (int)(H * 64), mask, flags, vmax, bad, nullptr, nullptr, want_attn ? 0 : 1);
     GW_HIP_LAUNCH_CHECK("dense_mask_kernel launch");
   }
   hipLaunchKernelGGL(dense_vmax_kernel, dim3((unsigned)((S + kVmaxKeys - 1) / kVmaxKeys), (unsigned)H, (unsigned)B),

@@ -667,7 +667,7 @@ extern "C" int gw_sparse_attn_bwd_dense(int dtype, const void* q, const int64_t*
                         : 0;
     hipLaunchKernelGGL(dense_mask_kernel, dim3(L.nchunk, L.nqb_pad, (unsigned)B), dim3(256), 0, st, kv_pos,
                        pos_stride_b, pos_stride_t, (int)T, (int)S, L.spad, (int)K, L.nqb, L.tpad, L.nchunk, vec, 0,
-                       mask, flags, nullptr, nullptr, maskT, route);
+                       mask, flags, nullptr, nullptr, maskT, route, 0);
     GW_HIP_LAUNCH_CHECK("dense_mask_kernel launch");
   }
   {
