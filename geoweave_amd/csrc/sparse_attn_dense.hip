@@ -16,7 +16,8 @@
 // already the lane's B operand of the P·V product (V^T stored with the keys in that operand
 // order). V enters in fp16 scaled per column by an exact power of two that fits its range.
 // P holds 11 significant bits (the reference's fp32 weights, rounded to nearest); the row
-// sums add the fp32 weights.
+// sums add that fp16 operand itself (v_dot2_f32_f16 against ones, fp32 accumulation), so that
+// o = O / l divides by the sum of the weights the product used.
 //
 // Online softmax with a lazy reference maximum: the weights p = exp2(t - m) of a sub-tile are
 // formed with the query's current m, and m is raised (O and the row sum rescaled, the weights
@@ -374,13 +375,29 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
       // lane's sum exceeds kSumCap every p fits fp16, and the maximum stays where it is.
       float pv[16];
       float ls = 0.f;
-      {
-        const float nm = -m[a];
+      uint4 pb[2];
+      // The P operand in fp16, and its row sum: v_dot2_f32_f16 against ones adds the fp16
+      // operand in fp32 (half the instructions of adding the fp32 weights), so the sum is that
+      // of the weights the product used.
+      auto weights = [&](float nm) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) pv[r] = fexp2(fmaf(s[a][r], sl2, nm));
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ls += pv[r];
-      }
+        for (int ks = 0; ks < 2; ++ks)
+          pb[ks] = make_uint4(pack_f16(pv[8 * ks], pv[8 * ks + 1]), pack_f16(pv[8 * ks + 2], pv[8 * ks + 3]),
+                              pack_f16(pv[8 * ks + 4], pv[8 * ks + 5]), pack_f16(pv[8 * ks + 6], pv[8 * ks + 7]));
+        constexpr uint32_t kOnes = 0x3C003C00u;  // (1.0, 1.0) in fp16
+        float t = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          t = dot2(FP16{}, pb[ks].x, kOnes, t);
+          t = dot2(FP16{}, pb[ks].y, kOnes, t);
+          t = dot2(FP16{}, pb[ks].z, kOnes, t);
+          t = dot2(FP16{}, pb[ks].w, kOnes, t);
+        }
+        return t;
+      };
+      ls = weights(-m[a]);
       if (__builtin_amdgcn_ballot_w64(!(ls <= kSumCap)) != 0ull) {
         // Some query of the block has an entry above its maximum by more than log2(kSumCap /
         // 16) (or its first selected entry): every query of the block moves its maximum to
@@ -397,21 +414,9 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
         for (int db = 0; db < 2; ++db)
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[a][db][r] *= alpha;
-        const float nm = -mn;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) pv[r] = fexp2(fmaf(s[a][r], sl2, nm));
-        ls = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) ls += pv[r];
+        ls = weights(-mn);
       }
-      // Row sums of the fp32 weights (as the gather kernel's): lse and the attn_sum
-      // normalisation do not see the fp16 rounding of the product's operand.
       l[a] += ls;
-      uint4 pb[2];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        pb[ks] = make_uint4(pack_f16(pv[8 * ks], pv[8 * ks + 1]), pack_f16(pv[8 * ks + 2], pv[8 * ks + 3]),
-                            pack_f16(pv[8 * ks + 4], pv[8 * ks + 5]), pack_f16(pv[8 * ks + 6], pv[8 * ks + 7]));
 #pragma unroll
       for (int db = 0; db < 2; ++db)
 #pragma unroll
