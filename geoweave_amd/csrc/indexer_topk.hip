@@ -680,13 +680,16 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
 struct RowLists {
   int64_t base;  // row * nlist * stride
   int off[kMaxLists + 1];
+  int adj[kMaxLists];  // stride - (entries of list l - 1): the gap skipped past list l's start
   int nlist, stride;
+  // The lists' entries lie within nlist * stride <= kSubTotal slots of the row: 32-bit
+  // offsets, one compare and select per list start at or below e.
   __device__ __forceinline__ int64_t at(int e) const {
-    int64_t a = base + e;
+    int a = e;
 #pragma unroll
     for (int s2 = 1; s2 < kMaxLists; ++s2)
-      if (s2 < nlist && e >= off[s2]) a += stride - (off[s2] - off[s2 - 1]);
-    return a;
+      if (s2 < nlist) a += e >= off[s2] ? adj[s2] : 0;
+    return base + a;
   }
 };
 
@@ -699,13 +702,16 @@ __device__ __forceinline__ bool row_lists(const SelectParams& p, int64_t row, Ro
 #pragma unroll
   for (int s2 = 0; s2 < kMaxLists; ++s2) {
     rl.off[s2] = acc;
+    rl.adj[s2] = 0;
     if (s2 < p.nlist) {
-      const int c = p.counts[row * p.nlist + s2];
+      const int c = __builtin_amdgcn_readfirstlane(p.counts[row * p.nlist + s2]);  // row is wave-uniform
       bad |= c > p.cap;
       acc += min(c, p.cap);
     }
   }
   rl.off[kMaxLists] = acc;
+#pragma unroll
+  for (int s2 = 1; s2 < kMaxLists; ++s2) rl.adj[s2] = p.stride - (rl.off[s2] - rl.off[s2 - 1]);
   return bad;
 }
 
@@ -733,18 +739,38 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
 
   // Slots past the end hold key 0, below the key of every finite score; chunks of 8 slots
   // past the last one in use are skipped with a uniform branch.
+  // Each slot's key (order-preserving score bits) and key index stay in registers for the
+  // output, so the list position of an entry is computed once.
+  // All loads are issued before any is used (the score bits land in kv and become keys in a
+  // second pass), so the chunks of 8 slots do not wait for each other.
   uint32_t kv[KS];
+  int32_t ky[KS];
   uint32_t lmin = 0xFFFFFFFFu, lmax = 0u;
 #pragma unroll
   for (int m0 = 0; m0 < KS; m0 += 8) {
 #pragma unroll
-    for (int m = m0; m < m0 + 8; ++m) kv[m] = 0u;
+    for (int m = m0; m < m0 + 8; ++m) {
+      kv[m] = 0u;
+      ky[m] = 0;
+    }
     if (m0 < nch) {
 #pragma unroll
       for (int m = m0; m < m0 + 8; ++m) {
         const int e = m * 64 + lane;
-        if (e < total) kv[m] = f2key(__int_as_float(p.cand[rl.at(e)].x));
+        if (e < total) {
+          const int2 cdt = p.cand[rl.at(e)];
+          kv[m] = (uint32_t)cdt.x;
+          ky[m] = cdt.y;
+        }
       }
+    }
+  }
+#pragma unroll
+  for (int m0 = 0; m0 < KS; m0 += 8) {
+    if (m0 < nch) {
+#pragma unroll
+      for (int m = m0; m < m0 + 8; ++m)
+        if (m * 64 + lane < total) kv[m] = f2key(__uint_as_float(kv[m]));
     }
   }
   // Key range of the live slots: empty slots hold 0, which kv - 1 wraps to the maximum (the
@@ -787,9 +813,8 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
         const int slot_out = base + lanes_below(selm);
         base += __popcll(selm);
         if (sel) {
-          const int2 cdt = p.cand[rl.at(m * 64 + lane)];
-          oi[slot_out] = cdt.y;
-          os[slot_out] = (uint16_t)pack1(E{}, __int_as_float(cdt.x));
+          oi[slot_out] = ky[m];
+          os[slot_out] = (uint16_t)pack1(E{}, key2f(kv[m]));
         }
       }
     }
