@@ -305,6 +305,10 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
   // One 32-key sub-tile: S^T for both blocks from the selection bias, the softmax in
   // registers, O^T += V^T P^T.
   auto sub = [&](const uint8_t* kt, const uint8_t* vt, int st, const uint32_t (&w)[kQPW]) {
+    // The sub-tile's four K operands first: their LDS latency passes under the bias.
+    uint4 ka[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) ka[ks] = *reinterpret_cast<const uint4*>(kt + koff(st, ks));
     f32x16 s[kQPW];
 #pragma unroll
     for (int a = 0; a < kQPW; ++a) {
@@ -330,11 +334,9 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
       }
     }
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const uint4 ka = *reinterpret_cast<const uint4*>(kt + koff(st, ks));
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int a = 0; a < kQPW; ++a) s[a] = mma(E{}, ka, qa[a][ks], s[a]);
-    }
+      for (int a = 0; a < kQPW; ++a) s[a] = mma(E{}, ka[ks], qa[a][ks], s[a]);
     if constexpr (ATTN) {
       // Each selected entry's score (unscaled: dense_attn_sum_kernel applies the scale), at
       // the slot of its key's rank. The lane's 16 scores go to its LDS row, and a loop over the
