@@ -16,7 +16,7 @@
 //                           topk keys of the whole row score >= tau with very high
 //                           probability (about 1.7 x topk keys on average).
 //  K1 score_kernel<FILTER>: MFMA scores against all keys; the epilogue appends
-//                           (score, key) pairs with score >= tau to the query's candidate
+//                           (score, key) pairs with score > tau to the query's candidate
 //                           list (one list per query and key split).
 //  K2 select_kernel:        one wave per query: exact top-k of the candidates held in
 //                           registers (bisection on the order-preserving score bits,
@@ -27,9 +27,10 @@
 //                           LDS, block radix select.
 //  K3 fallback_kernel:      exact brute force for queued queries (scores to scratch, radix
 //                           select) - correct for any input, used rarely.
-// Exactness: if count(score >= tau) >= topk, every member of the top-k scores >= tau and
-// is a candidate, so selecting among the candidates is exact. Ties at the k-th value are
-// broken deterministically (candidate order: split, then position in the list).
+// Exactness: if count(score > tau) >= topk, every member of the top-k scores > tau and is a
+// candidate, so selecting among the candidates is exact (otherwise the query has fewer than
+// topk candidates and goes to the brute force). Ties at the k-th value are broken
+// deterministically (candidate order: split, then position in the list).
 //
 // MFMA layout (v_mfma_f32_32x32x16_{bf16,f16}), transposed: per tile of 32 keys a wave
 // forms S^T[32 keys x 32 queries] = K Q^T with A = key rows staged through LDS (XOR-swizzled
@@ -392,7 +393,7 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
   // Gate values travel as raw 16-bit patterns until wstore converts them at the end of the
   // stage: converting at load time would make the wave wait (vmcnt) for the key tile
   // loads issued just before. Keys past the end: K rows are loaded from the last valid key
-  // (harmless), and the gate is NaN (FILTER: the score is NaN and fails every `>= tau`)
+  // (harmless), and the gate is NaN (FILTER: the mark clears keys past the end)
   // or 0 (SAMPLE: not stored).
   constexpr uint32_t kNoGate = 0xFFFFFFFFu;
   uint32_t wraw[WLOADS];
@@ -535,13 +536,22 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
   uint32_t pmask = 0;  // marked elements of the pending stage
   int kb_pend = 0;     // its first key + 4 half (this lane's key base)
   char* const lbytes = reinterpret_cast<char*>(lbase);
-  auto mark = [&](const float (&sv)[16], int t) {
+  // An element passes when score > tau: bit r = sign bit of tau - score, appended by
+  // v_alignbit_b32 (two instructions per element). Keys past the end (NaN scores) are
+  // cleared explicitly in the last stage.
+  auto mark = [&](const float (&sv)[16], int t, int kb) {
 #pragma unroll
     for (int g = 0; g < 4; ++g)
       *reinterpret_cast<float4*>(stg + 16 * t + 4 * g) = make_float4(sv[4 * g], sv[4 * g + 1], sv[4 * g + 2], sv[4 * g + 3]);
     uint32_t tb = 0;
 #pragma unroll
-    for (int r = 15; r >= 0; --r) tb = tb * 2u + (sv[r] >= tau_l ? 1u : 0u);  // NaN never passes
+    for (int r = 15; r >= 0; --r) tb = __builtin_amdgcn_alignbit(tb, __float_as_uint(tau_l - sv[r]), 31);
+    if (kb + BN > S) {
+      const int k4 = kb + 32 * t + 4 * half;
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (k4 + 8 * (r >> 2) + (r & 3) >= S) tb &= ~(1u << r);
+    }
     pmask |= tb << (16 * t);
   };
   // Element idx = 16 t + r of the stage holds key 32 t + 8 (r / 4) + r % 4 + 4 half past the
@@ -587,7 +597,7 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
     for (int t = 0; t < NT; ++t) {
       float s0[16];
       tile_scores(s0, kb, t, kt, wt);
-      if constexpr (!SAMPLE) mark(s0, t);
+      if constexpr (!SAMPLE) mark(s0, t, kb);
     }
     kb_pend = kb + 4 * half;
 
