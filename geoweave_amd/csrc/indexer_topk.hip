@@ -272,6 +272,24 @@ __device__ __forceinline__ void lds_dma16(const void* src, const void* lds_dst) 
       : "memory");
 }
 
+// The same load from a wave-uniform base (an SGPR pair) plus a 32-bit per-lane offset: no
+// 64-bit address arithmetic per load.
+__device__ __forceinline__ void lds_dma16_s(const void* base, uint32_t off, const void* lds_dst) {
+  const uint32_t lds = (uint32_t)(uintptr_t)lds_dst;
+  const uint64_t b = reinterpret_cast<uintptr_t>(base);
+  const uint64_t bu = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+                      (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(off), "s"(bu), "s"(__builtin_amdgcn_readfirstlane(lds))
+      : "memory");
+}
+
 // Workgroup shape of the score kernel: NW waves of 32 queries share every key tile (a
 // key tile read from L2 serves NW * 32 queries). HI <= 4 keeps its register file within
 // 256 per lane, so 8 waves (two per SIMD) fit one workgroup; HI = 8 needs 4.
@@ -377,6 +395,9 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
   const int kl0 = wave * RPW + (lane * 16) / ROW_BYTES;
   const int lc0 = (lane % CHUNKS) ^ (kl0 & SWZ);
   auto voff = [&](int i) { return (uint32_t)(kl0 * ROW_BYTES + (lc0 ^ ((i * RPI) & SWZ)) * 16); };
+  uint32_t voffs[LOADS];  // byte offset of load i from the stage's first key row
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) voffs[i] = (uint32_t)(i * (NW * 1024)) + voff(i);
   // Operand read offsets: key row (nb*32 + col), logical chunk h*8 + 2*ks + half, physical
   // chunk (h*8 + 2*ks + half) ^ (col & SWZ) = 8*(h ^ c3) + ((2*ks + half) ^ (col & 7)) with
   // c3 = bit 3 of col when SWZ = 15: head h sits at 128*h + 128*c3 (h even) or
@@ -403,10 +424,7 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
       // Full stage of consecutive keys: uniform base + lane offset + i * NW KB.
       const char* kbase = reinterpret_cast<const char*>(p.k + ((int64_t)b * S + kb) * (HI * kDI));
 #pragma unroll
-      for (int i = 0; i < LOADS; ++i) {
-        const char* src = kbase + i * (NW * 1024) + voff(i);
-        lds_dma16(src, &ktile[(i * NW + wave) * 1024]);
-      }
+      for (int i = 0; i < LOADS; ++i) lds_dma16_s(kbase, voffs[i], &ktile[(i * NW + wave) * 1024]);
     } else {
       // Sample keys or the last stage: rows past the end re-read the last valid key.
 #pragma unroll
