@@ -4,7 +4,7 @@ fp32 CPU oracle and the gather kernel.
 The dense pass computes every (query, key) product on the matrix cores and masks the keys a
 query did not select; o and lse must equal the sparse attention's. Tolerance: 2e-2 abs/rel for
 bf16/fp16 outputs (P enters the P·V product in fp16 against V scaled per column by a power of
-two; the row sums add the fp32 weights), 1e-4 for lse. Cases: V columns far outside the fp16
+two; the row sums add that fp16 operand in fp32), 1e-4 for lse. Cases: V columns far outside the fp16
 range and far below it (the per-column scaling), odd head counts, a softmax scale other than
 1/8, the layer's per-view shape in bf16 and fp16, ragged -1
 padding with T and S not multiples of 32 or 64, cross attention (T != S), empty rows,
