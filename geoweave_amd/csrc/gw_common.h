@@ -131,4 +131,27 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// A wave-uniform address pinned to scalar registers (both halves read from the first active
+// lane).
+__device__ __forceinline__ const char* uniform_ptr(const char* p) {
+  const uint64_t u = reinterpret_cast<uint64_t>(p);
+  const uint64_t r = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(u >> 32)) << 32) |
+                     (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)u);
+  return reinterpret_cast<const char*>(r);
+}
+
+// Loads through a buffer descriptor built in scalar registers from a wave-uniform base (raw
+// buffer, stride 0, the full 32-bit range: no clamping of in-range offsets) and a 32-bit lane
+// offset in bytes. The descriptor's third word is the gfx9-family data format for raw loads.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const char* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(uniform_ptr(base)), (short)0, -1, 0x00020000);
+}
+__device__ __forceinline__ uint4 buffer_load16(const char* base, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(uniform_rsrc(base), (int)off, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint32_t buffer_load4(const char* base, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(uniform_rsrc(base), (int)off, 0, 0);
+}
+
 }  // namespace gw

@@ -212,6 +212,10 @@ struct DenseParams {
 // Waves per workgroup, sharing each K/V tile. Two workgroups share a CU (two waves per SIMD
 // from different workgroups): one wave's barrier or memory wait is not the other's.
 constexpr int kDW = 4;
+// Limits of the 32-bit lane offsets of the tile loads: a K token stride below 2^23 elements
+// (2^24 bytes, a 24-bit multiply), 64 rows of V^T (S padded to 64) below 2^32 bytes.
+constexpr int64_t kDenseMaxKRowStride = 1ll << 23;
+constexpr int64_t kDenseMaxS = (1ll << 25) - 64;
 constexpr int kQPW = 2;  // 32-query blocks per wave (one head): each K and V^T operand feeds two products
 constexpr int kQBW = kDW * kQPW;  // 32-query blocks per workgroup
 static_assert(kDW == 4, "the tile staging moves two K and two V^T rows of 64 per thread");
@@ -227,7 +231,7 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: addresses built from it stay scalar
   const int h = blockIdx.x % p.H;  // consecutive workgroups (different XCDs) take different heads
   const int qb0 = (blockIdx.x / p.H) * kQBW + wave * kQPW;  // this wave's blocks qb0, qb0 + 1 (< nqb_pad)
   const int b = blockIdx.y;
@@ -269,15 +273,23 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
   // srow and srow + 32), loaded into registers a tile ahead of their LDS store.
   const int srow = tid >> 3, sc = tid & 7;
   const int soff = srow * 128 + ((sc ^ swz(srow)) << 4);  // swz(srow + 32) = swz(srow)
-  const uint16_t* ksrc = p.k + b * p.ksb + (int64_t)h * p.ksh + sc * 8;
-  const uint16_t* vsrc = p.vt + (((int64_t)b * p.H + h) * 64 + srow) * p.Spad + sc * 8;
+  // A tile's base addresses are uniform (scalar registers); a lane adds a 32-bit byte offset
+  // (the host keeps a K row stride below 2^24 bytes and 64 rows of V^T below 2^32 bytes).
+  const char* kbase = uniform_ptr(reinterpret_cast<const char*>(p.k + b * p.ksb + (int64_t)h * p.ksh));
+  const char* vbase = uniform_ptr(reinterpret_cast<const char*>(p.vt + ((int64_t)b * p.H + h) * 64 * p.Spad));
+  const uint32_t kss_b = (uint32_t)p.kss * 2u;
+  const uint32_t kcol = (uint32_t)sc * 16u;
+  const uint32_t vo0 = ((uint32_t)srow * (uint32_t)p.Spad + (uint32_t)sc * 8u) * 2u;
+  const uint32_t vo1 = vo0 + (uint32_t)p.Spad * 64u;  // row srow + 32
   auto gload = [&](int k0, uint4& ka, uint4& kb, uint4& va, uint4& vb) {
-    const int64_t key = min(k0 + srow, p.S - 1);
-    const int64_t key2 = min(k0 + srow + 32, p.S - 1);
-    ka = *reinterpret_cast<const uint4*>(ksrc + key * p.kss);
-    kb = *reinterpret_cast<const uint4*>(ksrc + key2 * p.kss);
-    va = *reinterpret_cast<const uint4*>(vsrc + k0);
-    vb = *reinterpret_cast<const uint4*>(vsrc + (int64_t)32 * p.Spad + k0);
+    // Rows past the end read row S - 1 (their keys are never selected).
+    const int lim = p.S - 1 - k0;
+    const char* kt = kbase + (int64_t)k0 * kss_b;
+    ka = buffer_load16(kt, __umul24((uint32_t)min(srow, lim), kss_b) + kcol);
+    kb = buffer_load16(kt, __umul24((uint32_t)min(srow + 32, lim), kss_b) + kcol);
+    const char* vtile0 = vbase + (int64_t)k0 * 2;
+    va = buffer_load16(vtile0, vo0);
+    vb = buffer_load16(vtile0, vo1);
   };
   auto lstore = [&](int bf, const uint4& ka, const uint4& kb, const uint4& va, const uint4& vb) {
     *reinterpret_cast<uint4*>(&ktile[bf][soff]) = ka;
@@ -292,8 +304,11 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
   auto voff = [&](int db, int st, int ks) { return col * 128 + db * 4096 + (((4 * st + 2 * ks + half) ^ fc) << 4); };
   // Mask words of the lane's queries, one per 32-key sub-tile.
   const int nsub = p.Spad >> 5;
-  const uint32_t* mcol = p.mask + (int64_t)b * nsub * p.tpad + tq[0];  // block qb0 + 1: + 32
-  auto mword = [&](int j, int a) { return mcol[(int64_t)min(j, nsub - 1) * p.tpad + 32 * a]; };
+  const char* mblk = uniform_ptr(reinterpret_cast<const char*>(p.mask + (int64_t)b * nsub * p.tpad + qb0 * 32));
+  const int64_t mrow_b = (int64_t)p.tpad * 4;  // bytes per sub-tile row of mask words
+  auto mword = [&](int j, int a) {
+    return buffer_load4(mblk + min(j, nsub - 1) * mrow_b, (uint32_t)(col + 32 * a) * 4u);
+  };
 
   uint32_t rank_base[kQPW] = {0u, 0u};  // attn_sum: selected keys of the query before the sub-tile
   float* srow_ws[kQPW];
@@ -748,6 +763,10 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
   }
   const DenseLayout L = dense_layout(B, T, S, H, K, want_attn);
   GW_CHECK_ARG((int64_t)(L.nqb_pad / kQBW) * H < (1ll << 31) && L.nqb_pad <= 65535, "too many query blocks");
+  if (k_strides[1] >= kDenseMaxKRowStride || (int64_t)L.spad * 128 >= (1ll << 32))
+    return set_error(GW_ERR_UNSUPPORTED,
+                     "the dense forward needs a K token stride below %lld elements and S <= %lld, got %lld and %lld",
+                     (long long)kDenseMaxKRowStride, (long long)kDenseMaxS, (long long)k_strides[1], (long long)S);
   GW_CHECK_ARG(workspace != nullptr && workspace_bytes >= L.total && aligned16(workspace),
                "the dense forward needs a 16-byte aligned %zu-byte workspace, got %zu", L.total, workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);

@@ -95,10 +95,13 @@ def _check_inputs(q, k, v, kv_positions, bias, causal, layout):
 # Forward: "auto" picks the masked dense pass (gw_sparse_attn_fwd_dense) when a query
 # selects at least 1 / DENSE_MAX_RATIO of the keys (and, with attn_sum, K <=
 # DENSE_ATTN_SUM_MAX_K), "dense" / "gather" force one path (tests and measurements). The
-# dense pass costs ~ T·S, the gather ~ T·K: on MI355X they break even near S = 117·K.
+# dense pass costs ~ T·S, the gather ~ T·K: on MI355X they break even near S = 124·K.
+# The dense kernel's 32-bit load offsets bound the K token stride and S (DENSE_MAX_*).
 FORWARD_PATH = "auto"
 DENSE_MAX_RATIO = 96
 DENSE_ATTN_SUM_MAX_K = 1024
+DENSE_MAX_K_ROW_STRIDE = 1 << 23
+DENSE_MAX_S = (1 << 25) - 64
 
 
 def _use_dense(seqlen_k: int, num_kv: int, nheads: int, d: int, softmax_scale: float = 1.0) -> bool:
@@ -171,7 +174,9 @@ def _flash_attn_forward(
         code = _lib.GW_DTYPE_FP32 if kl_logits.dtype == torch.float32 else _lib.dtype_code(kl_logits.dtype)
         kl_args = (kl_logits.data_ptr(), code, kl_logits.stride(0), kl_logits.stride(1), float(kl_eps),
                    kl_row_loss.data_ptr())
-    if _use_dense(seqlen_k, num_kv, nheads, d, softmax_scale) and (attn_sum is None or num_kv <= DENSE_ATTN_SUM_MAX_K):
+    dense_fits = _bthd_strides(k, q_layout)[1] < DENSE_MAX_K_ROW_STRIDE and seqlen_k <= DENSE_MAX_S
+    if (_use_dense(seqlen_k, num_kv, nheads, d, softmax_scale) and dense_fits
+            and (attn_sum is None or num_kv <= DENSE_ATTN_SUM_MAX_K)):
         dense_bytes = int(lib.gw_sparse_attn_fwd_dense_workspace_size(batch, seqlen_q, seqlen_k, nheads, d, num_kv,
                                                                       int(attn_sum is not None)))
         dws = torch.empty(max(dense_bytes, 1), device=q.device, dtype=torch.uint8)
