@@ -404,15 +404,16 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
           pb[ks] = make_uint4(pack_f16(pv[8 * ks], pv[8 * ks + 1]), pack_f16(pv[8 * ks + 2], pv[8 * ks + 3]),
                               pack_f16(pv[8 * ks + 4], pv[8 * ks + 5]), pack_f16(pv[8 * ks + 6], pv[8 * ks + 7]));
         constexpr uint32_t kOnes = 0x3C003C00u;  // (1.0, 1.0) in fp16
-        float t = 0.f;
+        // Two independent accumulation chains (a wave has few others to hide their latency).
+        float t[2] = {0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          t = dot2(FP16{}, pb[ks].x, kOnes, t);
-          t = dot2(FP16{}, pb[ks].y, kOnes, t);
-          t = dot2(FP16{}, pb[ks].z, kOnes, t);
-          t = dot2(FP16{}, pb[ks].w, kOnes, t);
+          t[ks] = dot2(FP16{}, pb[ks].x, kOnes, t[ks]);
+          t[ks] = dot2(FP16{}, pb[ks].y, kOnes, t[ks]);
+          t[ks] = dot2(FP16{}, pb[ks].z, kOnes, t[ks]);
+          t[ks] = dot2(FP16{}, pb[ks].w, kOnes, t[ks]);
         }
-        return t;
+        return t[0] + t[1];
       };
       ls = weights(-m[a]);
       if (__builtin_amdgcn_ballot_w64(!(ls <= kSumCap)) != 0ull) {
