@@ -376,8 +376,8 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
     else tau_l = p.tau[grow];
   }
   // FILTER: the list of this lane's query for this split is list grow * nsplit + split,
-  // kSubTotal / nsplit slots long; the two lanes of a query (l and l ^ 32) append to it in
-  // step, so both keep the same byte cursor woff. The wave's 32 rows have consecutive list
+  // kSubTotal / nsplit slots long; the two lanes of a query (l and l ^ 32) append to it
+  // stage by stage, so both keep the same byte cursor woff. The wave's 32 rows have consecutive list
   // blocks, so a list is addressed as a byte offset (< 2 MB) from the wave's first list.
   const int stride = SAMPLE ? 0 : kSubTotal / nsplit;
   int2* const lbase = SAMPLE ? nullptr : p.cand + (((int64_t)b * T + q0) * nsplit + split) * stride;
@@ -573,11 +573,18 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
     pmask |= tb << (16 * t);
   };
   // Element idx = 16 t + r of the stage holds key 32 t + 8 (r / 4) + r % 4 + 4 half past the
-  // stage's first key: idx + (idx & ~3) + 4 half. Two entries per round, so that their LDS
-  // reads share one wait.
+  // stage's first key: idx + (idx & ~3) + 4 half. The stage's entries of a query follow its
+  // list in one block: lane l (half 0) first, then lane l ^ 32, each in element order, so a
+  // lane needs only its partner's count (one lane swap per stage) and writes its own entries
+  // to consecutive slots; two per round, so that their LDS reads share one wait.
   auto flush = [&]() {
     uint32_t mm = pmask;
     pmask = 0;
+    const uint32_t cnt = (uint32_t)__builtin_popcount(mm);
+    const auto sw = __builtin_amdgcn_permlane32_swap(cnt, cnt, false, false);
+    const uint32_t other = sw[0] ^ sw[1] ^ cnt;  // the partner lane's count
+    uint32_t pos = woff + (half ? 8u * other : 0u);
+    woff += 8u * (cnt + other);
     while (__ballot(mm != 0u) != 0ull) {
       uint32_t idx[2], has[2];
 #pragma unroll
@@ -591,13 +598,10 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
       for (int u = 0; u < 2; ++u) sv[u] = stg[idx[u]];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const auto sw = __builtin_amdgcn_permlane32_swap(has[u], has[u], false, false);
-        const uint32_t other = sw[0] ^ sw[1] ^ has[u];  // the partner lane's flag
-        const uint32_t pos = woff + ((half && other) ? 8u : 0u);
         if (has[u] && pos < wend)
           *reinterpret_cast<int2*>(lbytes + pos) =
               make_int2(__float_as_int(sv[u]), kb_pend + (int)(idx[u] + (idx[u] & ~3u)));
-        woff += 8u * (has[u] + other);
+        pos += 8u * has[u];
       }
     }
   };
