@@ -576,7 +576,7 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
   // stage's first key: idx + (idx & ~3) + 4 half. The stage's entries of a query follow its
   // list in one block: lane l (half 0) first, then lane l ^ 32, each in element order, so a
   // lane needs only its partner's count (one lane swap per stage) and writes its own entries
-  // to consecutive slots; two per round, so that their LDS reads share one wait.
+  // to consecutive slots; four per round, so that their LDS reads share one wait.
   auto flush = [&]() {
     uint32_t mm = pmask;
     pmask = 0;
@@ -586,18 +586,18 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
     uint32_t pos = woff + (half ? 8u * other : 0u);
     woff += 8u * (cnt + other);
     while (__ballot(mm != 0u) != 0ull) {
-      uint32_t idx[2], has[2];
+      uint32_t idx[4], has[4];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
+      for (int u = 0; u < 4; ++u) {
         has[u] = mm != 0u ? 1u : 0u;
         idx[u] = has[u] ? (uint32_t)__builtin_ctz(mm) : 0u;
         mm &= mm - 1u;
       }
-      float sv[2];
+      float sv[4];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) sv[u] = stg[idx[u]];
+      for (int u = 0; u < 4; ++u) sv[u] = stg[idx[u]];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
+      for (int u = 0; u < 4; ++u) {
         if (has[u] && pos < wend)
           *reinterpret_cast<int2*>(lbytes + pos) =
               make_int2(__float_as_int(sv[u]), kb_pend + (int)(idx[u] + (idx[u] & ~3u)));
