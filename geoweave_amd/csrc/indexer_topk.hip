@@ -607,6 +607,7 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
   };
 
   // One stage on buffer (kt, wt), prefetching the next stage into (kn, wn).
+  const bool OFFSET_GROUP = wave >= NW / 2;
   auto stage = [&](const uint8_t* kt, const float* wt, uint8_t* kn, float* wn) {
     const int kb = st * BN;
     const bool more = st + nsplit < p.nstages;
@@ -614,12 +615,34 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
     // The previous stage's candidates are written here, after its stage-end vmcnt(0) +
     // barrier: vmcnt counts stores as well as the direct LDS loads it waits for, so the
     // stores are followed by a stage of MFMA work before that wait.
-    if constexpr (!SAMPLE) flush();
+    if constexpr (SAMPLE) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
+      for (int t = 0; t < NT; ++t) {
+        float s0[16];
+        tile_scores(s0, kb, t, kt, wt);
+      }
+    } else if (OFFSET_GROUP) {
+      // The other wave of each SIMD starts with the first tile's products and writes the
+      // previous stage's candidates after them, so the two waves of a SIMD leave the barrier
+      // out of phase (one on the matrix cores while the other issues the writes).
       float s0[16];
-      tile_scores(s0, kb, t, kt, wt);
-      if constexpr (!SAMPLE) mark(s0, t, kb);
+      tile_scores(s0, kb, 0, kt, wt);
+      flush();
+      mark(s0, 0, kb);
+#pragma unroll
+      for (int t = 1; t < NT; ++t) {
+        float s1[16];
+        tile_scores(s1, kb, t, kt, wt);
+        mark(s1, t, kb);
+      }
+    } else {
+      flush();
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        float s0[16];
+        tile_scores(s0, kb, t, kt, wt);
+        mark(s0, t, kb);
+      }
     }
     kb_pend = kb + 4 * half;
 
