@@ -205,5 +205,81 @@ __global__ __launch_bounds__(256) void dense_mask_kernel(const int32_t* __restri
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// The forward's selection words in one pass over the positions: a workgroup builds the words
+// of 16 queries over every key (half hq of 32-query block qb) in LDS, [sub-tile][17 words],
+// so each position is read once. Same words, bit order and repeat detection as
+// dense_mask_kernel; the repeat flag of half hq goes to flags[b][qb][hq] (two entries per
+// block). Holds S_pad / 32 <= kMaskRowsMaxSub sub-tiles (dynamic LDS: 68 bytes each).
+// ---------------------------------------------------------------------------------------
+constexpr int kMaskRowsQ = 16;              // queries per workgroup
+constexpr int kMaskRowsMaxSub = 2048;       // sub-tiles held in LDS (139 KB)
+constexpr int kMaskRowsThreads = 512;
+
+__global__ __launch_bounds__(kMaskRowsThreads) void dense_mask_rows_kernel(
+    const int32_t* __restrict__ pos, int64_t psb, int64_t pst, int T, int S, int Spad, int K, int nqb, int tpad,
+    int vec, int vmax_words, uint32_t* __restrict__ mask, int* __restrict__ flags, uint32_t* __restrict__ vmax,
+    int* __restrict__ bad, int bias_order) {
+  extern __shared__ uint32_t words[];  // [sub-tile][kMaskRowsQ + 1]
+  __shared__ int dup_any;
+  constexpr int RW = kMaskRowsQ + 1;
+  const int qb = blockIdx.x >> 1, hq = blockIdx.x & 1, b = blockIdx.y;
+  const int q0 = qb * 32 + hq * kMaskRowsQ;
+  const int nkt = Spad >> 5;
+  for (int i = threadIdx.x; i < nkt * RW; i += kMaskRowsThreads) words[i] = 0u;
+  if (blockIdx.x == 0 && vmax != nullptr) {
+    for (int i = threadIdx.x; i < vmax_words; i += kMaskRowsThreads) vmax[(int64_t)b * vmax_words + i] = 0u;
+    if (threadIdx.x == 0) bad[b] = 0;
+  }
+  if (threadIdx.x == 0) dup_any = 0;
+  __syncthreads();
+  bool dup = false;
+  const int rows = min(kMaskRowsQ, T - q0);  // <= 0 for the padding queries
+  const int32_t* pblk = pos + b * psb + (int64_t)min(q0, T - 1) * pst;
+  // Positions outside [0, S) (negative padding included) wrap to large unsigned values.
+  auto put = [&](int32_t sidx, int i) {
+    const uint32_t sl = (uint32_t)sidx;
+    if (sl < (uint32_t)S) {
+      const uint32_t kk = sl & 31u;
+      const uint32_t bit = 1u << (bias_order ? 8u * (kk & 3u) + 7u - (kk >> 3) - 4u * ((kk >> 2) & 1u) : kk);
+      dup |= (atomicOr(&words[(sl >> 5) * RW + i], bit) & bit) != 0u;
+    }
+  };
+  if (vec) {
+    const int n4 = K >> 2;
+    for (int j4 = threadIdx.x; j4 < n4; j4 += kMaskRowsThreads) {
+#pragma unroll 1
+      for (int r0 = 0; r0 < rows; r0 += 8) {
+        int4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          v[u] = r0 + u < rows ? reinterpret_cast<const int4*>(pblk + (int64_t)(r0 + u) * pst)[j4] : make_int4(-1, -1, -1, -1);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          put(v[u].x, r0 + u);
+          put(v[u].y, r0 + u);
+          put(v[u].z, r0 + u);
+          put(v[u].w, r0 + u);
+        }
+      }
+    }
+  } else {
+#pragma unroll 1
+    for (int i = 0; i < rows; ++i) {
+      const int32_t* prow = pblk + (int64_t)i * pst;
+      for (int j = threadIdx.x; j < K; j += kMaskRowsThreads) put(prow[j], i);
+    }
+  }
+  if (dup) dup_any = 1;
+  __syncthreads();
+  uint32_t* out = mask + (int64_t)b * nkt * tpad + q0;
+  for (int idx = threadIdx.x; idx < nkt * kMaskRowsQ; idx += kMaskRowsThreads) {
+    const int kt = idx / kMaskRowsQ, i = idx % kMaskRowsQ;
+    const uint32_t wv = words[kt * RW + i];
+    out[(int64_t)kt * tpad + i] = bias_order ? ~wv : wv;
+  }
+  if (threadIdx.x == 0 && qb < nqb) flags[((int64_t)b * nqb + qb) * 2 + hq] = dup_any;
+}
+
 }  // namespace
 }  // namespace gw

@@ -663,15 +663,19 @@ __global__ __launch_bounds__(256) void dense_attn_sum_kernel(const AttnSumParams
 struct DenseLayout {
   size_t mask, flags, bad, vmax, vt, sws, total;
   int nqb, nqb_pad, nchunk, spad;
+  bool rows_pass;  // selection words built by dense_mask_rows_kernel
 };
 
 DenseLayout dense_layout(int64_t B, int64_t T, int64_t S, int64_t H, int64_t K, bool attn) {
   DenseLayout L;
   L.nqb = (int)((T + 31) / 32);
   L.nqb_pad = (L.nqb + kQBW - 1) / kQBW * kQBW;
-  L.nchunk = (int)((S + kMaskChunk - 1) / kMaskChunk);
-  if (L.nchunk < 1) L.nchunk = 1;
   L.spad = (int)((S + 63) / 64 * 64);
+  // One pass over the positions (two 16-query halves per block) when the sub-tile words of
+  // 16 queries fit the LDS, else chunks of kMaskChunk keys.
+  L.rows_pass = L.spad / 32 <= kMaskRowsMaxSub;
+  L.nchunk = L.rows_pass ? 2 : (int)((S + kMaskChunk - 1) / kMaskChunk);
+  if (L.nchunk < 1) L.nchunk = 1;
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
   size_t o = 0;
   L.mask = o;
@@ -785,10 +789,18 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
                      (reinterpret_cast<uintptr_t>(kv_pos) & 15) == 0)
                         ? 1
                         : 0;
-    hipLaunchKernelGGL(dense_mask_kernel, dim3(L.nchunk, L.nqb_pad, (unsigned)B), dim3(256), 0, st, kv_pos,
-                       pos_stride_b, pos_stride_t, (int)T, (int)S, L.spad, (int)K, L.nqb, L.nqb_pad * 32, L.nchunk,
-                       vec, (int)(H * 64), mask, flags, vmax, bad, nullptr, nullptr, want_attn ? 0 : 1);
-    GW_HIP_LAUNCH_CHECK("dense_mask_kernel launch");
+    if (L.rows_pass) {
+      const size_t lds = (size_t)(L.spad / 32) * (kMaskRowsQ + 1) * 4;
+      hipLaunchKernelGGL(dense_mask_rows_kernel, dim3((unsigned)(L.nqb_pad * 2), (unsigned)B), dim3(kMaskRowsThreads),
+                         lds, st, kv_pos, pos_stride_b, pos_stride_t, (int)T, (int)S, L.spad, (int)K, L.nqb,
+                         L.nqb_pad * 32, vec, (int)(H * 64), mask, flags, vmax, bad, want_attn ? 0 : 1);
+      GW_HIP_LAUNCH_CHECK("dense_mask_rows_kernel launch");
+    } else {
+      hipLaunchKernelGGL(dense_mask_kernel, dim3(L.nchunk, L.nqb_pad, (unsigned)B), dim3(256), 0, st, kv_pos,
+                         pos_stride_b, pos_stride_t, (int)T, (int)S, L.spad, (int)K, L.nqb, L.nqb_pad * 32, L.nchunk,
+                         vec, (int)(H * 64), mask, flags, vmax, bad, nullptr, nullptr, want_attn ? 0 : 1);
+      GW_HIP_LAUNCH_CHECK("dense_mask_kernel launch");
+    }
   }
   hipLaunchKernelGGL(dense_vmax_kernel, dim3((unsigned)((S + kVmaxKeys - 1) / kVmaxKeys), (unsigned)H, (unsigned)B),
                      dim3(256), 0, st, static_cast<const uint16_t*>(v), v_strides[0], v_strides[1], v_strides[2],
