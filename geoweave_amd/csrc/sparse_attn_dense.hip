@@ -282,11 +282,12 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
   const uint32_t vo0 = ((uint32_t)srow * (uint32_t)p.Spad + (uint32_t)sc * 8u) * 2u;
   const uint32_t vo1 = vo0 + (uint32_t)p.Spad * 64u;  // row srow + 32
   auto gload = [&](int k0, uint4& ka, uint4& kb, uint4& va, uint4& vb) {
-    // Rows past the end read row S - 1 (their keys are never selected).
-    const int lim = p.S - 1 - k0;
-    const char* kt = kbase + (int64_t)k0 * kss_b;
-    ka = buffer_load16(kt, __umul24((uint32_t)min(srow, lim), kss_b) + kcol);
-    kb = buffer_load16(kt, __umul24((uint32_t)min(srow + 32, lim), kss_b) + kcol);
+    // Rows past the end read row S - 1 (their keys are never selected), taken from a base row
+    // at most S - 1 so that the lane offsets stay in [0, 63] rows wherever the tile starts.
+    const int r_base = min(k0, p.S - 1);
+    const char* kt = kbase + (int64_t)r_base * kss_b;
+    ka = buffer_load16(kt, __umul24((uint32_t)(min(k0 + srow, p.S - 1) - r_base), kss_b) + kcol);
+    kb = buffer_load16(kt, __umul24((uint32_t)(min(k0 + srow + 32, p.S - 1) - r_base), kss_b) + kcol);
     const char* vtile0 = vbase + (int64_t)k0 * 2;
     va = buffer_load16(vtile0, vo0);
     vb = buffer_load16(vtile0, vo1);

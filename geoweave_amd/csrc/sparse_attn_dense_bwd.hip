@@ -43,6 +43,8 @@ namespace {
 // ---------------------------------------------------------------------------------------
 // Clears the route flags and the |dO|, |V| maxima before the other kernels set them.
 // ---------------------------------------------------------------------------------------
+constexpr int64_t kDenseBwdMaxRowStride = 1ll << 23;
+
 __global__ __launch_bounds__(256) void dense_bwd_clear_kernel(int* __restrict__ route, int B,
                                                               uint32_t* __restrict__ amax, int n_amax) {
   const int i = blockIdx.x * 256 + threadIdx.x;
@@ -209,7 +211,7 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dq_kernel(const DenseBw
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: addresses built from it stay scalar
   const int h = blockIdx.x % p.H;
   const int qb0 = (blockIdx.x / p.H) * kBQPB + wave * kBQPW;
   const int b = blockIdx.y;
@@ -251,20 +253,34 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dq_kernel(const DenseBw
   // (rows srow and srow + 32).
   const int srow = tid >> 3, sc = tid & 7;
   const int soff = srow * 128 + ((sc ^ swz(srow)) << 4);  // swz(srow + 32) = swz(srow)
-  const uint16_t* ksrc = p.k + b * p.ksb + (int64_t)h * p.ksh + sc * 8;
-  const uint16_t* vsrc = p.v + b * p.vsb + (int64_t)h * p.vsh + sc * 8;
-  const uint16_t* tsrc = p.kt + (((int64_t)b * p.H + h) * 64 + srow) * p.spad + sc * 8;
+  // A tile's base addresses are uniform (scalar registers); a lane adds a 32-bit byte offset
+  // (the host keeps the K and V token strides below 2^24 bytes and 64 rows of K^T below 2^32
+  // bytes).
+  const char* kbase = uniform_ptr(reinterpret_cast<const char*>(p.k + b * p.ksb + (int64_t)h * p.ksh));
+  const char* vbase = uniform_ptr(reinterpret_cast<const char*>(p.v + b * p.vsb + (int64_t)h * p.vsh));
+  const char* tbase = uniform_ptr(reinterpret_cast<const char*>(p.kt + ((int64_t)b * p.H + h) * 64 * p.spad));
+  const uint32_t kss_b = (uint32_t)p.kss * 2u, vss_b = (uint32_t)p.vss * 2u;
+  const uint32_t ccol = (uint32_t)sc * 16u;
+  const uint32_t to0 = ((uint32_t)srow * (uint32_t)p.spad + (uint32_t)sc * 8u) * 2u;
+  const uint32_t to1 = to0 + (uint32_t)p.spad * 64u;  // row srow + 32
   // Named staging registers: an array passed into these lambdas would live in scratch memory.
   uint4 g0, g1, g2, g3, g4, g5;
   auto gload = [&](int k0) {
-    const int64_t key = min(k0 + srow, p.S - 1);
-    const int64_t key2 = min(k0 + srow + 32, p.S - 1);
-    g0 = *reinterpret_cast<const uint4*>(ksrc + key * p.kss);
-    g1 = *reinterpret_cast<const uint4*>(ksrc + key2 * p.kss);
-    g2 = *reinterpret_cast<const uint4*>(vsrc + key * p.vss);
-    g3 = *reinterpret_cast<const uint4*>(vsrc + key2 * p.vss);
-    g4 = *reinterpret_cast<const uint4*>(tsrc + k0);
-    g5 = *reinterpret_cast<const uint4*>(tsrc + (int64_t)32 * p.spad + k0);
+    // Rows past the end read row S - 1 (their keys are never selected). The tile may start
+    // past it (S_pad is a whole number of key blocks): rows are taken from a base row at most
+    // S - 1, so the lane offsets stay in [0, 63] rows.
+    const int r_base = min(k0, p.S - 1);
+    const uint32_t r0 = (uint32_t)(min(k0 + srow, p.S - 1) - r_base);
+    const uint32_t r1 = (uint32_t)(min(k0 + srow + 32, p.S - 1) - r_base);
+    const char* kt = kbase + (int64_t)r_base * kss_b;
+    const char* vt = vbase + (int64_t)r_base * vss_b;
+    const char* tt = tbase + (int64_t)k0 * 2;
+    g0 = buffer_load16(kt, __umul24(r0, kss_b) + ccol);
+    g1 = buffer_load16(kt, __umul24(r1, kss_b) + ccol);
+    g2 = buffer_load16(vt, __umul24(r0, vss_b) + ccol);
+    g3 = buffer_load16(vt, __umul24(r1, vss_b) + ccol);
+    g4 = buffer_load16(tt, to0);
+    g5 = buffer_load16(tt, to1);
   };
   auto lstore = [&](int bf) {
     *reinterpret_cast<uint4*>(&ktile[bf][soff]) = g0;
@@ -280,8 +296,11 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dq_kernel(const DenseBw
   auto koff = [&](int st, int ks) { return col * 128 + st * 4096 + (((2 * ks + half) ^ fc) << 4); };
   auto toff = [&](int db, int st, int ks) { return col * 128 + db * 4096 + (((4 * st + 2 * ks + half) ^ fc) << 4); };
   const int nsub = p.spad >> 5;
-  const uint32_t* mcol = p.mask + (int64_t)b * nsub * p.tpad + tq[0];  // block qb0 + 1: + 32
-  auto mword = [&](int j, int a) { return mcol[(int64_t)min(j, nsub - 1) * p.tpad + 32 * a]; };
+  const char* mblk = uniform_ptr(reinterpret_cast<const char*>(p.mask + (int64_t)b * nsub * p.tpad + qb0 * 32));
+  const int64_t mrow_b = (int64_t)p.tpad * 4;  // bytes per sub-tile row of selection words
+  auto mword = [&](int j, int a) {
+    return buffer_load4(mblk + min(j, nsub - 1) * mrow_b, (uint32_t)(col + 32 * a) * 4u);
+  };
   const float ninf = -INFINITY;
 
   auto sub = [&](const uint8_t* kt, const uint8_t* vt, const uint8_t* ktt, int st, const uint32_t (&w)[kBQPW]) {
@@ -399,7 +418,7 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dkdv_kernel(const Dense
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: addresses built from it stay scalar
   const int h = blockIdx.x % p.H;
   const int kb = (blockIdx.x / p.H) * kBKPB + wave;
   const int b = blockIdx.y;
@@ -436,23 +455,41 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dkdv_kernel(const Dense
   // two queries each.
   const int srow = tid >> 3, sc = tid & 7;
   const int soff = srow * 128 + ((sc ^ swz(srow)) << 4);
-  const uint16_t* qsrc = p.q + b * p.qsb + (int64_t)h * p.qsh + sc * 8;
-  const uint16_t* dsrc = p.dout + b * p.dosb + (int64_t)h * p.dosh + sc * 8;
-  const int64_t tbase = (((int64_t)b * p.H + h) * 64 + srow) * p.tpad + sc * 8;
-  const float2* lsrc = p.ls + ((int64_t)b * p.H + h) * p.tpad + 2 * (tid & 31);
+  // A tile's base addresses are uniform (scalar registers); a lane adds a 32-bit byte offset
+  // (the host keeps the q and dO token strides below 2^24 bytes and 64 rows of Q^T below
+  // 2^32 bytes).
+  const char* qbase = uniform_ptr(reinterpret_cast<const char*>(p.q + b * p.qsb + (int64_t)h * p.qsh));
+  const char* dbase = uniform_ptr(reinterpret_cast<const char*>(p.dout + b * p.dosb + (int64_t)h * p.dosh));
+  const int64_t thead = ((int64_t)b * p.H + h) * 64 * p.tpad;
+  const char* qtbase = uniform_ptr(reinterpret_cast<const char*>(p.qt + thead));
+  const char* dtbase = uniform_ptr(reinterpret_cast<const char*>(p.dot + thead));
+  const char* lbase = uniform_ptr(reinterpret_cast<const char*>(p.ls + ((int64_t)b * p.H + h) * p.tpad));
+  const uint32_t qst_b = (uint32_t)p.qst * 2u, dst_b = (uint32_t)p.dost * 2u;
+  const uint32_t ccol = (uint32_t)sc * 16u;
+  const uint32_t to0 = ((uint32_t)srow * (uint32_t)p.tpad + (uint32_t)sc * 8u) * 2u;
+  const uint32_t to1 = to0 + (uint32_t)p.tpad * 64u;  // row srow + 32
+  const uint32_t lo = (uint32_t)(tid & 31) * 16u;     // two {lse2, delta} per thread
   uint4 g0, g1, g2, g3, g4, g5, g6, g7, g8;
   auto gload = [&](int t0) {
-    const int64_t t = min(t0 + srow, p.T - 1);
-    const int64_t t2 = min(t0 + srow + 32, p.T - 1);
-    g0 = *reinterpret_cast<const uint4*>(qsrc + t * p.qst);
-    g1 = *reinterpret_cast<const uint4*>(qsrc + t2 * p.qst);
-    g2 = *reinterpret_cast<const uint4*>(dsrc + t * p.dost);
-    g3 = *reinterpret_cast<const uint4*>(dsrc + t2 * p.dost);
-    g4 = *reinterpret_cast<const uint4*>(p.qt + tbase + t0);
-    g5 = *reinterpret_cast<const uint4*>(p.qt + tbase + (int64_t)32 * p.tpad + t0);
-    g6 = *reinterpret_cast<const uint4*>(p.dot + tbase + t0);
-    g7 = *reinterpret_cast<const uint4*>(p.dot + tbase + (int64_t)32 * p.tpad + t0);
-    if (tid < 32) g8 = *reinterpret_cast<const uint4*>(lsrc + t0);
+    // Rows past the end read row T - 1 (their queries never selected a key). The tile may
+    // start past it (T_pad is a whole number of query blocks): rows are taken from a base row
+    // at most T - 1, so the lane offsets stay in [0, 63] rows.
+    const int r_base = min(t0, p.T - 1);
+    const uint32_t r0 = (uint32_t)(min(t0 + srow, p.T - 1) - r_base);
+    const uint32_t r1 = (uint32_t)(min(t0 + srow + 32, p.T - 1) - r_base);
+    const char* qt = qbase + (int64_t)r_base * qst_b;
+    const char* dt = dbase + (int64_t)r_base * dst_b;
+    const char* qtt = qtbase + (int64_t)t0 * 2;
+    const char* dtt = dtbase + (int64_t)t0 * 2;
+    g0 = buffer_load16(qt, __umul24(r0, qst_b) + ccol);
+    g1 = buffer_load16(qt, __umul24(r1, qst_b) + ccol);
+    g2 = buffer_load16(dt, __umul24(r0, dst_b) + ccol);
+    g3 = buffer_load16(dt, __umul24(r1, dst_b) + ccol);
+    g4 = buffer_load16(qtt, to0);
+    g5 = buffer_load16(qtt, to1);
+    g6 = buffer_load16(dtt, to0);
+    g7 = buffer_load16(dtt, to1);
+    if (tid < 32) g8 = buffer_load16(lbase + (int64_t)t0 * 8, lo);
   };
   auto lstore = [&](int bf) {
     *reinterpret_cast<uint4*>(&qtile[bf][soff]) = g0;
@@ -470,8 +507,9 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dkdv_kernel(const Dense
   auto toff = [&](int db, int st, int ks) { return col * 128 + db * 4096 + (((4 * st + 2 * ks + half) ^ fc) << 4); };
   // Key-major selection words of the lane's key, one per 32-query block.
   const int nqbp = p.tpad >> 5;
-  const uint32_t* mrow = p.maskT + (int64_t)b * nqbp * p.spad + key;
-  auto mword = [&](int j) { return mrow[(int64_t)min(j, nqbp - 1) * p.spad]; };
+  const char* mblk = uniform_ptr(reinterpret_cast<const char*>(p.maskT + (int64_t)b * nqbp * p.spad + kb * 32));
+  const int64_t mrow_b = (int64_t)p.spad * 4;  // bytes per query-block row of selection words
+  auto mword = [&](int j) { return buffer_load4(mblk + min(j, nqbp - 1) * mrow_b, (uint32_t)col * 4u); };
   const float ninf = -INFINITY;
 
   auto sub = [&](const uint8_t* qtl, const uint8_t* dtl, const uint8_t* qttl, const uint8_t* dttl,
@@ -640,6 +678,14 @@ extern "C" int gw_sparse_attn_bwd_dense(int dtype, const void* q, const int64_t*
   GW_CHECK_ARG((int64_t)(L.nqb_pad / kBQPB) * H < (1ll << 31) && (int64_t)(L.spad / (32 * kBKPB)) * H < (1ll << 31) &&
                    L.nqb_pad <= 65535 && H <= 65535,
                "too many query or key blocks");
+  // Limits of the kernels' 32-bit lane offsets: token strides of q, k, v, dO below 2^23
+  // elements (a 24-bit multiply), 64 rows of the transposed operands below 2^32 bytes.
+  if (q_strides[1] >= kDenseBwdMaxRowStride || k_strides[1] >= kDenseBwdMaxRowStride ||
+      v_strides[1] >= kDenseBwdMaxRowStride || do_strides[1] >= kDenseBwdMaxRowStride ||
+      (int64_t)L.spad * 128 >= (1ll << 32) || (int64_t)L.tpad * 128 >= (1ll << 32))
+    return set_error(GW_ERR_UNSUPPORTED,
+                     "the dense backward needs token strides below %lld elements and T, S <= %lld",
+                     (long long)kDenseBwdMaxRowStride, (long long)((1ll << 25) - 64));
   GW_CHECK_ARG(workspace != nullptr && workspace_bytes >= L.total && aligned16(workspace),
                "the dense backward needs a 16-byte aligned %zu-byte workspace, got %zu", L.total, workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);

@@ -25,6 +25,9 @@ from .. import _csr, _lib
 # the dense passes whenever they can run at all, "csr" the CSR path (tests, measurements).
 BACKWARD_PATH = "auto"
 DENSE_MAX_RATIO = 96
+# The dense kernels' 32-bit load offsets bound the token strides and T, S (DENSE_MAX_*).
+DENSE_MAX_ROW_STRIDE = 1 << 23
+DENSE_MAX_LEN = (1 << 25) - 64
 # The path the last call took ("dense" or "csr"), for tests.
 last_path = None
 
@@ -68,7 +71,8 @@ def sparse_attn_backward(do, q, k, v, kv_positions, o, lse, dattn_sum, softmax_s
     lib = _lib.load()
     global last_path
     dense_ok = (d == 64 and dattn_sum is None and 0.0 < float(softmax_scale) < float("inf")
-                and BACKWARD_PATH != "csr")
+                and BACKWARD_PATH != "csr" and seqlen_q <= DENSE_MAX_LEN and seqlen_k <= DENSE_MAX_LEN
+                and all(_strides(x, q_layout)[1] < DENSE_MAX_ROW_STRIDE for x in (q, k, v, do)))
     if dense_ok and (BACKWARD_PATH == "dense" or seqlen_k <= DENSE_MAX_RATIO * num_kv):
         ws_bytes = int(lib.gw_sparse_attn_bwd_dense_workspace_size(batch, seqlen_q, seqlen_k, nheads, d, num_kv))
         ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
