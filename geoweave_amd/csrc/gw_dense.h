@@ -108,10 +108,11 @@ __device__ __forceinline__ uint32_t lane_bit_transpose32(uint32_t x, int lane) {
 // is flagged (flags[b][qb][chunk]; dup_b[b] = 1 too when dup_b is given). Positions are read
 // 8 rows at a time (16 bytes per lane when the table allows), so the loads of a group are in
 // flight together. With maskT, the same bits key-major as well: maskT[b][qb][s] has bit i set
-// when query 32 qb + i selected key s (s < S_pad). With bias_order the query-major words are
-// stored for the plain forward's bias instead: key 8 g + 4 h + j (g, j < 4, h < 2) at bit
-// 8 j + 7 - g - 4 h, and inverted (a set bit = not selected), so that shifting the word left
-// by g + 4 h puts the keys of accumulator group g of lane half h at the sign bits of the four
+// when query 32 qb + i selected key s (s < S_pad). With bias_order the words are stored for
+// the kernels' selection bias instead: in a query-major word key 8 g + 4 h + j (g, j < 4,
+// h < 2) sits at bit beta = 8 j + 7 - g - 4 h, in a key-major word query 8 g + 4 h + j does,
+// and both are inverted (a set bit = not selected), so that shifting a word left by g + 4 h
+// puts the entries of accumulator group g of lane half h at the sign bits of the four
 // bytes. The first workgroup of each batch element clears vmax_words words of vmax and bad[b]
 // (for the forward's dense_vmax_kernel), when given.
 // ---------------------------------------------------------------------------------------
@@ -189,14 +190,19 @@ __global__ __launch_bounds__(256) void dense_mask_kernel(const int32_t* __restri
   }
   if (maskT != nullptr) {
     // Two sub-tiles per wave at a time, one per half-wave: lane i reads query i's word and
-    // after the transpose holds key 32 kt + i's word over the block's 32 queries.
+    // after the transpose holds key 32 kt + i's word over the block's 32 queries. With
+    // bias_order the LDS words hold key kk at bit beta(kk) (the permutation above): lane i
+    // then reads query beta^-1(i)'s word, so that after the transpose lane i holds key
+    // beta^-1(i)'s word with query q at bit beta(q), and stores it inverted at that key.
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int li = lane & 31;
+    const int pi = bias_order ? 8 * ((7 - (li & 7)) & 3) + 4 * ((7 - (li & 7)) >> 2) + (li >> 3) : li;
     uint32_t* outT = maskT + ((int64_t)b * (tpad >> 5) + qb) * Spad + c0;
     for (int kt2 = wave * 2; kt2 < nkt; kt2 += 8) {
       const int kt = kt2 + (lane >> 5);
-      uint32_t x = kt < nkt ? words[kt * 33 + (lane & 31)] : 0u;
+      uint32_t x = kt < nkt ? words[kt * 33 + pi] : 0u;
       x = lane_bit_transpose32(x, lane);
-      if (kt < nkt) outT[kt * 32 + (lane & 31)] = x;
+      if (kt < nkt) outT[kt * 32 + pi] = bias_order ? ~x : x;
     }
   }
   if (threadIdx.x == 0 && qb < nqb) {

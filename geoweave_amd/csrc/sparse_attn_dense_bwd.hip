@@ -301,19 +301,22 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dq_kernel(const DenseBw
   auto mword = [&](int j, int a) {
     return buffer_load4(mblk + min(j, nsub - 1) * mrow_b, (uint32_t)(col + 32 * a) * 4u);
   };
-  const float ninf = -INFINITY;
 
   auto sub = [&](const uint8_t* kt, const uint8_t* vt, const uint8_t* ktt, int st, const uint32_t (&w)[kBQPW]) {
     f32x16 s[kBQPW], dp[kBQPW];
 #pragma unroll
     for (int a = 0; a < kBQPW; ++a) {
-      // Entry r of this lane is bit 8(r/4) + r%4 of w >> 4 half.
-      const uint32_t own = w[a] >> (4 * half);
+      // Bias-order words: entry 4 g + j of this lane is the sign bit of byte j of w << (g + 4
+      // half), set when the key is not selected; a sign-extended byte select masks -inf (one
+      // instruction per entry).
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int sel = __builtin_amdgcn_sbfe((int)own, 8 * (r >> 2) + (r & 3), 1);  // 0 or -1
-        s[a][r] = select_bias(sel, ninf);
-        dp[a][r] = 0.f;
+      for (int g = 0; g < 4; ++g) {
+        const uint32_t sh = w[a] << (g + 4 * half);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          s[a][4 * g + j] = __uint_as_float((uint32_t)(int32_t)(int8_t)(sh >> (8 * j)) & 0xFF800000u);
+          dp[a][4 * g + j] = 0.f;
+        }
       }
     }
 #pragma unroll
@@ -510,18 +513,21 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dkdv_kernel(const Dense
   const char* mblk = uniform_ptr(reinterpret_cast<const char*>(p.maskT + (int64_t)b * nqbp * p.spad + kb * 32));
   const int64_t mrow_b = (int64_t)p.spad * 4;  // bytes per query-block row of selection words
   auto mword = [&](int j) { return buffer_load4(mblk + min(j, nqbp - 1) * mrow_b, (uint32_t)col * 4u); };
-  const float ninf = -INFINITY;
 
   auto sub = [&](const uint8_t* qtl, const uint8_t* dtl, const uint8_t* qttl, const uint8_t* dttl,
                  const float2* lsl, int st, uint32_t w) {
     f32x16 s, dp;
-    // Entry r of this lane is query 8(r/4) + 4 half + r%4 of the sub-tile: bit 8(r/4) + r%4 of w >> 4 half.
-    const uint32_t own = w >> (4 * half);
+    // Entry r = 4 g + j of this lane is query 8 g + 4 half + j of the sub-tile. Bias-order
+    // words: it is the sign bit of byte j of w << (g + 4 half), set when the query did not
+    // select the key; a sign-extended byte select masks -inf (one instruction per entry).
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int sel = __builtin_amdgcn_sbfe((int)own, 8 * (r >> 2) + (r & 3), 1);
-      s[r] = select_bias(sel, ninf);
-      dp[r] = 0.f;
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t sh = w << (g + 4 * half);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        s[4 * g + j] = __uint_as_float((uint32_t)(int32_t)(int8_t)(sh >> (8 * j)) & 0xFF800000u);
+        dp[4 * g + j] = 0.f;
+      }
     }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) s = mma(E{}, *reinterpret_cast<const uint4*>(qtl + koff(st, ks)), kbo[ks], s);
@@ -713,7 +719,7 @@ extern "C" int gw_sparse_attn_bwd_dense(int dtype, const void* q, const int64_t*
                         : 0;
     hipLaunchKernelGGL(dense_mask_kernel, dim3(L.nchunk, L.nqb_pad, (unsigned)B), dim3(256), 0, st, kv_pos,
                        pos_stride_b, pos_stride_t, (int)T, (int)S, L.spad, (int)K, L.nqb, L.tpad, L.nchunk, vec, 0,
-                       mask, flags, nullptr, nullptr, maskT, route, 0);
+                       mask, flags, nullptr, nullptr, maskT, route, 1);
     GW_HIP_LAUNCH_CHECK("dense_mask_kernel launch");
   }
   {
