@@ -225,9 +225,10 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
   __shared__ __align__(16) uint8_t ktile[2][8192];
   __shared__ __align__(16) uint8_t vtile[2][8192];
   __shared__ float vsc_s[64];
-  // attn_sum: per lane a row of 16 scores (rows of 20 floats: 16-byte stores of 8
-  // consecutive lanes touch distinct banks)
-  __shared__ __align__(16) float ascore[ATTN ? kDW : 1][ATTN ? 64 * 20 : 4];
+  // attn_sum: per lane a row of the 16 scores of each block (rows of 16 kQPW + 4 floats:
+  // 16-byte stores of 16 consecutive lanes touch distinct banks)
+  constexpr int kArow = 16 * kQPW + 4;
+  __shared__ __align__(16) float ascore[ATTN ? kDW : 1][ATTN ? 64 * kArow : 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -355,29 +356,44 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
       for (int a = 0; a < kQPW; ++a) s[a] = mma(E{}, ka[ks], qa[a][ks], s[a]);
     if constexpr (ATTN) {
       // Each selected entry's score (unscaled: dense_attn_sum_kernel applies the scale), at
-      // the slot of its key's rank. The lane's 16 scores go to its LDS row, and a loop over the
-      // lane's selected entries (most lanes have none or one per sub-tile) reads each back and
-      // stores it.
-      float* st_l = &ascore[wave][lane * 20];
+      // the slot of its key's rank. The lane's scores of both blocks go to its LDS row first
+      // (so both blocks' products complete before the loop), then one loop over the lane's
+      // selected entries of both blocks (most lanes have none or one per sub-tile) reads each
+      // back and stores it.
+      float* st_l = &ascore[wave][lane * kArow];
+#pragma unroll
+      for (int a = 0; a < kQPW; ++a)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<float4*>(st_l + 16 * a + 4 * g) =
+              make_float4(s[a][4 * g], s[a][4 * g + 1], s[a][4 * g + 2], s[a][4 * g + 3]);
+      // bit 16 a + r = entry r of block a (key 8(r/4) + 4 half + r%4)
+      uint32_t bits = 0;
 #pragma unroll
       for (int a = 0; a < kQPW; ++a) {
         const uint32_t own = w[a] >> (4 * half);
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<float4*>(st_l + 4 * g) = make_float4(s[a][4 * g], s[a][4 * g + 1], s[a][4 * g + 2], s[a][4 * g + 3]);
-        // bit r = entry r (key 8(r/4) + 4 half + r%4)
-        uint32_t bits = (own & 0xFu) | ((own >> 4) & 0xF0u) | ((own >> 8) & 0xF00u) | ((own >> 12) & 0xF000u);
-        while (__builtin_amdgcn_ballot_w64(bits != 0u) != 0ull) {
-          if (bits != 0u) {
-            const int r = __builtin_ctz(bits);
-            const int kk = 8 * (r >> 2) + 4 * half + (r & 3);
-            const uint32_t slot = rank_base[a] + __popc(w[a] & ((1u << kk) - 1u));
-            srow_ws[a][slot] = st_l[r];
-            bits &= bits - 1u;
-          }
-        }
-        rank_base[a] += __popc(w[a]);
+        bits |= ((own & 0xFu) | ((own >> 4) & 0xF0u) | ((own >> 8) & 0xF00u) | ((own >> 12) & 0xF000u)) << (16 * a);
       }
+      while (__builtin_amdgcn_ballot_w64(bits != 0u) != 0ull) {
+        if (bits != 0u) {
+          const int e = __builtin_ctz(bits);
+          const int a = e >> 4, r = e & 15;
+          const int kk = 8 * (r >> 2) + 4 * half + (r & 3);
+          uint32_t wa = w[0], rb = rank_base[0];
+          float* dst = srow_ws[0];
+#pragma unroll
+          for (int a2 = 1; a2 < kQPW; ++a2)
+            if (a == a2) {
+              wa = w[a2];
+              rb = rank_base[a2];
+              dst = srow_ws[a2];
+            }
+          dst[rb + __popc(wa & ((1u << kk) - 1u))] = st_l[e];
+          bits &= bits - 1u;
+        }
+      }
+#pragma unroll
+      for (int a = 0; a < kQPW; ++a) rank_base[a] += __popc(w[a]);
     }
     // Per block: the weights, then its P·V products, so that the second block's exp2 (which
     // co-executes with matrix products on this GPU, unlike fp32 VALU) overlaps the first
