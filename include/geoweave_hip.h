@@ -427,7 +427,9 @@ int gw_source_downsample_static_pack4(int dtype, const void* sub_w, int64_t B, i
  * sparse_index_flash_attn_inference_func :3138-3163; the fused KL as in gw_sparse_attn_fwd_kl);
  * it pays off when a query selects more than roughly 1 % of the keys.
  * Needs D = 64 and a positive softmax_scale, and K <= 1024 and H <= 64 when attn_sum is
- * asked for; otherwise GW_ERR_UNSUPPORTED (use gw_sparse_attn_fwd / gw_sparse_attn_fwd_kl).
+ * asked for; the kernels' 32-bit load offsets also need a K token stride below 2^23 elements
+ * and S <= 2^25 - 64. Otherwise GW_ERR_UNSUPPORTED (use gw_sparse_attn_fwd /
+ * gw_sparse_attn_fwd_kl).
  * The P·V product takes P in fp16 (the fp32 weights rounded to nearest, 11 significant bits)
  * against V in fp16 scaled per (head, d) column by an exact power of two; row sums and lse
  * come from the fp32 weights. A batch element whose K or V holds an inf or nan anywhere is
@@ -497,7 +499,9 @@ int gw_sparse_attn_fwd_dense_noalloc(int dtype,
  * presets train with: the attention mass is detached before the indexer loss (detach_input,
  * easyvolcap/official_vggt/layers/dsa_attention.py:4694-4695), so dattn_sum is absent or zero.
  * It pays off when a query selects more than roughly 1 % of the keys.
- * Needs D = 64 and a positive softmax_scale; otherwise GW_ERR_UNSUPPORTED.
+ * Needs D = 64, a positive softmax_scale, token strides of q, k, v and dO below 2^23
+ * elements and T, S <= 2^25 - 64 (the kernels' 32-bit load offsets); otherwise
+ * GW_ERR_UNSUPPORTED.
  * Arguments as for gw_sparse_attn_bwd (no dattn_sum, no CSR). route: device int array of B
  * entries, written by this call: route[b] = 1 for a batch element it left untouched
  * (dq/dk/dv of that element not written) because a row lists a position twice (the reference
