@@ -44,6 +44,14 @@ def _aligned(x: torch.Tensor) -> torch.Tensor:
     return x
 
 
+def _dense_fits(q, k, v, do, q_layout: str) -> bool:
+    """The dense backward's 32-bit load offsets: token strides and T, S within its limits."""
+    t_dim = 2 if q_layout == "bhtd" else 1
+    lens = (q.shape[t_dim], k.shape[t_dim])
+    return (all(n <= DENSE_MAX_LEN for n in lens)
+            and all(_strides(x, q_layout)[1] < DENSE_MAX_ROW_STRIDE for x in (q, k, v, do)))
+
+
 def sparse_attn_backward(do, q, k, v, kv_positions, o, lse, dattn_sum, softmax_scale, q_layout):
     """(dq, dk, dv) in the dtype and layout of (q, k, v)."""
     if q_layout == "bthd":
@@ -71,8 +79,7 @@ def sparse_attn_backward(do, q, k, v, kv_positions, o, lse, dattn_sum, softmax_s
     lib = _lib.load()
     global last_path
     dense_ok = (d == 64 and dattn_sum is None and 0.0 < float(softmax_scale) < float("inf")
-                and BACKWARD_PATH != "csr" and seqlen_q <= DENSE_MAX_LEN and seqlen_k <= DENSE_MAX_LEN
-                and all(_strides(x, q_layout)[1] < DENSE_MAX_ROW_STRIDE for x in (q, k, v, do)))
+                and BACKWARD_PATH != "csr" and _dense_fits(q, k, v, do, q_layout))
     if dense_ok and (BACKWARD_PATH == "dense" or seqlen_k <= DENSE_MAX_RATIO * num_kv):
         ws_bytes = int(lib.gw_sparse_attn_bwd_dense_workspace_size(batch, seqlen_q, seqlen_k, nheads, d, num_kv))
         ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)

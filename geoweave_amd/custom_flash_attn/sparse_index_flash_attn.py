@@ -110,6 +110,11 @@ def _use_dense(seqlen_k: int, num_kv: int, nheads: int, d: int, softmax_scale: f
     return FORWARD_PATH == "dense" or seqlen_k <= DENSE_MAX_RATIO * num_kv
 
 
+def _dense_fits(k: torch.Tensor, q_layout: str, seqlen_k: int) -> bool:
+    """The dense forward's 32-bit load offsets: K token stride and S within its limits."""
+    return _bthd_strides(k, q_layout)[1] < DENSE_MAX_K_ROW_STRIDE and seqlen_k <= DENSE_MAX_S
+
+
 def _prep(x: torch.Tensor) -> torch.Tensor:
     # Last dim contiguous and 16-byte aligned b/t/h strides (reference :3207-3209 makes
     # the last dim contiguous; the gfx950 kernel also needs 16-byte rows).
@@ -174,8 +179,7 @@ def _flash_attn_forward(
         code = _lib.GW_DTYPE_FP32 if kl_logits.dtype == torch.float32 else _lib.dtype_code(kl_logits.dtype)
         kl_args = (kl_logits.data_ptr(), code, kl_logits.stride(0), kl_logits.stride(1), float(kl_eps),
                    kl_row_loss.data_ptr())
-    dense_fits = _bthd_strides(k, q_layout)[1] < DENSE_MAX_K_ROW_STRIDE and seqlen_k <= DENSE_MAX_S
-    if (_use_dense(seqlen_k, num_kv, nheads, d, softmax_scale) and dense_fits
+    if (_use_dense(seqlen_k, num_kv, nheads, d, softmax_scale) and _dense_fits(k, q_layout, seqlen_k)
             and (attn_sum is None or num_kv <= DENSE_ATTN_SUM_MAX_K)):
         dense_bytes = int(lib.gw_sparse_attn_fwd_dense_workspace_size(batch, seqlen_q, seqlen_k, nheads, d, num_kv,
                                                                       int(attn_sum is not None)))
