@@ -709,6 +709,7 @@ __global__ __launch_bounds__(256) void indexer_tau_kernel(const float* samp, int
 // the LDS selection. No barriers: reductions are wave-wide.
 // ---------------------------------------------------------------------------------------
 constexpr int kSelRegs = 48;
+static_assert(kSelRegs % 8 == 0, "the select kernel moves register slots in chunks of 8");
 
 struct SelectParams {
   const int2* cand;
