@@ -151,18 +151,23 @@ def test_full_size_sampled_rows(gpu_device, views):
     torch.testing.assert_close(lse[:, rows], rl, atol=1e-4, rtol=1e-4)
 
 
-def test_repeated_position_in_an_upper_key_chunk(gpu_device):
-    # S > 16,384: the mask is built in several key chunks; a repeat in the last chunk flags
-    # its block like one in the first, and the gather kernel computes that block.
-    T, S, H, K = 80, 40000, 2, 256
+@pytest.mark.parametrize("S", [40000, 90000])
+def test_repeated_position_in_an_upper_key_range(gpu_device, S):
+    # The selection words come from one pass over the positions with 16 queries per workgroup
+    # (S = 40,000) or from key chunks of 16,384 (S = 90,000: more sub-tiles than the LDS of one
+    # pass holds); a repeat among the last keys flags its block like one among the first, and
+    # the gather kernel computes that block.
+    T, H, K = 80, 2, 256
     g = torch.Generator().manual_seed(31)
     q = torch.randn(1, T, H, 64, generator=g).bfloat16()
     k = torch.randn(1, S, H, 64, generator=g).bfloat16()
     v = torch.randn(1, S, H, 64, generator=g).bfloat16()
     pos = _distinct_positions(1, T, S, K, seed=32)
-    pos[0, 40, 7] = 39999
-    pos[0, 40, 8] = 39999      # block 1 (rows 32..63): repeat in chunk 2
-    pos[0, 75, :5] = 20000     # block 2: five copies in chunk 1
+    pos[0, 40, 7] = S - 1
+    pos[0, 40, 8] = S - 1      # block 1 (rows 32..63): repeat among the last keys
+    pos[0, 75, :5] = S // 2    # block 2: five copies
+    pos[0, 20, 3] = S - 2      # block 0: a key near the end
+    print(f"[dense] repeated positions S={S}", flush=True)
     o, lse = _run(q, k, v, pos)
     ro, _, rl = oatt.sparse_attention(q, k, v, pos)
     torch.testing.assert_close(o, ro, **TOL)
