@@ -226,13 +226,18 @@ __global__ __launch_bounds__(kMaskRowsThreads) void dense_mask_rows_kernel(
     const int32_t* __restrict__ pos, int64_t psb, int64_t pst, int T, int S, int Spad, int K, int nqb, int tpad,
     int vec, int vmax_words, uint32_t* __restrict__ mask, int* __restrict__ flags, uint32_t* __restrict__ vmax,
     int* __restrict__ bad, int bias_order) {
-  extern __shared__ uint32_t words[];  // [sub-tile][kMaskRowsQ + 1]
+  extern __shared__ __align__(16) uint32_t words[];  // [sub-tile][kMaskRowsQ + 1]
   __shared__ int dup_any;
   constexpr int RW = kMaskRowsQ + 1;
   const int qb = blockIdx.x >> 1, hq = blockIdx.x & 1, b = blockIdx.y;
   const int q0 = qb * 32 + hq * kMaskRowsQ;
   const int nkt = Spad >> 5;
-  for (int i = threadIdx.x; i < nkt * RW; i += kMaskRowsThreads) words[i] = 0u;
+  {
+    // Clear the words with 16-byte stores (the dynamic LDS array is 16-byte aligned).
+    const int n = nkt * RW, n4 = n >> 2;
+    for (int i = threadIdx.x; i < n4; i += kMaskRowsThreads) reinterpret_cast<uint4*>(words)[i] = make_uint4(0, 0, 0, 0);
+    if (threadIdx.x < (n & 3)) words[4 * n4 + threadIdx.x] = 0u;
+  }
   if (blockIdx.x == 0 && vmax != nullptr) {
     for (int i = threadIdx.x; i < vmax_words; i += kMaskRowsThreads) vmax[(int64_t)b * vmax_words + i] = 0u;
     if (threadIdx.x == 0) bad[b] = 0;
@@ -278,11 +283,15 @@ __global__ __launch_bounds__(kMaskRowsThreads) void dense_mask_rows_kernel(
   }
   if (dup) dup_any = 1;
   __syncthreads();
+  // Four consecutive words of a sub-tile row per thread, one 16-byte store (q0 and tpad are
+  // multiples of 16 and 32).
   uint32_t* out = mask + (int64_t)b * nkt * tpad + q0;
-  for (int idx = threadIdx.x; idx < nkt * kMaskRowsQ; idx += kMaskRowsThreads) {
-    const int kt = idx / kMaskRowsQ, i = idx % kMaskRowsQ;
-    const uint32_t wv = words[kt * RW + i];
-    out[(int64_t)kt * tpad + i] = bias_order ? ~wv : wv;
+  const uint32_t inv = bias_order ? 0xFFFFFFFFu : 0u;
+  for (int idx = threadIdx.x; idx < nkt * (kMaskRowsQ / 4); idx += kMaskRowsThreads) {
+    const int kt = idx / (kMaskRowsQ / 4), i = 4 * (idx % (kMaskRowsQ / 4));
+    const uint32_t* wr = &words[kt * RW + i];
+    *reinterpret_cast<uint4*>(out + (int64_t)kt * tpad + i) =
+        make_uint4(wr[0] ^ inv, wr[1] ^ inv, wr[2] ^ inv, wr[3] ^ inv);
   }
   if (threadIdx.x == 0 && qb < nqb) flags[((int64_t)b * nqb + qb) * 2 + hq] = dup_any;
 }
