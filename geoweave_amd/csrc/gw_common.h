@@ -154,4 +154,13 @@ __device__ __forceinline__ uint32_t buffer_load4(const char* base, uint32_t off)
   return __builtin_amdgcn_raw_buffer_load_b32(uniform_rsrc(base), (int)off, 0, 0);
 }
 
+// 16-byte buffer load straight into LDS (no registers): lane i of the wave writes the 16
+// bytes it reads at lds + 16 i, whatever its offset; lds must be the same in every lane of
+// the wave. The data is in LDS once vmcnt has drained (s_waitcnt vmcnt(0), then a barrier
+// for the other waves).
+__device__ __forceinline__ void buffer_load16_lds(const char* base, uint32_t off, void* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(uniform_rsrc(base), (__attribute__((address_space(3))) void*)lds, 16,
+                                           (int)off, 0, 0, 0);
+}
+
 }  // namespace gw

@@ -199,7 +199,7 @@ constexpr int kBKPB = kBW;          // 32-key blocks per workgroup in the dk/dv 
 // ---------------------------------------------------------------------------------------
 // dq pass: 4 waves per workgroup, each on two 32-query blocks of one head (the forward's
 // decomposition). Per 64-key tile the K rows, V rows and K^T (8 KB each for 64 keys of one
-// head) are staged through LDS, registers a tile ahead, one barrier per tile.
+// head) are loaded straight into LDS a tile ahead, one barrier per tile.
 // Per 32-key sub-tile and block: S^T = K Q^T from the selection bias, dP^T = V dO^T,
 // p = exp2(s log2(e) scale - lse2), ds = p (dp - delta), dQ^T += K^T dS^T.
 // ---------------------------------------------------------------------------------------
@@ -250,9 +250,12 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dq_kernel(const DenseBw
       for (int r = 0; r < 16; ++r) acc[a][db][r] = 0.f;
 
   // Tile staging: each thread moves two 16-byte chunks of each of K, V and K^T per tile
-  // (rows srow and srow + 32).
+  // (rows srow and srow + 32), loaded straight into LDS. Lane i of a wave writes the 16 bytes
+  // at the wave's 1 KB segment + 16 i = row srow, physical chunk sc, so it reads the chunk
+  // sc ^ swz(srow) that the swizzled layout keeps there (swz(srow + 32) = swz(srow)).
   const int srow = tid >> 3, sc = tid & 7;
-  const int soff = srow * 128 + ((sc ^ swz(srow)) << 4);  // swz(srow + 32) = swz(srow)
+  const int lc = sc ^ swz(srow);
+  const int wseg = wave * 1024;
   // A tile's base addresses are uniform (scalar registers); a lane adds a 32-bit byte offset
   // (the host keeps the K and V token strides below 2^24 bytes and 64 rows of K^T below 2^32
   // bytes).
@@ -260,12 +263,10 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dq_kernel(const DenseBw
   const char* vbase = uniform_ptr(reinterpret_cast<const char*>(p.v + b * p.vsb + (int64_t)h * p.vsh));
   const char* tbase = uniform_ptr(reinterpret_cast<const char*>(p.kt + ((int64_t)b * p.H + h) * 64 * p.spad));
   const uint32_t kss_b = (uint32_t)p.kss * 2u, vss_b = (uint32_t)p.vss * 2u;
-  const uint32_t ccol = (uint32_t)sc * 16u;
-  const uint32_t to0 = ((uint32_t)srow * (uint32_t)p.spad + (uint32_t)sc * 8u) * 2u;
+  const uint32_t ccol = (uint32_t)lc * 16u;
+  const uint32_t to0 = ((uint32_t)srow * (uint32_t)p.spad + (uint32_t)lc * 8u) * 2u;
   const uint32_t to1 = to0 + (uint32_t)p.spad * 64u;  // row srow + 32
-  // Named staging registers: an array passed into these lambdas would live in scratch memory.
-  uint4 g0, g1, g2, g3, g4, g5;
-  auto gload = [&](int k0) {
+  auto dload = [&](int k0, int bf) {
     // Rows past the end read row S - 1 (their keys are never selected). The tile may start
     // past it (S_pad is a whole number of key blocks): rows are taken from a base row at most
     // S - 1, so the lane offsets stay in [0, 63] rows.
@@ -275,20 +276,12 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dq_kernel(const DenseBw
     const char* kt = kbase + (int64_t)r_base * kss_b;
     const char* vt = vbase + (int64_t)r_base * vss_b;
     const char* tt = tbase + (int64_t)k0 * 2;
-    g0 = buffer_load16(kt, __umul24(r0, kss_b) + ccol);
-    g1 = buffer_load16(kt, __umul24(r1, kss_b) + ccol);
-    g2 = buffer_load16(vt, __umul24(r0, vss_b) + ccol);
-    g3 = buffer_load16(vt, __umul24(r1, vss_b) + ccol);
-    g4 = buffer_load16(tt, to0);
-    g5 = buffer_load16(tt, to1);
-  };
-  auto lstore = [&](int bf) {
-    *reinterpret_cast<uint4*>(&ktile[bf][soff]) = g0;
-    *reinterpret_cast<uint4*>(&ktile[bf][soff + 4096]) = g1;
-    *reinterpret_cast<uint4*>(&vtile[bf][soff]) = g2;
-    *reinterpret_cast<uint4*>(&vtile[bf][soff + 4096]) = g3;
-    *reinterpret_cast<uint4*>(&kttile[bf][soff]) = g4;
-    *reinterpret_cast<uint4*>(&kttile[bf][soff + 4096]) = g5;
+    buffer_load16_lds(kt, __umul24(r0, kss_b) + ccol, &ktile[bf][wseg]);
+    buffer_load16_lds(kt, __umul24(r1, kss_b) + ccol, &ktile[bf][wseg + 4096]);
+    buffer_load16_lds(vt, __umul24(r0, vss_b) + ccol, &vtile[bf][wseg]);
+    buffer_load16_lds(vt, __umul24(r1, vss_b) + ccol, &vtile[bf][wseg + 4096]);
+    buffer_load16_lds(tt, to0, &kttile[bf][wseg]);
+    buffer_load16_lds(tt, to1, &kttile[bf][wseg + 4096]);
   };
   // Operand reads: K and V rows 32 st + col (chunk 2 ks + half); K^T rows 32 db + col (chunk
   // 4 st + 2 ks + half); swz of these rows is swz(col).
@@ -353,22 +346,20 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dq_kernel(const DenseBw
       }
   };
 
-  // Tile n (64 keys) lives in LDS buffer n % 2; while computing it a thread stores tile n + 1
-  // from registers into the other buffer and loads tile n + 2; one barrier per tile.
+  // Tile n (64 keys) lives in LDS buffer n % 2; while computing it the workgroup loads tile
+  // n + 1 into the other buffer; one barrier per tile.
   const int ntiles = p.spad >> 6;
-  const int last = (ntiles - 1) * 64;
-  gload(0);
-  lstore(0);
-  gload(min(64, last));
+  dload(0, 0);
   uint32_t w0[kBQPW] = {mword(0, 0), mword(0, 1)}, w1[kBQPW] = {mword(1, 0), mword(1, 1)};
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): tile 0 is in LDS
   __syncthreads();
 #pragma unroll 1
   for (int n = 0; n < ntiles; ++n) {
     const int buf = n & 1;
     const uint32_t wn0[kBQPW] = {mword(2 * n + 2, 0), mword(2 * n + 2, 1)};
     const uint32_t wn1[kBQPW] = {mword(2 * n + 3, 0), mword(2 * n + 3, 1)};
-    lstore(buf ^ 1);  // past the last tile: never read
-    gload(min((n + 2) * 64, last));
+    // the other buffer was last read before the previous barrier
+    if (n + 1 < ntiles) dload((n + 1) * 64, buf ^ 1);
     sub(ktile[buf], vtile[buf], kttile[buf], 0, w0);
     sub(ktile[buf], vtile[buf], kttile[buf], 1, w1);
 #pragma unroll
@@ -376,7 +367,7 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dq_kernel(const DenseBw
       w0[a] = wn0[a];
       w1[a] = wn1[a];
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this thread's LDS stores are done
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): the next tile is in LDS
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -407,7 +398,7 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dq_kernel(const DenseBw
 // dk/dv pass: 4 waves per workgroup, each on one 32-key block of one head; the key block's K
 // and V rows are the stationary B operands, dK^T and dV^T accumulate in registers over every
 // query. Per 64-query tile the Q rows, dO rows, Q^T, dO^T (8 KB each) and the queries' {lse2,
-// delta} are staged through LDS, registers a tile ahead, one barrier per tile. Per 32-query
+// delta} are loaded straight into LDS a tile ahead, one barrier per tile. Per 32-query
 // sub-tile: S = Q K^T from the selection bias (key-major words), dP = dO V^T, p and ds as in
 // the dq pass, dV^T += dO^T P, dK^T += Q^T dS.
 // ---------------------------------------------------------------------------------------
@@ -454,10 +445,13 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dkdv_kernel(const Dense
     }
 
   // Tile staging: two 16-byte chunks of each of Q, dO (rows = queries srow, srow + 32), Q^T
-  // and dO^T (rows = d srow, srow + 32) per thread; threads 0..31 move the {lse2, delta} of
-  // two queries each.
+  // and dO^T (rows = d srow, srow + 32) per thread, loaded straight into LDS; threads 0..31
+  // move the {lse2, delta} of two queries each. Lane i of a wave writes the 16 bytes at the
+  // wave's 1 KB segment + 16 i = row srow, physical chunk sc, so it reads the chunk
+  // sc ^ swz(srow) that the swizzled layout keeps there (swz(srow + 32) = swz(srow)).
   const int srow = tid >> 3, sc = tid & 7;
-  const int soff = srow * 128 + ((sc ^ swz(srow)) << 4);
+  const int lc = sc ^ swz(srow);
+  const int wseg = wave * 1024;
   // A tile's base addresses are uniform (scalar registers); a lane adds a 32-bit byte offset
   // (the host keeps the q and dO token strides below 2^24 bytes and 64 rows of Q^T below
   // 2^32 bytes).
@@ -468,12 +462,11 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dkdv_kernel(const Dense
   const char* dtbase = uniform_ptr(reinterpret_cast<const char*>(p.dot + thead));
   const char* lbase = uniform_ptr(reinterpret_cast<const char*>(p.ls + ((int64_t)b * p.H + h) * p.tpad));
   const uint32_t qst_b = (uint32_t)p.qst * 2u, dst_b = (uint32_t)p.dost * 2u;
-  const uint32_t ccol = (uint32_t)sc * 16u;
-  const uint32_t to0 = ((uint32_t)srow * (uint32_t)p.tpad + (uint32_t)sc * 8u) * 2u;
+  const uint32_t ccol = (uint32_t)lc * 16u;
+  const uint32_t to0 = ((uint32_t)srow * (uint32_t)p.tpad + (uint32_t)lc * 8u) * 2u;
   const uint32_t to1 = to0 + (uint32_t)p.tpad * 64u;  // row srow + 32
   const uint32_t lo = (uint32_t)(tid & 31) * 16u;     // two {lse2, delta} per thread
-  uint4 g0, g1, g2, g3, g4, g5, g6, g7, g8;
-  auto gload = [&](int t0) {
+  auto dload = [&](int t0, int bf) {
     // Rows past the end read row T - 1 (their queries never selected a key). The tile may
     // start past it (T_pad is a whole number of query blocks): rows are taken from a base row
     // at most T - 1, so the lane offsets stay in [0, 63] rows.
@@ -484,26 +477,15 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dkdv_kernel(const Dense
     const char* dt = dbase + (int64_t)r_base * dst_b;
     const char* qtt = qtbase + (int64_t)t0 * 2;
     const char* dtt = dtbase + (int64_t)t0 * 2;
-    g0 = buffer_load16(qt, __umul24(r0, qst_b) + ccol);
-    g1 = buffer_load16(qt, __umul24(r1, qst_b) + ccol);
-    g2 = buffer_load16(dt, __umul24(r0, dst_b) + ccol);
-    g3 = buffer_load16(dt, __umul24(r1, dst_b) + ccol);
-    g4 = buffer_load16(qtt, to0);
-    g5 = buffer_load16(qtt, to1);
-    g6 = buffer_load16(dtt, to0);
-    g7 = buffer_load16(dtt, to1);
-    if (tid < 32) g8 = buffer_load16(lbase + (int64_t)t0 * 8, lo);
-  };
-  auto lstore = [&](int bf) {
-    *reinterpret_cast<uint4*>(&qtile[bf][soff]) = g0;
-    *reinterpret_cast<uint4*>(&qtile[bf][soff + 4096]) = g1;
-    *reinterpret_cast<uint4*>(&dotile[bf][soff]) = g2;
-    *reinterpret_cast<uint4*>(&dotile[bf][soff + 4096]) = g3;
-    *reinterpret_cast<uint4*>(&qttile[bf][soff]) = g4;
-    *reinterpret_cast<uint4*>(&qttile[bf][soff + 4096]) = g5;
-    *reinterpret_cast<uint4*>(&dottile[bf][soff]) = g6;
-    *reinterpret_cast<uint4*>(&dottile[bf][soff + 4096]) = g7;
-    if (tid < 32) *reinterpret_cast<uint4*>(&lstile[bf][2 * tid]) = g8;
+    buffer_load16_lds(qt, __umul24(r0, qst_b) + ccol, &qtile[bf][wseg]);
+    buffer_load16_lds(qt, __umul24(r1, qst_b) + ccol, &qtile[bf][wseg + 4096]);
+    buffer_load16_lds(dt, __umul24(r0, dst_b) + ccol, &dotile[bf][wseg]);
+    buffer_load16_lds(dt, __umul24(r1, dst_b) + ccol, &dotile[bf][wseg + 4096]);
+    buffer_load16_lds(qtt, to0, &qttile[bf][wseg]);
+    buffer_load16_lds(qtt, to1, &qttile[bf][wseg + 4096]);
+    buffer_load16_lds(dtt, to0, &dottile[bf][wseg]);
+    buffer_load16_lds(dtt, to1, &dottile[bf][wseg + 4096]);
+    if (tid < 32) buffer_load16_lds(lbase + (int64_t)t0 * 8, lo, &lstile[bf][0]);
   };
   const int fc = swz(col);
   auto koff = [&](int st, int ks) { return col * 128 + st * 4096 + (((2 * ks + half) ^ fc) << 4); };
@@ -560,23 +542,21 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dkdv_kernel(const Dense
   };
 
   const int ntiles = p.tpad >> 6;
-  const int last = (ntiles - 1) * 64;
-  gload(0);
-  lstore(0);
-  gload(min(64, last));
+  dload(0, 0);
   uint32_t w0 = mword(0), w1 = mword(1);
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): tile 0 is in LDS
   __syncthreads();
 #pragma unroll 1
   for (int n = 0; n < ntiles; ++n) {
     const int buf = n & 1;
     const uint32_t wn0 = mword(2 * n + 2), wn1 = mword(2 * n + 3);
-    lstore(buf ^ 1);  // past the last tile: never read
-    gload(min((n + 2) * 64, last));
+    // the other buffer was last read before the previous barrier
+    if (n + 1 < ntiles) dload((n + 1) * 64, buf ^ 1);
     sub(qtile[buf], dotile[buf], qttile[buf], dottile[buf], lstile[buf], 0, w0);
     sub(qtile[buf], dotile[buf], qttile[buf], dottile[buf], lstile[buf], 1, w1);
     w0 = wn0;
     w1 = wn1;
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): the next tile is in LDS
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
