@@ -270,33 +270,31 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
   }
 
   // Tile staging: each thread moves two 16-byte chunks of K and two of V^T per tile (rows
-  // srow and srow + 32), loaded into registers a tile ahead of their LDS store.
+  // srow and srow + 32), loaded straight into LDS. Lane i of a wave writes the 16 bytes at the
+  // wave's 1 KB segment + 16 i = row srow, physical chunk sc, so it reads the chunk
+  // sc ^ swz(srow) that the swizzled layout keeps there (swz(srow + 32) = swz(srow)).
   const int srow = tid >> 3, sc = tid & 7;
-  const int soff = srow * 128 + ((sc ^ swz(srow)) << 4);  // swz(srow + 32) = swz(srow)
+  const int lc = sc ^ swz(srow);
+  const int wseg = wave * 1024;
   // A tile's base addresses are uniform (scalar registers); a lane adds a 32-bit byte offset
   // (the host keeps a K row stride below 2^24 bytes and 64 rows of V^T below 2^32 bytes).
   const char* kbase = uniform_ptr(reinterpret_cast<const char*>(p.k + b * p.ksb + (int64_t)h * p.ksh));
   const char* vbase = uniform_ptr(reinterpret_cast<const char*>(p.vt + ((int64_t)b * p.H + h) * 64 * p.Spad));
   const uint32_t kss_b = (uint32_t)p.kss * 2u;
-  const uint32_t kcol = (uint32_t)sc * 16u;
-  const uint32_t vo0 = ((uint32_t)srow * (uint32_t)p.Spad + (uint32_t)sc * 8u) * 2u;
+  const uint32_t kcol = (uint32_t)lc * 16u;
+  const uint32_t vo0 = ((uint32_t)srow * (uint32_t)p.Spad + (uint32_t)lc * 8u) * 2u;
   const uint32_t vo1 = vo0 + (uint32_t)p.Spad * 64u;  // row srow + 32
-  auto gload = [&](int k0, uint4& ka, uint4& kb, uint4& va, uint4& vb) {
+  auto dload = [&](int k0, int bf) {
     // Rows past the end read row S - 1 (their keys are never selected), taken from a base row
     // at most S - 1 so that the lane offsets stay in [0, 63] rows wherever the tile starts.
     const int r_base = min(k0, p.S - 1);
     const char* kt = kbase + (int64_t)r_base * kss_b;
-    ka = buffer_load16(kt, __umul24((uint32_t)(min(k0 + srow, p.S - 1) - r_base), kss_b) + kcol);
-    kb = buffer_load16(kt, __umul24((uint32_t)(min(k0 + srow + 32, p.S - 1) - r_base), kss_b) + kcol);
+    buffer_load16_lds(kt, __umul24((uint32_t)(min(k0 + srow, p.S - 1) - r_base), kss_b) + kcol, &ktile[bf][wseg]);
+    buffer_load16_lds(kt, __umul24((uint32_t)(min(k0 + srow + 32, p.S - 1) - r_base), kss_b) + kcol,
+                      &ktile[bf][wseg + 4096]);
     const char* vtile0 = vbase + (int64_t)k0 * 2;
-    va = buffer_load16(vtile0, vo0);
-    vb = buffer_load16(vtile0, vo1);
-  };
-  auto lstore = [&](int bf, const uint4& ka, const uint4& kb, const uint4& va, const uint4& vb) {
-    *reinterpret_cast<uint4*>(&ktile[bf][soff]) = ka;
-    *reinterpret_cast<uint4*>(&ktile[bf][soff + 4096]) = kb;
-    *reinterpret_cast<uint4*>(&vtile[bf][soff]) = va;
-    *reinterpret_cast<uint4*>(&vtile[bf][soff + 4096]) = vb;
+    buffer_load16_lds(vtile0, vo0, &vtile[bf][wseg]);
+    buffer_load16_lds(vtile0, vo1, &vtile[bf][wseg + 4096]);
   };
   // Operand reads: K rows 32 st + col (chunk 2 ks + half), V^T rows 32 db + col (chunk
   // 4 st + 2 ks + half); swz of these rows is swz(col).
@@ -452,29 +450,21 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
     }
   };
 
-  // Tile n (64 keys) lives in LDS buffer n % 2. While computing tile n a thread stores tile
-  // n + 1 from registers into the other buffer (last read before the previous barrier) and
-  // loads tile n + 2 into the freed registers; one barrier per tile.
+  // Tile n (64 keys) lives in LDS buffer n % 2. While computing tile n the workgroup loads
+  // tile n + 1 into the other buffer (last read before the previous barrier); one barrier per
+  // tile.
   const int ntiles = p.Spad >> 6;
-  const int last = (ntiles - 1) * 64;
-  uint4 kra, krb, vra, vrb;
-  {
-    uint4 a0, a1, a2, a3;
-    gload(0, a0, a1, a2, a3);
-    lstore(0, a0, a1, a2, a3);
-  }
-  gload(min(64, last), kra, krb, vra, vrb);
+  dload(0, 0);
   uint32_t w0[kQPW] = {mword(0, 0), mword(0, 1)}, w1[kQPW] = {mword(1, 0), mword(1, 1)};
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): tile 0 is in LDS
   __syncthreads();
 #pragma unroll 1
   for (int n = 0; n < ntiles; ++n) {
     const int buf = n & 1;
-    // The next tile's mask words before the tile loads: waiting for them later does not
-    // wait for the tile loads.
+    // The next tile's mask words before the tile loads.
     const uint32_t wn0[kQPW] = {mword(2 * n + 2, 0), mword(2 * n + 2, 1)};
     const uint32_t wn1[kQPW] = {mword(2 * n + 3, 0), mword(2 * n + 3, 1)};
-    lstore(buf ^ 1, kra, krb, vra, vrb);  // past the last tile: never read
-    gload(min((n + 2) * 64, last), kra, krb, vra, vrb);
+    if (n + 1 < ntiles) dload((n + 1) * 64, buf ^ 1);
     sub(ktile[buf], vtile[buf], 0, w0);
     sub(ktile[buf], vtile[buf], 1, w1);
 #pragma unroll
@@ -482,10 +472,9 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
       w0[a] = wn0[a];
       w1[a] = wn1[a];
     }
-    // This thread's LDS stores of the next tile are done; after the barrier every thread's
-    // are, and every wave is done with this tile's buffer before it is refilled. No wait for
-    // the global loads in flight (a raw barrier, unlike __syncthreads).
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    // This thread's loads of the next tile have reached LDS; after the barrier every thread's
+    // have, and every wave is done with this tile's buffer before it is refilled.
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
