@@ -498,6 +498,15 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dkdv_kernel(const Dense
 
   auto sub = [&](const uint8_t* qtl, const uint8_t* dtl, const uint8_t* qttl, const uint8_t* dttl,
                  const float2* lsl, int st, uint32_t w) {
+    // {lse2, delta} of queries 32 st + 8 gq + 4 half + 0..3, read before the products so that
+    // their LDS latency hides behind them
+    float4 u[8];
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const float4* l4 = reinterpret_cast<const float4*>(lsl + 32 * st + 8 * gq + 4 * half);
+      u[2 * gq] = l4[0];
+      u[2 * gq + 1] = l4[1];
+    }
     f32x16 s, dp;
     // Entry r = 4 g + j of this lane is query 8 g + 4 half + j of the sub-tile. Bias-order
     // words: it is the sign bit of byte j of w << (g + 4 half), set when the query did not
@@ -518,9 +527,7 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dkdv_kernel(const Dense
     float pv[16], dsv[16];
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
-      // {lse2, delta} of queries 32 st + 8 gq + 4 half + 0..3
-      const float4* l4 = reinterpret_cast<const float4*>(lsl + 32 * st + 8 * gq + 4 * half);
-      const float4 u0 = l4[0], u1 = l4[1];
+      const float4 u0 = u[2 * gq], u1 = u[2 * gq + 1];
       const float l2[4] = {u0.x, u0.z, u1.x, u1.z};
       const float dl[4] = {u0.y, u0.w, u1.y, u1.w};
 #pragma unroll
