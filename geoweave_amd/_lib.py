@@ -168,12 +168,17 @@ def check(rc: int, what: str) -> None:
         raise RuntimeError(f"{what} failed (code {rc}): {msg}")
 
 
-def dtype_code(dtype: torch.dtype) -> int:
+def dtype_code(dtype: torch.dtype, allow_fp32: bool = False) -> int:
+    """The C ABI's dtype code. fp32 only where the entry point takes it (``allow_fp32``:
+    the indexer top-k, its backward and the KL loss)."""
     if dtype == torch.bfloat16:
         return GW_DTYPE_BF16
     if dtype == torch.float16:
         return GW_DTYPE_FP16
-    raise TypeError(f"unsupported dtype {dtype}; the HIP kernels take bfloat16 or float16")
+    if allow_fp32 and dtype == torch.float32:
+        return GW_DTYPE_FP32
+    kinds = "bfloat16, float16 or float32" if allow_fp32 else "bfloat16 or float16"
+    raise TypeError(f"unsupported dtype {dtype}; this HIP kernel takes {kinds}")
 
 
 def strides3(*vals: int):

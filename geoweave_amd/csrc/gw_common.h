@@ -39,9 +39,29 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // ---------------------------------------------------------------------------------------
 namespace gw {
 
-// Element-type tags. Storage is always the 16-bit pattern.
+// Element-type tags. BF16/FP16 are stored as their 16-bit pattern, FP32 as the float.
 struct BF16 {};
 struct FP16 {};
+struct FP32 {};
+
+template <typename E>
+struct ElemBytes {
+  static constexpr int value = 2;
+};
+template <>
+struct ElemBytes<FP32> {
+  static constexpr int value = 4;
+};
+
+// Element i of a tensor of element type E, as fp32 / stored from fp32 (16-bit types: round
+// to nearest even).
+__device__ __forceinline__ float ld_f32(BF16, const void* p, int64_t i) {
+  return __uint_as_float((uint32_t)static_cast<const uint16_t*>(p)[i] << 16);
+}
+__device__ __forceinline__ float ld_f32(FP16, const void* p, int64_t i) {
+  return (float)__builtin_bit_cast(_Float16, static_cast<const uint16_t*>(p)[i]);
+}
+__device__ __forceinline__ float ld_f32(FP32, const void* p, int64_t i) { return static_cast<const float*>(p)[i]; }
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
@@ -97,6 +117,47 @@ __device__ __forceinline__ uint32_t pack1(FP16, float f) {
   _Float16 h = (_Float16)f;
   return (uint32_t)__builtin_bit_cast(uint16_t, h);
 }
+__device__ __forceinline__ void st_f32(BF16, void* p, int64_t i, float f) {
+  static_cast<uint16_t*>(p)[i] = (uint16_t)pack1(BF16{}, f);
+}
+__device__ __forceinline__ void st_f32(FP16, void* p, int64_t i, float f) {
+  static_cast<uint16_t*>(p)[i] = (uint16_t)pack1(FP16{}, f);
+}
+__device__ __forceinline__ void st_f32(FP32, void* p, int64_t i, float f) { static_cast<float*>(p)[i] = f; }
+
+// Eight consecutive elements: one 16-byte word for the 16-bit types, two for fp32.
+template <typename E>
+struct Raw8 {
+  uint4 v;
+};
+template <>
+struct Raw8<FP32> {
+  uint4 lo, hi;
+};
+// Loads elements [i, i + 8) (16-byte aligned for 16-bit types, 32-byte for fp32).
+template <typename E>
+__device__ __forceinline__ Raw8<E> ld8(const void* p, int64_t i) {
+  Raw8<E> r;
+  if constexpr (ElemBytes<E>::value == 4) {
+    const uint4* s = reinterpret_cast<const uint4*>(static_cast<const float*>(p) + i);
+    r.lo = s[0];
+    r.hi = s[1];
+  } else {
+    r.v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i);
+  }
+  return r;
+}
+template <typename E>
+__device__ __forceinline__ Raw8<E> zero8() {
+  Raw8<E> r;
+  if constexpr (ElemBytes<E>::value == 4) {
+    r.lo = make_uint4(0, 0, 0, 0);
+    r.hi = make_uint4(0, 0, 0, 0);
+  } else {
+    r.v = make_uint4(0, 0, 0, 0);
+  }
+  return r;
+}
 template <typename E>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   return pack1(E{}, lo) | (pack1(E{}, hi) << 16);
@@ -105,6 +166,47 @@ template <typename E>
 __device__ __forceinline__ uint4 pack8(const float* f) {
   return make_uint4(pack2<E>(f[0], f[1]), pack2<E>(f[2], f[3]), pack2<E>(f[4], f[5]),
                     pack2<E>(f[6], f[7]));
+}
+
+// Raw8 <-> fp32, its 8-element dot product (fp32 accumulation in element order) and store.
+template <typename E>
+__device__ __forceinline__ void up8(const Raw8<E>& r, float* f) {
+  if constexpr (ElemBytes<E>::value == 4) {
+    f[0] = __uint_as_float(r.lo.x);
+    f[1] = __uint_as_float(r.lo.y);
+    f[2] = __uint_as_float(r.lo.z);
+    f[3] = __uint_as_float(r.lo.w);
+    f[4] = __uint_as_float(r.hi.x);
+    f[5] = __uint_as_float(r.hi.y);
+    f[6] = __uint_as_float(r.hi.z);
+    f[7] = __uint_as_float(r.hi.w);
+  } else {
+    unpack8<E>(r.v, f);
+  }
+}
+template <typename E>
+__device__ __forceinline__ float dot8r(const Raw8<E>& a, const Raw8<E>& b) {
+  if constexpr (ElemBytes<E>::value == 4) {
+    float x[8], y[8];
+    up8<E>(a, x);
+    up8<E>(b, y);
+    float s = x[0] * y[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) s = fmaf(x[i], y[i], s);
+    return s;
+  } else {
+    return dot8<E>(a.v, b.v);
+  }
+}
+template <typename E>
+__device__ __forceinline__ void st8(void* p, int64_t i, const float* f) {
+  if constexpr (ElemBytes<E>::value == 4) {
+    uint4* d = reinterpret_cast<uint4*>(static_cast<float*>(p) + i);
+    d[0] = make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
+    d[1] = make_uint4(__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]), __float_as_uint(f[7]));
+  } else {
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p) + i) = pack8<E>(f);
+  }
 }
 
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }

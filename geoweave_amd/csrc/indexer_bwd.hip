@@ -9,7 +9,7 @@
 //   dq[t,h] += f * k[s,h]      dk[s,h] += f * q[t,h]      dw[s,h] += g * relu(z)
 // The reference accumulates dk and dw with fp32 atomics (:1936-1941). Here:
 //  dq pass  (query-major): one wave per query holds q[t, all heads] and gathers the
-//           selected k rows (Hi * 64 * 2 bytes each) and gates.
+//           selected k rows (Hi * 64 elements each) and gates.
 //  dkw pass (key-major over the CSR of kv_csr.hip, shared with the attention backward):
 //           one wave per work item holds k[s, all heads] and w[s, :], gathers q rows and
 //           gradients of the entries, and reduces dk and dw in fp32 in a fixed order.
@@ -23,23 +23,21 @@ namespace {
 
 constexpr int kDI = 64;
 
+// Tensors other than idx and part are in the element type E of the launch.
 struct IdxBwdParams {
-  const uint16_t* q;     // [B, T, HI, 64]
-  const uint16_t* k;     // [B, S, HI, 64]
-  const uint16_t* w;     // [B, S, HI]
-  const int32_t* idx;    // [B, T, K]
-  const uint16_t* grad;  // [B, T, K]
-  uint16_t* dq;
-  uint16_t* dk;
-  uint16_t* dw;
+  const void* q;       // [B, T, HI, 64]
+  const void* k;       // [B, S, HI, 64]
+  const void* w;       // [B, S, HI]
+  const int32_t* idx;  // [B, T, K]
+  const void* grad;    // [B, T, K]
+  void* dq;
+  void* dk;
+  void* dw;
   float* part;  // [parts, HI * 64 + HI]
   CsrView csr;
   int T, S, K;
   float scale;
 };
-
-__device__ __forceinline__ float to_f32(BF16, uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
-__device__ __forceinline__ float to_f32(FP16, uint16_t x) { return (float)__builtin_bit_cast(_Float16, x); }
 
 // Lane layout (both passes): HL = HI * 8 lanes hold one token's HI heads (8 lanes x 8
 // elements per head); G = 64 / HL entries are processed side by side.
@@ -57,11 +55,11 @@ __global__ __launch_bounds__(256) void indexer_bwd_dq_kernel(const IdxBwdParams 
   const int h = (lane % HL) / 8;
   const int c = lane % 8;
   const int64_t row = (int64_t)b * p.T + t;
-  const uint4 qv = *reinterpret_cast<const uint4*>(p.q + (row * HI + h) * kDI + c * 8);
+  const Raw8<E> qv = ld8<E>(p.q, (row * HI + h) * kDI + c * 8);
   const int32_t* irow = p.idx + row * p.K;
-  const uint16_t* grow = p.grad + row * p.K;
-  const uint16_t* kb = p.k + (int64_t)b * p.S * HI * kDI + h * kDI + c * 8;
-  const uint16_t* wb = p.w + (int64_t)b * p.S * HI + h;
+  const int64_t grow = row * p.K;
+  const int64_t kb = (int64_t)b * p.S * HI * kDI + h * kDI + c * 8;  // element offsets
+  const int64_t wb = (int64_t)b * p.S * HI + h;
 
   float acc[8];
 #pragma unroll
@@ -74,7 +72,7 @@ __global__ __launch_bounds__(256) void indexer_bwd_dq_kernel(const IdxBwdParams 
     float g;
   };
   struct Row {
-    uint4 k;
+    Raw8<E> k;
     float gw;  // g * w * scale
   };
   auto load_idx = [&](Idx (&xi)[U], int j0) {
@@ -83,7 +81,7 @@ __global__ __launch_bounds__(256) void indexer_bwd_dq_kernel(const IdxBwdParams 
       const int j = j0 + u * G + g;
       const int s = j < p.K ? irow[j] : -1;
       xi[u].s = (s >= 0 && s < p.S) ? s : -1;
-      xi[u].g = j < p.K ? to_f32(E{}, grow[j]) : 0.f;
+      xi[u].g = j < p.K ? ld_f32(E{}, p.grad, grow + j) : 0.f;
     }
   };
   auto load_row = [&](Row (&xr)[U], const Idx (&xi)[U]) {
@@ -91,10 +89,10 @@ __global__ __launch_bounds__(256) void indexer_bwd_dq_kernel(const IdxBwdParams 
     for (int u = 0; u < U; ++u) {
       const int s = xi[u].s;
       if (s >= 0) {
-        xr[u].k = *reinterpret_cast<const uint4*>(kb + (int64_t)s * HI * kDI);
-        xr[u].gw = xi[u].g * to_f32(E{}, wb[(int64_t)s * HI]) * p.scale;
+        xr[u].k = ld8<E>(p.k, kb + (int64_t)s * HI * kDI);
+        xr[u].gw = xi[u].g * ld_f32(E{}, p.w, wb + (int64_t)s * HI) * p.scale;
       } else {
-        xr[u].k = make_uint4(0, 0, 0, 0);
+        xr[u].k = zero8<E>();
         xr[u].gw = 0.f;
       }
     }
@@ -110,10 +108,10 @@ __global__ __launch_bounds__(256) void indexer_bwd_dq_kernel(const IdxBwdParams 
     load_idx(in, j0 + 2 * STEP);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const float z = group_sum<8>(dot8<E>(qv, cur[u].k)) * p.scale;
+      const float z = group_sum<8>(dot8r<E>(qv, cur[u].k)) * p.scale;
       const float f = z > 0.f ? cur[u].gw : 0.f;
       float kf[8];
-      unpack8<E>(cur[u].k, kf);
+      up8<E>(cur[u].k, kf);
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[i] = fmaf(f, kf[i], acc[i]);
     }
@@ -124,7 +122,7 @@ __global__ __launch_bounds__(256) void indexer_bwd_dq_kernel(const IdxBwdParams 
   for (int off = HL; off < 64; off <<= 1)
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] += __shfl_xor(acc[i], off);
-  if (g == 0) *reinterpret_cast<uint4*>(p.dq + (row * HI + h) * kDI + c * 8) = pack8<E>(acc);
+  if (g == 0) st8<E>(p.dq, (row * HI + h) * kDI + c * 8, acc);
 }
 
 template <typename E, int HI>
@@ -143,10 +141,10 @@ __global__ __launch_bounds__(256) void indexer_bwd_dkw_kernel(const IdxBwdParams
   const int h = (lane % HL) / 8;
   const int c = lane % 8;
   const int64_t krow = (int64_t)b * p.S + s;
-  const uint4 kv = *reinterpret_cast<const uint4*>(p.k + (krow * HI + h) * kDI + c * 8);
-  const float wsc = to_f32(E{}, p.w[krow * HI + h]) * p.scale;
-  const uint16_t* qb = p.q + (int64_t)b * p.T * HI * kDI + h * kDI + c * 8;
-  const uint16_t* gb = p.grad + (int64_t)b * p.T * p.K;
+  const Raw8<E> kv = ld8<E>(p.k, (krow * HI + h) * kDI + c * 8);
+  const float wsc = ld_f32(E{}, p.w, krow * HI + h) * p.scale;
+  const int64_t qb = (int64_t)b * p.T * HI * kDI + h * kDI + c * 8;  // element offsets
+  const int64_t gb = (int64_t)b * p.T * p.K;
 
   float ak[8];
 #pragma unroll
@@ -154,7 +152,7 @@ __global__ __launch_bounds__(256) void indexer_bwd_dkw_kernel(const IdxBwdParams
   float aw = 0.f;
 
   struct Slot {
-    uint4 q;
+    Raw8<E> q;
     float g;
   };
   auto load = [&](Slot (&sl)[U], int i0) {
@@ -164,10 +162,10 @@ __global__ __launch_bounds__(256) void indexer_bwd_dkw_kernel(const IdxBwdParams
       Slot& x = sl[u];
       if (i < it.end) {
         const int2 e = p.csr.entries[i];
-        x.q = *reinterpret_cast<const uint4*>(qb + (int64_t)e.x * HI * kDI);
-        x.g = to_f32(E{}, gb[(int64_t)e.x * p.K + e.y]);
+        x.q = ld8<E>(p.q, qb + (int64_t)e.x * HI * kDI);
+        x.g = ld_f32(E{}, p.grad, gb + (int64_t)e.x * p.K + e.y);
       } else {
-        x.q = make_uint4(0, 0, 0, 0);
+        x.q = zero8<E>();
         x.g = 0.f;
       }
     }
@@ -179,12 +177,12 @@ __global__ __launch_bounds__(256) void indexer_bwd_dkw_kernel(const IdxBwdParams
     load(nxt, i0 + STEP);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const float z = group_sum<8>(dot8<E>(cur[u].q, kv)) * p.scale;
+      const float z = group_sum<8>(dot8r<E>(cur[u].q, kv)) * p.scale;
       const bool on = z > 0.f;
       const float f = on ? cur[u].g * wsc : 0.f;
       aw = on ? fmaf(cur[u].g, z, aw) : aw;
       float qf[8];
-      unpack8<E>(cur[u].q, qf);
+      up8<E>(cur[u].q, qf);
 #pragma unroll
       for (int i = 0; i < 8; ++i) ak[i] = fmaf(f, qf[i], ak[i]);
     }
@@ -199,8 +197,8 @@ __global__ __launch_bounds__(256) void indexer_bwd_dkw_kernel(const IdxBwdParams
   }
   if (g == 0) {
     if (it.nchunk == 1) {
-      *reinterpret_cast<uint4*>(p.dk + (krow * HI + h) * kDI + c * 8) = pack8<E>(ak);
-      if (c == 0) p.dw[krow * HI + h] = (uint16_t)pack1(E{}, aw);
+      st8<E>(p.dk, (krow * HI + h) * kDI + c * 8, ak);
+      if (c == 0) st_f32(E{}, p.dw, krow * HI + h, aw);
     } else {
       float* pk = p.part + (int64_t)it.part * (HI * kDI + HI);
 #pragma unroll
@@ -221,8 +219,8 @@ __global__ __launch_bounds__(256) void indexer_bwd_reduce_kernel(const IdxBwdPar
   for (int i = threadIdx.x; i < ROW; i += 256) {
     float sum = 0.f;
     for (int c = 0; c < n; ++c) sum += p.part[(int64_t)(base + c) * ROW + i];
-    if (i < HI * kDI) p.dk[(int64_t)key * HI * kDI + i] = (uint16_t)pack1(E{}, sum);
-    else p.dw[(int64_t)key * HI + (i - HI * kDI)] = (uint16_t)pack1(E{}, sum);
+    if (i < HI * kDI) st_f32(E{}, p.dk, (int64_t)key * HI * kDI + i, sum);
+    else st_f32(E{}, p.dw, (int64_t)key * HI + (i - HI * kDI), sum);
   }
 }
 
@@ -264,7 +262,8 @@ extern "C" int gw_indexer_topk_bwd(int dtype, const void* q, const void* k, cons
                                    size_t workspace_bytes, void* stream) {
   using namespace gw;
   clear_error();
-  GW_CHECK_ARG(dtype == GW_DTYPE_BF16 || dtype == GW_DTYPE_FP16, "unsupported dtype code %d", dtype);
+  GW_CHECK_ARG(dtype == GW_DTYPE_BF16 || dtype == GW_DTYPE_FP16 || dtype == GW_DTYPE_FP32, "unsupported dtype code %d",
+               dtype);
   GW_CHECK_ARG(B >= 0 && T >= 0 && S >= 0 && K >= 0, "invalid sizes B=%lld T=%lld S=%lld K=%lld", (long long)B,
                (long long)T, (long long)S, (long long)K);
   if (Di != kDI || !(Hi == 1 || Hi == 2 || Hi == 4 || Hi == 8))
@@ -284,14 +283,14 @@ extern "C" int gw_indexer_topk_bwd(int dtype, const void* q, const void* k, cons
   GW_CHECK_ARG(softmax_scale > 0.f, "softmax_scale must be positive");
   const CsrLayout L = csr_layout(B, T, S, K);
   IdxBwdParams p{};
-  p.q = static_cast<const uint16_t*>(q);
-  p.k = static_cast<const uint16_t*>(k);
-  p.w = static_cast<const uint16_t*>(w);
+  p.q = q;
+  p.k = k;
+  p.w = w;
   p.idx = topk_indices;
-  p.grad = static_cast<const uint16_t*>(grad_scores);
-  p.dq = static_cast<uint16_t*>(dq);
-  p.dk = static_cast<uint16_t*>(dk);
-  p.dw = static_cast<uint16_t*>(dw);
+  p.grad = grad_scores;
+  p.dq = dq;
+  p.dk = dk;
+  p.dw = dw;
   p.part = static_cast<float*>(workspace);
   p.csr = csr_view(csr, L);
   p.T = (int)T;
@@ -300,6 +299,7 @@ extern "C" int gw_indexer_topk_bwd(int dtype, const void* q, const void* k, cons
   p.scale = softmax_scale;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == GW_DTYPE_BF16) return dispatch_idx_bwd<BF16>((int)Hi, p, (int)B, L.max_items, st);
+  if (dtype == GW_DTYPE_FP32) return dispatch_idx_bwd<FP32>((int)Hi, p, (int)B, L.max_items, st);
   return dispatch_idx_bwd<FP16>((int)Hi, p, (int)B, L.max_items, st);
 }
 
@@ -321,7 +321,7 @@ __device__ __forceinline__ int clamp_bin(int v, int n) { return v < 0 ? 0 : (v >
 
 template <typename E>
 __global__ __launch_bounds__(64) void view_bias_rows_kernel(const int32_t* __restrict__ idx,
-                                                            const uint16_t* __restrict__ grad,
+                                                            const void* __restrict__ grad,
                                                             const int32_t* __restrict__ sview, int T, int S,
                                                             int K, int Vs, float* __restrict__ part) {
   __shared__ float hist[64 * kViewChunk];  // [lane][bin of the current chunk]
@@ -330,7 +330,7 @@ __global__ __launch_bounds__(64) void view_bias_rows_kernel(const int32_t* __res
   const int b = (int)(row / T);
   float* mine = hist + lane * kViewChunk;
   const int32_t* ir = idx + row * K;
-  const uint16_t* gr = grad + row * K;
+  const int64_t gr = row * K;
   const int32_t* sv = sview + (int64_t)b * S;
   for (int v0 = 0; v0 < Vs; v0 += kViewChunk) {
     const int nb = min(kViewChunk, Vs - v0);
@@ -339,7 +339,7 @@ __global__ __launch_bounds__(64) void view_bias_rows_kernel(const int32_t* __res
       const int s = ir[j];
       if (s >= 0 && s < S) {
         const int v = clamp_bin(sv[s], Vs) - v0;
-        if (v >= 0 && v < nb) mine[v] += to_f32(E{}, gr[j]);
+        if (v >= 0 && v < nb) mine[v] += ld_f32(E{}, grad, gr + j);
       }
     }
     __syncthreads();
@@ -360,7 +360,8 @@ extern "C" int gw_indexer_view_bias_bwd_rows(int dtype, const int32_t* topk_indi
                                              int64_t K, int64_t Vs, float* row_grad, void* stream) {
   using namespace gw;
   clear_error();
-  GW_CHECK_ARG(dtype == GW_DTYPE_BF16 || dtype == GW_DTYPE_FP16, "unsupported dtype code %d", dtype);
+  GW_CHECK_ARG(dtype == GW_DTYPE_BF16 || dtype == GW_DTYPE_FP16 || dtype == GW_DTYPE_FP32, "unsupported dtype code %d",
+               dtype);
   GW_CHECK_ARG(B >= 0 && T >= 0 && S >= 1 && K >= 0, "invalid sizes B=%lld T=%lld S=%lld K=%lld", (long long)B,
                (long long)T, (long long)S, (long long)K);
   GW_CHECK_ARG(Vs >= 1 && Vs < (1ll << 20), "invalid key view count %lld", (long long)Vs);
@@ -370,12 +371,13 @@ extern "C" int gw_indexer_view_bias_bwd_rows(int dtype, const int32_t* topk_indi
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == GW_DTYPE_BF16)
     hipLaunchKernelGGL(view_bias_rows_kernel<BF16>, dim3((unsigned)(B * T)), dim3(64), 0, st, topk_indices,
-                       static_cast<const uint16_t*>(grad_scores), s_view_ids, (int)T, (int)S, (int)K, (int)Vs,
-                       row_grad);
+                       grad_scores, s_view_ids, (int)T, (int)S, (int)K, (int)Vs, row_grad);
+  else if (dtype == GW_DTYPE_FP32)
+    hipLaunchKernelGGL(view_bias_rows_kernel<FP32>, dim3((unsigned)(B * T)), dim3(64), 0, st, topk_indices,
+                       grad_scores, s_view_ids, (int)T, (int)S, (int)K, (int)Vs, row_grad);
   else
     hipLaunchKernelGGL(view_bias_rows_kernel<FP16>, dim3((unsigned)(B * T)), dim3(64), 0, st, topk_indices,
-                       static_cast<const uint16_t*>(grad_scores), s_view_ids, (int)T, (int)S, (int)K, (int)Vs,
-                       row_grad);
+                       grad_scores, s_view_ids, (int)T, (int)S, (int)K, (int)Vs, row_grad);
   GW_HIP_LAUNCH_CHECK("view_bias_rows_kernel");
   return GW_OK;
 }

@@ -85,10 +85,21 @@ __device__ __forceinline__ f32x16 mfma32(FP16, uint4 a, uint4 b, f32x16 c) {
                                                 __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float to_f32(BF16, uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
-__device__ __forceinline__ float to_f32(FP16, uint16_t x) {
-  return (float)__builtin_bit_cast(_Float16, x);
+// fp32 operands: v_mfma_f32_32x32x2_f32, one fp32 element of A and of B per lane (k index
+// lane / 32), exact fp32 products accumulated in fp32.
+__device__ __forceinline__ f32x16 mfma32_f32(uint32_t a, uint32_t b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a), __uint_as_float(b), c, 0, 0, 0);
 }
+
+// A gate value from its raw bits (the 16-bit pattern, or the fp32 bits).
+__device__ __forceinline__ float to_f32(BF16, uint32_t x) { return __uint_as_float(x << 16); }
+__device__ __forceinline__ float to_f32(FP16, uint32_t x) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)x);
+}
+__device__ __forceinline__ float to_f32(FP32, uint32_t x) { return __uint_as_float(x); }
+__device__ __forceinline__ uint32_t raw_bits(BF16, const void* p, int64_t i) { return static_cast<const uint16_t*>(p)[i]; }
+__device__ __forceinline__ uint32_t raw_bits(FP16, const void* p, int64_t i) { return static_cast<const uint16_t*>(p)[i]; }
+__device__ __forceinline__ uint32_t raw_bits(FP32, const void* p, int64_t i) { return static_cast<const uint32_t*>(p)[i]; }
 
 // relu on the bit pattern: every negative float (sign bit set) becomes +0, every
 // non-negative one is kept bit for bit. One v_max_i32, where fmaxf(x, 0) costs a NaN
@@ -218,12 +229,13 @@ constexpr int kBiasView = 2;
 
 __device__ __forceinline__ int clamp_view(int v, int n) { return v < 0 ? 0 : (v >= n ? n - 1 : v); }
 
+// Tensors are in the element type E of the launch (bf16, fp16 or fp32).
 struct ScoreParams {
-  const uint16_t* q;     // [B, T, HI, 64]
-  const uint16_t* k;     // [B, S, HI, 64]
-  const uint16_t* w;     // [B, S, HI]
-  const uint16_t* mask;  // [B, T, S] or null
-  const uint16_t* vbias;  // kBiasView: [B, Vq, Vs]
+  const void* q;      // [B, T, HI, 64]
+  const void* k;      // [B, S, HI, 64]
+  const void* w;      // [B, S, HI]
+  const void* mask;   // [B, T, S] or null
+  const void* vbias;  // kBiasView: [B, Vq, Vs]
   const int* qview;       // kBiasView: [B, T]
   const int* sview;       // kBiasView: [B, S]
   int Vq, Vs;
@@ -290,20 +302,25 @@ __device__ __forceinline__ void lds_dma16_s(const void* base, uint32_t off, cons
       : "memory");
 }
 
-// Workgroup shape of the score kernel: NW waves of 32 queries share every key tile (a
-// key tile read from L2 serves NW * 32 queries). HI <= 4 keeps its register file within
-// 256 per lane, so 8 waves (two per SIMD) fit one workgroup; HI = 8 needs 4.
-template <int HI>
+// Workgroup shape of the score kernel, by the bytes of a key row (HI heads of 64 elements):
+// NW waves of 32 queries share every key tile (a key tile read from L2 serves NW * 32
+// queries). Rows of <= 512 bytes (16-bit HI <= 4, fp32 HI <= 2) keep the register file
+// within 256 per lane, so 8 waves (two per SIMD) fit one workgroup; 1 KB rows (16-bit
+// HI = 8, fp32 HI = 4: 128 registers of stationary query operands) need 4.
+template <int ROW_BYTES>
 struct ScoreShape {
   // keys per LDS stage (and split interleave granule): two 32-key tiles between barriers
-  // (one for HI = 8, whose key rows are 1 KB), so that two stage buffers and the score
-  // staging below fit the LDS.
-  static constexpr int BN = HI <= 4 ? 64 : 32;
-  static constexpr int NW = HI <= 4 ? 8 : 4;
+  // (one for 1 KB rows), so that two stage buffers and the score staging below fit the LDS.
+  static constexpr int BN = ROW_BYTES <= 512 ? 64 : 32;
+  static constexpr int NW = ROW_BYTES <= 512 ? 8 : 4;
   static constexpr int BM = NW * kQW;        // queries per workgroup
   static constexpr int THREADS = NW * 64;
-  static constexpr int MIN_WAVES_PER_EU = HI <= 4 ? 2 : 1;
+  static constexpr int MIN_WAVES_PER_EU = ROW_BYTES <= 512 ? 2 : 1;
 };
+template <typename E, int HI>
+constexpr int row_bytes() {
+  return HI * kDI * ElemBytes<E>::value;
+}
 
 // The products are transposed: per tile of 32 keys a wave forms S^T = K Q^T (A = key rows
 // from LDS, B = its 32 query rows, stationary in VGPRs), so lane l holds query l % 32 and
@@ -315,14 +332,18 @@ struct ScoreShape {
 constexpr int kStageRow = 36;  // two tiles of 16 scores per lane, padded
 
 template <typename E, int HI, bool SAMPLE, int BIAS>
-__global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_PER_EU) void indexer_score_kernel(
-    const ScoreParams p) {
-  constexpr int NW = ScoreShape<HI>::NW;
-  constexpr int BM = ScoreShape<HI>::BM;
-  constexpr int THREADS = ScoreShape<HI>::THREADS;
-  constexpr int ROW_BYTES = HI * kDI * 2;
+__global__ __launch_bounds__((ScoreShape<row_bytes<E, HI>()>::THREADS),
+                             (ScoreShape<row_bytes<E, HI>()>::MIN_WAVES_PER_EU)) void indexer_score_kernel(const ScoreParams p) {
+  constexpr int ROW_BYTES = row_bytes<E, HI>();
+  using Shape = ScoreShape<ROW_BYTES>;
+  constexpr int NW = Shape::NW;
+  constexpr int BM = Shape::BM;
+  constexpr int THREADS = Shape::THREADS;
+  constexpr bool F32 = ElemBytes<E>::value == 4;
+  constexpr int HEAD_BYTES = kDI * ElemBytes<E>::value;
+  constexpr int HC = HEAD_BYTES / 32;                 // 16-byte chunks per head and lane half
   constexpr int CHUNKS = ROW_BYTES / 16;              // 16-byte chunks per key row (>= 8)
-  constexpr int BN = ScoreShape<HI>::BN;
+  constexpr int BN = Shape::BN;
   constexpr int TILE_BYTES = BN * ROW_BYTES;
   constexpr int LOADS = TILE_BYTES / (THREADS * 16);  // direct loads per thread per stage
   constexpr int WVALS = BN * HI;
@@ -353,20 +374,22 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
   const int row = q0 + col;  // this lane's query
   const bool row_ok = row < T;
   const int64_t grow = (int64_t)b * T + (row_ok ? row : 0);
-  // kBiasView: the view-bias table row of this lane's query.
-  const uint16_t* vrow = nullptr;
-  if constexpr ((BIAS & kBiasView) != 0)
-    vrow = p.vbias + ((int64_t)b * p.Vq + clamp_view(p.qview[grow], p.Vq)) * p.Vs;
+  // kBiasView: the view-bias table row of this lane's query (element offset).
+  int64_t vrow = 0;
+  if constexpr ((BIAS & kBiasView) != 0) vrow = ((int64_t)b * p.Vq + clamp_view(p.qview[grow], p.Vq)) * p.Vs;
 
-  // B operands: this lane's query row, k-chunk (lane / 32) of each 16-wide step.
-  uint4 qop[HI][4];
+  // B operands: this lane's query row; chunk 2 m + half (16 bytes) of each head for step m.
+  // 16-bit: one k = 16 product per chunk (k-chunk lane / 32 of the step); fp32: four k = 2
+  // products per chunk, its element i with element i of the partner lane's chunk (the
+  // products' k indices pair dims 8m + i and 8m + 4 + i, every dim once).
+  uint4 qop[HI][HC];
   {
-    const uint16_t* qr = p.q + grow * (HI * kDI) + half * 8;
+    const char* qr = static_cast<const char*>(p.q) + grow * ROW_BYTES + half * 16;
 #pragma unroll
     for (int h = 0; h < HI; ++h)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        qop[h][ks] = row_ok ? *reinterpret_cast<const uint4*>(qr + h * kDI + ks * 16) : make_uint4(0, 0, 0, 0);
+      for (int m = 0; m < HC; ++m)
+        qop[h][m] = row_ok ? *reinterpret_cast<const uint4*>(qr + h * HEAD_BYTES + m * 32) : make_uint4(0, 0, 0, 0);
   }
   // Threshold of this lane's query (rows past T never pass).
   float tau_l = INFINITY;
@@ -398,17 +421,23 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
   uint32_t voffs[LOADS];  // byte offset of load i from the stage's first key row
 #pragma unroll
   for (int i = 0; i < LOADS; ++i) voffs[i] = (uint32_t)(i * (NW * 1024)) + voff(i);
-  // Operand read offsets: key row (nb*32 + col), logical chunk h*8 + 2*ks + half, physical
-  // chunk (h*8 + 2*ks + half) ^ (col & SWZ) = 8*(h ^ c3) + ((2*ks + half) ^ (col & 7)) with
-  // c3 = bit 3 of col when SWZ = 15: head h sits at 128*h + 128*c3 (h even) or
-  // 128*h - 128*c3 (h odd), so the head part stays an immediate offset.
-  const int c3 = SWZ == 15 ? ((col >> 3) & 1) : 0;
-  uint32_t rd_even[4], rd_odd[4];
+  // Operand read offsets. 16-bit: key row (nb*32 + col), logical chunk h*8 + 2*ks + half,
+  // physical chunk (h*8 + 2*ks + half) ^ (col & SWZ) = 8*(h ^ c3) + ((2*ks + half) ^ (col & 7))
+  // with c3 = bit 3 of col when SWZ = 15: head h sits at 128*h + 128*c3 (h even) or
+  // 128*h - 128*c3 (h odd), so the head part stays an immediate offset. fp32: logical chunk
+  // h*16 + 2*m + half, physical h*16 + ((2*m + half) ^ (col & 15)) (SWZ = 15): head h at 256*h.
+  const int c3 = (!F32 && SWZ == 15) ? ((col >> 3) & 1) : 0;
+  uint32_t rd_even[HC], rd_odd[HC];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const uint32_t base = col * ROW_BYTES + 16 * ((2 * ks + half) ^ (col & 7));
-    rd_even[ks] = base + 128 * c3;
-    rd_odd[ks] = base - 128 * c3;
+  for (int ks = 0; ks < HC; ++ks) {
+    if constexpr (F32) {
+      static_assert(SWZ == 15, "fp32 rows hold >= 16 chunks");
+      rd_even[ks] = rd_odd[ks] = col * ROW_BYTES + 16 * ((2 * ks + half) ^ (col & 15));
+    } else {
+      const uint32_t base = col * ROW_BYTES + 16 * ((2 * ks + half) ^ (col & 7));
+      rd_even[ks] = base + 128 * c3;
+      rd_odd[ks] = base - 128 * c3;
+    }
   }
 
   // Gate values travel as raw 16-bit patterns until wstore converts them at the end of the
@@ -422,7 +451,7 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
     const int live = min(BN, nkeys - kb);
     if (!SAMPLE && live == BN) {
       // Full stage of consecutive keys: uniform base + lane offset + i * NW KB.
-      const char* kbase = reinterpret_cast<const char*>(p.k + ((int64_t)b * S + kb) * (HI * kDI));
+      const char* kbase = static_cast<const char*>(p.k) + ((int64_t)b * S + kb) * ROW_BYTES;
 #pragma unroll
       for (int i = 0; i < LOADS; ++i) lds_dma16_s(kbase, voffs[i], &ktile[(i * NW + wave) * 1024]);
     } else {
@@ -432,7 +461,7 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
         const int kl = min(kl0 + i * RPI, live - 1);
         const int key = sweep_key<SAMPLE>(kb + kl, p);
         const int lc = lc0 ^ ((i * RPI) & SWZ);
-        const uint16_t* src = p.k + ((int64_t)b * S + key) * (HI * kDI) + lc * 8;
+        const char* src = static_cast<const char*>(p.k) + ((int64_t)b * S + key) * ROW_BYTES + lc * 16;
         lds_dma16(src, &ktile[(i * NW + wave) * 1024]);
       }
     }
@@ -443,7 +472,7 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
       uint32_t wv = kNoGate;
       if (c < WVALS && kl < live) {
         const int key = sweep_key<SAMPLE>(kb + kl, p);
-        wv = p.w[((int64_t)b * S + key) * HI + h];
+        wv = raw_bits(E{}, p.w, ((int64_t)b * S + key) * HI + h);
       }
       wraw[i] = wv;
     }
@@ -454,7 +483,7 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
       const int c = tid + THREADS * i;
       if (c < WVALS) {
         const float wv = wraw[i] == kNoGate ? (SAMPLE ? 0.f : __builtin_nanf(""))
-                                            : to_f32(E{}, (uint16_t)wraw[i]) * p.scale;
+                                            : to_f32(E{}, wraw[i]) * p.scale;
         wtile[(c % HI) * BN + c / HI] = wv;
       }
     }
@@ -479,9 +508,17 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
     auto products = [&](int h) {
       f32x16 acc = f32x16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const uint4 kop = *reinterpret_cast<const uint4*>(tile + ((h & 1) ? rd_odd[ks] : rd_even[ks]) + h * 128);
-        acc = mfma32(E{}, kop, qop[h][ks], acc);
+      for (int ks = 0; ks < HC; ++ks) {
+        if constexpr (F32) {
+          const uint4 kop = *reinterpret_cast<const uint4*>(tile + rd_even[ks] + h * HEAD_BYTES);
+          acc = mfma32_f32(kop.x, qop[h][ks].x, acc);
+          acc = mfma32_f32(kop.y, qop[h][ks].y, acc);
+          acc = mfma32_f32(kop.z, qop[h][ks].z, acc);
+          acc = mfma32_f32(kop.w, qop[h][ks].w, acc);
+        } else {
+          const uint4 kop = *reinterpret_cast<const uint4*>(tile + ((h & 1) ? rd_odd[ks] : rd_even[ks]) + h * 128);
+          acc = mfma32(E{}, kop, qop[h][ks], acc);
+        }
       }
       return acc;
     };
@@ -511,7 +548,7 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int kidx = k4 + 8 * (r >> 2) + (r & 3);
-          if (kidx < nkeys) s[r] += to_f32(E{}, p.mask[grow * S + sweep_key<SAMPLE>(kidx, p)]);
+          if (kidx < nkeys) s[r] += ld_f32(E{}, p.mask, grow * S + sweep_key<SAMPLE>(kidx, p));
         }
       }
     }
@@ -521,7 +558,7 @@ __global__ __launch_bounds__(ScoreShape<HI>::THREADS, ScoreShape<HI>::MIN_WAVES_
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int kidx = k4 + 8 * (r >> 2) + (r & 3);
-          if (kidx < nkeys) s[r] += to_f32(E{}, vrow[clamp_view(sv[sweep_key<SAMPLE>(kidx, p)], p.Vs)]);
+          if (kidx < nkeys) s[r] += ld_f32(E{}, p.vbias, vrow + clamp_view(sv[sweep_key<SAMPLE>(kidx, p)], p.Vs));
         }
       }
     }
@@ -716,7 +753,7 @@ struct SelectParams {
   const int* counts;
   int nlist, cap, stride;
   int32_t* out_idx;
-  uint16_t* out_scores;
+  void* out_scores;  // [rows, Kk] in the element type of the launch
   int Kk;
   int* fb_count;
   int* fb_list;
@@ -853,7 +890,7 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
   }
   const int need_eq = p.Kk - n_gt;
   int32_t* oi = p.out_idx + row * p.Kk;
-  uint16_t* os = p.out_scores + row * p.Kk;
+  const int64_t os = row * p.Kk;
   int base = 0, eq_run = 0;
 #pragma unroll
   for (int m0 = 0; m0 < KS; m0 += 8) {
@@ -870,7 +907,7 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
         base += __popcll(selm);
         if (sel) {
           oi[slot_out] = ky[m];
-          os[slot_out] = (uint16_t)pack1(E{}, key2f(kv[m]));
+          st_f32(E{}, p.out_scores, os + slot_out, key2f(kv[m]));
         }
       }
     }
@@ -907,12 +944,12 @@ __global__ __launch_bounds__(256) void indexer_select_wide_kernel(const SelectPa
     auto key_at = [&](int i) { return keys[i]; };
     const uint32_t kth = block_radix_select(key_at, total, p.Kk, sh, take_eq);
     int32_t* oi = p.out_idx + row * p.Kk;
-    uint16_t* os = p.out_scores + row * p.Kk;
+    const int64_t os = row * p.Kk;
     block_emit_topk(key_at, total, p.Kk, kth, take_eq,
                     [&](int slot, int i) {
                       if (slot < p.Kk) {
                         oi[slot] = vals[i];
-                        os[slot] = (uint16_t)pack1(E{}, key2f(keys[i]));
+                        st_f32(E{}, p.out_scores, os + slot, key2f(keys[i]));
                       }
                     },
                     sh);
@@ -924,11 +961,11 @@ __global__ __launch_bounds__(256) void indexer_select_wide_kernel(const SelectPa
 // Exact brute force for queued queries.
 // ---------------------------------------------------------------------------------------
 struct FallbackParams {
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* w;
-  const uint16_t* mask;
-  const uint16_t* vbias;
+  const void* q;
+  const void* k;
+  const void* w;
+  const void* mask;
+  const void* vbias;
   const int* qview;
   const int* sview;
   int Vq, Vs;
@@ -936,14 +973,37 @@ struct FallbackParams {
   const int* fb_list;
   float* scratch;  // [gridDim.x, S]
   int32_t* out_idx;
-  uint16_t* out_scores;
+  void* out_scores;
   int T, S, Kk;
   float scale;
 };
 
+// Dot product of two 16-byte chunks accumulated onto z: 8 x 16-bit elements (dot2 pairs)
+// or 4 x fp32.
+__device__ __forceinline__ float dot_chunk(BF16, uint4 a, uint4 b, float z) {
+  z = dot2(BF16{}, a.x, b.x, z);
+  z = dot2(BF16{}, a.y, b.y, z);
+  z = dot2(BF16{}, a.z, b.z, z);
+  return dot2(BF16{}, a.w, b.w, z);
+}
+__device__ __forceinline__ float dot_chunk(FP16, uint4 a, uint4 b, float z) {
+  z = dot2(FP16{}, a.x, b.x, z);
+  z = dot2(FP16{}, a.y, b.y, z);
+  z = dot2(FP16{}, a.z, b.z, z);
+  return dot2(FP16{}, a.w, b.w, z);
+}
+__device__ __forceinline__ float dot_chunk(FP32, uint4 a, uint4 b, float z) {
+  z = fmaf(__uint_as_float(a.x), __uint_as_float(b.x), z);
+  z = fmaf(__uint_as_float(a.y), __uint_as_float(b.y), z);
+  z = fmaf(__uint_as_float(a.z), __uint_as_float(b.z), z);
+  return fmaf(__uint_as_float(a.w), __uint_as_float(b.w), z);
+}
+
 template <typename E, int HI, int BIAS>
 __global__ __launch_bounds__(256) void indexer_fallback_kernel(const FallbackParams p) {
-  __shared__ __attribute__((aligned(16))) uint32_t qs[HI * kDI / 2];
+  constexpr int ROW_BYTES = row_bytes<E, HI>();
+  constexpr int HEAD_CHUNKS = kDI * ElemBytes<E>::value / 16;
+  __shared__ __attribute__((aligned(16))) uint4 qs[ROW_BYTES / 16];
   __shared__ SelectShared sh;
   const int tid = threadIdx.x;
   const int nitems = *((volatile const int*)p.fb_count);
@@ -951,31 +1011,25 @@ __global__ __launch_bounds__(256) void indexer_fallback_kernel(const FallbackPar
   for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
     const int row = p.fb_list[item];
     const int b = row / p.T;
-    const uint32_t* qrow = reinterpret_cast<const uint32_t*>(p.q + (int64_t)row * HI * kDI);
-    for (int i = tid; i < HI * kDI / 2; i += kSelThreads) qs[i] = qrow[i];
+    const uint4* qrow = reinterpret_cast<const uint4*>(static_cast<const char*>(p.q) + (int64_t)row * ROW_BYTES);
+    for (int i = tid; i < ROW_BYTES / 16; i += kSelThreads) qs[i] = qrow[i];
     __syncthreads();
     for (int j = tid; j < p.S; j += kSelThreads) {
-      const uint4* kr = reinterpret_cast<const uint4*>(p.k + ((int64_t)b * p.S + j) * HI * kDI);
+      const uint4* kr = reinterpret_cast<const uint4*>(static_cast<const char*>(p.k) + ((int64_t)b * p.S + j) * ROW_BYTES);
       float s = 0.f;
 #pragma unroll
       for (int h = 0; h < HI; ++h) {
         float z = 0.f;
 #pragma unroll
-        for (int c = 0; c < kDI / 8; ++c) {
-          const uint4 kv = kr[h * (kDI / 8) + c];
-          const uint4 qv = *reinterpret_cast<const uint4*>(&qs[h * (kDI / 2) + c * 4]);
-          z = dot2(E{}, qv.x, kv.x, z);
-          z = dot2(E{}, qv.y, kv.y, z);
-          z = dot2(E{}, qv.z, kv.z, z);
-          z = dot2(E{}, qv.w, kv.w, z);
-        }
-        const float wv = to_f32(E{}, p.w[((int64_t)b * p.S + j) * HI + h]) * p.scale;
+        for (int c = 0; c < HEAD_CHUNKS; ++c) z = dot_chunk(E{}, qs[h * HEAD_CHUNKS + c], kr[h * HEAD_CHUNKS + c], z);
+        const float wv = ld_f32(E{}, p.w, ((int64_t)b * p.S + j) * HI + h) * p.scale;
         s = fmaf(wv, relu_bits(z), s);
       }
-      if constexpr ((BIAS & kBiasMask) != 0) s += to_f32(E{}, p.mask[(int64_t)row * p.S + j]);
+      if constexpr ((BIAS & kBiasMask) != 0) s += ld_f32(E{}, p.mask, (int64_t)row * p.S + j);
       if constexpr ((BIAS & kBiasView) != 0)
-        s += to_f32(E{}, p.vbias[((int64_t)b * p.Vq + clamp_view(p.qview[row], p.Vq)) * p.Vs +
-                                 clamp_view(p.sview[(int64_t)b * p.S + j], p.Vs)]);
+        s += ld_f32(E{}, p.vbias,
+                    ((int64_t)b * p.Vq + clamp_view(p.qview[row], p.Vq)) * p.Vs +
+                        clamp_view(p.sview[(int64_t)b * p.S + j], p.Vs));
       sc[j] = s;
     }
     __threadfence_block();
@@ -984,12 +1038,12 @@ __global__ __launch_bounds__(256) void indexer_fallback_kernel(const FallbackPar
     auto key_at = [&](int i) { return f2key(sc[i]); };
     const uint32_t kth = block_radix_select(key_at, p.S, p.Kk, sh, take_eq);
     int32_t* oi = p.out_idx + (int64_t)row * p.Kk;
-    uint16_t* os = p.out_scores + (int64_t)row * p.Kk;
+    const int64_t os = (int64_t)row * p.Kk;
     block_emit_topk(key_at, p.S, p.Kk, kth, take_eq,
                     [&](int slot, int i) {
                       if (slot < p.Kk) {
                         oi[slot] = i;
-                        os[slot] = (uint16_t)pack1(E{}, sc[i]);
+                        st_f32(E{}, p.out_scores, os + slot, sc[i]);
                       }
                     },
                     sh);
@@ -1091,9 +1145,10 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   int* fb_count = reinterpret_cast<int*>(ws + pl.off_fb);  // [0] brute force, [1] wide select
   hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(64), 0, st, fb_count, 0);
   GW_HIP_LAUNCH_CHECK("set_int_kernel");
-  constexpr int BM = ScoreShape<HI>::BM;
-  constexpr int THREADS = ScoreShape<HI>::THREADS;
-  constexpr int BN = ScoreShape<HI>::BN;
+  using Shape = ScoreShape<row_bytes<E, HI>()>;
+  constexpr int BM = Shape::BM;
+  constexpr int THREADS = Shape::THREADS;
+  constexpr int BN = Shape::BN;
   const int64_t tiles = (base.T + BM - 1) / BM;
   const int64_t rows = B * (int64_t)base.T;
   pl.nsplit = choose_nsplit(tiles * B, base.S, filter_slots((const void*)indexer_score_kernel<E, HI, false, BIAS>, THREADS),
@@ -1139,7 +1194,7 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   fs.cap = pl.cap;
   fs.stride = stride;
   fs.out_idx = out_idx;
-  fs.out_scores = static_cast<uint16_t*>(out_scores);
+  fs.out_scores = out_scores;
   fs.Kk = pl.Kk;
   fs.fb_count = fb_count;
   fs.fb_list = reinterpret_cast<int*>(ws + pl.off_fblist);
@@ -1183,7 +1238,12 @@ int dispatch_hi(int hi, const ScoreParams& base, const Plan& pl, int64_t B, int3
     case 1: return run_typed<E, 1, BIAS>(base, pl, B, out_idx, out_scores, ws, st);
     case 2: return run_typed<E, 2, BIAS>(base, pl, B, out_idx, out_scores, ws, st);
     case 4: return run_typed<E, 4, BIAS>(base, pl, B, out_idx, out_scores, ws, st);
-    default: return run_typed<E, 8, BIAS>(base, pl, B, out_idx, out_scores, ws, st);
+    default:
+      // fp32 rows of 8 heads would need 256 registers of stationary query operands.
+      if constexpr (ElemBytes<E>::value == 4)
+        return set_error(GW_ERR_UNSUPPORTED, "fp32 indexer inputs support 1, 2 or 4 heads, got %d", hi);
+      else
+        return run_typed<E, 8, BIAS>(base, pl, B, out_idx, out_scores, ws, st);
   }
 }
 
@@ -1203,12 +1263,15 @@ int indexer_topk_impl(int dtype, const void* q, const void* k, const void* w, co
                       int64_t Vs, int64_t B, int64_t T, int64_t S, int64_t Hi, int64_t Di, int64_t topk,
                       float softmax_scale, int flags, int32_t* out_indices, void* out_scores, void* workspace,
                       size_t workspace_bytes, void* stream) {
-  GW_CHECK_ARG(dtype == GW_DTYPE_BF16 || dtype == GW_DTYPE_FP16, "unsupported dtype code %d", dtype);
+  GW_CHECK_ARG(dtype == GW_DTYPE_BF16 || dtype == GW_DTYPE_FP16 || dtype == GW_DTYPE_FP32, "unsupported dtype code %d",
+               dtype);
   GW_CHECK_ARG(B >= 0 && T >= 0 && S >= 0 && topk >= 1, "invalid sizes B=%lld T=%lld S=%lld topk=%lld",
                (long long)B, (long long)T, (long long)S, (long long)topk);
   if (Di != kDI || !(Hi == 1 || Hi == 2 || Hi == 4 || Hi == 8))
     return set_error(GW_ERR_UNSUPPORTED, "indexer heads x dim %lld x %lld not supported (1/2/4/8 x 64)",
                      (long long)Hi, (long long)Di);
+  if (dtype == GW_DTYPE_FP32 && Hi == 8)
+    return set_error(GW_ERR_UNSUPPORTED, "fp32 indexer inputs support 1, 2 or 4 heads, got %lld", (long long)Hi);
   GW_CHECK_ARG(softmax_scale > 0.f, "softmax_scale must be positive, got %g", (double)softmax_scale);
   GW_CHECK_ARG((flags & ~7) == 0 && (flags & 3) != 3, "invalid flags %d", flags);
   const bool has_view = view_bias != nullptr;
@@ -1233,11 +1296,11 @@ int indexer_topk_impl(int dtype, const void* q, const void* k, const void* w, co
   GW_CHECK_ARG(gw::aligned16(workspace), "workspace must be 16-byte aligned");
 
   ScoreParams base{};
-  base.q = static_cast<const uint16_t*>(q);
-  base.k = static_cast<const uint16_t*>(k);
-  base.w = static_cast<const uint16_t*>(w);
-  base.mask = static_cast<const uint16_t*>(mask);
-  base.vbias = static_cast<const uint16_t*>(view_bias);
+  base.q = q;
+  base.k = k;
+  base.w = w;
+  base.mask = mask;
+  base.vbias = view_bias;
   base.qview = q_view_ids;
   base.sview = s_view_ids;
   base.Vq = (int)Vq;
@@ -1259,6 +1322,14 @@ int indexer_topk_impl(int dtype, const void* q, const void* k, const void* w, co
       case kBiasMask: return dispatch_hi<BF16, kBiasMask>(hi, base, pl, B, out_indices, out_scores, ws, st);
       case kBiasView: return dispatch_hi<BF16, kBiasView>(hi, base, pl, B, out_indices, out_scores, ws, st);
       default: return dispatch_hi<BF16, kBiasMask | kBiasView>(hi, base, pl, B, out_indices, out_scores, ws, st);
+    }
+  }
+  if (dtype == GW_DTYPE_FP32) {
+    switch (bias) {
+      case 0: return dispatch_hi<FP32, 0>(hi, base, pl, B, out_indices, out_scores, ws, st);
+      case kBiasMask: return dispatch_hi<FP32, kBiasMask>(hi, base, pl, B, out_indices, out_scores, ws, st);
+      case kBiasView: return dispatch_hi<FP32, kBiasView>(hi, base, pl, B, out_indices, out_scores, ws, st);
+      default: return dispatch_hi<FP32, kBiasMask | kBiasView>(hi, base, pl, B, out_indices, out_scores, ws, st);
     }
   }
   switch (bias) {

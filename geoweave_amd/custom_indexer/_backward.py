@@ -29,7 +29,7 @@ def indexer_topk_backward(q, k, w, topk_indices, grad_scores, softmax_scale):
     ws_bytes = int(lib.gw_indexer_topk_bwd_workspace_size(bsz, tgt_len, src_len, n_heads, head_dim, num_topk))
     ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
     rc = lib.gw_indexer_topk_bwd(
-        _lib.dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), w.data_ptr(),
+        _lib.dtype_code(q.dtype, allow_fp32=True), q.data_ptr(), k.data_ptr(), w.data_ptr(),
         topk_indices.data_ptr(), grad_scores.data_ptr(), dq.data_ptr(), dk.data_ptr(), dw.data_ptr(),
         bsz, tgt_len, src_len, n_heads, head_dim, num_topk, float(softmax_scale),
         csr.data_ptr(), csr_bytes, ws.data_ptr(), ws_bytes, _lib.stream_handle(q.device),

@@ -12,9 +12,13 @@ blockwise host loop; this implementation has no such loop and ignores them.
 used by the reference caller (``easyvolcap/official_vggt/layers/indexer.py:570-581``);
 the reference package leaves it ``None`` (``custom_indexer/__init__.py:7``).
 
-Inputs: q ``[B,T,Hi,Di]``, k ``[B,S,Hi,Di]``, w ``[B,S,Hi]`` in one 16-bit float dtype on
-the GPU; mask: ``None``, an empty tensor, or an additive ``[B,T,S]`` (broadcast from
-``[T,S]``/``[1,T,S]``). Supported: ``Di = 64``, ``Hi in {1,2,4,8}``, ``K <= 2048``.
+Inputs: q ``[B,T,Hi,Di]``, k ``[B,S,Hi,Di]``, w ``[B,S,Hi]`` in one float dtype on the GPU:
+bfloat16 or float16 (bf16/fp16 matrix-core products, fp32 accumulation) or float32 (fp32
+matrix-core products; the reference computes in ``q.dtype`` too, ``:1293``, and its caller
+may cast to ``score_dtype="float32"``, ``indexer.py:321-326``); scores come back in
+``q.dtype``. mask: ``None``, an empty tensor, or an additive ``[B,T,S]`` (broadcast from
+``[T,S]``/``[1,T,S]``), cast to ``q.dtype`` as the reference does (``:1299-1300``).
+Supported: ``Di = 64``, ``Hi in {1,2,4,8}`` (``{1,2,4}`` in float32), ``K <= 2048``.
 
 ``view_bias_data`` (the soft view-bias training kernel, reference ``:2108-2186``): a dict
 with ``q_view_ids`` ``[B,T]``/``[T]``, ``s_view_ids`` ``[B,S]``/``[S]`` and ``view_bias``
@@ -62,12 +66,14 @@ def _check(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor):
         raise ValueError(f"w shape {tuple(w.shape)} mismatches q {tuple(q.shape)} and k {tuple(k.shape)}")
     if not (q.dtype == k.dtype == w.dtype):
         raise TypeError("q, k and w must have the same dtype")
-    if q.dtype not in (torch.float16, torch.bfloat16):
-        raise TypeError(f"the HIP indexer takes bfloat16 or float16 inputs, got {q.dtype}")
+    if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise TypeError(f"the HIP indexer takes bfloat16, float16 or float32 inputs, got {q.dtype}")
     if not (q.is_cuda and k.is_cuda and w.is_cuda):
         raise ValueError("q, k and w must be GPU tensors")
     if head_dim != 64 or n_heads not in (1, 2, 4, 8):
         raise NotImplementedError(f"indexer heads x dim {n_heads} x {head_dim} not built (1/2/4/8 x 64)")
+    if q.dtype == torch.float32 and n_heads == 8:
+        raise NotImplementedError("float32 indexer inputs are built for 1, 2 or 4 heads")
 
 
 def _normalize_view_bias_data(view_bias_data: Optional[dict], bsz: int, tgt_len: int, src_len: int,
@@ -151,7 +157,7 @@ def indexer_topk_forward(
     if view_bias is not None:
         qv, sv, table = view_bias
         rc = lib.gw_indexer_topk_fwd_view_bias(
-            _lib.dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), w.data_ptr(), _lib.ptr(mask),
+            _lib.dtype_code(q.dtype, allow_fp32=True), q.data_ptr(), k.data_ptr(), w.data_ptr(), _lib.ptr(mask),
             table.data_ptr(), qv.data_ptr(), sv.data_ptr(), int(table.shape[1]), int(table.shape[2]),
             bsz, tgt_len, src_len, n_heads, head_dim, kk, float(softmax_scale), int(flags),
             idx.data_ptr(), scores.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_handle(q.device),
@@ -159,7 +165,7 @@ def indexer_topk_forward(
         _lib.check(rc, "gw_indexer_topk_fwd_view_bias")
         return idx, scores
     rc = lib.gw_indexer_topk_fwd(
-        _lib.dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), w.data_ptr(), _lib.ptr(mask),
+        _lib.dtype_code(q.dtype, allow_fp32=True), q.data_ptr(), k.data_ptr(), w.data_ptr(), _lib.ptr(mask),
         bsz, tgt_len, src_len, n_heads, head_dim, kk, float(softmax_scale), int(flags),
         idx.data_ptr(), scores.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_handle(q.device),
     )
@@ -213,10 +219,10 @@ def view_bias_backward(topk_indices: torch.Tensor, grad_scores: torch.Tensor, q_
     rows = torch.empty((bsz, tgt_len, n_s), device=grad_scores.device, dtype=torch.float32)
     if bsz * tgt_len > 0:
         g = grad_scores.to(topk_indices.device).contiguous()
-        if g.dtype not in (torch.float16, torch.bfloat16):
-            raise TypeError(f"grad_scores must be bfloat16 or float16, got {g.dtype}")
+        if g.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            raise TypeError(f"grad_scores must be bfloat16, float16 or float32, got {g.dtype}")
         rc = _lib.load().gw_indexer_view_bias_bwd_rows(
-            _lib.dtype_code(g.dtype), topk_indices.contiguous().data_ptr(), g.data_ptr(), s_view_ids.data_ptr(),
+            _lib.dtype_code(g.dtype, allow_fp32=True), topk_indices.contiguous().data_ptr(), g.data_ptr(), s_view_ids.data_ptr(),
             bsz, tgt_len, src_len, kk, n_s, rows.data_ptr(), _lib.stream_handle(g.device))
         _lib.check(rc, "gw_indexer_view_bias_bwd_rows")
     onehot = torch.nn.functional.one_hot(q_view_ids.long(), n_q).to(torch.float32)  # [B, T, Vq]

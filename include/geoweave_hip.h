@@ -15,8 +15,12 @@
  *  - Return value: GW_OK or an error code; gw_last_error() then gives a message for the
  *    calling thread. The Python binding turns a non-zero code into RuntimeError, as the
  *    reference's TORCH_CHECK does (custom_indexer/csrc/topk_exact.cpp:12-35).
- *  - dtype: GW_DTYPE_BF16 or GW_DTYPE_FP16 for q/k/v/w (the reference accepts only
- *    fp16/bf16 on its kernel path: sparse_index_flash_attn.py:2036).
+ *  - dtype: the attention entry points take GW_DTYPE_BF16 or GW_DTYPE_FP16 for q/k/v (the
+ *    reference's attention accepts only fp16/bf16: sparse_index_flash_attn.py:2036; its
+ *    caller casts fp32 to 16 bits first, dsa_attention.py:5296-5300). The indexer top-k,
+ *    its backward and its view-bias gradient also take GW_DTYPE_FP32 (the reference's
+ *    indexer computes in q.dtype, any float type: sparse_topk_indexer.py:1293, and its
+ *    caller may cast to score_dtype float32: indexer.py:321-326).
  */
 #ifndef GEOWEAVE_HIP_H
 #define GEOWEAVE_HIP_H
@@ -35,7 +39,7 @@ extern "C" {
 
 #define GW_DTYPE_BF16 0
 #define GW_DTYPE_FP16 1
-#define GW_DTYPE_FP32 2 /* accepted only by the gw_indexer_kl_* entry points */
+#define GW_DTYPE_FP32 2 /* the indexer entry points and gw_indexer_kl_* only */
 
 /* Message for the last failed call on this thread ("" if none). */
 const char* gw_last_error(void);
@@ -95,10 +99,12 @@ int gw_sparse_attn_fwd(int dtype,
  * out_indices[b,t,:] (int32) = the Kk = min(topk, S) keys with the largest scores, in
  * unspecified order (the reference uses sorted=False); out_scores (same dtype as q) = their
  * scores. Exact: the set equals the fp32 top-k except where scores tie within rounding;
- * ties are broken deterministically. Scores are accumulated in fp32.
+ * ties are broken deterministically. Scores are accumulated in fp32 (bf16/fp16 products
+ * are exact in fp32; fp32 inputs use fp32 matrix-core products).
  *
- * q: [B,T,Hi,Di], k: [B,S,Hi,Di], w: [B,S,Hi], mask: [B,T,S], all contiguous, same dtype.
- * Supported: Di = 64, Hi in {1,2,4,8}, topk <= 2048, softmax_scale > 0.
+ * q: [B,T,Hi,Di], k: [B,S,Hi,Di], w: [B,S,Hi], mask: [B,T,S], all contiguous, same dtype
+ * (bf16, fp16 or fp32). Supported: Di = 64, Hi in {1,2,4,8} ({1,2,4} for fp32),
+ * topk <= 2048, softmax_scale > 0.
  * workspace: gw_indexer_topk_workspace_size(B, T, S, topk) bytes, 16-byte aligned.
  * flags: 0 normally. Test hooks that force the exact fallback paths:
  *   GW_TOPK_FLAG_TAU_PLUS_INF  - no key passes the candidate filter (every query falls
@@ -210,8 +216,8 @@ int gw_sparse_attn_bwd(int dtype,
  * 2091-2106, :757-895, :1847-1944). For every selected (t, j), s = topk_indices[b,t,j],
  * g = grad_scores[b,t,j], per head h: z = scale * q[t,h].k[s,h];
  * f = g * w[s,h] * [z > 0] * scale; dq[t,h] += f k[s,h]; dk[s,h] += f q[t,h];
- * dw[s,h] += g relu(z). q/k/w/grad contiguous in one 16-bit dtype; outputs dq, dk, dw
- * in that dtype, accumulated in fp32 with no atomics; every element is written.
+ * dw[s,h] += g relu(z). q/k/w/grad contiguous in one dtype (bf16, fp16 or fp32); outputs
+ * dq, dk, dw in that dtype, accumulated in fp32 with no atomics; every element is written.
  * csr: built by gw_kv_csr_build from topk_indices (strides K*T, K). Supported: Di = 64,
  * Hi in {1,2,4,8}. workspace: gw_indexer_topk_bwd_workspace_size(...) bytes.
  */
@@ -232,8 +238,8 @@ int gw_indexer_topk_bwd(int dtype, const void* q, const void* k, const void* w,
  * sum of grad_scores[b,t,j] over the j whose key s = topk_indices[b,t,j] has
  * s_view_ids[b,s] == v, summed in a fixed order (no atomics); positions outside [0, S) add
  * nothing. grad_view_bias[b, vq, v] is then the sum of row_grad[b,t,v] over the rows with
- * q_view_ids[b,t] == vq (the host's one-hot product). grad_scores: [B, T, K] in the 16-bit
- * dtype; s_view_ids: [B, S] int32.
+ * q_view_ids[b,t] == vq (the host's one-hot product). grad_scores: [B, T, K] in bf16, fp16
+ * or fp32; s_view_ids: [B, S] int32.
  */
 int gw_indexer_view_bias_bwd_rows(int dtype, const int32_t* topk_indices, const void* grad_scores,
                                   const int32_t* s_view_ids, int64_t B, int64_t T, int64_t S, int64_t K,

@@ -185,3 +185,32 @@ def test_dense_fwd_workspace_and_argument_checks_without_gpu():
     assert b"lse" in lib.gw_last_error()
     assert _dense_call(q=18, ws=4096, ws_bytes=1 << 20) == 1
     assert _dense_call(B=0) == 0  # nothing to do
+
+
+def _topk_call(**over):
+    lib = _lib.load()
+    args = dict(dtype=2, q=16, k=16, w=16, mask=None, B=1, T=4, S=4, Hi=4, Di=64, topk=2, scale=0.125,
+                flags=0, idx=16, sc=16, ws=None, ws_bytes=0)
+    args.update(over)
+    return lib.gw_indexer_topk_fwd(args["dtype"], args["q"], args["k"], args["w"], args["mask"], args["B"],
+                                   args["T"], args["S"], args["Hi"], args["Di"], args["topk"], args["scale"],
+                                   args["flags"], args["idx"], args["sc"], args["ws"], args["ws_bytes"], None)
+
+
+def test_indexer_fwd_dtype_rules_without_gpu():
+    # fp32 is a valid indexer dtype (the reference computes in q.dtype,
+    # sparse_topk_indexer.py:1293); 8 fp32 heads are not built; other codes are invalid.
+    lib = _lib.load()
+    assert _topk_call(dtype=3) == 1 and b"dtype" in lib.gw_last_error()
+    assert _topk_call(dtype=2, Hi=8) == 2 and b"fp32" in lib.gw_last_error()
+    for dt in (0, 1, 2):
+        assert _topk_call(dtype=dt) == 1 and b"workspace" in lib.gw_last_error()  # passes the dtype check
+    assert _topk_call(dtype=2, B=0) == 0
+
+
+def test_indexer_dtype_codes_in_python():
+    assert _lib.dtype_code(torch.float32, allow_fp32=True) == _lib.GW_DTYPE_FP32
+    with pytest.raises(TypeError, match="bfloat16 or float16"):
+        _lib.dtype_code(torch.float32)
+    with pytest.raises(TypeError):
+        _lib.dtype_code(torch.float64, allow_fp32=True)

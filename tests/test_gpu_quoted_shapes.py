@@ -127,6 +127,57 @@ def test_c4_indexer_indices_training_forward_and_backward(gpu_device):
     assert dk.sum(1).abs().max() < 0.5
 
 
+def _euler_sums(x, dx, rows_dim):
+    """sum over heads and dims of x * dx per row (fp32)."""
+    return (x.float() * dx.float()).reshape(x.shape[0], x.shape[1], -1).sum(-1)
+
+
+def test_c4_indexer_backward(gpu_device):
+    # The indexer backward at C4 (B = 2, S = 24, N = 32,976) on the indexer's own indices:
+    # dq on sampled rows of both batch elements and dk/dw on sampled keys (the most-selected
+    # key of each element among them) against the oracle; a z within rounding of 0 may flip
+    # the relu gate relative to the oracle, so at most 0.1 % of elements may exceed the
+    # tolerance. Every row and key is then checked through the score's degree-1 homogeneity
+    # (score = sum_h w relu(scale q.k) is linear in q, in k and in w along each ray):
+    #   sum_h q[t,h].dq[t,h] = sum_j g[t,j] score[t,j]                 (every row t)
+    #   sum_h k[s,h].dk[s,h] = sum_h w[s,h] dw[s,h] = sum_{idx[t,j]=s} g[t,j] score[t,j]
+    views, B = 24, 2
+    lay = workloads.layer_inputs(views, B, torch.bfloat16)
+    n = lay.tokens
+    print(f"[C4 indexer backward] B={B} S={views} N={n}", flush=True)
+    qi, ki, wi = (x.cuda() for x in (lay.q_idx, lay.k_idx, lay.w_idx))
+    idx, sc = sti.sparse_topk_indexer_inference_func(qi, ki, wi, qi.new_empty(0), 1024, 0.125, 256, 0)
+    g = torch.Generator().manual_seed(2400)
+    gs = torch.randn(B, n, 1024, generator=g).bfloat16()
+    dq, dk, dw = sti.indexer_topk_backward(qi, ki, wi, idx, gs.cuda(), 0.125)
+    torch.cuda.synchronize()
+    idx, sc = idx.cpu(), sc.cpu()
+    dq, dk, dw = dq.float().cpu(), dk.float().cpu(), dw.float().cpu()
+    for b in range(B):
+        rows = torch.randperm(n, generator=g)[:64]
+        rq, _, _ = oidx.indexer_topk_bwd(lay.q_idx[b:b + 1, rows], lay.k_idx[b:b + 1], lay.w_idx[b:b + 1],
+                                         idx[b:b + 1, rows], gs[b:b + 1, rows], 0.125)
+        counts = torch.bincount(idx[b].reshape(-1).long(), minlength=n)
+        keys = torch.cat([counts.argmax().view(1), torch.randperm(n, generator=g)[:15]])
+        rk, rw = oidx.indexer_topk_bwd_keys(lay.q_idx[b:b + 1], lay.k_idx[b:b + 1], lay.w_idx[b:b + 1],
+                                            idx[b:b + 1], gs[b:b + 1], keys, 0.125)
+        for got, ref in ((dq[b:b + 1, rows], rq), (dk[b:b + 1, keys], rk), (dw[b:b + 1, keys], rw)):
+            bad = ~torch.isclose(got, ref, **TOL)
+            assert bad.float().mean() <= 1e-3, f"batch {b}: {int(bad.sum())} of {bad.numel()} outside tolerance"
+    gsc = gs.float() * sc.float()  # [B, T, K]
+    row_rhs, row_mag = gsc.sum(-1), gsc.abs().sum(-1)
+    row_lhs = _euler_sums(lay.q_idx, dq, 2)
+    assert bool(((row_lhs - row_rhs).abs() <= 2e-2 * row_mag + 1e-3).all()), "row identity sum q.dq"
+    for b in range(B):
+        flat = idx[b].reshape(-1).long()
+        key_rhs = torch.zeros(n).index_add_(0, flat, gsc[b].reshape(-1))
+        key_mag = torch.zeros(n).index_add_(0, flat, gsc[b].reshape(-1).abs())
+        lhs_k = _euler_sums(lay.k_idx[b:b + 1], dk[b:b + 1], 2)[0]
+        lhs_w = (lay.w_idx[b].float() * dw[b]).sum(-1)
+        assert bool(((lhs_k - key_rhs).abs() <= 2e-2 * key_mag + 1e-3).all()), f"batch {b}: key identity k.dk"
+        assert bool(((lhs_w - key_rhs).abs() <= 2e-2 * key_mag + 1e-3).all()), f"batch {b}: key identity w.dw"
+
+
 def test_c5_aggregator_sparse_layers_sampled(gpu_device, monkeypatch):
     # The C5 workload of the bench (aggregator.random_init_, seeded images); the first (9)
     # and last (19) sparse layers' indexer and attention inputs are captured in the forward.
