@@ -70,8 +70,9 @@ def parse_score_dtype(value) -> Optional[torch.dtype]:
     """The reference's dtype spelling (``DSAAttention._parse_dtype``,
     ``dsa_attention.py:503-518``): a torch dtype, or "fp16"/"float16"/"half"/"f16",
     "bf16"/"bfloat16", "fp32"/"float32"/"f32"; None, "", "none" and (as in the reference)
-    any other string mean "the activations' dtype". fp32 is refused: the HIP kernels
-    compute on 16-bit inputs."""
+    any other string mean "the activations' dtype". With float32 the indexer computes in
+    fp32 and the attention casts its fp32 q/k/v to bfloat16, as the reference does
+    (``dsa_attention.py:4943-4948,5296-5300``)."""
     if value is None:
         return None
     if isinstance(value, str):
@@ -86,9 +87,9 @@ def parse_score_dtype(value) -> Optional[torch.dtype]:
         value = table[text]
     if not isinstance(value, torch.dtype):
         raise TypeError(f"score_dtype must be a torch dtype or a string, not {type(value).__name__}")
-    if value not in (torch.bfloat16, torch.float16):
-        raise TypeError(f"score_dtype {value} is not supported: the indexer and attention kernels take "
-                        "bfloat16 or float16")
+    if value not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError(f"score_dtype {value} is not supported: the indexer takes bfloat16, float16 or "
+                        "float32 and the attention bfloat16 or float16")
     return value
 
 
@@ -334,11 +335,16 @@ class SparseGlobalAttention(nn.Module):
         self.layout = GlueLayout(num_heads, self.head_dim, indexer_heads, indexer_dim)
         self._fused = None
 
-    def _to_score_dtype(self, x_dtype: torch.dtype, *tensors):
+    def _to_score_dtype(self, x_dtype: torch.dtype, q, k, v, iq, ik, iw):
+        """Attention q/k/v and indexer q/k/w in the score dtype (``dsa_attention.py:4943-4948``,
+        ``indexer.py:321-326``); a float32 score dtype reaches the attention as bfloat16
+        (``dsa_attention.py:5296-5300``: fp32 q/k/v become bf16 before the sparse kernel)."""
         sd = self.score_dtype
         if sd is None or sd == x_dtype:
-            return tensors
-        return tuple(None if t is None else t.to(sd) for t in tensors)
+            return q, k, v, iq, ik, iw
+        ad = torch.bfloat16 if sd == torch.float32 else sd
+        cast = lambda t, dt: None if t is None else t.to(dt)  # noqa: E731
+        return cast(q, ad), cast(k, ad), cast(v, ad), cast(iq, sd), cast(ik, sd), cast(iw, sd)
 
     def fused_projection(self, dtype: torch.dtype):
         """(W [ldy, dim], b [ldy]) in ``dtype``: ``[qkv | q_proj | k_proj | w_proj]`` plus zero

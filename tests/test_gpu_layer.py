@@ -265,13 +265,14 @@ def test_glue_backward_matches_autograd_of_the_oracle(gpu_device, with_ln, with_
                 assert err < 2e-3, (key, err)
 
 
-@pytest.mark.parametrize("score_dtype", [None, "float16"])
+@pytest.mark.parametrize("score_dtype", [None, "float16", "float32"])
 def test_layer_training_gradients_match_the_fp32_pipeline(gpu_device, score_dtype):
     # forward_train + KL loss through every HIP backward (glue, indexer, attention, KL) vs
     # autograd of the fp32 CPU pipeline on the same bf16 inputs/weights and the GPU's own
     # top-k indices. Bar: per-tensor relative error (norm) within 2e-2. With score_dtype
     # "float16" the indexer and attention run on fp16 casts of the glue's bf16 outputs and
-    # their gradients return through the casts.
+    # their gradients return through the casts; with "float32" the indexer runs in fp32 and
+    # the attention in bf16.
     from geoweave_amd.custom_indexer import sparse_indexer_kl_loss
     from oracle import kl_loss as okl
 
@@ -294,7 +295,7 @@ def test_layer_training_gradients_match_the_fp32_pipeline(gpu_device, score_dtyp
 
     xd = x.cuda().requires_grad_()
     out, attn, scores, idx = m.forward_train(xd, pos.cuda())
-    assert scores.dtype == (torch.float16 if score_dtype else torch.bfloat16)
+    assert scores.dtype == {None: torch.bfloat16, "float16": torch.float16, "float32": torch.float32}[score_dtype]
     assert out.dtype == torch.bfloat16
     p = attn.to(torch.bfloat16)
     p = p / (p.sum(-1, keepdim=True) + 1e-6)

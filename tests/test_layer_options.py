@@ -16,13 +16,24 @@ def test_score_dtype_spellings_follow_the_reference(text, want):
     assert dsa_layer.parse_score_dtype(text) == want
 
 
-def test_score_dtype_accepts_torch_dtypes_and_refuses_fp32():
+def test_score_dtype_accepts_torch_dtypes():
     assert dsa_layer.parse_score_dtype(torch.float16) == torch.float16
-    for bad in ("fp32", "float32", torch.float32):
+    for fp32 in ("fp32", "float32", "f32", torch.float32):
+        assert dsa_layer.parse_score_dtype(fp32) == torch.float32
+    for bad in (torch.float64, torch.int8):
         with pytest.raises(TypeError):
             dsa_layer.parse_score_dtype(bad)
     with pytest.raises(TypeError):
         dsa_layer.parse_score_dtype(16)
+
+
+def test_float32_score_dtype_casts_the_attention_to_bfloat16():
+    # dsa_attention.py:4943-4948 casts q/k/v to the score dtype, :5296-5300 casts fp32 q/k/v
+    # to bf16 before the sparse kernel; indexer.py:321-326 casts the indexer q/k/w.
+    m = dsa_layer.SparseGlobalAttention(dim=128, num_heads=2, topk=8, score_dtype="float32")
+    t = torch.zeros(2, dtype=torch.float16)
+    out = m._to_score_dtype(torch.float16, t, t, t, t, t, t)
+    assert [x.dtype for x in out] == [torch.bfloat16] * 3 + [torch.float32] * 3
 
 
 def test_layer_keeps_the_score_dtype():
