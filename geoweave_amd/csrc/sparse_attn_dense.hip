@@ -44,6 +44,7 @@
 //                        feeds the products of both blocks.
 #include <math.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "gw_attn.h"
@@ -766,7 +767,10 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
     GW_CHECK_ARG(eps >= 0.f, "eps must be non-negative, got %g", (double)eps);
   }
   const DenseLayout L = dense_layout(B, T, S, H, K, want_attn);
-  GW_CHECK_ARG((int64_t)(L.nqb_pad / kQBW) * H < (1ll << 31) && L.nqb_pad <= 65535, "too many query blocks");
+  // Query blocks: at most 65535 (T <= 65528 * 32 once padded to whole workgroups).
+  if ((int64_t)(L.nqb_pad / kQBW) * H >= (1ll << 31) || L.nqb_pad > 65535)
+    return set_error(GW_ERR_UNSUPPORTED, "the dense forward takes at most %d queries, got %lld", 65528 * 32,
+                     (long long)T);
   if (k_strides[1] >= kDenseMaxKRowStride || (int64_t)L.spad * 128 >= (1ll << 32))
     return set_error(GW_ERR_UNSUPPORTED,
                      "the dense forward needs a K token stride below %lld elements and S <= %lld, got %lld and %lld",
@@ -887,10 +891,11 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
 // ---------------------------------------------------------------------------------------
 // Allocation-free variant: the workspace is a file-scope device array of a fixed size
 // (each GPU the library runs on holds its own copy until the process ends). Its device
-// address is looked up once per device (hipGetSymbolAddress with that device current) and
-// kept; host code never passes the array's name itself to a kernel. Every kernel of the call
-// clears what it needs before use (selection words, flags, column maxima), so the array's
-// contents from an earlier call do not matter; two calls that overlap on one GPU race on it.
+// address is looked up on the first call on a device (hipGetSymbolAddress with that device
+// current; a failed lookup is reported and tried again on the next call) and kept; host code
+// never passes the array's name itself to a kernel. Every kernel of the call clears what it
+// needs before use (selection words, flags, column maxima), so the array's contents from an
+// earlier call do not matter; two calls that overlap on one GPU race on it.
 // ---------------------------------------------------------------------------------------
 namespace gw {
 namespace {
@@ -900,9 +905,25 @@ constexpr int kNoAllocMaxDevices = 64;
 
 __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
-void* g_scratch_ptr[kNoAllocMaxDevices];
-hipError_t g_scratch_err[kNoAllocMaxDevices];
-std::once_flag g_scratch_once[kNoAllocMaxDevices];
+std::atomic<void*> g_scratch_ptr[kNoAllocMaxDevices];  // null until a lookup succeeded
+std::mutex g_scratch_mu;
+
+// The scratch array's address on the current device dev (looked up once it succeeds).
+int scratch_address(int dev, void** out) {
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || ptr == nullptr) return hip_error(e != hipSuccess ? e : hipErrorInvalidSymbol,
+                                                              "hipGetSymbolAddress(scratch)");
+      g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return GW_OK;
+}
 
 }  // namespace
 }  // namespace gw
@@ -925,10 +946,8 @@ extern "C" int gw_sparse_attn_fwd_dense_noalloc(int dtype, const void* q, const 
   if (dev < 0 || dev >= kNoAllocMaxDevices)
     return set_error(GW_ERR_UNSUPPORTED, "device %d is beyond the %d devices the allocation-free entry point serves",
                      dev, kNoAllocMaxDevices);
-  std::call_once(g_scratch_once[dev], [dev] {
-    g_scratch_err[dev] = hipGetSymbolAddress(&g_scratch_ptr[dev], HIP_SYMBOL(scratch));
-  });
-  if (g_scratch_err[dev] != hipSuccess) return hip_error(g_scratch_err[dev], "hipGetSymbolAddress(scratch)");
+  void* scratch_ptr = nullptr;
+  if (const int rc = scratch_address(dev, &scratch_ptr); rc != GW_OK) return rc;
   const size_t need = gw_sparse_attn_fwd_dense_workspace_size(B, T, S, H, D, K, attn_sum != nullptr ? 1 : 0);
   if (need > kNoAllocScratchBytes)
     return set_error(GW_ERR_UNSUPPORTED,
@@ -937,6 +956,6 @@ extern "C" int gw_sparse_attn_fwd_dense_noalloc(int dtype, const void* q, const 
                      need, kNoAllocScratchBytes);
   return gw_sparse_attn_fwd_dense(dtype, q, q_strides, k, k_strides, v, v_strides, kv_pos, pos_stride_b, pos_stride_t,
                                   o, o_strides, lse, attn_sum, B, T, S, H, D, K, softmax_scale, logits, logits_dtype,
-                                  logits_stride_b, logits_stride_t, eps, row_loss, g_scratch_ptr[dev],
+                                  logits_stride_b, logits_stride_t, eps, row_loss, scratch_ptr,
                                   kNoAllocScratchBytes, stream);
 }

@@ -668,17 +668,21 @@ extern "C" int gw_sparse_attn_bwd_dense(int dtype, const void* q, const int64_t*
     for (int i = 0; i < 3; ++i) GW_CHECK_ARG(st[i] % 8 == 0, "b/t/h strides must be multiples of 8 elements");
   GW_CHECK_ARG(B <= 65535 && T < (1ll << 30) && S < (1ll << 30) && K < (1ll << 31), "size exceeds the grid range");
   const DenseBwdLayout L = dense_bwd_layout(B, T, S, H);
-  GW_CHECK_ARG((int64_t)(L.nqb_pad / kBQPB) * H < (1ll << 31) && (int64_t)(L.spad / (32 * kBKPB)) * H < (1ll << 31) &&
-                   L.nqb_pad <= 65535 && H <= 65535,
-               "too many query or key blocks");
+  // Query blocks: at most 65535 (T <= 65528 * 32 once padded to whole workgroups).
+  if ((int64_t)(L.nqb_pad / kBQPB) * H >= (1ll << 31) || (int64_t)(L.spad / (32 * kBKPB)) * H >= (1ll << 31) ||
+      L.nqb_pad > 65535 || H > 65535)
+    return set_error(GW_ERR_UNSUPPORTED, "the dense backward takes at most %d queries, got %lld", 65528 * 32,
+                     (long long)T);
   // Limits of the kernels' 32-bit lane offsets: token strides of q, k, v, dO below 2^23
-  // elements (a 24-bit multiply), 64 rows of the transposed operands below 2^32 bytes.
+  // elements (a 24-bit multiply), 64 rows of the transposed operands below 2^32 bytes. T is
+  // padded to a multiple of 256 and S to one of 128, so T, S <= 2^25 - 256 keeps both padded
+  // lengths below 2^25.
   if (q_strides[1] >= kDenseBwdMaxRowStride || k_strides[1] >= kDenseBwdMaxRowStride ||
       v_strides[1] >= kDenseBwdMaxRowStride || do_strides[1] >= kDenseBwdMaxRowStride ||
       (int64_t)L.spad * 128 >= (1ll << 32) || (int64_t)L.tpad * 128 >= (1ll << 32))
     return set_error(GW_ERR_UNSUPPORTED,
                      "the dense backward needs token strides below %lld elements and T, S <= %lld",
-                     (long long)kDenseBwdMaxRowStride, (long long)((1ll << 25) - 64));
+                     (long long)kDenseBwdMaxRowStride, (long long)((1ll << 25) - 256));
   GW_CHECK_ARG(workspace != nullptr && workspace_bytes >= L.total && aligned16(workspace),
                "the dense backward needs a 16-byte aligned %zu-byte workspace, got %zu", L.total, workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);

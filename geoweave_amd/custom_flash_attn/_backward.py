@@ -25,9 +25,13 @@ from .. import _csr, _lib
 # the dense passes whenever they can run at all, "csr" the CSR path (tests, measurements).
 BACKWARD_PATH = "auto"
 DENSE_MAX_RATIO = 96
-# The dense kernels' 32-bit load offsets bound the token strides and T, S (DENSE_MAX_*).
+# The dense kernels' 32-bit load offsets bound the token strides and T, S (DENSE_MAX_*): 64
+# rows of the transposed operands stay below 2^32 bytes while T (padded to a multiple of 256)
+# and S (padded to a multiple of 128) stay below 2^25.
+# The grid of at most 65535 query blocks (whole workgroups of 8) bounds T further.
 DENSE_MAX_ROW_STRIDE = 1 << 23
-DENSE_MAX_LEN = (1 << 25) - 64
+DENSE_MAX_LEN = (1 << 25) - 256
+DENSE_MAX_T = 65528 * 32
 # The path the last call took ("dense" or "csr"), for tests.
 last_path = None
 
@@ -45,10 +49,10 @@ def _aligned(x: torch.Tensor) -> torch.Tensor:
 
 
 def _dense_fits(q, k, v, do, q_layout: str) -> bool:
-    """The dense backward's 32-bit load offsets: token strides and T, S within its limits."""
+    """The dense backward's limits: token strides and T, S (32-bit load offsets), T (grid)."""
     t_dim = 2 if q_layout == "bhtd" else 1
     lens = (q.shape[t_dim], k.shape[t_dim])
-    return (all(n <= DENSE_MAX_LEN for n in lens)
+    return (all(n <= DENSE_MAX_LEN for n in lens) and lens[0] <= DENSE_MAX_T
             and all(_strides(x, q_layout)[1] < DENSE_MAX_ROW_STRIDE for x in (q, k, v, do)))
 
 

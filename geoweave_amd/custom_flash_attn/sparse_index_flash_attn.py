@@ -96,12 +96,14 @@ def _check_inputs(q, k, v, kv_positions, bias, causal, layout):
 # selects at least 1 / DENSE_MAX_RATIO of the keys (and, with attn_sum, K <=
 # DENSE_ATTN_SUM_MAX_K), "dense" / "gather" force one path (tests and measurements). The
 # dense pass costs ~ T·S, the gather ~ T·K: on MI355X they break even near S = 124·K.
-# The dense kernel's 32-bit load offsets bound the K token stride and S (DENSE_MAX_*).
+# The dense kernel's 32-bit load offsets bound the K token stride and S, its grid of at most
+# 65535 query blocks (whole workgroups of 8) bounds T (DENSE_MAX_*).
 FORWARD_PATH = "auto"
 DENSE_MAX_RATIO = 96
 DENSE_ATTN_SUM_MAX_K = 1024
 DENSE_MAX_K_ROW_STRIDE = 1 << 23
 DENSE_MAX_S = (1 << 25) - 64
+DENSE_MAX_T = 65528 * 32
 
 
 def _use_dense(seqlen_k: int, num_kv: int, nheads: int, d: int, softmax_scale: float = 1.0) -> bool:
@@ -110,9 +112,10 @@ def _use_dense(seqlen_k: int, num_kv: int, nheads: int, d: int, softmax_scale: f
     return FORWARD_PATH == "dense" or seqlen_k <= DENSE_MAX_RATIO * num_kv
 
 
-def _dense_fits(k: torch.Tensor, q_layout: str, seqlen_k: int) -> bool:
-    """The dense forward's 32-bit load offsets: K token stride and S within its limits."""
-    return _bthd_strides(k, q_layout)[1] < DENSE_MAX_K_ROW_STRIDE and seqlen_k <= DENSE_MAX_S
+def _dense_fits(k: torch.Tensor, q_layout: str, seqlen_k: int, seqlen_q: int = 0) -> bool:
+    """The dense forward's limits: K token stride and S (32-bit load offsets), T (grid)."""
+    return (_bthd_strides(k, q_layout)[1] < DENSE_MAX_K_ROW_STRIDE and seqlen_k <= DENSE_MAX_S
+            and seqlen_q <= DENSE_MAX_T)
 
 
 def _prep(x: torch.Tensor) -> torch.Tensor:
@@ -179,7 +182,7 @@ def _flash_attn_forward(
         code = _lib.GW_DTYPE_FP32 if kl_logits.dtype == torch.float32 else _lib.dtype_code(kl_logits.dtype)
         kl_args = (kl_logits.data_ptr(), code, kl_logits.stride(0), kl_logits.stride(1), float(kl_eps),
                    kl_row_loss.data_ptr())
-    if (_use_dense(seqlen_k, num_kv, nheads, d, softmax_scale) and _dense_fits(k, q_layout, seqlen_k)
+    if (_use_dense(seqlen_k, num_kv, nheads, d, softmax_scale) and _dense_fits(k, q_layout, seqlen_k, seqlen_q)
             and (attn_sum is None or num_kv <= DENSE_ATTN_SUM_MAX_K)):
         dense_bytes = int(lib.gw_sparse_attn_fwd_dense_workspace_size(batch, seqlen_q, seqlen_k, nheads, d, num_kv,
                                                                       int(attn_sum is not None)))

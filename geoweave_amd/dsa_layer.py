@@ -209,17 +209,29 @@ def sparse_attention_streaming(q, k, v, idx_q, idx_k, idx_w, topk: int, query_ch
     """Indexer top-k and sparse attention ``query_chunk`` queries at a time (reference
     ``DSAAttention._run_sparse_streaming_direct``, ``dsa_attention.py:1017-1283``): each
     chunk's top-k indices live only while its attention runs, so peak memory for indices and
-    the indexer workspace scales with the chunk, not with N. Per-row results equal the
-    unchunked path's (rows are independent); q/idx_q ``[B, N, ...]``, k/v/idx_k/idx_w over all
-    keys. Returns o ``[B, N, H, D]``. ``source_downsample``: select each chunk's keys with the
-    coarse selector (pooled keys built once for all chunks, as the reference's stream does,
-    ``dsa_attention.py:1369-1435``)."""
+    the indexer workspace scales with the chunk, not with N. q/idx_q ``[B, N, ...]``,
+    k/v/idx_k/idx_w over all keys. Returns o ``[B, N, H, D]``.
+
+    ``source_downsample``: select each chunk's keys with the coarse selector (pooled keys built
+    once for all chunks, as the reference's stream does, ``dsa_attention.py:1369-1435``). With
+    qk_sym_x2_broadcast the outer chunk is the selector's own query chunk
+    (``min(N, source_downsample_query_chunk)``, falling back to ``query_chunk`` when that is 0;
+    ``dsa_attention.py:870-881,1127-1136``), because its coarse queries pool the tokens of a
+    chunk's source cells.
+
+    Rows are independent for the full indexer and for the legacy and subcell_static_pack4
+    selectors, so those give the unchunked path's rows. exact_rerank and subcell_top1 (retries
+    per selector chunk, counted from the outer chunk's start) and qk_sym_x2_broadcast (query
+    cells per chunk) depend on the chunking, as in the reference's stream."""
     B, N = q.shape[0], q.shape[1]
     out = torch.empty(q.shape, device=q.device, dtype=q.dtype)
     empty = idx_q.new_empty(0)
     prepared = None
     if source_downsample is not None and int(source_downsample.factor) > 1:
         prepared = sdown.prepare(idx_k, idx_w, source_downsample)
+        if prepared is not None and prepared.strategy == "qk_sym_x2_broadcast":
+            qc = int(source_downsample.query_chunk or 0)
+            query_chunk = min(N, qc if qc > 0 else int(query_chunk))
     for s0 in range(0, N, query_chunk):
         s1 = min(s0 + query_chunk, N)
         idx = None

@@ -434,7 +434,7 @@ int gw_source_downsample_static_pack4(int dtype, const void* sub_w, int64_t B, i
  * it pays off when a query selects more than roughly 1 % of the keys.
  * Needs D = 64 and a positive softmax_scale, and K <= 1024 and H <= 64 when attn_sum is
  * asked for; the kernels' 32-bit load offsets also need a K token stride below 2^23 elements
- * and S <= 2^25 - 64. Otherwise GW_ERR_UNSUPPORTED (use gw_sparse_attn_fwd /
+ * and S <= 2^25 - 64, and its grid T <= 65528 * 32. Otherwise GW_ERR_UNSUPPORTED (use gw_sparse_attn_fwd /
  * gw_sparse_attn_fwd_kl).
  * The P·V product takes P in fp16 (the fp32 weights rounded to nearest, 11 significant bits)
  * against V in fp16 scaled per (head, d) column by an exact power of two; row sums and lse
@@ -506,7 +506,8 @@ int gw_sparse_attn_fwd_dense_noalloc(int dtype,
  * easyvolcap/official_vggt/layers/dsa_attention.py:4694-4695), so dattn_sum is absent or zero.
  * It pays off when a query selects more than roughly 1 % of the keys.
  * Needs D = 64, a positive softmax_scale, token strides of q, k, v and dO below 2^23
- * elements and T, S <= 2^25 - 64 (the kernels' 32-bit load offsets); otherwise
+ * elements and T, S <= 2^25 - 256 (the kernels' 32-bit load offsets; T is padded to a multiple
+ * of 256, S to one of 128) and T <= 65528 * 32 (the grid); otherwise
  * GW_ERR_UNSUPPORTED.
  * Arguments as for gw_sparse_attn_bwd (no dattn_sum, no CSR). route: device int array of B
  * entries, written by this call: route[b] = 1 for a batch element it left untouched

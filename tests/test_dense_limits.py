@@ -41,3 +41,56 @@ def test_backward_dense_fits():
         assert not _backward._dense_fits(*args, "bthd")
     long_q = _view(_backward.DENSE_MAX_LEN + 1, 1, 64, 64)
     assert not _backward._dense_fits(long_q, small, small, long_q, "bthd")
+
+
+def _bwd_dense_rc(T, S):
+    """Return code of gw_sparse_attn_bwd_dense for lengths T, S with fake (aligned, never
+    dereferenced) pointers and no workspace: the length limits are checked before the
+    workspace, so UNSUPPORTED (2) means refused on length, INVALID (1) means past it."""
+    import ctypes
+
+    from geoweave_amd import _lib
+
+    lib = _lib.load()
+    s3 = _lib.strides3(1024 * 64, 1024, 64)
+    route = ctypes.c_void_p(16)
+    return lib.gw_sparse_attn_bwd_dense(0, 16, s3, 16, s3, 16, s3, 16, 1, 1, 16, s3, 16, s3, 16, 16, s3, 16, s3, 16,
+                                        s3, 1, T, S, 16, 64, 1, 0.125, route, None, 0, None)
+
+
+def _fwd_dense_rc(T, S):
+    """gw_sparse_attn_fwd_dense's return code, as _bwd_dense_rc."""
+    from geoweave_amd import _lib
+
+    lib = _lib.load()
+    s3 = _lib.strides3(1024 * 64, 1024, 64)
+    return lib.gw_sparse_attn_fwd_dense(0, 16, s3, 16, s3, 16, s3, 16, 1, 1, 16, s3, 16, None, 1, T, S, 16, 64, 1,
+                                        0.125, None, 0, 0, 0, 0.0, None, None, 0, None)
+
+
+def test_length_limits_match_the_kernels():
+    # Whatever the Python routing keeps on the dense passes, the C entry points accept (past
+    # the length checks: INVALID, 1, for the missing workspace); what they refuse
+    # (UNSUPPORTED, 2) the routing sends to the gather/CSR paths. Backward: T padded to 256
+    # and S to 128 below 2^25 and at most 65535 query blocks; forward: S padded to 64 below
+    # 2^25, same query blocks. T = 2^25 - 128 passed the old routing and then failed.
+    small = _view(8, 1, 64, 64)
+    tmax = _backward.DENSE_MAX_T
+    assert tmax == sifa.DENSE_MAX_T == 65528 * 32 and _backward.DENSE_MAX_LEN == (1 << 25) - 256
+    lens = [8, tmax, tmax + 1, (1 << 25) - 256, (1 << 25) - 255, (1 << 25) - 128, (1 << 25) - 64, (1 << 25) - 63]
+    for t in lens:
+        for s_len in lens:
+            tq, tk = _view(t, 1, 64, 64), _view(s_len, 1, 64, 64)
+            rc = _bwd_dense_rc(t, s_len)
+            assert rc in (1, 2)
+            if _backward._dense_fits(tq, tk, tk, tq, "bthd"):
+                assert rc == 1, (t, s_len)
+            rc = _fwd_dense_rc(t, s_len)
+            assert rc in (1, 2)
+            if sifa._dense_fits(small, "bthd", s_len, t):
+                assert rc == 1, (t, s_len)
+    long_q = _view((1 << 25) - 128, 1, 64, 64)
+    assert not _backward._dense_fits(long_q, small, small, long_q, "bthd")
+    assert _bwd_dense_rc((1 << 25) - 128, 8) == 2
+    at_lim = _view(tmax, 1, 64, 64)
+    assert _backward._dense_fits(at_lim, small, small, at_lim, "bthd")

@@ -281,3 +281,30 @@ def test_layer_runs_each_strategy(gpu_device, factor, strategy):
     torch.cuda.synchronize()
     assert idx.shape == (1, N, topk) and int(idx.min()) >= 0 and int(idx.max()) < N
     assert bool(torch.isfinite(out.float()).all()) and torch.equal(out, again)
+
+
+def test_stream_with_qk_sym_takes_the_selector_chunk(gpu_device):
+    # dsa_attention.py:870-881,1127-1136: with qk_sym_x2_broadcast the stream's outer chunk is
+    # min(N, source_downsample_query_chunk), not the layer's query chunk; a layer chunk of 700
+    # (a source cell straddles token 700) must give the rows of 1024-token selector chunks.
+    from geoweave_amd import dsa_layer, workloads
+    from geoweave_amd.custom_flash_attn.sparse_index_flash_attn import sparse_index_flash_attn_inference_func
+
+    tpv, views, psi, topk, qc = 5 + 37 * 37, 2, 5, 512, 1024
+    q, k, w = _inputs(tpv, views, 33)
+    N = q.shape[1]
+    aq, ak, av = (x.cuda() for x in workloads.attention_inputs(1, 1, torch.bfloat16, tokens=N, seed=34))
+    qd, kd, wd = q.cuda(), k.cuda(), w.cuda()
+    cfg = sd.SourceDownsample(tpv, views, psi, factor=2, strategy="qk_sym_x2_broadcast", query_chunk=qc)
+    o = dsa_layer.sparse_attention_streaming(aq, ak, av, qd, kd, wd, topk, 700, SCALE, 0.125, cfg)
+
+    def chunked(step):
+        return torch.cat([sd.select_topk(qd[:, s0:s0 + step].contiguous(), kd, wd, topk, SCALE, cfg, q_offset=s0)
+                          for s0 in range(0, N, step)], dim=1)
+
+    idx = chunked(qc)
+    o_ref, _ = sparse_index_flash_attn_inference_func(aq, ak, av, idx, softmax_scale=0.125)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_ref)
+    # the layer's chunking would select other rows (cells cut at 700)
+    assert not torch.equal(chunked(700), idx)

@@ -3,7 +3,8 @@ the C ABI: two calls in a row (the second smaller, so stale contents of the shar
 from the first call would show), each against gw_sparse_attn_fwd_dense with a caller
 workspace on the same inputs. Both run the same kernels, so o, lse and attn_sum must be
 bit-identical; the first case is also checked against the fp32 oracle at the attention
-tolerance. A call beyond the scratch capacity is refused on the host.
+tolerance. A call beyond the scratch capacity is refused on the host. The entry point is
+also captured into a graph (its first call on the device inside the capture) and replayed.
 """
 import pytest
 import torch
@@ -46,6 +47,41 @@ def _both(q, k, v, pos, with_attn, scale=0.125):
         torch.cuda.synchronize()
         outs.append((o.cpu(), lse.cpu(), None if attn is None else attn.cpu()))
     return outs
+
+
+def test_noalloc_under_graph_capture_allocates_nothing(gpu_device):
+    # The callers this entry point is for capture it into a graph. It runs first in this
+    # file and nothing else calls it, so the process's first call on the device (the scratch
+    # address lookup included) happens inside the capture. Every replay, with eager work
+    # between replays, equals the workspace entry's eager result. Afterwards an eager call
+    # (its kernels' code already loaded) leaves the device's free memory unchanged.
+    lib = _lib.load()
+    q, k, v = workloads.attention_inputs(2, 1, torch.bfloat16, seed=61)
+    pos = workloads.distinct_positions(1, q.shape[1], k.shape[1], 512, seed=62)
+    qd, kd, vd, pd = (x.cuda() for x in (q, k, v, pos))
+    B, T, H, _ = q.shape
+    o = torch.full_like(qd, float("nan"))
+    lse = torch.full((B, T, H), float("nan"), device="cuda")
+    args = _args(qd, kd, vd, pd, o, lse, None, 0.125)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=side):
+        rc = lib.gw_sparse_attn_fwd_dense_noalloc(*args, _lib.stream_handle(qd.device))
+    torch.cuda.synchronize()
+    assert rc == 0, lib.gw_last_error()
+    _, (o_w, l_w, _) = _both(qd, kd, vd, pd, False)
+    for replay in range(3):
+        o.fill_(float("nan"))
+        lse.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"[noalloc] graph replay {replay}", flush=True)
+        assert torch.equal(o.cpu(), o_w) and torch.equal(lse.cpu(), l_w)
+    free0 = torch.cuda.mem_get_info()[0]
+    rc = lib.gw_sparse_attn_fwd_dense_noalloc(*args, _lib.stream_handle(qd.device))
+    torch.cuda.synchronize()
+    assert rc == 0 and torch.cuda.mem_get_info()[0] == free0
 
 
 @pytest.mark.parametrize("with_attn", [False, True])
