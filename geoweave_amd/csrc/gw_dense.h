@@ -6,6 +6,7 @@
 #include <math.h>
 
 #include "gw_common.h"
+#include "gw_tile_rows.h"
 
 namespace gw {
 namespace {

@@ -288,10 +288,10 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
   auto dload = [&](int k0, int bf) {
     // Rows past the end read row S - 1 (their keys are never selected), taken from a base row
     // at most S - 1 so that the lane offsets stay in [0, 63] rows wherever the tile starts.
-    const int r_base = min(k0, p.S - 1);
-    const char* kt = kbase + (int64_t)r_base * kss_b;
-    buffer_load16_lds(kt, __umul24((uint32_t)(min(k0 + srow, p.S - 1) - r_base), kss_b) + kcol, &ktile[bf][wseg]);
-    buffer_load16_lds(kt, __umul24((uint32_t)(min(k0 + srow + 32, p.S - 1) - r_base), kss_b) + kcol,
+    const TileRows tr = tile_rows(k0, srow, p.S);
+    const char* kt = kbase + (int64_t)tr.base * kss_b;
+    buffer_load16_lds(kt, __umul24(tr.r0, kss_b) + kcol, &ktile[bf][wseg]);
+    buffer_load16_lds(kt, __umul24(tr.r1, kss_b) + kcol,
                       &ktile[bf][wseg + 4096]);
     const char* vtile0 = vbase + (int64_t)k0 * 2;
     buffer_load16_lds(vtile0, vo0, &vtile[bf][wseg]);

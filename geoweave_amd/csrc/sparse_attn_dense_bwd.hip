@@ -270,11 +270,10 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dq_kernel(const DenseBw
     // Rows past the end read row S - 1 (their keys are never selected). The tile may start
     // past it (S_pad is a whole number of key blocks): rows are taken from a base row at most
     // S - 1, so the lane offsets stay in [0, 63] rows.
-    const int r_base = min(k0, p.S - 1);
-    const uint32_t r0 = (uint32_t)(min(k0 + srow, p.S - 1) - r_base);
-    const uint32_t r1 = (uint32_t)(min(k0 + srow + 32, p.S - 1) - r_base);
-    const char* kt = kbase + (int64_t)r_base * kss_b;
-    const char* vt = vbase + (int64_t)r_base * vss_b;
+    const TileRows tr = tile_rows(k0, srow, p.S);
+    const uint32_t r0 = tr.r0, r1 = tr.r1;
+    const char* kt = kbase + (int64_t)tr.base * kss_b;
+    const char* vt = vbase + (int64_t)tr.base * vss_b;
     const char* tt = tbase + (int64_t)k0 * 2;
     buffer_load16_lds(kt, __umul24(r0, kss_b) + ccol, &ktile[bf][wseg]);
     buffer_load16_lds(kt, __umul24(r1, kss_b) + ccol, &ktile[bf][wseg + 4096]);
@@ -470,11 +469,10 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dkdv_kernel(const Dense
     // Rows past the end read row T - 1 (their queries never selected a key). The tile may
     // start past it (T_pad is a whole number of query blocks): rows are taken from a base row
     // at most T - 1, so the lane offsets stay in [0, 63] rows.
-    const int r_base = min(t0, p.T - 1);
-    const uint32_t r0 = (uint32_t)(min(t0 + srow, p.T - 1) - r_base);
-    const uint32_t r1 = (uint32_t)(min(t0 + srow + 32, p.T - 1) - r_base);
-    const char* qt = qbase + (int64_t)r_base * qst_b;
-    const char* dt = dbase + (int64_t)r_base * dst_b;
+    const TileRows tr = tile_rows(t0, srow, p.T);
+    const uint32_t r0 = tr.r0, r1 = tr.r1;
+    const char* qt = qbase + (int64_t)tr.base * qst_b;
+    const char* dt = dbase + (int64_t)tr.base * dst_b;
     const char* qtt = qtbase + (int64_t)t0 * 2;
     const char* dtt = dtbase + (int64_t)t0 * 2;
     buffer_load16_lds(qt, __umul24(r0, qst_b) + ccol, &qtile[bf][wseg]);
