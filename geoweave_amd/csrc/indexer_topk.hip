@@ -52,6 +52,7 @@
 // over the splits, so every list receives about candidates / (2 nsplit) entries.
 #include <math.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "gw_common.h"
@@ -67,6 +68,9 @@ constexpr int kMaxSplit = 8;
 constexpr int kMaxLists = kMaxSplit;
 constexpr int kMaxTopk = 2048;
 constexpr int kFallbackBlocks = 256;
+// Rows per batch element whose fallback scores come from the matrix cores (the rest, rare,
+// are scored by the fallback kernel itself).
+constexpr int kFullRows = 512;
 // Candidate layout: int2 {score bits, key} lists, one per row and key split: list l = split
 // of row r starts at cand[(r * nsplit + l) * cap], cap = kSubTotal / nsplit, and holds
 // counts[r * nsplit + l] entries (more than cap: the list overflowed; entries past cap were
@@ -240,7 +244,12 @@ struct ScoreParams {
   const int* sview;       // kBiasView: [B, S]
   int Vq, Vs;
   const float* tau;      // [B*T] or null (-inf)
-  float* samp;           // SAMPLE: [B*T, Ms]
+  float* samp;           // SAMPLE: [B*T, Ms] (with rows: [B, rows_cap, Ms])
+  // SAMPLE with rows != null: the queries are rows[b * T + j] (flat b * T + t indices) for j
+  // below min(nrows[b], rows_cap), and row j's scores go to samp[(b * rows_cap + j) * Ms].
+  const int* rows;
+  const int* nrows;
+  int rows_cap;
   int2* cand;            // FILTER: candidate lists (see kSubTotal)
   int* counts;           // FILTER: [B*T, nsplit] entries per list (more than cap: overflowed)
   int T, S;
@@ -371,9 +380,23 @@ __global__ __launch_bounds__((ScoreShape<row_bytes<E, HI>()>::THREADS),
   const int nkeys = SAMPLE ? p.Ms : S;
   const int col = lane & 31;
   const int half = lane >> 5;
-  const int row = q0 + col;  // this lane's query
-  const bool row_ok = row < T;
-  const int64_t grow = (int64_t)b * T + (row_ok ? row : 0);
+  const int row = q0 + col;  // this lane's query (SAMPLE with rows: its position in the list)
+  int nrow = T;
+  if constexpr (SAMPLE) {
+    if (p.rows != nullptr) {
+      nrow = min(p.nrows[b], p.rows_cap);
+      if ((int)blockIdx.x * BM >= nrow) return;  // the whole workgroup, before any barrier
+    }
+  }
+  const bool row_ok = row < nrow;
+  int64_t grow = (int64_t)b * T + (row_ok ? row : 0);
+  int64_t out_row = grow;  // SAMPLE: row of samp
+  if constexpr (SAMPLE) {
+    if (p.rows != nullptr) {
+      grow = row_ok ? (int64_t)p.rows[(int64_t)b * T + row] : (int64_t)b * T;
+      out_row = (int64_t)b * p.rows_cap + row;
+    }
+  }
   // kBiasView: the view-bias table row of this lane's query (element offset).
   int64_t vrow = 0;
   if constexpr ((BIAS & kBiasView) != 0) vrow = ((int64_t)b * p.Vq + clamp_view(p.qview[grow], p.Vq)) * p.Vs;
@@ -564,7 +587,7 @@ __global__ __launch_bounds__((ScoreShape<row_bytes<E, HI>()>::THREADS),
     }
     if constexpr (SAMPLE) {
       if (row_ok) {
-        float* dst = p.samp + grow * p.Ms;
+        float* dst = p.samp + out_row * p.Ms;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int kidx = k4 + 8 * g;
@@ -755,8 +778,9 @@ struct SelectParams {
   int32_t* out_idx;
   void* out_scores;  // [rows, Kk] in the element type of the launch
   int Kk;
-  int* fb_count;
-  int* fb_list;
+  int T;
+  int* fb_count;  // [B]: rows queued for the exact fallback, per batch element
+  int* fb_list;   // [B * T]: batch element b's rows from fb_list[b * T]
   int* wide_count;
   int* wide_list;
   int64_t rows;
@@ -820,7 +844,10 @@ __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams 
   const int total = rl.off[kMaxLists];
   if (bad || total < p.Kk) {
     // The candidates may miss part of the top-k: exact brute force.
-    if (lane == 0) p.fb_list[atomicAdd(p.fb_count, 1)] = (int)row;
+    if (lane == 0) {
+      const int bb = (int)(row / p.T);
+      p.fb_list[(int64_t)bb * p.T + atomicAdd(&p.fb_count[bb], 1)] = (int)row;
+    }
     return;
   }
   if (p.force_wide || total > 64 * KS) {
@@ -969,12 +996,16 @@ struct FallbackParams {
   const int* qview;
   const int* sview;
   int Vq, Vs;
-  const int* fb_count;
-  const int* fb_list;
-  float* scratch;  // [gridDim.x, S]
+  const int* fb_count;  // [B]
+  const int* fb_list;   // [B * T], batch element b's rows from b * T
+  // Scores of the first rows_cap queued rows of each batch element, computed on the matrix
+  // cores by indexer_score_kernel<SAMPLE> over all keys: [B, rows_cap, S] (null: none).
+  const float* full;
+  int rows_cap;
+  float* scratch;  // [gridDim.x, S]: rows beyond rows_cap are scored here
   int32_t* out_idx;
   void* out_scores;
-  int T, S, Kk;
+  int B, T, S, Kk;
   float scale;
 };
 
@@ -1006,34 +1037,9 @@ __global__ __launch_bounds__(256) void indexer_fallback_kernel(const FallbackPar
   __shared__ __attribute__((aligned(16))) uint4 qs[ROW_BYTES / 16];
   __shared__ SelectShared sh;
   const int tid = threadIdx.x;
-  const int nitems = *((volatile const int*)p.fb_count);
-  float* sc = p.scratch + (int64_t)blockIdx.x * p.S;
-  for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
-    const int row = p.fb_list[item];
-    const int b = row / p.T;
-    const uint4* qrow = reinterpret_cast<const uint4*>(static_cast<const char*>(p.q) + (int64_t)row * ROW_BYTES);
-    for (int i = tid; i < ROW_BYTES / 16; i += kSelThreads) qs[i] = qrow[i];
-    __syncthreads();
-    for (int j = tid; j < p.S; j += kSelThreads) {
-      const uint4* kr = reinterpret_cast<const uint4*>(static_cast<const char*>(p.k) + ((int64_t)b * p.S + j) * ROW_BYTES);
-      float s = 0.f;
-#pragma unroll
-      for (int h = 0; h < HI; ++h) {
-        float z = 0.f;
-#pragma unroll
-        for (int c = 0; c < HEAD_CHUNKS; ++c) z = dot_chunk(E{}, qs[h * HEAD_CHUNKS + c], kr[h * HEAD_CHUNKS + c], z);
-        const float wv = ld_f32(E{}, p.w, ((int64_t)b * p.S + j) * HI + h) * p.scale;
-        s = fmaf(wv, relu_bits(z), s);
-      }
-      if constexpr ((BIAS & kBiasMask) != 0) s += ld_f32(E{}, p.mask, (int64_t)row * p.S + j);
-      if constexpr ((BIAS & kBiasView) != 0)
-        s += ld_f32(E{}, p.vbias,
-                    ((int64_t)b * p.Vq + clamp_view(p.qview[row], p.Vq)) * p.Vs +
-                        clamp_view(p.sview[(int64_t)b * p.S + j], p.Vs));
-      sc[j] = s;
-    }
-    __threadfence_block();
-    __syncthreads();
+  float* const own = p.scratch + (int64_t)blockIdx.x * p.S;
+  // Exact top-k of one row's scores sc[0, S).
+  auto select_row = [&](const float* sc, int row) {
     int take_eq;
     auto key_at = [&](int i) { return f2key(sc[i]); };
     const uint32_t kth = block_radix_select(key_at, p.S, p.Kk, sh, take_eq);
@@ -1048,12 +1054,229 @@ __global__ __launch_bounds__(256) void indexer_fallback_kernel(const FallbackPar
                     },
                     sh);
     __syncthreads();
+  };
+  // Rows below rows_cap have their scores computed on the matrix cores and are selected by
+  // indexer_full_select_kernel; this kernel scores and selects the rest.
+  const int first = p.full != nullptr ? p.rows_cap : 0;
+  for (int b = 0; b < p.B; ++b) {
+    const int nitems = *((volatile const int*)(p.fb_count + b));
+    for (int item = first + blockIdx.x; item < nitems; item += gridDim.x) {
+      const int row = p.fb_list[(int64_t)b * p.T + item];
+      const uint4* qrow = reinterpret_cast<const uint4*>(static_cast<const char*>(p.q) + (int64_t)row * ROW_BYTES);
+      for (int i = tid; i < ROW_BYTES / 16; i += kSelThreads) qs[i] = qrow[i];
+      __syncthreads();
+      for (int j = tid; j < p.S; j += kSelThreads) {
+        const uint4* kr =
+            reinterpret_cast<const uint4*>(static_cast<const char*>(p.k) + ((int64_t)b * p.S + j) * ROW_BYTES);
+        float s = 0.f;
+#pragma unroll
+        for (int h = 0; h < HI; ++h) {
+          float z = 0.f;
+#pragma unroll
+          for (int c = 0; c < HEAD_CHUNKS; ++c) z = dot_chunk(E{}, qs[h * HEAD_CHUNKS + c], kr[h * HEAD_CHUNKS + c], z);
+          const float wv = ld_f32(E{}, p.w, ((int64_t)b * p.S + j) * HI + h) * p.scale;
+          s = fmaf(wv, relu_bits(z), s);
+        }
+        if constexpr ((BIAS & kBiasMask) != 0) s += ld_f32(E{}, p.mask, (int64_t)row * p.S + j);
+        if constexpr ((BIAS & kBiasView) != 0)
+          s += ld_f32(E{}, p.vbias,
+                      ((int64_t)b * p.Vq + clamp_view(p.qview[row], p.Vq)) * p.Vs +
+                          clamp_view(p.sview[(int64_t)b * p.S + j], p.Vs));
+        own[j] = s;
+      }
+      __threadfence_block();
+      __syncthreads();
+      select_row(own, row);
+    }
   }
 }
 
-__global__ void set_int_kernel(int* ptr, int value) {
-  if (threadIdx.x < 2 && blockIdx.x == 0) ptr[threadIdx.x] = value;
+// ---------------------------------------------------------------------------------------
+// Exact top-k of queued rows whose scores the matrix cores computed (full[b, j, :] for the
+// first rows_cap queued rows of batch element b). Per row, on the order-preserving keys:
+//  1. the row's smallest and largest key;
+//  2. a 2048-bin histogram over the key range [lo, hi] (bins of 2^sh keys from the top)
+//     finds the bin of the k-th largest key; while that bin holds more keys than the LDS
+//     buffer and is wider than one key, the range narrows to it and step 2 repeats (at most
+//     three times: each level takes 11 bits);
+//  3. keys above the range go straight out and the range's keys are gathered into LDS, both
+//     in a fixed order (round, thread, key of the thread); a block radix select settles the
+//     rest (a one-key range with more keys than the buffer: its first keys in that order).
+// Ties at the k-th value are taken in that fixed order, the same on every run. Every pass
+// reads the row in rounds of kFullPer keys per thread (key r0 + m * 256 + thread: coalesced
+// loads, issued together).
+// ---------------------------------------------------------------------------------------
+constexpr int kFullBins = 2048;
+constexpr int kFullEqCap = 4096;
+constexpr int kFullPer = 64;  // contiguous keys per thread and round
+
+template <typename E>
+__global__ __launch_bounds__(256) void indexer_full_select_kernel(const FallbackParams p) {
+  __shared__ int hist[kFullBins];
+  __shared__ uint32_t ekeys[kFullEqCap];
+  __shared__ int eidx[kFullEqCap];
+  __shared__ SelectShared sh;
+  __shared__ uint32_t bcast[4][2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int Kk = p.Kk, S = p.S;
+  constexpr int ROUND = kFullPer * kSelThreads;
+  // Key m of this thread in round r0: r0 + m * 256 + tid (coalesced loads).
+  auto load_round = [&](const float* sc, int r0, uint32_t (&kv)[kFullPer]) {
+    const int i0 = r0 + tid;
+    float v[kFullPer];
+#pragma unroll
+    for (int m = 0; m < kFullPer; ++m) v[m] = i0 + m * kSelThreads < S ? sc[i0 + m * kSelThreads] : 0.f;
+#pragma unroll
+    for (int m = 0; m < kFullPer; ++m) kv[m] = f2key(v[m]);
+    return i0;
+  };
+  for (int b = 0; b < p.B; ++b) {
+    const int nitems = min(*((volatile const int*)(p.fb_count + b)), p.rows_cap);
+    for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+      const int row = p.fb_list[(int64_t)b * p.T + item];
+      const float* sc = p.full + ((int64_t)b * p.rows_cap + item) * S;
+      int32_t* oi = p.out_idx + (int64_t)row * Kk;
+      const int64_t os = (int64_t)row * Kk;
+      // 1. key range of the row
+      uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
+      for (int r0 = 0; r0 < S; r0 += ROUND) {
+        uint32_t kv[kFullPer];
+        const int i0 = load_round(sc, r0, kv);
+#pragma unroll
+        for (int m = 0; m < kFullPer; ++m)
+          if (i0 + m * kSelThreads < S) {
+            kmin = min(kmin, kv[m]);
+            kmax = max(kmax, kv[m]);
+          }
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) {
+        kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, off));
+        kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, off));
+      }
+      if (lane == 0) {
+        bcast[wave][0] = kmin;
+        bcast[wave][1] = kmax;
+      }
+      __syncthreads();
+      uint32_t lo = min(min(bcast[0][0], bcast[1][0]), min(bcast[2][0], bcast[3][0]));
+      uint32_t hi = max(max(bcast[0][1], bcast[1][1]), max(bcast[2][1], bcast[3][1]));
+      __syncthreads();
+      // 2. narrow [lo, hi] to the k-th key's bin
+      int above = 0, need = Kk, cnt = 0;
+      for (int level = 0; level < 3; ++level) {
+        const uint32_t span = hi - lo;
+        const int shb = span < (uint32_t)kFullBins ? 0 : 32 - __builtin_clz(span) - 11;
+        for (int i = tid; i < kFullBins; i += kSelThreads) hist[i] = 0;
+        __syncthreads();
+        for (int r0 = 0; r0 < S; r0 += ROUND) {
+          uint32_t kv[kFullPer];
+          const int i0 = load_round(sc, r0, kv);
+#pragma unroll
+          for (int m = 0; m < kFullPer; ++m)
+            if (i0 + m * kSelThreads < S && kv[m] - lo <= span) atomicAdd(&hist[(hi - kv[m]) >> shb], 1);
+        }
+        __syncthreads();
+        // bins 8 t .. 8 t + 7 per thread: thread order is descending key order
+        int c[8], local = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          c[j] = hist[8 * tid + j];
+          local += c[j];
+        }
+        int ex, ex_unused;
+        block_excl_scan2(local, 0, ex, ex_unused, sh);
+        if (ex < need && need <= ex + local) {
+          int acc = ex;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            if (acc + c[j] >= need) {
+              sh.bcast[0] = 8 * tid + j;
+              sh.bcast[1] = acc;
+              break;
+            }
+            acc += c[j];
+          }
+        }
+        __syncthreads();
+        const int d = sh.bcast[0];
+        above += sh.bcast[1];
+        need -= sh.bcast[1];
+        cnt = hist[d];
+        const uint32_t nhi = hi - ((uint32_t)d << shb);
+        const uint32_t width = shb >= 32 ? 0xFFFFFFFFu : ((1u << shb) - 1u);
+        lo = max(lo, nhi - min(width, nhi));
+        hi = nhi;
+        __syncthreads();
+        if (cnt <= kFullEqCap || shb == 0) break;
+      }
+      // 3. keys above hi out, keys in [lo, hi] to LDS (or, for a one-key range too large for
+      // the buffer, its first need keys out), in index order
+      const bool gather = cnt <= kFullEqCap;
+      int base_g = 0, base_e = 0;
+      for (int r0 = 0; r0 < S; r0 += ROUND) {
+        uint32_t kv[kFullPer];
+        const int i0 = load_round(sc, r0, kv);
+        int cg = 0, ce = 0;
+#pragma unroll
+        for (int m = 0; m < kFullPer; ++m) {
+          const bool ok = i0 + m * kSelThreads < S;
+          cg += ok && kv[m] > hi;
+          ce += ok && kv[m] >= lo && kv[m] <= hi;
+        }
+        int og, oe;
+        block_excl_scan2(cg, ce, og, oe, sh);
+        og += base_g;
+        oe += base_e;
+#pragma unroll
+        for (int m = 0; m < kFullPer; ++m) {
+          if (i0 + m * kSelThreads >= S) continue;
+          if (kv[m] > hi) {
+            oi[og] = i0 + m * kSelThreads;
+            st_f32(E{}, p.out_scores, os + og, key2f(kv[m]));
+            ++og;
+          } else if (kv[m] >= lo) {
+            if (gather) {
+              ekeys[oe] = kv[m];
+              eidx[oe] = i0 + m * kSelThreads;
+            } else if (oe < need) {
+              oi[above + oe] = i0 + m * kSelThreads;
+              st_f32(E{}, p.out_scores, os + above + oe, key2f(kv[m]));
+            }
+            ++oe;
+          }
+        }
+        if (tid == kSelThreads - 1) {
+          bcast[0][0] = (uint32_t)og;  // block totals so far (the last thread ends at them)
+          bcast[0][1] = (uint32_t)oe;
+        }
+        __syncthreads();
+        base_g = (int)bcast[0][0];
+        base_e = (int)bcast[0][1];
+        __syncthreads();
+      }
+      if (gather) {
+        int take_eq;
+        auto ekey_at = [&](int i) { return ekeys[i]; };
+        const uint32_t kth = block_radix_select(ekey_at, cnt, need, sh, take_eq);
+        block_emit_topk(ekey_at, cnt, need, kth, take_eq,
+                        [&](int slot, int i) {
+                          if (slot < need) {
+                            oi[above + slot] = eidx[i];
+                            st_f32(E{}, p.out_scores, os + above + slot, key2f(ekeys[i]));
+                          }
+                        },
+                        sh);
+      }
+      __syncthreads();
+    }
+  }
 }
+
+__global__ void set_ints_kernel(int* ptr, int n, int value) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) ptr[i] = value;
+}
+
 
 // ---------------------------------------------------------------------------------------
 // Host-side plan.
@@ -1066,7 +1289,7 @@ struct Plan {
   int Ms = 0, rank = 0;
   int nsplit = 1, cap = 0;
   size_t off_tau = 0, off_samp = 0, off_counts = 0, off_cand = 0, off_fb = 0, off_fblist = 0,
-         off_widelist = 0, off_scratch = 0, total = 0;
+         off_widelist = 0, off_scratch = 0, off_full = 0, total = 0;
 };
 
 // Workspace layout (independent of the split count, which depends on the device).
@@ -1086,10 +1309,11 @@ Plan make_layout(int64_t B, int64_t T, int64_t S, int64_t topk) {
   pl.off_samp = off;     off = align_up(off + (pl.sample ? rows * (size_t)pl.Ms * 4 : 0), 256);
   pl.off_counts = off;   off = align_up(off + rows * kMaxLists * 4, 256);
   pl.off_cand = off;     off = align_up(off + rows * (size_t)kSubTotal * 8, 256);
-  pl.off_fb = off;       off = align_up(off + 64, 256);
+  pl.off_fb = off;       off = align_up(off + (size_t)(B + 1) * 4, 256);  // wide count, then B fallback counts
   pl.off_fblist = off;   off = align_up(off + rows * 4, 256);
   pl.off_widelist = off; off = align_up(off + rows * 4, 256);
   pl.off_scratch = off;  off = align_up(off + (size_t)kFallbackBlocks * (size_t)S * 4, 256);
+  pl.off_full = off;     off = align_up(off + (size_t)B * kFullRows * (size_t)S * 4, 256);
   pl.total = off;
   return pl;
 }
@@ -1142,9 +1366,9 @@ int choose_nsplit(int64_t tiles, int64_t S, int slots, bool sample, int bn) {
 template <typename E, int HI, int BIAS>
 int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, void* out_scores,
               uint8_t* ws, hipStream_t st) {
-  int* fb_count = reinterpret_cast<int*>(ws + pl.off_fb);  // [0] brute force, [1] wide select
-  hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(64), 0, st, fb_count, 0);
-  GW_HIP_LAUNCH_CHECK("set_int_kernel");
+  int* counters = reinterpret_cast<int*>(ws + pl.off_fb);  // [0] wide select, [1 + b] fallback of b
+  hipLaunchKernelGGL(set_ints_kernel, dim3(1), dim3(256), 0, st, counters, (int)B + 1, 0);
+  GW_HIP_LAUNCH_CHECK("set_ints_kernel");
   using Shape = ScoreShape<row_bytes<E, HI>()>;
   constexpr int BM = Shape::BM;
   constexpr int THREADS = Shape::THREADS;
@@ -1196,9 +1420,10 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   fs.out_idx = out_idx;
   fs.out_scores = out_scores;
   fs.Kk = pl.Kk;
-  fs.fb_count = fb_count;
+  fs.T = base.T;
+  fs.fb_count = counters + 1;
   fs.fb_list = reinterpret_cast<int*>(ws + pl.off_fblist);
-  fs.wide_count = fb_count + 1;
+  fs.wide_count = counters;
   fs.wide_list = reinterpret_cast<int*>(ws + pl.off_widelist);
   fs.rows = rows;
   fs.force_wide = base.force_wide;
@@ -1207,6 +1432,29 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   GW_HIP_LAUNCH_CHECK("indexer_select_kernel");
   hipLaunchKernelGGL((indexer_select_wide_kernel<E>), dim3(kFallbackBlocks), dim3(256), 0, st, fs);
   GW_HIP_LAUNCH_CHECK("indexer_select_wide_kernel");
+  // Rows queued for the exact fallback (sampled threshold too high or a list overflowed):
+  // scores over all keys on the matrix cores, rows gathered from the queue, key range split
+  // finely so that a few hundred rows still fill the chip (workgroups of batch elements with
+  // fewer queued rows return at once).
+  float* full = reinterpret_cast<float*>(ws + pl.off_full);
+  {
+    ScoreParams fp2 = base;
+    fp2.samp = full;
+    fp2.Ms = base.S;
+    fp2.rows = fs.fb_list;
+    fp2.nrows = fs.fb_count;
+    fp2.rows_cap = kFullRows;
+    fp2.tau = nullptr;
+    fp2.tau_mode = kTauArray;
+    fp2.nstages = (base.S + BN - 1) / BN;
+    const int ftiles = (kFullRows + BM - 1) / BM;
+    const int fslots = filter_slots((const void*)indexer_score_kernel<E, HI, true, BIAS>, THREADS);
+    const int64_t want = (2 * (int64_t)fslots + (int64_t)ftiles * B - 1) / ((int64_t)ftiles * B);
+    fp2.nsplit = (int)std::max<int64_t>(1, std::min<int64_t>(want, std::max(1, fp2.nstages / 2)));
+    hipLaunchKernelGGL((indexer_score_kernel<E, HI, true, BIAS>),
+                       dim3((unsigned)ftiles, (unsigned)fp2.nsplit, (unsigned)B), dim3(THREADS), 0, st, fp2);
+    GW_HIP_LAUNCH_CHECK("indexer_score_kernel<fallback rows>");
+  }
   FallbackParams bp{};
   bp.q = base.q;
   bp.k = base.k;
@@ -1217,8 +1465,11 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   bp.sview = base.sview;
   bp.Vq = base.Vq;
   bp.Vs = base.Vs;
-  bp.fb_count = fb_count;
+  bp.fb_count = fs.fb_count;
   bp.fb_list = fs.fb_list;
+  bp.full = full;
+  bp.rows_cap = kFullRows;
+  bp.B = (int)B;
   bp.scratch = reinterpret_cast<float*>(ws + pl.off_scratch);
   bp.out_idx = out_idx;
   bp.out_scores = fs.out_scores;
@@ -1226,6 +1477,8 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   bp.S = base.S;
   bp.Kk = pl.Kk;
   bp.scale = base.scale;
+  hipLaunchKernelGGL((indexer_full_select_kernel<E>), dim3(2 * kFallbackBlocks), dim3(256), 0, st, bp);
+  GW_HIP_LAUNCH_CHECK("indexer_full_select_kernel");
   hipLaunchKernelGGL((indexer_fallback_kernel<E, HI, BIAS>), dim3(kFallbackBlocks), dim3(256), 0, st, bp);
   GW_HIP_LAUNCH_CHECK("indexer_fallback_kernel");
   return GW_OK;

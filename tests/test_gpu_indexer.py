@@ -304,3 +304,31 @@ def test_massive_ties_and_zero_scores_stay_exact(gpu_device):
     q, k, w = q.bfloat16(), k.bfloat16(), w.bfloat16()
     idx, sc = _gpu_topk(q, k, w, topk)
     _check(q, k, w, idx, sc, topk)
+
+
+def test_sample_defeating_scores_take_the_matrix_core_fallback(gpu_device):
+    # Scores built to defeat the strided threshold sample: the 2,048 sample keys (key
+    # floor(i S / 2048)) carry a component along every query's direction, the other keys
+    # none, so the sampled tau (rank 81 of the sample) sits far above the true 1,024th score
+    # and every row ends with too few candidates. 1,024 rows: the first 512 of the queue are
+    # scored on the matrix cores, the rest by the fallback kernel itself; all exact.
+    g = torch.Generator().manual_seed(61)
+    T, S, topk = 1024, 43968, 1024
+    d = torch.randn(4, 64, generator=g)
+    q = (torch.randn(1, T, 4, 64, generator=g) * 0.3 + d).bfloat16()
+    k = torch.randn(1, S, 4, 64, generator=g)
+    samp = (torch.arange(2048) * S) // 2048
+    k[0, samp] += 2.0 * d
+    k = k.bfloat16()
+    w = torch.ones(1, S, 4).bfloat16()
+    idx, sc = _gpu_topk(q, k, w, topk)
+    _check(q, k, w, idx, sc, topk)
+
+
+def test_fallback_queues_per_batch_element(gpu_device):
+    # B = 2 with every row queued (PLUS_INF): 600 rows per batch element, 512 scored on the
+    # matrix cores and 88 by the fallback kernel, the two batch elements' keys kept apart.
+    q, k, w = workloads.indexer_inputs(4, 2, torch.bfloat16)
+    q = q[:, :600].contiguous()
+    idx, sc = _gpu_topk(q, k, w, 1024, flags=sti.FLAG_TAU_PLUS_INF)
+    _check(q, k, w, idx, sc, 1024)
