@@ -61,6 +61,12 @@ _SIGNATURES = {
         [ctypes.c_int, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
          ctypes.c_float, _p, _sz, _p, _sz, _p],
     ),
+    "gw_indexer_topk_bwd_dense_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
+    "gw_indexer_topk_bwd_dense": (
+        ctypes.c_int,
+        [ctypes.c_int, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
+         ctypes.c_float, _p, _p, _sz, _p],
+    ),
     "gw_indexer_view_bias_bwd_rows": (
         ctypes.c_int, [ctypes.c_int, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p],
     ),

@@ -232,6 +232,34 @@ int gw_indexer_topk_bwd(int dtype, const void* q, const void* k, const void* w,
                         void* workspace, size_t workspace_bytes,
                         void* stream);
 
+/* The same backward as masked dense passes on the matrix cores (bf16, Di = 64, Hi in
+ * {1,2,4,8}, S <= 65536, K <= 2048; other inputs return GW_ERR_UNSUPPORTED). Every (query,
+ * key) pair of a head is computed: z = q.k on the matrix cores, the gradients of the
+ * selected pairs enter as a tile gathered from the row's gradients in key order, and
+ * dq = scale F (w o k), dk = scale w o (F^T q), dw_s = scale k_s . (F^T q)_s with
+ * F = g [z > 0]; fp32 accumulation in a fixed order (no atomics). Replaces the same
+ * reference kernel as gw_indexer_topk_bwd (sparse_topk_indexer.py:1847-1944) for layers
+ * where a query selects a sizable share of the keys; needs no CSR.
+ * route: B device ints, cleared here; route[b] is set when batch element b has a position
+ * listed twice in a row (the reference counts it twice) or a non-finite q, k, w or w k (it
+ * would reach unselected pairs). Such elements are left untouched: compute them with
+ * gw_indexer_topk_bwd. Every element of dq/dk/dw of the other batch elements is written.
+ * q/k/w/grad_scores/topk_indices contiguous. workspace:
+ * gw_indexer_topk_bwd_dense_workspace_size(...) bytes, 16-byte aligned (selection words and
+ * prefixes, 6 * B * round_up(S, 32) / 32 * round_up(T, 32) bytes; gradients in key order,
+ * 2 * B * T * K bytes; q^T and (w o k)^T, 2 * B * Hi * 64 * (round_up(T, 32) +
+ * round_up(S, 32)) bytes; stream-K partials, 128 KiB per persistent workgroup).
+ */
+size_t gw_indexer_topk_bwd_dense_workspace_size(int64_t B, int64_t T, int64_t S, int64_t Hi, int64_t Di,
+                                                int64_t K);
+int gw_indexer_topk_bwd_dense(int dtype, const void* q, const void* k, const void* w,
+                              const int32_t* topk_indices, const void* grad_scores,
+                              void* dq, void* dk, void* dw,
+                              int64_t B, int64_t T, int64_t S, int64_t Hi, int64_t Di, int64_t K,
+                              float softmax_scale, int* route,
+                              void* workspace, size_t workspace_bytes,
+                              void* stream);
+
 /* Soft view-bias gradient, per query row: the first half of _scatter_view_bias_grad
  * (easyvolcap/utils/custom_indexer/sparse_topk_indexer.py:898-932, called from
  * SparseTopkIndexerViewBiasFunc.backward, :2159-2186). row_grad[b,t,v] (fp32 [B, T, Vs]) =
