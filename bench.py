@@ -82,8 +82,8 @@ def train_step_c4(steps: int = 5, warmup: int = 2, views: int = 24, batch: int =
     sparse_indexer_kl_loss(p, topk_scores)), and the backward of o (a random dO) and of
     the KL loss. As in the reference presets (detach_input, vggt.json:17,
     dsa_attention.py:4694-4695) the loss sees the attention mass detached: it trains the
-    indexer (KL backward, indexer dq/dkw over the CSR) and the attention gets the gradient
-    of o alone (the masked dense backward). ``kl_into_attention`` times the same step with
+    indexer (KL backward, the indexer's masked dense backward) and the attention gets the
+    gradient of o alone (the masked dense backward): no CSR is built. ``kl_into_attention`` times the same step with
     the mass not detached (the KL gradient also flows into q, k, v: the CSR backward with
     dattn). Times each phase with HIP events on the launch stream."""
     import torch

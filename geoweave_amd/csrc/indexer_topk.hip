@@ -25,8 +25,12 @@
 //                           exceed the register slots is queued for K2b.
 //  K2b select_wide_kernel:  persistent workgroups: all candidates of a queued query in
 //                           LDS, block radix select.
-//  K3 fallback_kernel:      exact brute force for queued queries (scores to scratch, radix
-//                           select) - correct for any input, used rarely.
+//  K3 score_kernel<SAMPLE> on the queued rows (up to kFullRows per batch element): MFMA
+//                           scores of each queued row against every key, gathered rows,
+//                           the key range split finely; full_select_kernel: exact top-k
+//                           of those rows by range-relative histogram levels + block radix
+//                           select; fallback_kernel: scores and selects any rows past
+//                           kFullRows itself - correct for any input, used rarely.
 // Exactness: if count(score > tau) >= topk, every member of the top-k scores > tau and is a
 // candidate, so selecting among the candidates is exact (otherwise the query has fewer than
 // topk candidates and goes to the brute force). Ties at the k-th value are broken
