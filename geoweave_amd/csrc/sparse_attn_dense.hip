@@ -75,6 +75,11 @@ __device__ __forceinline__ int vscale_exp(uint32_t bits) {
   return min(15 - x, 126);
 }
 
+// LDS byte address of a pointer into a __shared__ array (the operand of a ds_* instruction).
+__device__ __forceinline__ uint32_t lds_addr(const float* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const float*)p;
+}
+
 constexpr int kVmaxKeys = 256;  // keys per workgroup of dense_vmax_kernel (one head)
 
 __global__ __launch_bounds__(256) void dense_vmax_kernel(const uint16_t* __restrict__ v, int64_t vsb, int64_t vss,
@@ -202,12 +207,18 @@ struct DenseParams {
   int T, S, Spad, H, nqb, tpad, nchunk;
   float scale_log2;
   // attn_sum (ATTN kernels only): the score q.k (not yet scaled) of every selected (query,
-  // key) and head, sws[((b * H + h) * T + t) * K + slot] (head-major: one workgroup, which
-  // holds one head, fills whole cache lines of a row), slot = rank of the key among the
-  // query's selected keys in ascending key order.
+  // key) and head, sws[((b * H + h) * T + t) * sws_row(K) + slot] (head-major: one
+  // workgroup, which holds one head, fills whole cache lines of a row), slot = rank of the
+  // key among the query's selected keys in ascending key order.
   float* sws;
   int K;
 };
+
+// attn_sum score rows are K rounded up to 8, plus kSwsPad floats long (32-byte aligned): the
+// forward writes a query's selected scores 4 slots at a time, so the last 4 written may run
+// past its last slot in use (those are never read).
+constexpr int kSwsPad = 8;
+__host__ __device__ __forceinline__ int64_t sws_row(int64_t K) { return (K + 7) / 8 * 8 + kSwsPad; }
 
 // Waves per workgroup, sharing each K/V tile. Two workgroups share a CU (two waves per SIMD
 // from different workgroups): one wave's barrier or memory wait is not the other's.
@@ -222,13 +233,19 @@ static_assert(kDW == 4, "the tile staging moves two K and two V^T rows of 64 per
 
 template <typename E, bool ATTN>
 __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DenseParams p) {
-  __shared__ __align__(16) uint8_t ktile[2][8192];
-  __shared__ __align__(16) uint8_t vtile[2][8192];
+  // Two buffers of each tile, as separate arrays indexed at compile time (the tile loop is
+  // unrolled by two): the compiler then knows which LDS reads a pending direct-to-LDS load
+  // can overlap, and waits for none of them in the loop.
+  __shared__ __align__(16) uint8_t ktile0[8192], ktile1[8192];
+  __shared__ __align__(16) uint8_t vtile0[8192], vtile1[8192];
   __shared__ float vsc_s[64];
-  // attn_sum: per lane a row of the 16 scores of each block (rows of 16 kQPW + 4 floats:
-  // 16-byte stores of 16 consecutive lanes touch distinct banks)
-  constexpr int kArow = 16 * kQPW + 4;
-  __shared__ __align__(16) float ascore[ATTN ? kDW : 1][ATTN ? 64 * kArow : 4];
+  // attn_sum: per query of the wave (block a, column col) a row of 44 floats (176 bytes, so the
+  // 16-byte stores of 16 consecutive lanes touch distinct banks): a ring of 8 slots that gathers
+  // the query's selected scores until 4 consecutive slots of its row are complete (32-byte
+  // aligned: at byte 0 of even rows, 16 of odd ones), then the sub-tile's 32 scores in key order
+  // (at byte 32 of even rows, 48 of odd ones).
+  constexpr int kArow = 44;
+  __shared__ __align__(32) float ascore[ATTN ? kDW * 32 * kQPW * kArow : 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -285,17 +302,16 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
   const uint32_t kcol = (uint32_t)lc * 16u;
   const uint32_t vo0 = ((uint32_t)srow * (uint32_t)p.Spad + (uint32_t)lc * 8u) * 2u;
   const uint32_t vo1 = vo0 + (uint32_t)p.Spad * 64u;  // row srow + 32
-  auto dload = [&](int k0, int bf) {
+  auto dload = [&](int k0, uint8_t* kdst, uint8_t* vdst) {
     // Rows past the end read row S - 1 (their keys are never selected), taken from a base row
     // at most S - 1 so that the lane offsets stay in [0, 63] rows wherever the tile starts.
     const TileRows tr = tile_rows(k0, srow, p.S);
     const char* kt = kbase + (int64_t)tr.base * kss_b;
-    buffer_load16_lds(kt, __umul24(tr.r0, kss_b) + kcol, &ktile[bf][wseg]);
-    buffer_load16_lds(kt, __umul24(tr.r1, kss_b) + kcol,
-                      &ktile[bf][wseg + 4096]);
-    const char* vtile0 = vbase + (int64_t)k0 * 2;
-    buffer_load16_lds(vtile0, vo0, &vtile[bf][wseg]);
-    buffer_load16_lds(vtile0, vo1, &vtile[bf][wseg + 4096]);
+    buffer_load16_lds(kt, __umul24(tr.r0, kss_b) + kcol, kdst + wseg);
+    buffer_load16_lds(kt, __umul24(tr.r1, kss_b) + kcol, kdst + wseg + 4096);
+    const char* vsrc = vbase + (int64_t)k0 * 2;
+    buffer_load16_lds(vsrc, vo0, vdst + wseg);
+    buffer_load16_lds(vsrc, vo1, vdst + wseg + 4096);
   };
   // Operand reads: K rows 32 st + col (chunk 2 ks + half), V^T rows 32 db + col (chunk
   // 4 st + 2 ks + half); swz of these rows is swz(col).
@@ -310,16 +326,101 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
     return buffer_load4(mblk + min(j, nsub - 1) * mrow_b, (uint32_t)(col + 32 * a) * 4u);
   };
 
-  uint32_t rank_base[kQPW] = {0u, 0u};  // attn_sum: selected keys of the query before the sub-tile
-  float* srow_ws[kQPW];
-#pragma unroll
-  for (int a = 0; a < kQPW; ++a)
-    srow_ws[a] = ATTN ? p.sws + (((int64_t)b * p.H + h) * p.T + min(tq[a], p.T - 1)) * p.K : nullptr;
+  // attn_sum: lane (col, half) stores the scores of query tq[half] (block half), whose selected
+  // keys before the current sub-tile number rank_base; slots [0, fl) of its row are written.
+  uint32_t rank_base = 0u, fl = 0u;
+  float* const srow_ws =
+      ATTN ? p.sws + (((int64_t)b * p.H + h) * p.T + min(tq[half], p.T - 1)) * sws_row(p.K) : nullptr;
+  // LDS byte addresses (see ascore): this lane's chunk of group 0 of block 0 in the staging
+  // (group g at + 32 g, block 1 at + 32 rows), and its query's staging and ring.
+  uint32_t st_w = 0u, st_r = 0u, st_f = 0u;
+  if constexpr (ATTN) {
+    const uint32_t rows = lds_addr(ascore + wave * (32 * kQPW * kArow));
+    const uint32_t par = 16u * (uint32_t)(col & 1);  // rows 32 a + col and 32 half + col: parity of col
+    st_w = rows + (uint32_t)col * (kArow * 4) + 32u + par + 16u * (uint32_t)half;
+    st_f = rows + (uint32_t)(32 * half + col) * (kArow * 4) + par;
+    st_r = st_f + 32u;
+  }
+  // Writes slots [fl, fl + 4) of the row (read from the ring by the caller) when `flush`,
+  // then advances fl.
+  auto ring_store = [&](bool flush, const float4& f) {
+    if (flush) {
+      *reinterpret_cast<float4*>(srow_ws + fl) = f;
+      fl += 4u;
+    }
+  };
   const float ninf = -INFINITY;
 
   // One 32-key sub-tile: S^T for both blocks from the selection bias, the softmax in
   // registers, O^T += V^T P^T.
-  auto sub = [&](const uint8_t* kt, const uint8_t* vt, int st, const uint32_t (&w)[kQPW]) {
+  auto sub = [&](const uint8_t* kt, const uint8_t* vt, int st, const uint32_t (&w)[kQPW]) __attribute__((always_inline)) {
+    // attn_sum round state (see below): the selected-key word of this lane's query, its count,
+    // and the entries and ring slots read by issue() for finish().
+    uint32_t selw = 0u, cnt = 0u;
+    bool flush0 = false;
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    float rv0 = 0.f, rv1 = 0.f, rv2 = 0.f, rv3 = 0.f;
+    f32x4 rf = {0.f, 0.f, 0.f, 0.f};
+    // One round of the attn_sum stores, in two parts. issue(): the ring's oldest 4 slots (rf)
+    // and the next four selected entries (rv) read without waiting (selw = 0: v_ffbl gives -1,
+    // the float before the staging, inside the row; not used). finish(): the wait, the flush
+    // when `flush`, then the entries into the ring at slots rank_base + done + i (mod 8) when
+    // `append`. Between the two the sub-tile's weights and products run, and no instruction
+    // touches rv or rf.
+    auto issue = [&]() {
+      uint32_t ad[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t e;
+        asm("v_ffbl_b32 %0, %1" : "=v"(e) : "v"(selw));
+        ad[i] = st_r + (e << 2);
+        selw &= selw - 1u;
+      }
+      const uint32_t fa = st_f + ((fl << 2) & 16u);
+      asm volatile(
+          "ds_read_b32 %0, %5\n\tds_read_b32 %1, %6\n\tds_read_b32 %2, %7\n\tds_read_b32 %3, %8\n\t"
+          "ds_read_b128 %4, %9"
+          : "=&v"(rv0), "=&v"(rv1), "=&v"(rv2), "=&v"(rv3), "=&v"(rf)
+          : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3]), "v"(fa)
+          : "memory");
+    };
+    // The staging of block a's scores (see the attn_sum stores below), by the lanes that hold
+    // a selected key of the sub-tile (only selected entries are read back).
+    auto stage = [&](const f32x16& sa, int a) {
+      static_assert(kQPW == 2 && kArow * 32 * 4 == 5632, "block 1 rows at +5632 bytes");
+      if ((w[a] & (0x0F0F0F0Fu << (4 * half))) == 0u) return;
+      if (a == 0)
+        asm volatile(
+            "ds_write_b128 %0, %1\n\tds_write_b128 %0, %2 offset:32\n\t"
+            "ds_write_b128 %0, %3 offset:64\n\tds_write_b128 %0, %4 offset:96"
+            :
+            : "v"(st_w), "v"(__builtin_shufflevector(sa, sa, 0, 1, 2, 3)),
+              "v"(__builtin_shufflevector(sa, sa, 4, 5, 6, 7)), "v"(__builtin_shufflevector(sa, sa, 8, 9, 10, 11)),
+              "v"(__builtin_shufflevector(sa, sa, 12, 13, 14, 15))
+            : "memory");
+      else
+        asm volatile(
+            "ds_write_b128 %0, %1 offset:5632\n\tds_write_b128 %0, %2 offset:5664\n\t"
+            "ds_write_b128 %0, %3 offset:5696\n\tds_write_b128 %0, %4 offset:5728"
+            :
+            : "v"(st_w), "v"(__builtin_shufflevector(sa, sa, 0, 1, 2, 3)),
+              "v"(__builtin_shufflevector(sa, sa, 4, 5, 6, 7)), "v"(__builtin_shufflevector(sa, sa, 8, 9, 10, 11)),
+              "v"(__builtin_shufflevector(sa, sa, 12, 13, 14, 15))
+            : "memory");
+    };
+    auto finish = [&](uint32_t done, bool flush, bool append) {
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(rv0), "+v"(rv1), "+v"(rv2), "+v"(rv3), "+v"(rf) : : "memory");
+      ring_store(flush, make_float4(rf[0], rf[1], rf[2], rf[3]));
+      if (append) {
+        const uint32_t r4 = (rank_base + done) << 2;
+        asm volatile(
+            "ds_write_b32 %0, %4\n\tds_write_b32 %1, %5\n\tds_write_b32 %2, %6\n\tds_write_b32 %3, %7"
+            :
+            : "v"(st_f + (r4 & 28u)), "v"(st_f + ((r4 + 4u) & 28u)), "v"(st_f + ((r4 + 8u) & 28u)),
+              "v"(st_f + ((r4 + 12u) & 28u)), "v"(rv0), "v"(rv1), "v"(rv2), "v"(rv3)
+            : "memory");
+      }
+    };
     // The sub-tile's four K operands first: their LDS latency passes under the bias.
     uint4 ka[4];
 #pragma unroll
@@ -328,12 +429,16 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
 #pragma unroll
     for (int a = 0; a < kQPW; ++a) {
       if constexpr (ATTN) {
-        // Entry r of this lane is bit 8(r/4) + r%4 of w >> 4 half.
-        const uint32_t own = w[a] >> (4 * half);
+        // Natural-order words (bit i: key i selected): entry 4 g + j of this lane, key 8 g + 4
+        // half + j, is the sign bit of byte g of ~w << (7 - 4 half - j), set when the key is not
+        // selected; a sign-extended byte select masks -inf (one instruction per entry).
+        const uint32_t nw = ~w[a];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int sel = __builtin_amdgcn_sbfe((int)own, 8 * (r >> 2) + (r & 3), 1);  // 0 or -1
-          s[a][r] = select_bias(sel, ninf);
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t sh = nw << (7 - 4 * half - j);
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            s[a][4 * g + j] = __uint_as_float((uint32_t)(int32_t)(int8_t)(sh >> (8 * g)) & 0xFF800000u);
         }
       } else {
         // Bias-order words: entry 4 g + j of this lane is the sign bit of byte j of w << (g + 4
@@ -352,47 +457,6 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int a = 0; a < kQPW; ++a) s[a] = mma(E{}, ka[ks], qa[a][ks], s[a]);
-    if constexpr (ATTN) {
-      // Each selected entry's score (unscaled: dense_attn_sum_kernel applies the scale), at
-      // the slot of its key's rank. The lane's scores of both blocks go to its LDS row first
-      // (so both blocks' products complete before the loop), then one loop over the lane's
-      // selected entries of both blocks (most lanes have none or one per sub-tile) reads each
-      // back and stores it.
-      float* st_l = &ascore[wave][lane * kArow];
-#pragma unroll
-      for (int a = 0; a < kQPW; ++a)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<float4*>(st_l + 16 * a + 4 * g) =
-              make_float4(s[a][4 * g], s[a][4 * g + 1], s[a][4 * g + 2], s[a][4 * g + 3]);
-      // bit 16 a + r = entry r of block a (key 8(r/4) + 4 half + r%4)
-      uint32_t bits = 0;
-#pragma unroll
-      for (int a = 0; a < kQPW; ++a) {
-        const uint32_t own = w[a] >> (4 * half);
-        bits |= ((own & 0xFu) | ((own >> 4) & 0xF0u) | ((own >> 8) & 0xF00u) | ((own >> 12) & 0xF000u)) << (16 * a);
-      }
-      while (__builtin_amdgcn_ballot_w64(bits != 0u) != 0ull) {
-        if (bits != 0u) {
-          const int e = __builtin_ctz(bits);
-          const int a = e >> 4, r = e & 15;
-          const int kk = 8 * (r >> 2) + 4 * half + (r & 3);
-          uint32_t wa = w[0], rb = rank_base[0];
-          float* dst = srow_ws[0];
-#pragma unroll
-          for (int a2 = 1; a2 < kQPW; ++a2)
-            if (a == a2) {
-              wa = w[a2];
-              rb = rank_base[a2];
-              dst = srow_ws[a2];
-            }
-          dst[rb + __popc(wa & ((1u << kk) - 1u))] = st_l[e];
-          bits &= bits - 1u;
-        }
-      }
-#pragma unroll
-      for (int a = 0; a < kQPW; ++a) rank_base[a] += __popc(w[a]);
-    }
     // Per block: the weights, then its P·V products, so that the second block's exp2 (which
     // co-executes with matrix products on this GPU, unlike fp32 VALU) overlaps the first
     // block's products. The V^T operands are read once for both blocks.
@@ -403,6 +467,26 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
       for (int ks = 0; ks < 2; ++ks) va[db][ks] = *reinterpret_cast<const uint4*>(vt + voff(db, st, ks));
 #pragma unroll
     for (int a = 0; a < kQPW; ++a) {
+      if constexpr (ATTN) {
+        // attn_sum: each selected entry's score (unscaled: dense_attn_sum_kernel applies the
+        // scale) goes to the slot of its key's rank. The sub-tile's selected keys of a query take
+        // consecutive slots from rank_base on, so no lane works per entry: the two lanes of each
+        // query put its 32 scores in key order into the query's LDS row (block a's, as soon as
+        // its products are done), then lane (col, half) reads the scores of query tq[half] at its
+        // four lowest selected keys (issue(), here, while block 1's weights and products run)
+        // and appends them to the query's ring (finish(), at the end); whenever 4 slots of the
+        // row are complete they go to memory in one 16-byte store. The staging array is written
+        // and read by inline asm only: for any access the compiler sees it would first wait for
+        // the next tile's direct-to-LDS loads. A wave's LDS operations complete in issue order,
+        // so the partner lane's half of a row written here is in place for the reads.
+        stage(s[a], a);
+        if (a == kQPW - 1) {
+          selw = half ? w[1] : w[0];
+          cnt = __popc(selw);
+          flush0 = rank_base - fl >= 4u;
+          issue();
+        }
+      }
       // Weights with the current reference maximum. Their sum bounds each weight: while no
       // lane's sum exceeds kSumCap every p fits fp16, and the maximum stays where it is.
       float pv[16];
@@ -449,25 +533,38 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) acc[a][db] = mma(FP16{}, va[db][ks], pb[ks], acc[a][db]);
     }
+    if constexpr (ATTN) {
+      // The ring holds slots [fl, rank_base) (at most 7) and receives at most four more per
+      // round: a block of 4 completed earlier is written out first. Rarely a query selects
+      // more than four keys of a sub-tile: further rounds, each read and finished at once.
+      finish(0u, flush0, true);
+      for (uint32_t done = 4; __builtin_amdgcn_ballot_w64(cnt > done) != 0ull; done += 4) {
+        const bool more = cnt > done;
+        const bool fl_more = more && rank_base + done - fl >= 4u;
+        issue();
+        finish(done, fl_more, more);
+      }
+      rank_base += cnt;
+      asm volatile("" ::: "memory");
+    }
   };
 
   // Tile n (64 keys) lives in LDS buffer n % 2. While computing tile n the workgroup loads
   // tile n + 1 into the other buffer (last read before the previous barrier); one barrier per
   // tile.
   const int ntiles = p.Spad >> 6;
-  dload(0, 0);
+  dload(0, ktile0, vtile0);
   uint32_t w0[kQPW] = {mword(0, 0), mword(0, 1)}, w1[kQPW] = {mword(1, 0), mword(1, 1)};
   __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): tile 0 is in LDS
   __syncthreads();
-#pragma unroll 1
-  for (int n = 0; n < ntiles; ++n) {
-    const int buf = n & 1;
+  auto tile = [&](int n, const uint8_t* kc, const uint8_t* vc, uint8_t* kn, uint8_t* vn)
+                  __attribute__((always_inline)) {
     // The next tile's mask words before the tile loads.
     const uint32_t wn0[kQPW] = {mword(2 * n + 2, 0), mword(2 * n + 2, 1)};
     const uint32_t wn1[kQPW] = {mword(2 * n + 3, 0), mword(2 * n + 3, 1)};
-    if (n + 1 < ntiles) dload((n + 1) * 64, buf ^ 1);
-    sub(ktile[buf], vtile[buf], 0, w0);
-    sub(ktile[buf], vtile[buf], 1, w1);
+    if (n + 1 < ntiles) dload((n + 1) * 64, kn, vn);
+    sub(kc, vc, 0, w0);
+    sub(kc, vc, 1, w1);
 #pragma unroll
     for (int a = 0; a < kQPW; ++a) {
       w0[a] = wn0[a];
@@ -479,12 +576,29 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+  };
+#pragma unroll 1
+  for (int n = 0; n < ntiles; n += 2) {
+    tile(n, ktile0, vtile0, ktile1, vtile1);
+    if (n + 1 < ntiles) tile(n + 1, ktile1, vtile1, ktile0, vtile0);
   }
 
+  if constexpr (ATTN) {
+    // The ring's last slots (at most 7: two blocks of 4, the second partly past the row's
+    // count, inside its padding).
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t fa = st_f + ((fl << 2) & 16u);
+      float4 f;
+      asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(f) : "v"(fa) : "memory");
+      ring_store(fl < rank_base, f);
+    }
+  }
   // o = O / l scaled back by 2^-e per column, lse = (m + log2 l) ln 2; queries without any
   // selected key give o = 0, lse = -inf. Blocks holding a repeated position, and batch
   // elements with a non-finite K or V value, are written by the gather kernel.
   const bool finite = p.bad[b] == 0;
+
 #pragma unroll
   for (int a = 0; a < kQPW; ++a) {
     const int qb = qb0 + a, t = tq[a];
@@ -589,28 +703,22 @@ __global__ __launch_bounds__(256) void dense_attn_sum_kernel(const AttnSumParams
   // Per-slot sums over the heads, in slot order: head h's scores of this row are the K floats
   // at srow + h * hstride (head-major workspace), read four slots per lane and load; the
   // sums go through the wave's LDS row to the lanes that hold each slot's position.
-  const float* srow = p.sws + ((int64_t)b * p.H * p.T + t) * p.K;
-  const int64_t hstride = (int64_t)p.T * p.K;
+  const float* srow = p.sws + ((int64_t)b * p.H * p.T + t) * sws_row(p.K);
+  const int64_t hstride = (int64_t)p.T * sws_row(p.K);
   int nvalid = 0;  // valid positions sort first: slots [0, nvalid) are in use
 #pragma unroll
   for (int r = 0; r < R; ++r) nvalid += __popcll(__builtin_amdgcn_ballot_w64((key[r] >> 32) != 0xFFFFFFFFull));
   float* ssum = &slot_sum[wave][0];
-  const bool vec = (p.K & 3) == 0;  // head rows 16-byte aligned
   for (int i0 = 4 * lane; i0 < nvalid; i0 += 256) {
     float a4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
     for (int h = 0; h < p.H; ++h) {
       const float l2 = lse2_s[wave][h];
       if (l2 == -INFINITY) continue;  // a row without valid keys (the same for every head)
-      const float* sp = srow + h * hstride + i0;
-      float v[4];
-      if (vec) {
-        const float4 f = *reinterpret_cast<const float4*>(sp);  // i0 + 3 < K when K % 4 == 0
-        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
-      } else {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = i0 + u < p.K ? sp[u] : 0.f;
-      }
+      // 16-byte loads: head rows are 32-byte aligned and padded past any slot in use by at
+      // least 3 (slots at or past nvalid are never used)
+      const float4 f = *reinterpret_cast<const float4*>(srow + h * hstride + i0);
+      const float v[4] = {f.x, f.y, f.z, f.w};
 #pragma unroll
       for (int u = 0; u < 4; ++u) a4[u] += fexp2(fmaf(v[u], p.scale_log2, -l2));
     }
@@ -689,7 +797,7 @@ DenseLayout dense_layout(int64_t B, int64_t T, int64_t S, int64_t H, int64_t K, 
   L.vt = o;
   o = up(o + (size_t)B * (size_t)H * 64 * (size_t)L.spad * 2);
   L.sws = o;
-  if (attn) o = up(o + (size_t)B * (size_t)T * (size_t)K * (size_t)H * 4);
+  if (attn) o = up(o + (size_t)B * (size_t)T * (size_t)sws_row(K) * (size_t)H * 4);
   L.total = o;
   return L;
 }

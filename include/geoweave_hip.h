@@ -478,7 +478,7 @@ int gw_source_downsample_static_pack4(int dtype, const void* sub_w, int64_t B, i
  * 16-byte aligned: the selection words (B * round_up(S, 64) / 32 * round_up(T, 256) * 4
  * bytes), per-block and per-batch-element flags, the |V| column maxima (B * H * 64 * 4 bytes), the scaled fp16
  * V^T (B * H * 64 * round_up(S, 64) * 2 bytes) and, with attn_sum, the selected scores
- * (B * T * K * H * 4 bytes).
+ * (B * T * (round_up(K, 8) + 8) * H * 4 bytes).
  * ------------------------------------------------------------------------------------ */
 size_t gw_sparse_attn_fwd_dense_workspace_size(int64_t B, int64_t T, int64_t S, int64_t H, int64_t D,
                                                int64_t K, int want_attn_sum);

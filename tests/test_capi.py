@@ -167,8 +167,8 @@ def test_dense_fwd_workspace_and_argument_checks_without_gpu():
     # x 2 B
     base = 2560 + 16 * 64 * 4 + 16 * 64 * 64 * 2
     assert lib.gw_sparse_attn_fwd_dense_workspace_size(1, 4, 4, 16, 64, 4, 0) == base
-    # + the selected scores for attn_sum: T x K x H x 4 B
-    assert lib.gw_sparse_attn_fwd_dense_workspace_size(1, 4, 4, 16, 64, 4, 1) == base + 4 * 4 * 16 * 4
+    # + the selected scores for attn_sum: T x (K rounded up to 8, + 8) x H x 4 B
+    assert lib.gw_sparse_attn_fwd_dense_workspace_size(1, 4, 4, 16, 64, 4, 1) == base + 4 * 16 * 16 * 4
     assert lib.gw_sparse_attn_fwd_dense_workspace_size(1, 4, 4, 16, 128, 4, 0) == 0
     assert _dense_call(D=128) == 2
     assert b"head dim" in lib.gw_last_error()
