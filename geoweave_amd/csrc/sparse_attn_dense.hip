@@ -239,13 +239,12 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
   __shared__ __align__(16) uint8_t ktile0[8192], ktile1[8192];
   __shared__ __align__(16) uint8_t vtile0[8192], vtile1[8192];
   __shared__ float vsc_s[64];
-  // attn_sum: per query of the wave (block a, column col) a row of 44 floats (176 bytes, so the
-  // 16-byte stores of 16 consecutive lanes touch distinct banks): a ring of 8 slots that gathers
-  // the query's selected scores until 4 consecutive slots of its row are complete (32-byte
-  // aligned: at byte 0 of even rows, 16 of odd ones), then the sub-tile's 32 scores in key order
-  // (at byte 32 of even rows, 48 of odd ones).
+  // attn_sum: per query of the wave (block a, column col) a row of 44 floats (176 bytes, an odd
+  // multiple of 16, so the 16-byte stores of 16 consecutive lanes touch distinct banks): a ring
+  // of 8 slots that gathers the query's selected scores until 4 consecutive slots of its row
+  // are complete (bytes 0-31), then the sub-tile's 32 scores in key order (bytes 32-159).
   constexpr int kArow = 44;
-  __shared__ __align__(32) float ascore[ATTN ? kDW * 32 * kQPW * kArow : 4];
+  __shared__ __align__(16) float ascore[ATTN ? kDW * 32 * kQPW * kArow : 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -336,9 +335,8 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
   uint32_t st_w = 0u, st_r = 0u, st_f = 0u;
   if constexpr (ATTN) {
     const uint32_t rows = lds_addr(ascore + wave * (32 * kQPW * kArow));
-    const uint32_t par = 16u * (uint32_t)(col & 1);  // rows 32 a + col and 32 half + col: parity of col
-    st_w = rows + (uint32_t)col * (kArow * 4) + 32u + par + 16u * (uint32_t)half;
-    st_f = rows + (uint32_t)(32 * half + col) * (kArow * 4) + par;
+    st_w = rows + (uint32_t)col * (kArow * 4) + 32u + 16u * (uint32_t)half;
+    st_f = rows + (uint32_t)(32 * half + col) * (kArow * 4);
     st_r = st_f + 32u;
   }
   // Writes slots [fl, fl + 4) of the row (read from the ring by the caller) when `flush`,
