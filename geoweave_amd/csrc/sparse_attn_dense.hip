@@ -340,12 +340,18 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
     st_r = st_f + 32u;
   }
   // Writes slots [fl, fl + 4) of the row (read from the ring by the caller) when `flush`,
-  // then advances fl.
-  auto ring_store = [&](bool flush, const float4& f) {
-    if (flush) {
-      *reinterpret_cast<float4*>(srow_ws + fl) = f;
-      fl += 4u;
-    }
+  // then advances fl; lanes that do not flush are masked off inside the asm block (no branch).
+  typedef float f32x4r __attribute__((ext_vector_type(4)));
+  auto ring_store = [&](bool flush, const f32x4r& f) {
+    float* dst = srow_ws + fl;
+    uint64_t sv;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\tv_cmp_ne_u32 vcc, 0, %3\n\ts_and_b64 exec, exec, vcc\n\t"
+        "global_store_dwordx4 %1, %2, off\n\ts_mov_b64 exec, %0"
+        : "=&s"(sv)
+        : "v"(dst), "v"(f), "v"((uint32_t)flush)
+        : "vcc", "memory");
+    fl += flush ? 4u : 0u;
   };
   const float ninf = -INFINITY;
 
@@ -383,32 +389,36 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
           : "memory");
     };
     // The staging of block a's scores (see the attn_sum stores below), by the lanes that hold
-    // a selected key of the sub-tile (only selected entries are read back).
+    // a selected key of the sub-tile (only selected entries are read back): the other lanes are
+    // masked off inside the asm block, so the code around it stays one basic block.
     auto stage = [&](const f32x16& sa, int a) {
       static_assert(kQPW == 2 && kArow * 32 * 4 == 5632, "block 1 rows at +5632 bytes");
-      if ((w[a] & (0x0F0F0F0Fu << (4 * half))) == 0u) return;
+      const uint32_t bits = w[a] & (0x0F0F0F0Fu << (4 * half));
+      uint64_t sv;
       if (a == 0)
         asm volatile(
-            "ds_write_b128 %0, %1\n\tds_write_b128 %0, %2 offset:32\n\t"
-            "ds_write_b128 %0, %3 offset:64\n\tds_write_b128 %0, %4 offset:96"
-            :
+            "s_mov_b64 %0, exec\n\tv_cmp_ne_u32 vcc, 0, %6\n\ts_and_b64 exec, exec, vcc\n\t"
+            "ds_write_b128 %1, %2\n\tds_write_b128 %1, %3 offset:32\n\t"
+            "ds_write_b128 %1, %4 offset:64\n\tds_write_b128 %1, %5 offset:96\n\ts_mov_b64 exec, %0"
+            : "=&s"(sv)
             : "v"(st_w), "v"(__builtin_shufflevector(sa, sa, 0, 1, 2, 3)),
               "v"(__builtin_shufflevector(sa, sa, 4, 5, 6, 7)), "v"(__builtin_shufflevector(sa, sa, 8, 9, 10, 11)),
-              "v"(__builtin_shufflevector(sa, sa, 12, 13, 14, 15))
-            : "memory");
+              "v"(__builtin_shufflevector(sa, sa, 12, 13, 14, 15)), "v"(bits)
+            : "vcc", "memory");
       else
         asm volatile(
-            "ds_write_b128 %0, %1 offset:5632\n\tds_write_b128 %0, %2 offset:5664\n\t"
-            "ds_write_b128 %0, %3 offset:5696\n\tds_write_b128 %0, %4 offset:5728"
-            :
+            "s_mov_b64 %0, exec\n\tv_cmp_ne_u32 vcc, 0, %6\n\ts_and_b64 exec, exec, vcc\n\t"
+            "ds_write_b128 %1, %2 offset:5632\n\tds_write_b128 %1, %3 offset:5664\n\t"
+            "ds_write_b128 %1, %4 offset:5696\n\tds_write_b128 %1, %5 offset:5728\n\ts_mov_b64 exec, %0"
+            : "=&s"(sv)
             : "v"(st_w), "v"(__builtin_shufflevector(sa, sa, 0, 1, 2, 3)),
               "v"(__builtin_shufflevector(sa, sa, 4, 5, 6, 7)), "v"(__builtin_shufflevector(sa, sa, 8, 9, 10, 11)),
-              "v"(__builtin_shufflevector(sa, sa, 12, 13, 14, 15))
-            : "memory");
+              "v"(__builtin_shufflevector(sa, sa, 12, 13, 14, 15)), "v"(bits)
+            : "vcc", "memory");
     };
     auto finish = [&](uint32_t done, bool flush, bool append) {
       asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(rv0), "+v"(rv1), "+v"(rv2), "+v"(rv3), "+v"(rf) : : "memory");
-      ring_store(flush, make_float4(rf[0], rf[1], rf[2], rf[3]));
+      ring_store(flush, rf);
       if (append) {
         const uint32_t r4 = (rank_base + done) << 2;
         asm volatile(
@@ -589,7 +599,7 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
       const uint32_t fa = st_f + ((fl << 2) & 16u);
       float4 f;
       asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(f) : "v"(fa) : "memory");
-      ring_store(fl < rank_base, f);
+      ring_store(fl < rank_base, (f32x4r){f.x, f.y, f.z, f.w});
     }
   }
   // o = O / l scaled back by 2^-e per column, lse = (m + log2 l) ln 2; queries without any
