@@ -706,11 +706,11 @@ __global__ __launch_bounds__(256) void dense_attn_sum_kernel(const AttnSumParams
     // invalid positions (and padding past K) sort last, after every valid key
     key[r] = ((uint64_t)(ok ? (uint32_t)ps : 0xFFFFFFFFu) << 32) | (uint32_t)j;
   }
-  wave_bitonic_sort<R>(key);
-  lds_fence();
   // Per-slot sums over the heads, in slot order: head h's scores of this row are the K floats
-  // at srow + h * hstride (head-major workspace), read four slots per lane and load; the
-  // sums go through the wave's LDS row to the lanes that hold each slot's position.
+  // at srow + h * hstride (head-major workspace), four slots per lane and load, the loads of 16
+  // heads in flight at once; the sums go through the wave's LDS row to the lanes that hold each
+  // slot's position after the sort below (the sums do not depend on it).
+  lds_fence();
   const float* srow = p.sws + ((int64_t)b * p.H * p.T + t) * sws_row(p.K);
   const int64_t hstride = (int64_t)p.T * sws_row(p.K);
   int nvalid = 0;  // valid positions sort first: slots [0, nvalid) are in use
@@ -719,20 +719,28 @@ __global__ __launch_bounds__(256) void dense_attn_sum_kernel(const AttnSumParams
   float* ssum = &slot_sum[wave][0];
   for (int i0 = 4 * lane; i0 < nvalid; i0 += 256) {
     float a4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-    for (int h = 0; h < p.H; ++h) {
-      const float l2 = lse2_s[wave][h];
-      if (l2 == -INFINITY) continue;  // a row without valid keys (the same for every head)
+    for (int h0 = 0; h0 < p.H; h0 += 16) {
       // 16-byte loads: head rows are 32-byte aligned and padded past any slot in use by at
-      // least 3 (slots at or past nvalid are never used)
-      const float4 f = *reinterpret_cast<const float4*>(srow + h * hstride + i0);
-      const float v[4] = {f.x, f.y, f.z, f.w};
+      // least 3 (slots at or past nvalid are never used); heads past H re-read head H - 1.
+      float4 f[16];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) a4[u] += fexp2(fmaf(v[u], p.scale_log2, -l2));
+      for (int u = 0; u < 16; ++u)
+        f[u] = *reinterpret_cast<const float4*>(srow + min(h0 + u, p.H - 1) * hstride + i0);
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        if (h0 + u >= p.H) break;
+        const float l2 = lse2_s[wave][h0 + u];
+        if (l2 == -INFINITY) continue;  // a row without valid keys (the same for every head)
+        a4[0] += fexp2(fmaf(f[u].x, p.scale_log2, -l2));
+        a4[1] += fexp2(fmaf(f[u].y, p.scale_log2, -l2));
+        a4[2] += fexp2(fmaf(f[u].z, p.scale_log2, -l2));
+        a4[3] += fexp2(fmaf(f[u].w, p.scale_log2, -l2));
+      }
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) ssum[i0 + u] = a4[u];
   }
+  wave_bitonic_sort<R>(key);
   lds_fence();
   float av[R], zv[R];
   float sa = 0.f, mz = -INFINITY;

@@ -214,6 +214,45 @@ def test_attn_sum_matches_oracle(gpu_device, B, T, S, H, K, inv):
     torch.testing.assert_close(attn.sum(-1)[valid], torch.full((int(valid.sum()),), float(H)), atol=2e-3, rtol=1e-4)
 
 
+def test_attn_sum_clustered_selections(gpu_device):
+    # Rows selecting whole runs of consecutive keys (up to 32 selected keys of one query in a
+    # 32-key sub-tile: eight rounds of the per-query score runs, with flushes of the score ring
+    # between them), single keys, the last keys only with -1 padding, and random keys; every
+    # row listed in a random order, so the list position j of a key is arbitrary. K = 100 (not
+    # a multiple of 8), T and S ragged.
+    B, T, S, H, K = 2, 300, 700, 4, 100
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn(B, T, H, 64, generator=g).bfloat16()
+    k = torch.randn(B, S, H, 64, generator=g).bfloat16()
+    v = torch.randn(B, S, H, 64, generator=g).bfloat16()
+    pos = torch.full((B, T, K), -1, dtype=torch.int32)
+    for b in range(B):
+        for t in range(T):
+            kind = t % 4
+            if kind == 0:
+                start = int(torch.randint(0, S - K, (1,), generator=g))
+                row = torch.arange(start, start + K)
+            elif kind == 1:
+                starts = torch.randperm(S // 40, generator=g)[:3] * 40
+                row = torch.cat([torch.arange(int(s0), int(s0) + 33) for s0 in starts] + [torch.tensor([S - 1])])
+            elif kind == 2:
+                row = torch.randperm(S, generator=g)[:K]
+            else:
+                row = torch.cat([torch.arange(S - 10, S), torch.full((K - 10,), -1)])
+            pos[b, t] = row[torch.randperm(K, generator=g)].to(torch.int32)
+    pos[1, 5] = -1                    # a row without any valid key
+    pos[1, 6] = -1
+    pos[1, 6, 17] = 3                 # a row with a single key
+    print(f"[dense attn_sum] clustered B={B} T={T} S={S} H={H} K={K}", flush=True)
+    o, attn, lse, _ = _run_attn(q, k, v, pos, scale=0.125)
+    ro, ra, rl = oatt.sparse_attention(q, k, v, pos, 0.125)
+    torch.testing.assert_close(o, ro, **TOL)
+    torch.testing.assert_close(attn, ra, atol=1e-4, rtol=1e-3)
+    torch.testing.assert_close(lse, rl, atol=1e-4, rtol=1e-4)
+    assert torch.all(attn[1, 5] == 0)
+    torch.testing.assert_close(attn[1, 6, 17], torch.tensor(float(H)), atol=1e-5, rtol=1e-5)
+
+
 def test_attn_sum_repeated_positions_and_bhtd(gpu_device):
     q, k, v = workloads.attention_inputs(1, 1, torch.bfloat16, tokens=200, seed=19)
     pos = workloads.random_positions(1, 200, 200, 13, seed=20)
