@@ -17,8 +17,8 @@ Names, argument meaning and return values follow the reference API (``:3108-3456
 q: ``[B, T, H, D]``, k/v: ``[B, S, H, D]`` (bthd), kv_positions: int32 ``[B, T, K]``
 shared by all heads; entries outside ``[0, S)`` are masked. Preconditions are the
 reference's (``:2013-2039``): fp16/bf16 inputs of one dtype, CUDA(HIP) tensors, int32
-positions of shape ``(B, T, K)``; this build supports head dims 64 and 128 (the
-reference: any d <= 128). ``bias`` and ``causal=True`` are rejected, as the reference's
+positions of shape ``(B, T, K)``, any head dim d <= 128 (the kernels are built for 64 and
+128; other d run on inputs zero-padded to the next of those). ``bias`` and ``causal=True`` are rejected, as the reference's
 forward kernel asserts (``:199``, ``:203``).
 """
 from __future__ import annotations
@@ -87,9 +87,23 @@ def _check_inputs(q, k, v, kv_positions, bias, causal, layout):
         raise NotImplementedError("attention bias is not supported by the sparse forward kernel")
     if causal:
         raise NotImplementedError("causal sparse-index attention is not supported")
-    if d not in (64, 128):
-        raise NotImplementedError(f"head dim {d} is not built (supported: 64, 128)")
+    if d < 1:
+        raise ValueError(f"head dim must be positive, got {d}")
     return batch, seqlen_q, seqlen_k, nheads, d
+
+
+# Head dims the kernels are built for. Any other d <= 128 (the reference takes any d up to
+# 128, sparse_index_flash_attn.py:2034) runs on q, k, v (and o, dO) zero-padded to the next
+# built size: padded dims add nothing to q.k, and the outputs' padded dims are dropped.
+NATIVE_HEAD_DIMS = (64, 128)
+
+
+def _padded_head_dim(d: int) -> int:
+    return 64 if d <= 64 else 128
+
+
+def _pad_head_dim(x: torch.Tensor, dp: int) -> torch.Tensor:
+    return torch.nn.functional.pad(x, (0, dp - x.shape[-1]))
 
 
 # Forward: "auto" picks the masked dense pass (gw_sparse_attn_fwd_dense) when a query
@@ -147,6 +161,13 @@ def _flash_attn_forward(
     the indexer KL row losses are computed in the same launch (gw_sparse_attn_fwd_kl) into
     ``kl_row_loss`` (fp32 [B*T])."""
     batch, seqlen_q, seqlen_k, nheads, d = _check_inputs(q, k, v, kv_positions, bias, causal, q_layout)
+    if d not in NATIVE_HEAD_DIMS:
+        dp = _padded_head_dim(d)
+        o, attn_sum, lse, scale = _flash_attn_forward(
+            _pad_head_dim(q, dp), _pad_head_dim(k, dp), _pad_head_dim(v, dp), kv_positions,
+            softmax_scale=softmax_scale or 1.0 / math.sqrt(d), return_attn=return_attn, q_layout=q_layout,
+            kl_logits=kl_logits, kl_eps=kl_eps, kl_row_loss=kl_row_loss)
+        return o[..., :d].contiguous(), attn_sum, lse, scale
     q, k, v = _prep(q), _prep(k), _prep(v)
     if kv_positions.stride(-1) != 1:
         kv_positions = kv_positions.contiguous()
@@ -206,6 +227,15 @@ def _flash_attn_forward(
 def _flash_attn_backward(do, q, k, v, kv_positions, o, lse, dattn_sum, softmax_scale, q_layout):
     from . import _backward
 
+    d = q.shape[-1]
+    if d not in NATIVE_HEAD_DIMS:
+        dp = _padded_head_dim(d)
+        if do is None:
+            do = torch.zeros_like(o)
+        dq, dk, dv = _backward.sparse_attn_backward(
+            *(_pad_head_dim(x, dp) for x in (do, q, k, v)), kv_positions, _pad_head_dim(o, dp), lse, dattn_sum,
+            softmax_scale, q_layout)
+        return dq[..., :d].contiguous(), dk[..., :d].contiguous(), dv[..., :d].contiguous()
     return _backward.sparse_attn_backward(do, q, k, v, kv_positions, o, lse, dattn_sum, softmax_scale, q_layout)
 
 

@@ -46,6 +46,13 @@ def _dense_applies(q, num_topk, src_len, softmax_scale) -> bool:
 
 
 def indexer_topk_backward(q, k, w, topk_indices, grad_scores, softmax_scale):
+    from .sparse_topk_indexer import KERNEL_HEAD_DIM, pad_head_dim
+
+    d = q.shape[-1]
+    if d < KERNEL_HEAD_DIM:
+        dq, dk, dw = indexer_topk_backward(pad_head_dim(q), pad_head_dim(k), w, topk_indices, grad_scores,
+                                           softmax_scale)
+        return dq[..., :d].contiguous(), dk[..., :d].contiguous(), dw
     global last_path
     bsz, tgt_len, n_heads, head_dim = q.shape
     src_len = k.shape[1]

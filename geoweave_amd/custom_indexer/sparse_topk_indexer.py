@@ -18,7 +18,8 @@ matrix-core products; the reference computes in ``q.dtype`` too, ``:1293``, and 
 may cast to ``score_dtype="float32"``, ``indexer.py:321-326``); scores come back in
 ``q.dtype``. mask: ``None``, an empty tensor, or an additive ``[B,T,S]`` (broadcast from
 ``[T,S]``/``[1,T,S]``), cast to ``q.dtype`` as the reference does (``:1299-1300``).
-Supported: ``Di = 64``, ``Hi in {1,2,4,8}`` (``{1,2,4}`` in float32), ``K <= 2048``.
+Supported: ``Di <= 64`` (the kernels take 64; smaller head dims run zero-padded to it),
+``Hi in {1,2,4,8}`` (``{1,2,4}`` in float32), ``K <= 2048``.
 
 ``view_bias_data`` (the soft view-bias training kernel, reference ``:2108-2186``): a dict
 with ``q_view_ids`` ``[B,T]``/``[T]``, ``s_view_ids`` ``[B,S]``/``[S]`` and ``view_bias``
@@ -56,6 +57,16 @@ def _normalize_mask(mask: Optional[torch.Tensor], bsz: int, tgt_len: int, src_le
     return mask.to(dtype).expand(bsz, tgt_len, src_len).contiguous()
 
 
+# The kernels' head dim. Smaller ones (the reference takes any, sparse_topk_indexer.py:777,
+# 1143) run on q and k zero-padded to it: padded dims add nothing to q.k, and the backward's
+# dq, dk are cut back to the input's head dim.
+KERNEL_HEAD_DIM = 64
+
+
+def pad_head_dim(x: torch.Tensor) -> torch.Tensor:
+    return torch.nn.functional.pad(x, (0, KERNEL_HEAD_DIM - x.shape[-1]))
+
+
 def _check(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor):
     if q.dim() != 4 or k.dim() != 4 or w.dim() != 3:
         raise ValueError("q/k/w must be [B,T,H,D], [B,S,H,D], [B,S,H]")
@@ -70,8 +81,8 @@ def _check(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor):
         raise TypeError(f"the HIP indexer takes bfloat16, float16 or float32 inputs, got {q.dtype}")
     if not (q.is_cuda and k.is_cuda and w.is_cuda):
         raise ValueError("q, k and w must be GPU tensors")
-    if head_dim != 64 or n_heads not in (1, 2, 4, 8):
-        raise NotImplementedError(f"indexer heads x dim {n_heads} x {head_dim} not built (1/2/4/8 x 64)")
+    if not 1 <= head_dim <= 64 or n_heads not in (1, 2, 4, 8):
+        raise NotImplementedError(f"indexer heads x dim {n_heads} x {head_dim} not built (1/2/4/8 x up to 64)")
     if q.dtype == torch.float32 and n_heads == 8:
         raise NotImplementedError("float32 indexer inputs are built for 1, 2 or 4 heads")
 
@@ -134,13 +145,15 @@ def indexer_topk_forward(
     (q_view_ids int32 [B,T], s_view_ids int32 [B,S], table [B,Vq,Vs] in q's dtype), all
     contiguous) on the current stream; returns (indices, scores)."""
     _check(q, k, w)
-    q = q.contiguous()
-    k = k.contiguous()
-    w = w.contiguous()
     bsz, tgt_len, n_heads, head_dim = q.shape
     src_len = k.shape[1]
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(head_dim)
+    if head_dim != KERNEL_HEAD_DIM:
+        q, k, head_dim = pad_head_dim(q), pad_head_dim(k), KERNEL_HEAD_DIM
+    q = q.contiguous()
+    k = k.contiguous()
+    w = w.contiguous()
     if not softmax_scale > 0:
         raise ValueError(f"softmax_scale must be positive, got {softmax_scale}")
     mask = _normalize_mask(mask, bsz, tgt_len, src_len, q.dtype)
