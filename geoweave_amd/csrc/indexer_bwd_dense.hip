@@ -455,16 +455,16 @@ __global__ __launch_bounds__(256, 2) void idxd_pass_kernel(const IdxDenseParams 
       // Gradient tile entries of this lane: group gq = streamed rows 8 gq + 4 half + 0..3.
       const uint16_t* gt = gtile[gc];
       uint2 gv[2][4];
-      uint32_t any = 0u;
 #pragma unroll
       for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
+        for (int gq = 0; gq < 4; ++gq)
           gv[a][gq] = *reinterpret_cast<const uint2*>(gt + ((((2 * gq + half) * kXRows) + 64 * wave + 32 * a + col) << 2));
-          any |= gv[a][gq].x | gv[a][gq].y;
-        }
-      // Blocks of the wave with no selected pair in the tile add nothing: skip the products.
-      if (__builtin_amdgcn_ballot_w64(any != 0u) != 0ull) {
+      // Products for every tile, also where the wave's gradient entries are all zero: the
+      // gate clears F there (an integer product, whatever z is) and the staged tiles are
+      // finite (non-finite inputs flag the batch element), so they add exact zeros. A skip
+      // branch would split the step and cost more than the rare all-zero tile saves.
+      {
         f32x16 z[2];
 #pragma unroll
         for (int a = 0; a < 2; ++a)
@@ -506,7 +506,7 @@ __global__ __launch_bounds__(256, 2) void idxd_pass_kernel(const IdxDenseParams 
       asm volatile("" ::: "memory");
     };
     // Four tiles per trip, unconditionally: a tile past n1 has an all-zero gradient tile and
-    // skips its products.
+    // adds nothing.
 #pragma unroll 1
     for (int n = n0; n < n1; n += 4) {
       step(n, ys0, yts0, ys3, yts3, wp1, wp2, wp0, vb, va);
