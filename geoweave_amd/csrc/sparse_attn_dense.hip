@@ -511,9 +511,12 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
           pb[ks] = make_uint4(pack_f16(pv[8 * ks], pv[8 * ks + 1]), pack_f16(pv[8 * ks + 2], pv[8 * ks + 3]),
                               pack_f16(pv[8 * ks + 4], pv[8 * ks + 5]), pack_f16(pv[8 * ks + 6], pv[8 * ks + 7]));
         // Two independent accumulation chains (a wave has few others to hide their latency).
-        float t[2] = {0.f, 0.f};
+        float t[2] = {pv[0], pv[8]};
 #pragma unroll
-        for (int r = 0; r < 16; ++r) t[r >> 3] += pv[r];
+        for (int r = 1; r < 8; ++r) {
+          t[0] += pv[r];
+          t[1] += pv[8 + r];
+        }
         return t[0] + t[1];
       };
       ls = weights(-m[a]);
@@ -559,37 +562,50 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
 
   // Tile n (64 keys) lives in LDS buffer n % 2. While computing tile n the workgroup loads
   // tile n + 1 into the other buffer (last read before the previous barrier); one barrier per
-  // tile.
+  // tile. The mask words of tile n + 2 are loaded after tile n's products, into the registers
+  // tile n used: they have a whole tile to arrive and are not waited for at the barrier.
   const int ntiles = p.Spad >> 6;
   dload(0, ktile0, vtile0);
-  uint32_t w0[kQPW] = {mword(0, 0), mword(0, 1)}, w1[kQPW] = {mword(1, 0), mword(1, 1)};
+  uint32_t w0[kQPW], w1[kQPW], x0[kQPW], x1[kQPW];  // words of sub-tiles 0, 1 (tile 0) and 2, 3 (tile 1)
+#pragma unroll
+  for (int a = 0; a < kQPW; ++a) {
+    w0[a] = mword(0, a);
+    w1[a] = mword(1, a);
+    x0[a] = mword(2, a);
+    x1[a] = mword(3, a);
+  }
   __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): tile 0 is in LDS
   __syncthreads();
-  auto tile = [&](int n, const uint8_t* kc, const uint8_t* vc, uint8_t* kn, uint8_t* vn)
-                  __attribute__((always_inline)) {
-    // The next tile's mask words before the tile loads.
-    const uint32_t wn0[kQPW] = {mword(2 * n + 2, 0), mword(2 * n + 2, 1)};
-    const uint32_t wn1[kQPW] = {mword(2 * n + 3, 0), mword(2 * n + 3, 1)};
-    if (n + 1 < ntiles) dload((n + 1) * 64, kn, vn);
-    sub(kc, vc, 0, w0);
-    sub(kc, vc, 1, w1);
+  auto tile = [&](int n, const uint8_t* kc, const uint8_t* vc, uint8_t* kn, uint8_t* vn, uint32_t (&wa)[kQPW],
+                  uint32_t (&wb)[kQPW]) __attribute__((always_inline)) {
+    // Past the end the last tile again, into the buffer no tile reads any more: no branch
+    // around the loads, so the compiler's count of those in flight stays exact.
+    dload(min(n + 1, ntiles - 1) * 64, kn, vn);
+    sub(kc, vc, 0, wa);
+    sub(kc, vc, 1, wb);
 #pragma unroll
     for (int a = 0; a < kQPW; ++a) {
-      w0[a] = wn0[a];
-      w1[a] = wn1[a];
+      wa[a] = mword(2 * n + 4, a);
+      wb[a] = mword(2 * n + 5, a);
     }
-    // This thread's loads of the next tile have reached LDS; after the barrier every thread's
-    // have, and every wave is done with this tile's buffer before it is refilled.
-    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+    // vmcnt(4): all but the four word loads just issued have landed, so this thread's loads
+    // of the next tile are in LDS; after the barrier every thread's are, and every wave is
+    // done with this tile's buffer before it is refilled.
+    __builtin_amdgcn_s_waitcnt(0x0074);  // vmcnt(4) lgkmcnt(0)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
+  // Pairs of tiles, then a last odd one: the loop returns to its top only after both tiles
+  // of a pair, so the words it starts with are always two barriers old.
+  int n = 0;
 #pragma unroll 1
-  for (int n = 0; n < ntiles; n += 2) {
-    tile(n, ktile0, vtile0, ktile1, vtile1);
-    if (n + 1 < ntiles) tile(n + 1, ktile1, vtile1, ktile0, vtile0);
+  for (; n + 1 < ntiles; n += 2) {
+    tile(n, ktile0, vtile0, ktile1, vtile1, w0, w1);
+    tile(n + 1, ktile1, vtile1, ktile0, vtile0, x0, x1);
   }
+  if (n < ntiles) tile(n, ktile0, vtile0, ktile1, vtile1, w0, w1);
+  __builtin_amdgcn_s_waitcnt(0x0070);  // the loads issued past the end
 
   if constexpr (ATTN) {
     // The ring's last slots (at most 7: two blocks of 4, the second partly past the row's
