@@ -355,9 +355,48 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
   };
   const float ninf = -INFINITY;
 
-  // One 32-key sub-tile: S^T for both blocks from the selection bias, the softmax in
-  // registers, O^T += V^T P^T.
-  auto sub = [&](const uint8_t* kt, const uint8_t* vt, int st, const uint32_t (&w)[kQPW]) __attribute__((always_inline)) {
+  // One 32-key sub-tile in two parts. sub_qk: S^T for both blocks from the selection bias;
+  // sub_pv: the softmax in registers and O^T += V^T P^T.
+  auto sub_qk = [&](const uint8_t* kt, int st, const uint32_t (&w)[kQPW], f32x16 (&s)[kQPW])
+                    __attribute__((always_inline)) {
+    // The sub-tile's four K operands first: their LDS latency passes under the bias.
+    uint4 ka[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) ka[ks] = *reinterpret_cast<const uint4*>(kt + koff(st, ks));
+#pragma unroll
+    for (int a = 0; a < kQPW; ++a) {
+      if constexpr (ATTN) {
+        // Natural-order words (bit i: key i selected): entry 4 g + j of this lane, key 8 g + 4
+        // half + j, is the sign bit of byte g of ~w << (7 - 4 half - j), set when the key is not
+        // selected; a sign-extended byte select masks -inf (one instruction per entry).
+        const uint32_t nw = ~w[a];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t sh = nw << (7 - 4 * half - j);
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            s[a][4 * g + j] = __uint_as_float((uint32_t)(int32_t)(int8_t)(sh >> (8 * g)) & 0xFF800000u);
+        }
+      } else {
+        // Bias-order words: entry 4 g + j of this lane is the sign bit of byte j of w << (g + 4
+        // half), set when the key is not selected; a sign-extended byte select masks -inf
+        // (one instruction per entry).
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint32_t sh = w[a] << (g + 4 * half);
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            s[a][4 * g + j] = __uint_as_float((uint32_t)(int32_t)(int8_t)(sh >> (8 * j)) & 0xFF800000u);
+        }
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int a = 0; a < kQPW; ++a) s[a] = mma(E{}, ka[ks], qa[a][ks], s[a]);
+  };
+  auto sub_pv = [&](const uint8_t* vt, int st, const uint32_t (&w)[kQPW], f32x16 (&s)[kQPW])
+                    __attribute__((always_inline)) {
     // attn_sum round state (see below): the selected-key word of this lane's query, its count,
     // and the entries and ring slots read by issue() for finish().
     uint32_t selw = 0u, cnt = 0u;
@@ -429,42 +468,6 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
             : "memory");
       }
     };
-    // The sub-tile's four K operands first: their LDS latency passes under the bias.
-    uint4 ka[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) ka[ks] = *reinterpret_cast<const uint4*>(kt + koff(st, ks));
-    f32x16 s[kQPW];
-#pragma unroll
-    for (int a = 0; a < kQPW; ++a) {
-      if constexpr (ATTN) {
-        // Natural-order words (bit i: key i selected): entry 4 g + j of this lane, key 8 g + 4
-        // half + j, is the sign bit of byte g of ~w << (7 - 4 half - j), set when the key is not
-        // selected; a sign-extended byte select masks -inf (one instruction per entry).
-        const uint32_t nw = ~w[a];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t sh = nw << (7 - 4 * half - j);
-#pragma unroll
-          for (int g = 0; g < 4; ++g)
-            s[a][4 * g + j] = __uint_as_float((uint32_t)(int32_t)(int8_t)(sh >> (8 * g)) & 0xFF800000u);
-        }
-      } else {
-        // Bias-order words: entry 4 g + j of this lane is the sign bit of byte j of w << (g + 4
-        // half), set when the key is not selected; a sign-extended byte select masks -inf
-        // (one instruction per entry).
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const uint32_t sh = w[a] << (g + 4 * half);
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            s[a][4 * g + j] = __uint_as_float((uint32_t)(int32_t)(int8_t)(sh >> (8 * j)) & 0xFF800000u);
-        }
-      }
-    }
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int a = 0; a < kQPW; ++a) s[a] = mma(E{}, ka[ks], qa[a][ks], s[a]);
     // Per block: the weights, then its P·V products, so that the second block's exp2 (which
     // co-executes with matrix products on this GPU, unlike fp32 VALU) overlaps the first
     // block's products. The V^T operands are read once for both blocks.
@@ -581,8 +584,13 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
     // Past the end the last tile again, into the buffer no tile reads any more: no branch
     // around the loads, so the compiler's count of those in flight stays exact.
     dload(min(n + 1, ntiles - 1) * 64, kn, vn);
-    sub(kc, vc, 0, wa);
-    sub(kc, vc, 1, wb);
+    // Both sub-tiles' products first: the second's run on the matrix cores while the first's
+    // weights are formed.
+    f32x16 s0[kQPW], s1[kQPW];
+    sub_qk(kc, 0, wa, s0);
+    sub_qk(kc, 1, wb, s1);
+    sub_pv(vc, 0, wa, s0);
+    sub_pv(vc, 1, wb, s1);
 #pragma unroll
     for (int a = 0; a < kQPW; ++a) {
       wa[a] = mword(2 * n + 4, a);
