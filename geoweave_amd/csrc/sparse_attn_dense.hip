@@ -36,7 +36,7 @@
 //                        (0 * inf, -inf + inf), so such a batch element is computed by the
 //                        gather kernel, which reads only the selected rows, as the reference
 //                        does.
-//   dense_vt_kernel    — V^T as [B][H][64][S_pad] fp16 (S_pad = S rounded up to 64, zero
+//   dense_vt_kernel    — V^T as [B][H][64][S_pad] fp16 (S_pad = S rounded up to 128, zero
 //                        padded), keys in operand order: one 16-byte load per operand chunk.
 //   dense_attn_kernel  — 4 waves per workgroup, each on two 32-query blocks, all on one
 //                        head: each K and V^T tile is read from memory once per workgroup
@@ -224,7 +224,7 @@ __host__ __device__ __forceinline__ int64_t sws_row(int64_t K) { return (K + 7) 
 // from different workgroups): one wave's barrier or memory wait is not the other's.
 constexpr int kDW = 4;
 // Limits of the 32-bit lane offsets of the tile loads: a K token stride below 2^23 elements
-// (2^24 bytes, a 24-bit multiply), 64 rows of V^T (S padded to 64) below 2^32 bytes.
+// (2^24 bytes, a 24-bit multiply), 64 rows of V^T (S padded to 128, at most 2^25) below 2^32 bytes.
 constexpr int64_t kDenseMaxKRowStride = 1ll << 23;
 constexpr int64_t kDenseMaxS = (1ll << 25) - 64;
 constexpr int kQPW = 2;  // 32-query blocks per wave (one head): each K and V^T operand feeds two products
@@ -236,8 +236,11 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
   // Two buffers of each tile, as separate arrays indexed at compile time (the tile loop is
   // unrolled by two): the compiler then knows which LDS reads a pending direct-to-LDS load
   // can overlap, and waits for none of them in the loop.
-  __shared__ __align__(16) uint8_t ktile0[8192], ktile1[8192];
-  __shared__ __align__(16) uint8_t vtile0[8192], vtile1[8192];
+  // Tiles of kHT 64-key halves: one with attn_sum (whose staging rows need the LDS), two
+  // without.
+  constexpr int kHT = ATTN ? 1 : 2;
+  __shared__ __align__(16) uint8_t ktile0[kHT * 8192], ktile1[kHT * 8192];
+  __shared__ __align__(16) uint8_t vtile0[kHT * 8192], vtile1[kHT * 8192];
   __shared__ float vsc_s[64];
   // attn_sum: per query of the wave (block a, column col) a row of 44 floats (176 bytes, an odd
   // multiple of 16, so the 16-byte stores of 16 consecutive lanes touch distinct banks): a ring
@@ -563,43 +566,51 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
     }
   };
 
-  // Tile n (64 keys) lives in LDS buffer n % 2. While computing tile n the workgroup loads
-  // tile n + 1 into the other buffer (last read before the previous barrier); one barrier per
-  // tile. The mask words of tile n + 2 are loaded after tile n's products, into the registers
-  // tile n used: they have a whole tile to arrive and are not waited for at the barrier.
-  const int ntiles = p.Spad >> 6;
-  dload(0, ktile0, vtile0);
-  uint32_t w0[kQPW], w1[kQPW], x0[kQPW], x1[kQPW];  // words of sub-tiles 0, 1 (tile 0) and 2, 3 (tile 1)
+  // Tile n (kHT halves of 64 keys, kSPT sub-tiles) lives in LDS buffer n % 2. While computing
+  // tile n the workgroup loads tile n + 1 into the other buffer (last read before the previous
+  // barrier); one barrier per tile. The mask words of tile n + 2 are loaded after tile n's
+  // products, into the registers tile n used: they have a whole tile to arrive and are not
+  // waited for at the barrier.
+  constexpr int kSPT = 2 * kHT;
+  const int ntiles = p.Spad / (64 * kHT);  // Spad is a whole number of 128-key tiles
+  auto tload = [&](int n, uint8_t* kd, uint8_t* vd) __attribute__((always_inline)) {
 #pragma unroll
-  for (int a = 0; a < kQPW; ++a) {
-    w0[a] = mword(0, a);
-    w1[a] = mword(1, a);
-    x0[a] = mword(2, a);
-    x1[a] = mword(3, a);
-  }
+    for (int hf = 0; hf < kHT; ++hf) dload((n * kHT + hf) * 64, kd + hf * 8192, vd + hf * 8192);
+  };
+  auto words = [&](int n, uint32_t (&wd)[kSPT][kQPW]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < kSPT; ++j)
+#pragma unroll
+      for (int a = 0; a < kQPW; ++a) wd[j][a] = mword(kSPT * n + j, a);
+  };
+  uint32_t wA[kSPT][kQPW], wB[kSPT][kQPW];  // words of the even and the odd tiles
+  tload(0, ktile0, vtile0);
+  words(0, wA);
+  words(1, wB);
   __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): tile 0 is in LDS
   __syncthreads();
-  auto tile = [&](int n, const uint8_t* kc, const uint8_t* vc, uint8_t* kn, uint8_t* vn, uint32_t (&wa)[kQPW],
-                  uint32_t (&wb)[kQPW]) __attribute__((always_inline)) {
+  auto tile = [&](int n, const uint8_t* kc, const uint8_t* vc, uint8_t* kn, uint8_t* vn,
+                  uint32_t (&wd)[kSPT][kQPW]) __attribute__((always_inline)) {
     // Past the end the last tile again, into the buffer no tile reads any more: no branch
     // around the loads, so the compiler's count of those in flight stays exact.
-    dload(min(n + 1, ntiles - 1) * 64, kn, vn);
-    // Both sub-tiles' products first: the second's run on the matrix cores while the first's
-    // weights are formed.
-    f32x16 s0[kQPW], s1[kQPW];
-    sub_qk(kc, 0, wa, s0);
-    sub_qk(kc, 1, wb, s1);
-    sub_pv(vc, 0, wa, s0);
-    sub_pv(vc, 1, wb, s1);
+    tload(min(n + 1, ntiles - 1), kn, vn);
+    // The products run one sub-tile ahead of the softmax: sub-tile j's are issued before
+    // sub-tile j - 1's weights, so they run on the matrix cores while those are formed.
+    // (attn_sum takes the sub-tiles' scores in key order: sub_pv in order.)
+    f32x16 ss[2][kQPW];
+    sub_qk(kc, 0, wd[0], ss[0]);
 #pragma unroll
-    for (int a = 0; a < kQPW; ++a) {
-      wa[a] = mword(2 * n + 4, a);
-      wb[a] = mword(2 * n + 5, a);
+    for (int j = 1; j < kSPT; ++j) {
+      sub_qk(kc + (j >> 1) * 8192, j & 1, wd[j], ss[j & 1]);
+      sub_pv(vc + ((j - 1) >> 1) * 8192, (j - 1) & 1, wd[j - 1], ss[(j - 1) & 1]);
     }
-    // vmcnt(4): all but the four word loads just issued have landed, so this thread's loads
-    // of the next tile are in LDS; after the barrier every thread's are, and every wave is
-    // done with this tile's buffer before it is refilled.
-    __builtin_amdgcn_s_waitcnt(0x0074);  // vmcnt(4) lgkmcnt(0)
+    sub_pv(vc + ((kSPT - 1) >> 1) * 8192, (kSPT - 1) & 1, wd[kSPT - 1], ss[(kSPT - 1) & 1]);
+    words(n + 2, wd);
+    // vmcnt(kSPT kQPW): all but the word loads just issued have landed, so this thread's
+    // loads of the next tile are in LDS; after the barrier every thread's are, and every wave
+    // is done with this tile's buffer before it is refilled.
+    static_assert(kSPT * kQPW <= 15, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt(0x0070 | (kSPT * kQPW));  // vmcnt(kSPT kQPW) lgkmcnt(0)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -609,10 +620,10 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
   int n = 0;
 #pragma unroll 1
   for (; n + 1 < ntiles; n += 2) {
-    tile(n, ktile0, vtile0, ktile1, vtile1, w0, w1);
-    tile(n + 1, ktile1, vtile1, ktile0, vtile0, x0, x1);
+    tile(n, ktile0, vtile0, ktile1, vtile1, wA);
+    tile(n + 1, ktile1, vtile1, ktile0, vtile0, wB);
   }
-  if (n < ntiles) tile(n, ktile0, vtile0, ktile1, vtile1, w0, w1);
+  if (n < ntiles) tile(n, ktile0, vtile0, ktile1, vtile1, wA);
   __builtin_amdgcn_s_waitcnt(0x0070);  // the loads issued past the end
 
   if constexpr (ATTN) {
@@ -818,7 +829,7 @@ DenseLayout dense_layout(int64_t B, int64_t T, int64_t S, int64_t H, int64_t K, 
   DenseLayout L;
   L.nqb = (int)((T + 31) / 32);
   L.nqb_pad = (L.nqb + kQBW - 1) / kQBW * kQBW;
-  L.spad = (int)((S + 63) / 64 * 64);
+  L.spad = (int)((S + 127) / 128 * 128);  // whole 128-key tiles of the plain forward
   // One pass over the positions (two 16-query halves per block) when the sub-tile words of
   // 16 queries fit the LDS, else chunks of kMaskChunk keys.
   L.rows_pass = L.spad / 32 <= kMaskRowsMaxSub;
