@@ -476,24 +476,28 @@ __global__ __launch_bounds__(256, 2) void idxd_pass_kernel(const IdxDenseParams 
 #pragma unroll
           for (int a = 0; a < 2; ++a) z[a] = mma(BF16{}, ya, xa[a][ks], z[a]);
         }
-        uint4 fb[2][2];
+        // Per block: its gate, then its products, so that the second block's gate overlaps
+        // the first block's products (the Y'^T operands read once for both).
+        uint4 ta[2][2];
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) ta[db][ks] = *reinterpret_cast<const uint4*>(ytt + ytoff(db, ks));
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+          uint4 fb[2];
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) {
             const uint2 g0 = gv[a][2 * ks], g1 = gv[a][2 * ks + 1];
             const f32x16& zz = z[a];
-            fb[a][ks] = make_uint4(gate2(g0.x, zz[8 * ks + 0], zz[8 * ks + 1]), gate2(g0.y, zz[8 * ks + 2], zz[8 * ks + 3]),
-                                   gate2(g1.x, zz[8 * ks + 4], zz[8 * ks + 5]), gate2(g1.y, zz[8 * ks + 6], zz[8 * ks + 7]));
+            fb[ks] = make_uint4(gate2(g0.x, zz[8 * ks + 0], zz[8 * ks + 1]), gate2(g0.y, zz[8 * ks + 2], zz[8 * ks + 3]),
+                                gate2(g1.x, zz[8 * ks + 4], zz[8 * ks + 5]), gate2(g1.y, zz[8 * ks + 6], zz[8 * ks + 7]));
           }
 #pragma unroll
-        for (int db = 0; db < 2; ++db)
+          for (int db = 0; db < 2; ++db)
 #pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
-            const uint4 ta = *reinterpret_cast<const uint4*>(ytt + ytoff(db, ks));
-#pragma unroll
-            for (int a = 0; a < 2; ++a) acc[a][db] = mma(BF16{}, ta, fb[a][ks], acc[a][db]);
-          }
+            for (int ks = 0; ks < 2; ++ks) acc[a][db] = mma(BF16{}, ta[db][ks], fb[ks], acc[a][db]);
+        }
       }
 
       scatter(gtile[gn], n + 1, wn1, vcur);

@@ -475,9 +475,9 @@ int gw_source_downsample_static_pack4(int dtype, const void* sub_w, int64_t B, i
  * Queries that list a position twice are computed by the gather kernel inside this call
  * (the reference counts a repeated position twice).
  * Workspace: gw_sparse_attn_fwd_dense_workspace_size(B, T, S, H, D, K, want_attn_sum) bytes,
- * 16-byte aligned: the selection words (B * round_up(S, 64) / 32 * round_up(T, 256) * 4
+ * 16-byte aligned: the selection words (B * round_up(S, 128) / 32 * round_up(T, 256) * 4
  * bytes), per-block and per-batch-element flags, the |V| column maxima (B * H * 64 * 4 bytes), the scaled fp16
- * V^T (B * H * 64 * round_up(S, 64) * 2 bytes) and, with attn_sum, the selected scores
+ * V^T (B * H * 64 * round_up(S, 128) * 2 bytes) and, with attn_sum, the selected scores
  * (B * T * (round_up(K, 8) + 8) * H * 4 bytes).
  * ------------------------------------------------------------------------------------ */
 size_t gw_sparse_attn_fwd_dense_workspace_size(int64_t B, int64_t T, int64_t S, int64_t H, int64_t D,
