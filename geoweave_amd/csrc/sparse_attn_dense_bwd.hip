@@ -323,7 +323,13 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dq_kernel(const DenseBw
 #pragma unroll
       for (int a = 0; a < kBQPW; ++a) dp[a] = mma(E{}, va, da[a][ks], dp[a]);
     }
-    uint4 dsb[kBQPW][2];
+    // Per block: p and dS, then its dQ products, so that the second block's exp2 overlaps the
+    // first block's products (the K^T operands read once for both).
+    uint4 ta[2][2];
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) ta[db][ks] = *reinterpret_cast<const uint4*>(ktt + toff(db, st, ks));
 #pragma unroll
     for (int a = 0; a < kBQPW; ++a) {
       float dsv[16];
@@ -332,17 +338,12 @@ __global__ __launch_bounds__(kBW * 64, 2) void dense_bwd_dq_kernel(const DenseBw
         const float pv = fexp2(fmaf(s[a][r], sl2, -lse2[a]));
         dsv[r] = pv * ((dp[a][r] - dlt[a]) * sig);
       }
-      dsb[a][0] = pack_quad<E>(dsv);
-      dsb[a][1] = pack_quad<E>(dsv + 8);
+      const uint4 dsb[2] = {pack_quad<E>(dsv), pack_quad<E>(dsv + 8)};
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) acc[a][db] = mma(E{}, ta[db][ks], dsb[ks], acc[a][db]);
     }
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const uint4 ta = *reinterpret_cast<const uint4*>(ktt + toff(db, st, ks));
-#pragma unroll
-        for (int a = 0; a < kBQPW; ++a) acc[a][db] = mma(E{}, ta, dsb[a][ks], acc[a][db]);
-      }
   };
 
   // Tile n (64 keys) lives in LDS buffer n % 2; while computing it the workgroup loads tile
