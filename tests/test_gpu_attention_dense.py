@@ -10,8 +10,9 @@ range and far below it (the per-column scaling), odd head counts, a softmax scal
 padding with T and S not multiples of 32 or 64, cross attention (T != S), empty rows,
 out-of-range and repeated positions (repeats go to the gather kernel inside the call, also
 when the mask is built in several key chunks), scores with a large dynamic range rising along
-the key order (the lazy maximum is raised and O rescaled on many tiles), bhtd strides,
-determinism, and a full-size layer on sampled rows.
+the key order (the lazy maximum is raised and O rescaled on many tiles), key counts around
+the 64- and 128-key tile boundaries, bhtd strides, determinism, and a full-size layer on
+sampled rows.
 """
 import contextlib
 
@@ -352,6 +353,33 @@ def test_random_shapes_against_the_oracle(gpu_device, case):
         torch.testing.assert_close(o2, ro.float(), **TOL)
         torch.testing.assert_close(attn, ra, atol=1e-4, rtol=1e-3)
         torch.testing.assert_close(lse2, rl, atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("S", [63, 64, 65, 127, 128, 129, 191, 192, 193, 255, 256, 257, 383, 385])
+def test_key_counts_around_the_128_key_tiles(gpu_device, S):
+    # The plain pass sweeps keys in 128-key tiles (two 64-key halves; keys padded to 128), the
+    # attn_sum pass in 64-key tiles: key counts just below, at and above each boundary, with
+    # the last keys selected by every query, against the oracle.
+    B, T, H = 1, 97, 2
+    K = min(S, 48)
+    g = torch.Generator().manual_seed(S)
+    q = torch.randn(B, T, H, 64, generator=g).bfloat16()
+    k = torch.randn(B, S, H, 64, generator=g).bfloat16()
+    v = torch.randn(B, S, H, 64, generator=g).bfloat16()
+    pos = _distinct_positions(B, T, S, K, seed=S + 1)
+    # key S - 1 first in every row; an entry that already listed it becomes -1 (no repeats)
+    rest = pos[..., 1:]
+    pos[..., 1:] = torch.where(rest == S - 1, torch.full_like(rest, -1), rest)
+    pos[..., 0] = S - 1
+    print(f"[dense tiles] S={S}", flush=True)
+    ro, ra, rl = oatt.sparse_attention(q, k, v, pos, 0.125)
+    o, lse = _run(q, k, v, pos, scale=0.125)
+    torch.testing.assert_close(o, ro.float(), **TOL)
+    torch.testing.assert_close(lse, rl, atol=1e-4, rtol=1e-4)
+    o2, attn, lse2, _ = _run_attn(q, k, v, pos, scale=0.125)
+    torch.testing.assert_close(o2, ro.float(), **TOL)
+    torch.testing.assert_close(attn, ra, atol=1e-4, rtol=1e-3)
+    torch.testing.assert_close(lse2, rl, atol=1e-4, rtol=1e-4)
 
 
 def _nonfinite_case(seed=41):
