@@ -87,19 +87,29 @@ __global__ __launch_bounds__(256) void idxd_prep_kernel(const int32_t* __restric
       dup |= (atomicOr(&words[(s >> 5) * RW + i], bit) & bit) != 0u;
     }
   };
+  // 16-byte path (K % 4 == 0, aligned positions): a thread's positions and their gradients
+  // (four of each per row and step) stay in registers from the words to the ranks.
+  constexpr int kNJ = kXMaxK / 4 / 256;
+  const uint16_t* gblk = grad + ((int64_t)b * T + min(q0, T - 1)) * K;
+  int4 pv[kNJ][kPrepQ];
+  uint2 gv[kNJ][kPrepQ];
   if (vec) {
     const int n4 = K >> 2;
-    for (int j4 = tid; j4 < n4; j4 += 256) {
-      int4 v[kPrepQ];
 #pragma unroll
-      for (int u = 0; u < kPrepQ; ++u)
-        v[u] = u < rows ? reinterpret_cast<const int4*>(pblk + (int64_t)u * K)[j4] : make_int4(-1, -1, -1, -1);
+    for (int jj = 0; jj < kNJ; ++jj) {
+      const int j4 = tid + 256 * jj;
 #pragma unroll
       for (int u = 0; u < kPrepQ; ++u) {
-        put(v[u].x, u);
-        put(v[u].y, u);
-        put(v[u].z, u);
-        put(v[u].w, u);
+        const bool ok = j4 < n4 && u < rows;
+        pv[jj][u] = ok ? reinterpret_cast<const int4*>(pblk + (int64_t)u * K)[j4] : make_int4(-1, -1, -1, -1);
+        gv[jj][u] = ok ? reinterpret_cast<const uint2*>(gblk + (int64_t)u * K)[j4] : make_uint2(0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < kPrepQ; ++u) {
+        put(pv[jj][u].x, u);
+        put(pv[jj][u].y, u);
+        put(pv[jj][u].z, u);
+        put(pv[jj][u].w, u);
       }
     }
   } else {
@@ -130,25 +140,47 @@ __global__ __launch_bounds__(256) void idxd_prep_kernel(const int32_t* __restric
     }
   }
   __syncthreads();
-  // [b][t / 8][kb][t % 8]: this workgroup's words are one contiguous run.
+  // [b][t / 8][kb][t % 8]: this workgroup's words are one contiguous run; a thread writes
+  // one block's 8 words and 8 prefixes with 16-byte stores.
   {
     uint32_t* wo = words_g + ((int64_t)b * (tpad >> 3) + blockIdx.x) * nsub * kPrepQ;
     uint16_t* po = pre_g + ((int64_t)b * (tpad >> 3) + blockIdx.x) * nsub * kPrepQ;
-    for (int e = tid; e < nsub * kPrepQ; e += 256) {
-      wo[e] = words[(e >> 3) * RW + (e & 7)];
-      po[e] = pre[e];
+    static_assert(kPrepQ == 8, "one block of words is two 16-byte stores");
+    for (int kb = tid; kb < nsub; kb += 256) {
+      const uint32_t* wr = words + kb * RW;
+      reinterpret_cast<uint4*>(wo + kb * 8)[0] = make_uint4(wr[0], wr[1], wr[2], wr[3]);
+      reinterpret_cast<uint4*>(wo + kb * 8)[1] = make_uint4(wr[4], wr[5], wr[6], wr[7]);
+      reinterpret_cast<uint4*>(po + kb * 8)[0] = reinterpret_cast<const uint4*>(pre + kb * 8)[0];
     }
   }
   // Each selected key's rank in its row: the prefix of its block plus the bits below it.
-  const uint16_t* gblk = grad + ((int64_t)b * T + min(q0, T - 1)) * K;
-  for (int i = 0; i < rows; ++i)
-    for (int j = tid; j < K; j += 256) {
-      const int32_t s = pblk[(int64_t)i * K + j];
-      if ((uint32_t)s < (uint32_t)S) {
-        const int r = pre[(s >> 5) * kPrepQ + i] + __popc(words[(s >> 5) * RW + i] & ((1u << (s & 31)) - 1u));
-        if (r < K) grow[i * K + r] = gblk[(int64_t)i * K + j];
+  auto rank = [&](int32_t s, int i) {
+    return pre[(s >> 5) * kPrepQ + i] + __popc(words[(s >> 5) * RW + i] & ((1u << (s & 31)) - 1u));
+  };
+  if (vec) {
+#pragma unroll
+    for (int jj = 0; jj < kNJ; ++jj)
+#pragma unroll
+      for (int u = 0; u < kPrepQ; ++u) {
+        const int32_t sv[4] = {pv[jj][u].x, pv[jj][u].y, pv[jj][u].z, pv[jj][u].w};
+        const uint32_t gw[2] = {gv[jj][u].x, gv[jj][u].y};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if ((uint32_t)sv[c] < (uint32_t)S) {
+            const int r = rank(sv[c], u);
+            if (r < K) grow[u * K + r] = (uint16_t)(gw[c >> 1] >> (16 * (c & 1)));
+          }
       }
-    }
+  } else {
+    for (int i = 0; i < rows; ++i)
+      for (int j = tid; j < K; j += 256) {
+        const int32_t s = pblk[(int64_t)i * K + j];
+        if ((uint32_t)s < (uint32_t)S) {
+          const int r = rank(s, i);
+          if (r < K) grow[i * K + r] = gblk[(int64_t)i * K + j];
+        }
+      }
+  }
   __syncthreads();
   for (int i = 0; i < rows; ++i) {
     uint16_t* orow = gs + ((int64_t)b * T + q0 + i) * K;
@@ -775,7 +807,10 @@ extern "C" int gw_indexer_topk_bwd_dense(int dtype, const void* q, const void* k
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(idxd_clear_kernel, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, st, route, (int)B);
   GW_HIP_LAUNCH_CHECK("idxd_clear_kernel launch");
-  const int vec = (K % 4 == 0 && (reinterpret_cast<uintptr_t>(topk_indices) & 15u) == 0) ? 1 : 0;
+  const int vec = (K % 4 == 0 && (reinterpret_cast<uintptr_t>(topk_indices) & 15u) == 0 &&
+                   (reinterpret_cast<uintptr_t>(grad_scores) & 7u) == 0)
+                      ? 1
+                      : 0;
   hipLaunchKernelGGL(idxd_prep_kernel, dim3((unsigned)(L.tpad / kPrepQ), (unsigned)B), dim3(256),
                      idxd_prep_lds(L.nsub, (int)K), st, topk_indices, static_cast<const uint16_t*>(grad_scores),
                      (int)T, (int)S, (int)K, L.nsub, L.tpad, vec, reinterpret_cast<uint32_t*>(ws + L.words),
