@@ -201,53 +201,61 @@ __global__ __launch_bounds__(256) void idxd_prep_kernel(const int32_t* __restric
 // the operand's k-chunk l / 32 lists as k = 8 (l / 32) + r). Flags route[b] on a non-finite
 // x, w or product.
 // ---------------------------------------------------------------------------------------
+constexpr int kTTiles = 4;  // 64-row tiles per workgroup of idxd_t_kernel
+
 __global__ __launch_bounds__(256) void idxd_t_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                      int R, int Rpad, int HI, uint16_t* __restrict__ xt,
                                                      int* __restrict__ route) {
   __shared__ __align__(16) uint16_t tile[64][72];  // [d][row]
-  const int r0 = blockIdx.x * 64, h = blockIdx.y, b = blockIdx.z;
+  const int h = blockIdx.y, b = blockIdx.z;
   uint32_t nf = 0u;
+  // kTTiles tiles of 64 rows per workgroup (one tile alone is too little work for a workgroup).
+  for (int rt = 0; rt < kTTiles; ++rt) {
+    const int r0 = (blockIdx.x * kTTiles + rt) * 64;
+    if (r0 >= Rpad) break;
+    if (rt > 0) __syncthreads();  // the previous tile's reads of the LDS tile are done
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int e = threadIdx.x + it * 256;
-    const int row = e >> 3, c = e & 7;
-    uint4 val = make_uint4(0, 0, 0, 0);
-    float ws = 1.f;
-    if (r0 + row < R) {
-      const int64_t tok = ((int64_t)b * R + r0 + row) * HI + h;
-      val = *reinterpret_cast<const uint4*>(x + tok * kXD + c * 8);
-      if (w != nullptr) {
-        const uint32_t wb = w[tok];
-        nf |= (uint32_t)((wb & 0x7F80u) == 0x7F80u);
-        ws = __uint_as_float(wb << 16);
+    for (int it = 0; it < 2; ++it) {
+      const int e = threadIdx.x + it * 256;
+      const int row = e >> 3, c = e & 7;
+      uint4 val = make_uint4(0, 0, 0, 0);
+      float ws = 1.f;
+      if (r0 + row < R) {
+        const int64_t tok = ((int64_t)b * R + r0 + row) * HI + h;
+        val = *reinterpret_cast<const uint4*>(x + tok * kXD + c * 8);
+        if (w != nullptr) {
+          const uint32_t wb = w[tok];
+          nf |= (uint32_t)((wb & 0x7F80u) == 0x7F80u);
+          ws = __uint_as_float(wb << 16);
+        }
+      }
+      uint32_t u[4] = {val.x, val.y, val.z, val.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        nf |= nonfinite2(u[i], 0x7F80u);
+        if (w != nullptr) {
+          u[i] = pack_pair(BF16{}, __uint_as_float(u[i] << 16) * ws, __uint_as_float(u[i] & 0xFFFF0000u) * ws);
+          nf |= nonfinite2(u[i], 0x7F80u);
+        }
+        tile[c * 8 + 2 * i][row] = (uint16_t)(u[i] & 0xFFFFu);
+        tile[c * 8 + 2 * i + 1][row] = (uint16_t)(u[i] >> 16);
       }
     }
-    uint32_t u[4] = {val.x, val.y, val.z, val.w};
+    __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      nf |= nonfinite2(u[i], 0x7F80u);
-      if (w != nullptr) {
-        u[i] = pack_pair(BF16{}, __uint_as_float(u[i] << 16) * ws, __uint_as_float(u[i] & 0xFFFF0000u) * ws);
-        nf |= nonfinite2(u[i], 0x7F80u);
-      }
-      tile[c * 8 + 2 * i][row] = (uint16_t)(u[i] & 0xFFFFu);
-      tile[c * 8 + 2 * i + 1][row] = (uint16_t)(u[i] >> 16);
+    for (int it = 0; it < 2; ++it) {
+      const int e = threadIdx.x + it * 256;
+      const int d = e >> 3, kc = e & 7;
+      if (r0 + kc * 8 >= Rpad) continue;
+      // r' = 8 kc + 0..7 holds rows 16 (kc / 2) + 4 (kc % 2) + {0..3, 8..11}
+      const int k0 = 16 * (kc >> 1) + 4 * (kc & 1);
+      const uint2 lo = *reinterpret_cast<const uint2*>(&tile[d][k0]);
+      const uint2 hi = *reinterpret_cast<const uint2*>(&tile[d][k0 + 8]);
+      *reinterpret_cast<uint4*>(xt + (((int64_t)b * HI + h) * kXD + d) * Rpad + r0 + kc * 8) =
+          make_uint4(lo.x, lo.y, hi.x, hi.y);
     }
   }
   if (nf != 0u) route[b] = 1;  // every writer stores the same value
-  __syncthreads();
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int e = threadIdx.x + it * 256;
-    const int d = e >> 3, kc = e & 7;
-    if (r0 + kc * 8 >= Rpad) continue;
-    // r' = 8 kc + 0..7 holds rows 16 (kc / 2) + 4 (kc % 2) + {0..3, 8..11}
-    const int k0 = 16 * (kc >> 1) + 4 * (kc & 1);
-    const uint2 lo = *reinterpret_cast<const uint2*>(&tile[d][k0]);
-    const uint2 hi = *reinterpret_cast<const uint2*>(&tile[d][k0 + 8]);
-    *reinterpret_cast<uint4*>(xt + (((int64_t)b * HI + h) * kXD + d) * Rpad + r0 + kc * 8) =
-        make_uint4(lo.x, lo.y, hi.x, hi.y);
-  }
 }
 
 struct IdxDenseParams {
@@ -816,10 +824,12 @@ extern "C" int gw_indexer_topk_bwd_dense(int dtype, const void* q, const void* k
                      (int)T, (int)S, (int)K, L.nsub, L.tpad, vec, reinterpret_cast<uint32_t*>(ws + L.words),
                      reinterpret_cast<uint16_t*>(ws + L.pre), reinterpret_cast<uint16_t*>(ws + L.gs), route);
   GW_HIP_LAUNCH_CHECK("idxd_prep_kernel launch");
-  hipLaunchKernelGGL(idxd_t_kernel, dim3((unsigned)((L.tpad + 63) / 64), (unsigned)Hi, (unsigned)B), dim3(256), 0, st,
+  const unsigned tq = (unsigned)(((L.tpad + 63) / 64 + kTTiles - 1) / kTTiles);
+  const unsigned tk = (unsigned)(((L.spad + 63) / 64 + kTTiles - 1) / kTTiles);
+  hipLaunchKernelGGL(idxd_t_kernel, dim3(tq, (unsigned)Hi, (unsigned)B), dim3(256), 0, st,
                      p.q, nullptr, (int)T, L.tpad, (int)Hi, reinterpret_cast<uint16_t*>(ws + L.qt), route);
   GW_HIP_LAUNCH_CHECK("idxd_t_kernel<q> launch");
-  hipLaunchKernelGGL(idxd_t_kernel, dim3((unsigned)((L.spad + 63) / 64), (unsigned)Hi, (unsigned)B), dim3(256), 0, st,
+  hipLaunchKernelGGL(idxd_t_kernel, dim3(tk, (unsigned)Hi, (unsigned)B), dim3(256), 0, st,
                      p.k, p.w, (int)S, L.spad, (int)Hi, reinterpret_cast<uint16_t*>(ws + L.kwt), route);
   GW_HIP_LAUNCH_CHECK("idxd_t_kernel<wk> launch");
   const int rc = launch_pass<false>(p, (int)B, L, st);

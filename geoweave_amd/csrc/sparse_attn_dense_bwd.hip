@@ -100,53 +100,63 @@ __global__ __launch_bounds__(256) void dense_bwd_rowstats_kernel(const uint16_t*
 // null (check only). Sets route[b] when a value is an inf or a nan, and with amax the largest
 // |x| of the (b, h) slice (ordered float bits, atomic max).
 // ---------------------------------------------------------------------------------------
+constexpr int kTRows = 4;  // 64-row tiles per workgroup of dense_bwd_t_kernel
+
 __global__ __launch_bounds__(256) void dense_bwd_t_kernel(const uint16_t* __restrict__ x, int64_t xsb, int64_t xsr,
                                                           int64_t xsh, int R, int Rpad, int H, int in_fp16,
                                                           uint16_t* __restrict__ xt, int* __restrict__ route,
                                                           uint32_t* __restrict__ amax) {
   __shared__ __align__(16) uint16_t tile[64][72];  // [d][row], rows of 144 bytes
   __shared__ float wmax[4];
-  const int r0 = blockIdx.x * 64, h = blockIdx.y, b = blockIdx.z;
+  const int h = blockIdx.y, b = blockIdx.z;
   const uint32_t e = in_fp16 ? 0x7C00u : 0x7F80u;
   uint32_t nf = 0u;
   float mx = 0.f;
+  // kTRows tiles of 64 rows per workgroup (one tile alone is too little work for a workgroup).
+  for (int rt = 0; rt < kTRows; ++rt) {
+    const int r0 = (blockIdx.x * kTRows + rt) * 64;
+    if (r0 >= Rpad) break;
+    if (rt > 0) __syncthreads();  // the previous tile's reads of the LDS tile are done
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int idx = threadIdx.x + it * 256;
-    const int row = idx >> 3, c = idx & 7;
-    uint4 val = make_uint4(0, 0, 0, 0);
-    if (r0 + row < R) val = *reinterpret_cast<const uint4*>(x + b * xsb + (int64_t)(r0 + row) * xsr + h * xsh + c * 8);
-    const uint32_t w[4] = {val.x, val.y, val.z, val.w};
+    for (int it = 0; it < 2; ++it) {
+      const int idx = threadIdx.x + it * 256;
+      const int row = idx >> 3, c = idx & 7;
+      uint4 val = make_uint4(0, 0, 0, 0);
+      if (r0 + row < R) val = *reinterpret_cast<const uint4*>(x + b * xsb + (int64_t)(r0 + row) * xsr + h * xsh + c * 8);
+      const uint32_t w[4] = {val.x, val.y, val.z, val.w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      nf |= nonfinite2(w[i], e);
-      mx = fmaxf(mx, fmaxf(fabsf(in_to_float(in_fp16, w[i] & 0xFFFFu)), fabsf(in_to_float(in_fp16, w[i] >> 16))));
-      if (xt != nullptr) {
-        tile[c * 8 + 2 * i][row] = (uint16_t)(w[i] & 0xFFFFu);
-        tile[c * 8 + 2 * i + 1][row] = (uint16_t)(w[i] >> 16);
+      for (int i = 0; i < 4; ++i) {
+        nf |= nonfinite2(w[i], e);
+        mx = fmaxf(mx, fmaxf(fabsf(in_to_float(in_fp16, w[i] & 0xFFFFu)), fabsf(in_to_float(in_fp16, w[i] >> 16))));
+        if (xt != nullptr) {
+          tile[c * 8 + 2 * i][row] = (uint16_t)(w[i] & 0xFFFFu);
+          tile[c * 8 + 2 * i + 1][row] = (uint16_t)(w[i] >> 16);
+        }
       }
+    }
+    if (xt == nullptr) continue;
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int idx = threadIdx.x + it * 256;
+      const int d = idx >> 3, kc = idx & 7;
+      // r' = 8 kc + 0..7 holds rows 16 (kc / 2) + 4 (kc % 2) + {0..3, 8..11}
+      const int k0 = 16 * (kc >> 1) + 4 * (kc & 1);
+      const uint2 lo = *reinterpret_cast<const uint2*>(&tile[d][k0]);
+      const uint2 hi = *reinterpret_cast<const uint2*>(&tile[d][k0 + 8]);
+      *reinterpret_cast<uint4*>(xt + (((int64_t)b * H + h) * 64 + d) * Rpad + r0 + kc * 8) =
+          make_uint4(lo.x, lo.y, hi.x, hi.y);
     }
   }
   if (nf != 0u) route[b] = 1;  // every writer stores the same value
   if (amax != nullptr) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    __syncthreads();
     if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
-  }
-  __syncthreads();
-  if (amax != nullptr && threadIdx.x == 0)
-    atomicMax(amax + (int64_t)b * H + h, __float_as_uint(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]))));
-  if (xt == nullptr) return;
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int idx = threadIdx.x + it * 256;
-    const int d = idx >> 3, kc = idx & 7;
-    // r' = 8 kc + 0..7 holds rows 16 (kc / 2) + 4 (kc % 2) + {0..3, 8..11}
-    const int k0 = 16 * (kc >> 1) + 4 * (kc & 1);
-    const uint2 lo = *reinterpret_cast<const uint2*>(&tile[d][k0]);
-    const uint2 hi = *reinterpret_cast<const uint2*>(&tile[d][k0 + 8]);
-    *reinterpret_cast<uint4*>(xt + (((int64_t)b * H + h) * 64 + d) * Rpad + r0 + kc * 8) =
-        make_uint4(lo.x, lo.y, hi.x, hi.y);
+    __syncthreads();
+    if (threadIdx.x == 0)
+      atomicMax(amax + (int64_t)b * H + h, __float_as_uint(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]))));
   }
 }
 
@@ -727,14 +737,14 @@ extern "C" int gw_sparse_attn_bwd_dense(int dtype, const void* q, const int64_t*
     GW_HIP_LAUNCH_CHECK("dense_bwd_rowstats_kernel launch");
   }
   {
-    const dim3 gq((unsigned)(L.tpad / 64), (unsigned)H, (unsigned)B);
+    const dim3 gq((unsigned)((L.tpad / 64 + kTRows - 1) / kTRows), (unsigned)H, (unsigned)B);
     hipLaunchKernelGGL(dense_bwd_t_kernel, gq, dim3(256), 0, st, static_cast<const uint16_t*>(q), q_strides[0],
                        q_strides[1], q_strides[2], (int)T, L.tpad, (int)H, in_fp16, qt, route, nullptr);
     GW_HIP_LAUNCH_CHECK("dense_bwd_t_kernel (q) launch");
     hipLaunchKernelGGL(dense_bwd_t_kernel, gq, dim3(256), 0, st, static_cast<const uint16_t*>(dout), do_strides[0],
                        do_strides[1], do_strides[2], (int)T, L.tpad, (int)H, in_fp16, dot, route, amax);
     GW_HIP_LAUNCH_CHECK("dense_bwd_t_kernel (dO) launch");
-    const dim3 gk((unsigned)(L.spad / 64), (unsigned)H, (unsigned)B);
+    const dim3 gk((unsigned)((L.spad / 64 + kTRows - 1) / kTRows), (unsigned)H, (unsigned)B);
     hipLaunchKernelGGL(dense_bwd_t_kernel, gk, dim3(256), 0, st, static_cast<const uint16_t*>(k), k_strides[0],
                        k_strides[1], k_strides[2], (int)S, L.spad, (int)H, in_fp16, kt, route, nullptr);
     GW_HIP_LAUNCH_CHECK("dense_bwd_t_kernel (k) launch");
