@@ -224,9 +224,9 @@ __host__ __device__ __forceinline__ int64_t sws_row(int64_t K) { return (K + 7) 
 // from different workgroups): one wave's barrier or memory wait is not the other's.
 constexpr int kDW = 4;
 // Limits of the 32-bit lane offsets of the tile loads: a K token stride below 2^23 elements
-// (2^24 bytes, a 24-bit multiply), 64 rows of V^T (S padded to 128, at most 2^25) below 2^32 bytes.
+// (2^24 bytes, a 24-bit multiply), 64 rows of V^T (S padded to 128) below 2^32 bytes.
 constexpr int64_t kDenseMaxKRowStride = 1ll << 23;
-constexpr int64_t kDenseMaxS = (1ll << 25) - 64;
+constexpr int64_t kDenseMaxS = (1ll << 25) - 128;
 constexpr int kQPW = 2;  // 32-query blocks per wave (one head): each K and V^T operand feeds two products
 constexpr int kQBW = kDW * kQPW;  // 32-query blocks per workgroup
 static_assert(kDW == 4, "the tile staging moves two K and two V^T rows of 64 per thread");

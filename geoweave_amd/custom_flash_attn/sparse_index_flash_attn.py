@@ -116,7 +116,7 @@ FORWARD_PATH = "auto"
 DENSE_MAX_RATIO = 96
 DENSE_ATTN_SUM_MAX_K = 1024
 DENSE_MAX_K_ROW_STRIDE = 1 << 23
-DENSE_MAX_S = (1 << 25) - 64
+DENSE_MAX_S = (1 << 25) - 128
 DENSE_MAX_T = 65528 * 32
 
 

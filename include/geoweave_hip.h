@@ -462,7 +462,7 @@ int gw_source_downsample_static_pack4(int dtype, const void* sub_w, int64_t B, i
  * it pays off when a query selects more than roughly 1 % of the keys.
  * Needs D = 64 and a positive softmax_scale, and K <= 1024 and H <= 64 when attn_sum is
  * asked for; the kernels' 32-bit load offsets also need a K token stride below 2^23 elements
- * and S <= 2^25 - 64, and its grid T <= 65528 * 32. Otherwise GW_ERR_UNSUPPORTED (use gw_sparse_attn_fwd /
+ * and S <= 2^25 - 128, and its grid T <= 65528 * 32. Otherwise GW_ERR_UNSUPPORTED (use gw_sparse_attn_fwd /
  * gw_sparse_attn_fwd_kl).
  * The P·V product takes P in fp16 (the fp32 weights rounded to nearest, 11 significant bits)
  * against V in fp16 scaled per (head, d) column by an exact power of two; row sums and lse

@@ -161,11 +161,11 @@ def _dense_call(**over):
 
 def test_dense_fwd_workspace_and_argument_checks_without_gpu():
     lib = _lib.load()
-    # mask: 2 sub-tiles of 32 keys (S padded to 64) x 256 queries (1 block padded to the 8 of
-    # a workgroup) x 4 B = 2048; block flags 4 B -> 2304; non-finite flag per batch element
-    # 4 B -> 2560; |V| column maxima 16 heads x 64 x 4 B -> 6656; V^T 16 heads x 64 x 64 keys
-    # x 2 B
-    base = 2560 + 16 * 64 * 4 + 16 * 64 * 64 * 2
+    # mask: 4 sub-tiles of 32 keys (S padded to 128) x 256 queries (1 block padded to the 8 of
+    # a workgroup) x 4 B = 4096; block flags 4 B -> 4352; non-finite flag per batch element
+    # 4 B -> 4608; |V| column maxima 16 heads x 64 x 4 B -> 8704; V^T 16 heads x 64 x 128
+    # keys x 2 B
+    base = 4608 + 16 * 64 * 4 + 16 * 64 * 128 * 2
     assert lib.gw_sparse_attn_fwd_dense_workspace_size(1, 4, 4, 16, 64, 4, 0) == base
     # + the selected scores for attn_sum: T x (K rounded up to 8, + 8) x H x 4 B
     assert lib.gw_sparse_attn_fwd_dense_workspace_size(1, 4, 4, 16, 64, 4, 1) == base + 4 * 16 * 16 * 4

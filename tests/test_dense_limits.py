@@ -1,6 +1,6 @@
 """Routing of the masked dense passes around the limits of their 32-bit load offsets (CPU:
 only the host-side checks run). A K token stride of 2^23 elements or more, or S beyond
-2^25 - 64, must send the forward and the backward to the gather/CSR paths, which take any
+2^25 - 128, must send the forward and the backward to the gather/CSR paths, which take any
 stride; ordinary layer shapes, strided views of a packed qkv tensor included, stay dense."""
 import torch
 
@@ -27,7 +27,7 @@ def test_forward_dense_refuses_huge_strides_and_lengths():
     assert not sifa._dense_fits(_view(8, 1, 64, sifa.DENSE_MAX_K_ROW_STRIDE), "bthd", 8)
     assert sifa._dense_fits(_view(8, 1, 64, sifa.DENSE_MAX_K_ROW_STRIDE - 8), "bthd", 8)
     assert not sifa._dense_fits(_view(8, 1, 64, 64), "bthd", sifa.DENSE_MAX_S + 1)
-    assert sifa.DENSE_MAX_S == (1 << 25) - 64 and sifa.DENSE_MAX_K_ROW_STRIDE == 1 << 23
+    assert sifa.DENSE_MAX_S == (1 << 25) - 128 and sifa.DENSE_MAX_K_ROW_STRIDE == 1 << 23
 
 
 def test_backward_dense_fits():
@@ -72,7 +72,7 @@ def test_length_limits_match_the_kernels():
     # Whatever the Python routing keeps on the dense passes, the C entry points accept (past
     # the length checks: INVALID, 1, for the missing workspace); what they refuse
     # (UNSUPPORTED, 2) the routing sends to the gather/CSR paths. Backward: T padded to 256
-    # and S to 128 below 2^25 and at most 65535 query blocks; forward: S padded to 64 below
+    # and S to 128 below 2^25 and at most 65535 query blocks; forward: S padded to 128 below
     # 2^25, same query blocks. T = 2^25 - 128 passed the old routing and then failed.
     small = _view(8, 1, 64, 64)
     tmax = _backward.DENSE_MAX_T
