@@ -104,7 +104,7 @@ __device__ __forceinline__ uint32_t lane_bit_transpose32(uint32_t x, int lane) {
 // ---------------------------------------------------------------------------------------
 // Selection mask, query-major per 32-key sub-tile: word[b][j][t] has bit i set when query t
 // selected key 32 j + i (t < T_pad = nqb_pad * 32, j < S_pad / 32; zero words past S and T).
-// Built per (32-query block, chunk of kMaskChunk keys) with LDS atomics. The atomic returns
+// Built per (32-query block, chunk of chunk_keys keys) with LDS atomics. The atomic returns
 // the word as it was: a bit already set means the query listed the key twice, and the block
 // is flagged (flags[b][qb][chunk]; dup_b[b] = 1 too when dup_b is given). Positions are read
 // 8 rows at a time (16 bytes per lane when the table allows), so the loads of a group are in
@@ -117,7 +117,12 @@ __device__ __forceinline__ uint32_t lane_bit_transpose32(uint32_t x, int lane) {
 // bytes. The first workgroup of each batch element clears vmax_words words of vmax and bad[b]
 // (for the forward's dense_vmax_kernel), when given.
 // ---------------------------------------------------------------------------------------
-constexpr int kMaskChunk = 16384;  // keys per workgroup
+// Keys per workgroup: at most 606 sub-tiles of 33 words (two workgroups per CU), the key
+// range split into equal chunks of whole sub-tiles, so that a key range just past a multiple
+// of the largest chunk does not cost a chunk that rereads every position for a few keys.
+constexpr int kMaskChunkMax = 606 * 32;
+inline int mask_nchunk(int64_t spad) { return (int)((spad + kMaskChunkMax - 1) / kMaskChunkMax); }
+inline int mask_chunk_keys(int64_t spad, int nchunk) { return (int)((spad / 32 + nchunk - 1) / nchunk * 32); }
 
 __global__ __launch_bounds__(256) void dense_mask_kernel(const int32_t* __restrict__ pos, int64_t psb, int64_t pst,
                                                          int T, int S, int Spad, int K, int nqb, int tpad,
@@ -125,16 +130,16 @@ __global__ __launch_bounds__(256) void dense_mask_kernel(const int32_t* __restri
                                                          uint32_t* __restrict__ mask, int* __restrict__ flags,
                                                          uint32_t* __restrict__ vmax, int* __restrict__ bad,
                                                          uint32_t* __restrict__ maskT, int* __restrict__ dup_b,
-                                                         int bias_order) {
+                                                         int bias_order, int chunk_keys) {
   // [key / 32][query], rows padded to 33 words so that one query's atomics spread over banks
-  __shared__ uint32_t words[(kMaskChunk / 32) * 33];
+  __shared__ uint32_t words[(kMaskChunkMax / 32) * 33];
   __shared__ int dup_any;
   // The chunks of one block are consecutive workgroups: they run together and share the
   // block's positions through the caches.
   const int chunk = blockIdx.x, qb = blockIdx.y, b = blockIdx.z;
-  const int c0 = chunk * kMaskChunk;
-  const int len = min(kMaskChunk, S - c0);
-  const int nkt = min(kMaskChunk, Spad - c0) >> 5;
+  const int c0 = chunk * chunk_keys;
+  const int len = max(0, min(chunk_keys, S - c0));
+  const int nkt = max(0, min(chunk_keys, Spad - c0)) >> 5;
   for (int i = threadIdx.x; i < nkt * 33; i += 256) words[i] = 0u;
   if (qb == 0 && chunk == 0 && vmax != nullptr) {
     for (int i = threadIdx.x; i < vmax_words; i += 256) vmax[(int64_t)b * vmax_words + i] = 0u;

@@ -831,9 +831,9 @@ DenseLayout dense_layout(int64_t B, int64_t T, int64_t S, int64_t H, int64_t K, 
   L.nqb_pad = (L.nqb + kQBW - 1) / kQBW * kQBW;
   L.spad = (int)((S + 127) / 128 * 128);  // whole 128-key tiles of the plain forward
   // One pass over the positions (two 16-query halves per block) when the sub-tile words of
-  // 16 queries fit the LDS, else chunks of kMaskChunk keys.
+  // 16 queries fit the LDS, else equal chunks of at most kMaskChunkMax keys.
   L.rows_pass = L.spad / 32 <= kMaskRowsMaxSub;
-  L.nchunk = L.rows_pass ? 2 : (int)((S + kMaskChunk - 1) / kMaskChunk);
+  L.nchunk = L.rows_pass ? 2 : mask_nchunk(L.spad);
   if (L.nchunk < 1) L.nchunk = 1;
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
   size_t o = 0;
@@ -960,7 +960,8 @@ extern "C" int gw_sparse_attn_fwd_dense(int dtype, const void* q, const int64_t*
     } else {
       hipLaunchKernelGGL(dense_mask_kernel, dim3(L.nchunk, L.nqb_pad, (unsigned)B), dim3(256), 0, st, kv_pos,
                          pos_stride_b, pos_stride_t, (int)T, (int)S, L.spad, (int)K, L.nqb, L.nqb_pad * 32, L.nchunk,
-                         vec, (int)(H * 64), mask, flags, vmax, bad, nullptr, nullptr, want_attn ? 0 : 1);
+                         vec, (int)(H * 64), mask, flags, vmax, bad, nullptr, nullptr, want_attn ? 0 : 1,
+                         mask_chunk_keys(L.spad, L.nchunk));
       GW_HIP_LAUNCH_CHECK("dense_mask_kernel launch");
     }
   }

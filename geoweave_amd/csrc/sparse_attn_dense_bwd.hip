@@ -612,7 +612,7 @@ DenseBwdLayout dense_bwd_layout(int64_t B, int64_t T, int64_t S, int64_t H) {
   L.nqb_pad = (L.nqb + kBQPB - 1) / kBQPB * kBQPB;
   L.tpad = L.nqb_pad * 32;
   L.spad = (int)((S + 32 * kBKPB - 1) / (32 * kBKPB) * (32 * kBKPB));
-  L.nchunk = (int)((S + kMaskChunk - 1) / kMaskChunk);
+  L.nchunk = mask_nchunk(L.spad);
   if (L.nchunk < 1) L.nchunk = 1;
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
   size_t o = 0;
@@ -719,7 +719,7 @@ extern "C" int gw_sparse_attn_bwd_dense(int dtype, const void* q, const int64_t*
                         : 0;
     hipLaunchKernelGGL(dense_mask_kernel, dim3(L.nchunk, L.nqb_pad, (unsigned)B), dim3(256), 0, st, kv_pos,
                        pos_stride_b, pos_stride_t, (int)T, (int)S, L.spad, (int)K, L.nqb, L.tpad, L.nchunk, vec, 0,
-                       mask, flags, nullptr, nullptr, maskT, route, 1);
+                       mask, flags, nullptr, nullptr, maskT, route, 1, mask_chunk_keys(L.spad, L.nchunk));
     GW_HIP_LAUNCH_CHECK("dense_mask_kernel launch");
   }
   {
