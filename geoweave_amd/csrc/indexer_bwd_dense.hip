@@ -42,7 +42,6 @@ constexpr int kXRows = 256;        // stationary rows per row group (4 waves x 2
 constexpr int kXMaxS = 65536;      // keys: the prep kernel holds a row's words in LDS
 constexpr int kXMaxK = 2048;
 constexpr int kPrepQ = 8;          // queries per prep workgroup
-constexpr int kPrefetch = 4;       // gradients a builder thread loads a tile ahead
 
 __global__ __launch_bounds__(256) void idxd_clear_kernel(int* __restrict__ route, int B) {
   const int i = blockIdx.x * 256 + threadIdx.x;

@@ -356,7 +356,6 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
         : "vcc", "memory");
     fl += flush ? 4u : 0u;
   };
-  const float ninf = -INFINITY;
 
   // One 32-key sub-tile in two parts. sub_qk: S^T for both blocks from the selection bias;
   // sub_pv: the softmax in registers and O^T += V^T P^T.
