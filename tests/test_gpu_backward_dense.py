@@ -62,6 +62,7 @@ def _oracle(q, k, v, pos, o, lse, do, scale=None, layout="bthd"):
         (1, 1000, 700, 3, 100, torch.bfloat16, "bhtd", None, 0.0),  # T != S, bhtd
         (2, 513, 1029, 16, 64, torch.float16, "bthd", 0.2, 0.1),  # T, S off every tile size
         (1, 33, 5000, 1, 512, torch.bfloat16, "bthd", None, 0.0),  # one head, long key range
+        (1, 64, 41000, 2, 512, torch.bfloat16, "bthd", None, 0.0),  # selection words in 3 key chunks
     ],
 )
 def test_dense_backward_matches_oracle(gpu_device, batch, tq, tk, heads, topk, dtype, layout, scale, invalid):
