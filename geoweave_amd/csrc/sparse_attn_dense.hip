@@ -289,8 +289,8 @@ __global__ __launch_bounds__(kDW * 64, 2) void dense_attn_kernel(const DensePara
     l[a] = 0.f;
   }
 
-  // Tile staging: each thread moves two 16-byte chunks of K and two of V^T per tile (rows
-  // srow and srow + 32), loaded straight into LDS. Lane i of a wave writes the 16 bytes at the
+  // Tile staging: each thread moves two 16-byte chunks of K and two of V^T per 64-key half of
+  // a tile (rows srow and srow + 32), loaded straight into LDS. Lane i of a wave writes the 16 bytes at the
   // wave's 1 KB segment + 16 i = row srow, physical chunk sc, so it reads the chunk
   // sc ^ swz(srow) that the swizzled layout keeps there (swz(srow + 32) = swz(srow)).
   const int srow = tid >> 3, sc = tid & 7;
