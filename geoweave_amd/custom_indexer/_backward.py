@@ -46,13 +46,19 @@ def _dense_applies(q, num_topk, src_len, softmax_scale) -> bool:
 
 
 def indexer_topk_backward(q, k, w, topk_indices, grad_scores, softmax_scale):
-    from .sparse_topk_indexer import KERNEL_HEAD_DIM, pad_head_dim
+    from .sparse_topk_indexer import KERNEL_HEAD_DIM, kernel_heads, pad_head_dim, pad_heads
 
     d = q.shape[-1]
     if d < KERNEL_HEAD_DIM:
         dq, dk, dw = indexer_topk_backward(pad_head_dim(q), pad_head_dim(k), w, topk_indices, grad_scores,
                                            softmax_scale)
         return dq[..., :d].contiguous(), dk[..., :d].contiguous(), dw
+    h = q.shape[2]
+    hp = kernel_heads(h, q.dtype)
+    if hp is not None and hp != h:
+        dq, dk, dw = indexer_topk_backward(pad_heads(q, hp), pad_heads(k, hp), pad_heads(w, hp), topk_indices,
+                                           grad_scores, softmax_scale)
+        return dq[:, :, :h].contiguous(), dk[:, :, :h].contiguous(), dw[:, :, :h].contiguous()
     global last_path
     bsz, tgt_len, n_heads, head_dim = q.shape
     src_len = k.shape[1]

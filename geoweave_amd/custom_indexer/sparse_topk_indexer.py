@@ -19,7 +19,8 @@ may cast to ``score_dtype="float32"``, ``indexer.py:321-326``); scores come back
 ``q.dtype``. mask: ``None``, an empty tensor, or an additive ``[B,T,S]`` (broadcast from
 ``[T,S]``/``[1,T,S]``), cast to ``q.dtype`` as the reference does (``:1299-1300``).
 Supported: ``Di <= 64`` (the kernels take 64; smaller head dims run zero-padded to it),
-``Hi in {1,2,4,8}`` (``{1,2,4}`` in float32), ``K <= 2048``.
+``Hi <= 8`` (``<= 4`` in float32; the kernels take 1, 2, 4 or 8 heads, other counts run
+with zero heads appended), ``K <= 2048``.
 
 ``view_bias_data`` (the soft view-bias training kernel, reference ``:2108-2186``): a dict
 with ``q_view_ids`` ``[B,T]``/``[T]``, ``s_view_ids`` ``[B,S]``/``[S]`` and ``view_bias``
@@ -67,6 +68,26 @@ def pad_head_dim(x: torch.Tensor) -> torch.Tensor:
     return torch.nn.functional.pad(x, (0, KERNEL_HEAD_DIM - x.shape[-1]))
 
 
+# The kernels' head counts. Other counts up to the largest (the reference's block kernel takes
+# any, masking heads past n_heads, sparse_topk_indexer.py:1009,1029,1142) run with zero heads
+# appended: a zero head (q = k = 0, w = 0) adds w relu(q.k) = 0 to every score, and the
+# backward's gradients of the real heads do not depend on it (they are cut back).
+KERNEL_HEADS = (1, 2, 4, 8)
+KERNEL_HEADS_FP32 = (1, 2, 4)
+
+
+def kernel_heads(n_heads: int, dtype: torch.dtype) -> Optional[int]:
+    """The built head count that ``n_heads`` runs as (None: above every built count)."""
+    built = KERNEL_HEADS_FP32 if dtype == torch.float32 else KERNEL_HEADS
+    return next((h for h in built if h >= n_heads), None)
+
+
+def pad_heads(x: torch.Tensor, n_heads: int) -> torch.Tensor:
+    """q, k ``[B, T, H, D]`` or w ``[B, S, H]`` with zero heads appended up to ``n_heads``."""
+    extra = n_heads - x.shape[2]
+    return torch.nn.functional.pad(x, (0, 0, 0, extra) if x.dim() == 4 else (0, extra))
+
+
 def _check(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor):
     if q.dim() != 4 or k.dim() != 4 or w.dim() != 3:
         raise ValueError("q/k/w must be [B,T,H,D], [B,S,H,D], [B,S,H]")
@@ -81,10 +102,9 @@ def _check(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor):
         raise TypeError(f"the HIP indexer takes bfloat16, float16 or float32 inputs, got {q.dtype}")
     if not (q.is_cuda and k.is_cuda and w.is_cuda):
         raise ValueError("q, k and w must be GPU tensors")
-    if not 1 <= head_dim <= 64 or n_heads not in (1, 2, 4, 8):
-        raise NotImplementedError(f"indexer heads x dim {n_heads} x {head_dim} not built (1/2/4/8 x up to 64)")
-    if q.dtype == torch.float32 and n_heads == 8:
-        raise NotImplementedError("float32 indexer inputs are built for 1, 2 or 4 heads")
+    if not 1 <= head_dim <= 64 or kernel_heads(n_heads, q.dtype) is None:
+        raise NotImplementedError(f"indexer heads x dim {n_heads} x {head_dim} not built (up to 8 heads, "
+                                  f"4 in float32, x up to 64 dims)")
 
 
 def _normalize_view_bias_data(view_bias_data: Optional[dict], bsz: int, tgt_len: int, src_len: int,
@@ -151,6 +171,9 @@ def indexer_topk_forward(
         softmax_scale = 1.0 / math.sqrt(head_dim)
     if head_dim != KERNEL_HEAD_DIM:
         q, k, head_dim = pad_head_dim(q), pad_head_dim(k), KERNEL_HEAD_DIM
+    built_heads = kernel_heads(n_heads, q.dtype)
+    if built_heads != n_heads:
+        q, k, w, n_heads = pad_heads(q, built_heads), pad_heads(k, built_heads), pad_heads(w, built_heads), built_heads
     q = q.contiguous()
     k = k.contiguous()
     w = w.contiguous()

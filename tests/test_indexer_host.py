@@ -42,3 +42,26 @@ def test_view_ids_are_range_checked():
         sti._view_ids_int32(qv, sv, 2, 2)  # s view 2 of 2
     a, b = sti._view_ids_int32(qv, sv, 2, 3)
     assert a.dtype == torch.int32 and b.dtype == torch.int32
+
+
+def test_head_counts_run_on_built_counts_with_zero_heads():
+    # 3, 5, 6, 7 heads run as 4 or 8 (4 at most in float32) with zero heads appended, which
+    # leave every score unchanged (oracle scores on the padded and the plain inputs).
+    from oracle import indexer as oidx
+    assert [sti.kernel_heads(h, torch.bfloat16) for h in range(1, 10)] == [1, 2, 4, 4, 8, 8, 8, 8, None]
+    assert [sti.kernel_heads(h, torch.float32) for h in range(1, 6)] == [1, 2, 4, 4, None]
+    g = torch.Generator().manual_seed(3)
+    q, k, w = torch.randn(2, 50, 3, 64, generator=g), torch.randn(2, 70, 3, 64, generator=g), torch.randn(2, 70, 3, generator=g)
+    qp, kp, wp = sti.pad_heads(q, 4), sti.pad_heads(k, 4), sti.pad_heads(w, 4)
+    assert qp.shape == (2, 50, 4, 64) and wp.shape == (2, 70, 4)
+    assert torch.equal(qp[:, :, :3], q) and not qp[:, :, 3].any() and not wp[:, :, 3].any()
+    torch.testing.assert_close(oidx.indexer_scores(qp, kp, wp, None, 0.125),
+                               oidx.indexer_scores(q, k, w, None, 0.125), atol=1e-6, rtol=1e-6)
+    # the backward of the real heads is the same with the zero heads present
+    idx = torch.randint(0, 70, (2, 50, 8), generator=g)
+    gs = torch.randn(2, 50, 8, generator=g)
+    ref = oidx.indexer_topk_bwd(q, k, w, idx, gs, 0.125)
+    pad = oidx.indexer_topk_bwd(qp, kp, wp, idx, gs, 0.125)
+    torch.testing.assert_close(pad[0][:, :, :3], ref[0], atol=1e-6, rtol=1e-6)
+    torch.testing.assert_close(pad[1][:, :, :3], ref[1], atol=1e-6, rtol=1e-6)
+    torch.testing.assert_close(pad[2][:, :, :3], ref[2], atol=1e-6, rtol=1e-6)
