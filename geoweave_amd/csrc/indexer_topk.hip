@@ -34,7 +34,9 @@
 // Exactness: if count(score > tau) >= topk, every member of the top-k scores > tau and is a
 // candidate, so selecting among the candidates is exact (otherwise the query has fewer than
 // topk candidates and goes to the brute force). Ties at the k-th value are broken
-// deterministically (candidate order: split, then position in the list).
+// deterministically (candidate order: split, then position in the list). No step bounds
+// topk: a top-k larger than the candidate slots (kSubTotal) sends every query to K3, and
+// one above the register slots (kSelRegs per lane) sends most queries to K2b.
 //
 // MFMA layout (v_mfma_f32_32x32x16_{bf16,f16}), transposed: per tile of 32 keys a wave
 // forms S^T[32 keys x 32 queries] = K Q^T with A = key rows staged through LDS (XOR-swizzled
@@ -70,7 +72,6 @@ constexpr int kDI = 64;            // indexer head dim
 constexpr int kSubTotal = 8192;    // candidate slots per query over all lists
 constexpr int kMaxSplit = 8;
 constexpr int kMaxLists = kMaxSplit;
-constexpr int kMaxTopk = 2048;
 constexpr int kFallbackBlocks = 256;
 // Rows per batch element whose fallback scores come from the matrix cores (the rest, rare,
 // are scored by the fallback kernel itself).
@@ -1539,8 +1540,6 @@ int indexer_topk_impl(int dtype, const void* q, const void* k, const void* w, co
   if (B == 0 || T == 0) return GW_OK;
   GW_CHECK_ARG(S >= 1, "empty key set");
   const int64_t Kk = topk < S ? topk : S;
-  if (Kk > kMaxTopk)
-    return set_error(GW_ERR_UNSUPPORTED, "topk %lld exceeds the supported maximum %d", (long long)Kk, kMaxTopk);
   GW_CHECK_ARG(q && k && w && out_indices && out_scores, "null tensor pointer");
   GW_CHECK_ARG(aligned16(q) && aligned16(k), "q and k must be 16-byte aligned");
   GW_CHECK_ARG(B <= 65535 && T < (1ll << 30) && B * T < (1ll << 30), "size exceeds grid or int32 range");

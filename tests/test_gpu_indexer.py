@@ -121,6 +121,30 @@ def test_forced_fallback_paths_are_exact(gpu_device, flags, tokens):
     _check(q, k, w, idx, sc, 1024)
 
 
+@pytest.mark.parametrize("S,topk,T", [(12000, 3000, 700), (12000, 5000, 400), (9500, 9000, 600)])
+def test_topk_above_the_register_and_candidate_slots(gpu_device, S, topk, T):
+    # No step bounds the top-k: above the register slots (3,072 candidates) most rows take
+    # the LDS selection, above the 8,192 candidate slots every row the brute-force path (the
+    # first 512 scored on the matrix cores). Every row against the oracle, then the backward
+    # (the CSR path at these k) against the oracle on the GPU's indices.
+    from geoweave_amd.custom_indexer._backward import indexer_topk_backward
+    g = torch.Generator().manual_seed(topk)
+    q = torch.randn(1, T, 4, 64, generator=g).bfloat16()
+    k = torch.randn(1, S, 4, 64, generator=g).bfloat16()
+    w = (1 + 0.3 * torch.randn(1, S, 4, generator=g)).bfloat16()
+    print(f"[indexer] topk={topk} S={S} T={T}", flush=True)
+    idx, sc = _gpu_topk(q, k, w, topk)
+    assert idx.shape == (1, T, topk)
+    _check(q, k, w, idx, sc, topk)
+    gs = torch.randn(1, T, topk, generator=g).bfloat16()
+    dq, dk, dw = indexer_topk_backward(q.cuda(), k.cuda(), w.cuda(), idx.cuda(), gs.cuda(), 0.125)
+    torch.cuda.synchronize()
+    rq, rk, rw = oidx.indexer_topk_bwd(q, k, w, idx.long(), gs.float(), 0.125)
+    for got, ref in ((dq, rq), (dk, rk), (dw, rw)):
+        bad = ~torch.isclose(got.float().cpu(), ref, atol=2e-2, rtol=2e-2)
+        assert bad.float().mean() <= 1e-3, f"{int(bad.sum())} of {bad.numel()} outside tolerance"
+
+
 def test_topk_at_least_source_length(gpu_device):
     q, k, w = workloads.indexer_inputs(1, 1, torch.bfloat16, tokens=300)
     idx, sc = _gpu_topk(q, k, w, 1024)
