@@ -501,8 +501,9 @@ int gw_sparse_attn_fwd_dense(int dtype,
  * it is for callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). Same arguments and results as
  * gw_sparse_attn_fwd_dense without the workspace: the workspace is a file-scope device
- * array of gw_sparse_attn_fwd_dense_noalloc_capacity() bytes (64 MiB) that each GPU the
- * library runs on holds until the process ends. A call whose
+ * array of gw_sparse_attn_fwd_dense_noalloc_capacity() bytes (64 MiB) that a GPU holds
+ * from this entry point's first call on it until the process ends (processes that never
+ * call it hold none). A call whose
  * gw_sparse_attn_fwd_dense_workspace_size(...) exceeds it returns GW_ERR_UNSUPPORTED (for
  * example the inference forward, no attn_sum, of 16 heads fits up to about 10 views of 1,374
  * tokens). Works on the current device; the first call on a device looks up the array's

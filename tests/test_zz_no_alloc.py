@@ -4,8 +4,14 @@ from the first call would show), each against gw_sparse_attn_fwd_dense with a ca
 workspace on the same inputs. Both run the same kernels, so o, lse and attn_sum must be
 bit-identical; the first case is also checked against the fp32 oracle at the attention
 tolerance. A call beyond the scratch capacity is refused on the host. The entry point is
-also captured into a graph (its first call on the device inside the capture) and replayed.
+also captured into a graph (its first call on the device inside the capture) and replayed,
+and a fresh process shows that the scratch array takes device memory only from the first
+allocation-free call on, not when the library's other kernels run.
 """
+import subprocess
+import sys
+from pathlib import Path
+
 import pytest
 import torch
 
@@ -128,3 +134,17 @@ def test_noalloc_refuses_calls_beyond_its_scratch(gpu_device):
     rc = lib.gw_sparse_attn_fwd_dense_noalloc(*_args(q, q, q, pos, o, lse, None, 0.125), _lib.stream_handle(q.device))
     assert rc == 2  # GW_ERR_UNSUPPORTED
     assert b"allocation-free" in lib.gw_last_error()
+
+
+def test_scratch_is_resident_only_from_the_first_call(gpu_device):
+    # A fresh process (this one may have called the entry point already): a second workspace
+    # call leaves the device's free memory as it was (within 8 MiB of runtime bookkeeping),
+    # the first allocation-free call takes the 64 MiB array.
+    child = Path(__file__).resolve().parent / "noalloc_residency_child.py"
+    print("[noalloc] residency child process", flush=True)
+    res = subprocess.run([sys.executable, str(child)], capture_output=True, text=True, timeout=240)
+    assert res.returncode == 0, res.stderr[-2000:]
+    before, first = (int(x) for x in res.stdout.split()[-2:])
+    print(f"[noalloc] free-memory drop: second workspace call {before} B, first allocation-free call {first} B")
+    assert before < 8 << 20
+    assert first >= 64 << 20
