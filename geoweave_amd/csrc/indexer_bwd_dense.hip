@@ -407,9 +407,11 @@ __global__ __launch_bounds__(256, 2) void idxd_pass_kernel(const IdxDenseParams 
     const bool uok = KEYS ? ukb < p.nsub : sbase + tid < p.tpad;
     auto unit_t = [&](int n) { return KEYS ? 32 * n + qq : sbase + tid; };
     auto unit_kb = [&](int n) { return KEYS ? ukb : n; };
+    // dQ: (bit / 4) * 4 kXRows + 4 tid + bit % 4 = bit + (bit / 4) (4 kXRows - 4) + 4 tid
+    // (one shift and one 24-bit multiply-add per entry).
     auto gpos = [&](int bit) {
       return KEYS ? (((qq >> 2) * kXRows + 32 * wi + bit) << 2) + (qq & 3)
-                  : (((bit >> 2) * kXRows + tid) << 2) + (bit & 3);
+                  : (int)__umul24((uint32_t)bit >> 2, 4u * kXRows - 4u) + bit + 4 * tid;
     };
     // Words and prefixes: [b][t / 8][kb][t % 8]. Loads for tiles ahead are unconditional (an
     // invalid unit or a tile past n1 reads element 0) and are masked when used.
