@@ -145,6 +145,21 @@ def test_topk_above_the_register_and_candidate_slots(gpu_device, S, topk, T):
         assert bad.float().mean() <= 1e-3, f"{int(bad.sum())} of {bad.numel()} outside tolerance"
 
 
+def test_topk_above_the_candidate_slots_with_a_mask(gpu_device):
+    # The brute-force path (every row at k = 9,000 > 8,192 candidate slots) adds the additive
+    # mask too; -inf entries included.
+    g = torch.Generator().manual_seed(9)
+    T, S, topk = 300, 9500, 9000
+    q = torch.randn(1, T, 4, 64, generator=g).bfloat16()
+    k = torch.randn(1, S, 4, 64, generator=g).bfloat16()
+    w = (1 + 0.3 * torch.randn(1, S, 4, generator=g)).bfloat16()
+    mask = torch.randn(1, T, S, generator=g)
+    mask[torch.rand(1, T, S, generator=g) < 0.02] = float("-inf")
+    mask = mask.bfloat16()
+    idx, sc = _gpu_topk(q, k, w, topk, mask=mask)
+    _check(q, k, w, idx, sc, topk, mask=mask.float())
+
+
 def test_topk_at_least_source_length(gpu_device):
     q, k, w = workloads.indexer_inputs(1, 1, torch.bfloat16, tokens=300)
     idx, sc = _gpu_topk(q, k, w, 1024)
