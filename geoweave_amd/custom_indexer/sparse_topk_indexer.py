@@ -103,7 +103,7 @@ def _check(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor):
         raise TypeError(f"the HIP indexer takes bfloat16, float16 or float32 inputs, got {q.dtype}")
     if not (q.is_cuda and k.is_cuda and w.is_cuda):
         raise ValueError("q, k and w must be GPU tensors")
-    if not 1 <= head_dim <= 64 or kernel_heads(n_heads, q.dtype) is None:
+    if not 1 <= head_dim <= 64 or n_heads < 1 or kernel_heads(n_heads, q.dtype) is None:
         raise NotImplementedError(f"indexer heads x dim {n_heads} x {head_dim} not built (up to 8 heads, "
                                   f"4 in float32, x up to 64 dims)")
 
