@@ -35,8 +35,10 @@
 // candidate, so selecting among the candidates is exact (otherwise the query has fewer than
 // topk candidates and goes to the brute force). Ties at the k-th value are broken
 // deterministically (candidate order: split, then position in the list). No step bounds
-// topk: a top-k larger than the candidate slots (kSubTotal) sends every query to K3, and
-// one above the register slots (kSelRegs per lane) sends most queries to K2b.
+// topk: one whose expected candidates exceed 3/4 of the candidate slots (kSubTotal) sends
+// every row through K3's full scoring and row select, in rounds of kFullRows rows per batch
+// element (no threshold, filter or list select), and one above the register slots (kSelRegs
+// per lane) sends most queries to K2b.
 //
 // MFMA layout (v_mfma_f32_32x32x16_{bf16,f16}), transposed: per tile of 32 keys a wave
 // forms S^T[32 keys x 32 queries] = K Q^T with A = key rows staged through LDS (XOR-swizzled
@@ -1282,6 +1284,11 @@ __global__ void set_ints_kernel(int* ptr, int n, int value) {
   for (int i = threadIdx.x; i < n; i += blockDim.x) ptr[i] = value;
 }
 
+__global__ void iota_kernel(int* ptr, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    ptr[i] = (int)i;
+}
+
 
 // ---------------------------------------------------------------------------------------
 // Host-side plan.
@@ -1291,6 +1298,7 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 struct Plan {
   int Kk = 0;
   bool sample = false;
+  bool full_all = false;  // every row through the full scoring and the row select
   int Ms = 0, rank = 0;
   int nsplit = 1, cap = 0;
   size_t off_tau = 0, off_samp = 0, off_counts = 0, off_cand = 0, off_fb = 0, off_fblist = 0,
@@ -1307,6 +1315,10 @@ Plan make_layout(int64_t B, int64_t T, int64_t S, int64_t topk) {
     const double lam = (double)pl.Kk * pl.Ms / (double)S;
     int r = (int)ceil(lam + 4.5 * sqrt(lam) + 2.0);
     pl.rank = r > pl.Ms ? pl.Ms : r;
+    // Expected candidates per query (rank of Ms samples, scaled to S keys) beyond 3/4 of
+    // the candidate slots: the lists would overflow for many rows, so every row takes the
+    // full path instead.
+    pl.full_all = (double)pl.rank * (double)S / (double)pl.Ms > 0.75 * kSubTotal;
   }
   const size_t rows = (size_t)B * (size_t)T;
   size_t off = 0;
@@ -1368,9 +1380,73 @@ int choose_nsplit(int64_t tiles, int64_t S, int slots, bool sample, int bn) {
   return best;
 }
 
+// Launch configuration of indexer_score_kernel<SAMPLE> over every key for up to kFullRows
+// queued rows per batch element (rows and their count set by the caller).
+template <typename E, int HI, int BIAS>
+ScoreParams full_rows_params(const ScoreParams& base, float* full) {
+  using Shape = ScoreShape<row_bytes<E, HI>()>;
+  ScoreParams fp2 = base;
+  fp2.samp = full;
+  fp2.Ms = base.S;
+  fp2.rows_cap = kFullRows;
+  fp2.tau = nullptr;
+  fp2.tau_mode = kTauArray;
+  fp2.nstages = (base.S + Shape::BN - 1) / Shape::BN;
+  return fp2;
+}
+
+// A top-k whose expected candidates would overflow the lists (Plan::full_all): every row is
+// scored over every key on the matrix cores and selected exactly by
+// indexer_full_select_kernel, in rounds of kFullRows rows per batch element (round r0 takes
+// rows r0 .. r0 + kFullRows - 1 of each batch element through a queue that lists every row).
+template <typename E, int HI, int BIAS>
+int run_full_rows(const ScoreParams& base, const Plan& pl, int64_t B, int32_t* out_idx, void* out_scores,
+                  uint8_t* ws, hipStream_t st) {
+  using Shape = ScoreShape<row_bytes<E, HI>()>;
+  constexpr int BM = Shape::BM;
+  constexpr int THREADS = Shape::THREADS;
+  const int64_t rows = B * (int64_t)base.T;
+  int* counts = reinterpret_cast<int*>(ws + pl.off_fb) + 1;  // [B]: rows left from the round's first
+  int* list = reinterpret_cast<int*>(ws + pl.off_fblist);    // [B * T]: row i = i
+  float* full = reinterpret_cast<float*>(ws + pl.off_full);
+  hipLaunchKernelGGL(iota_kernel, dim3((unsigned)std::min<int64_t>((rows + 255) / 256, 4096)), dim3(256), 0, st,
+                     list, rows);
+  GW_HIP_LAUNCH_CHECK("iota_kernel");
+  ScoreParams fp2 = full_rows_params<E, HI, BIAS>(base, full);
+  fp2.nrows = counts;
+  const int ftiles = (kFullRows + BM - 1) / BM;
+  const int fslots = filter_slots((const void*)indexer_score_kernel<E, HI, true, BIAS>, THREADS);
+  const int64_t want = (2 * (int64_t)fslots + (int64_t)ftiles * B - 1) / ((int64_t)ftiles * B);
+  fp2.nsplit = (int)std::max<int64_t>(1, std::min<int64_t>(want, std::max(1, fp2.nstages / 2)));
+  FallbackParams bp{};
+  bp.fb_count = counts;
+  bp.full = full;
+  bp.rows_cap = kFullRows;
+  bp.B = (int)B;
+  bp.out_idx = out_idx;
+  bp.out_scores = out_scores;
+  bp.T = base.T;
+  bp.S = base.S;
+  bp.Kk = pl.Kk;
+  bp.scale = base.scale;
+  for (int r0 = 0; r0 < base.T; r0 += kFullRows) {
+    hipLaunchKernelGGL(set_ints_kernel, dim3(1), dim3(256), 0, st, counts, (int)B, base.T - r0);
+    GW_HIP_LAUNCH_CHECK("set_ints_kernel");
+    fp2.rows = list + r0;
+    hipLaunchKernelGGL((indexer_score_kernel<E, HI, true, BIAS>),
+                       dim3((unsigned)ftiles, (unsigned)fp2.nsplit, (unsigned)B), dim3(THREADS), 0, st, fp2);
+    GW_HIP_LAUNCH_CHECK("indexer_score_kernel<full rows>");
+    bp.fb_list = list + r0;
+    hipLaunchKernelGGL((indexer_full_select_kernel<E>), dim3(2 * kFallbackBlocks), dim3(256), 0, st, bp);
+    GW_HIP_LAUNCH_CHECK("indexer_full_select_kernel");
+  }
+  return GW_OK;
+}
+
 template <typename E, int HI, int BIAS>
 int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, void* out_scores,
               uint8_t* ws, hipStream_t st) {
+  if (pl.full_all) return run_full_rows<E, HI, BIAS>(base, pl, B, out_idx, out_scores, ws, st);
   int* counters = reinterpret_cast<int*>(ws + pl.off_fb);  // [0] wide select, [1 + b] fallback of b
   hipLaunchKernelGGL(set_ints_kernel, dim3(1), dim3(256), 0, st, counters, (int)B + 1, 0);
   GW_HIP_LAUNCH_CHECK("set_ints_kernel");
@@ -1443,15 +1519,9 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   // fewer queued rows return at once).
   float* full = reinterpret_cast<float*>(ws + pl.off_full);
   {
-    ScoreParams fp2 = base;
-    fp2.samp = full;
-    fp2.Ms = base.S;
+    ScoreParams fp2 = full_rows_params<E, HI, BIAS>(base, full);
     fp2.rows = fs.fb_list;
     fp2.nrows = fs.fb_count;
-    fp2.rows_cap = kFullRows;
-    fp2.tau = nullptr;
-    fp2.tau_mode = kTauArray;
-    fp2.nstages = (base.S + BN - 1) / BN;
     const int ftiles = (kFullRows + BM - 1) / BM;
     const int fslots = filter_slots((const void*)indexer_score_kernel<E, HI, true, BIAS>, THREADS);
     const int64_t want = (2 * (int64_t)fslots + (int64_t)ftiles * B - 1) / ((int64_t)ftiles * B);

@@ -20,8 +20,8 @@ may cast to ``score_dtype="float32"``, ``indexer.py:321-326``); scores come back
 ``[T,S]``/``[1,T,S]``), cast to ``q.dtype`` as the reference does (``:1299-1300``).
 Supported: ``Di <= 64`` (the kernels take 64; smaller head dims run zero-padded to it),
 ``Hi <= 8`` (``<= 4`` in float32; the kernels take 1, 2, 4 or 8 heads, other counts run
-with zero heads appended), any ``K`` (above 8,192 every query takes the exact brute-force
-path).
+with zero heads appended), any ``K`` (one whose expected candidates would overflow the
+8,192 candidate slots scores every row over every key and selects it exactly).
 
 ``view_bias_data`` (the soft view-bias training kernel, reference ``:2108-2186``): a dict
 with ``q_view_ids`` ``[B,T]``/``[T]``, ``s_view_ids`` ``[B,S]``/``[S]`` and ``view_bias``

@@ -104,8 +104,9 @@ int gw_sparse_attn_fwd(int dtype,
  *
  * q: [B,T,Hi,Di], k: [B,S,Hi,Di], w: [B,S,Hi], mask: [B,T,S], all contiguous, same dtype
  * (bf16, fp16 or fp32). Supported: Di = 64, Hi in {1,2,4,8} ({1,2,4} for fp32),
- * any topk >= 1 (K = min(topk, S); a K above the 8192 candidate slots per query runs every
- * query through the exact brute-force path), softmax_scale > 0.
+ * any topk >= 1 (K = min(topk, S); a K whose expected candidates exceed 3/4 of the 8192
+ * candidate slots per query scores every row over every key on the matrix cores and selects
+ * it exactly, in rounds of 512 rows per batch element), softmax_scale > 0.
  * workspace: gw_indexer_topk_workspace_size(B, T, S, topk) bytes, 16-byte aligned.
  * flags: 0 normally. Test hooks that force the exact fallback paths:
  *   GW_TOPK_FLAG_TAU_PLUS_INF  - no key passes the candidate filter (every query falls

@@ -160,6 +160,30 @@ def test_topk_above_the_candidate_slots_with_a_mask(gpu_device):
     _check(q, k, w, idx, sc, topk, mask=mask.float())
 
 
+def test_topk_full_rows_path_in_rounds_with_view_bias(gpu_device):
+    # k = 8,000 of 9,000 keys: every row is scored over every key and selected exactly, in
+    # rounds of 512 rows per batch element (1,100 rows: three rounds, the last partial), with
+    # the soft view bias on every score.
+    g = torch.Generator().manual_seed(12)
+    B, T, S, topk, Vq, Vs = 2, 1100, 9000, 8000, 3, 5
+    q = torch.randn(B, T, 4, 64, generator=g).bfloat16()
+    k = torch.randn(B, S, 4, 64, generator=g).bfloat16()
+    w = (1 + 0.3 * torch.randn(B, S, 4, generator=g)).bfloat16()
+    qv = torch.randint(0, Vq, (B, T), generator=g, dtype=torch.int32)
+    sv = torch.randint(0, Vs, (B, S), generator=g, dtype=torch.int32)
+    table = torch.randn(B, Vq, Vs, generator=g).bfloat16()
+    idx, sc = sti.indexer_topk_forward(q.cuda(), k.cuda(), w.cuda(), None, topk, 0.125,
+                                       view_bias=(qv.cuda(), sv.cuda(), table.cuda()))
+    torch.cuda.synchronize()
+    idx, sc = idx.cpu(), sc.cpu()
+    for b in range(B):
+        ref = oidx.indexer_scores(q[b:b + 1], k[b:b + 1], w[b:b + 1], None, 0.125,
+                                  view_bias=(qv[b:b + 1], sv[b:b + 1], table[b:b + 1].float()))[0]
+        rep = check_topk_rows(ref, idx[b], topk)
+        assert rep.ok, f"batch {b}: {rep}"
+        torch.testing.assert_close(sc[b].float(), ref.gather(1, idx[b].long()), atol=2e-2, rtol=2e-2)
+
+
 def test_topk_at_least_source_length(gpu_device):
     q, k, w = workloads.indexer_inputs(1, 1, torch.bfloat16, tokens=300)
     idx, sc = _gpu_topk(q, k, w, 1024)
