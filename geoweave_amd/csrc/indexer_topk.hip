@@ -37,8 +37,8 @@
 // deterministically (candidate order: split, then position in the list). No step bounds
 // topk: one whose expected candidates exceed 3/4 of the candidate slots (kSubTotal) sends
 // every row through K3's full scoring and row select, in rounds of kFullRows rows per batch
-// element (no threshold, filter or list select), and one above the register slots (kSelRegs
-// per lane) sends most queries to K2b.
+// element (no threshold, filter or list select), and one above the register slots (at most
+// 96 per lane) sends most queries to K2b.
 //
 // MFMA layout (v_mfma_f32_32x32x16_{bf16,f16}), transposed: per tile of 32 keys a wave
 // forms S^T[32 keys x 32 queries] = K Q^T with A = key rows staged through LDS (XOR-swizzled
@@ -770,13 +770,16 @@ __global__ __launch_bounds__(256) void indexer_tau_kernel(const float* samp, int
 // Exact top-k among the candidates: one wave per query row, candidates in registers.
 //
 // The row's lists (one per key split) are read as one sequence: entry e of the sequence
-// goes to register slot e / 64 of lane e % 64, for up to 64 * kSelRegs entries (about
-// 1.7 x topk are expected). A row with an overflowed list or fewer than topk candidates
-// goes to the exact fallback; one with more candidates than the registers hold goes to
-// the LDS selection. No barriers: reductions are wave-wide.
+// goes to register slot e / 64 of lane e % 64, for up to 64 * KS entries (about 1.7 x topk
+// are expected; KS is the smallest of kSelRegsTiers whose slots hold the expected count plus
+// five of its Poisson deviations, e.g. 48 for topk = 1024 and 64 for 2048 at S = 32). A row
+// with an overflowed list or fewer than topk candidates goes to the exact fallback; one with
+// more candidates than the registers hold goes to the LDS selection. No barriers:
+// reductions are wave-wide.
 // ---------------------------------------------------------------------------------------
-constexpr int kSelRegs = 48;
-static_assert(kSelRegs % 8 == 0, "the select kernel moves register slots in chunks of 8");
+constexpr int kSelRegsTiers[3] = {48, 64, 96};
+static_assert(kSelRegsTiers[0] % 8 == 0 && kSelRegsTiers[1] % 8 == 0 && kSelRegsTiers[2] % 8 == 0,
+              "the select kernel moves register slots in chunks of 8");
 
 struct SelectParams {
   const int2* cand;
@@ -839,10 +842,9 @@ __device__ __forceinline__ bool row_lists(const SelectParams& p, int64_t row, Ro
   return bad;
 }
 
-template <typename E>
+template <typename E, int KS>
 __global__ __launch_bounds__(256) void indexer_select_kernel(const SelectParams p) {
   __shared__ uint32_t cbuf[4][kCompactKeys];
-  constexpr int KS = kSelRegs;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (row >= p.rows) return;
@@ -1509,7 +1511,16 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   fs.rows = rows;
   fs.force_wide = base.force_wide;
   const dim3 sgrid2((unsigned)((rows + 3) / 4));
-  hipLaunchKernelGGL((indexer_select_kernel<E>), sgrid2, dim3(256), 0, st, fs);
+  // Register slots: the fewest that hold the expected candidates per query plus five Poisson
+  // deviations (the largest tier when none does: rows beyond it take the LDS selection).
+  const double expect = pl.sample ? (double)pl.rank * (double)base.S / (double)pl.Ms : (double)base.S;
+  const double need = expect + 5.0 * std::sqrt(expect);
+  if (need <= 64.0 * kSelRegsTiers[0])
+    hipLaunchKernelGGL((indexer_select_kernel<E, kSelRegsTiers[0]>), sgrid2, dim3(256), 0, st, fs);
+  else if (need <= 64.0 * kSelRegsTiers[1])
+    hipLaunchKernelGGL((indexer_select_kernel<E, kSelRegsTiers[1]>), sgrid2, dim3(256), 0, st, fs);
+  else
+    hipLaunchKernelGGL((indexer_select_kernel<E, kSelRegsTiers[2]>), sgrid2, dim3(256), 0, st, fs);
   GW_HIP_LAUNCH_CHECK("indexer_select_kernel");
   hipLaunchKernelGGL((indexer_select_wide_kernel<E>), dim3(kFallbackBlocks), dim3(256), 0, st, fs);
   GW_HIP_LAUNCH_CHECK("indexer_select_wide_kernel");

@@ -121,12 +121,14 @@ def test_forced_fallback_paths_are_exact(gpu_device, flags, tokens):
     _check(q, k, w, idx, sc, 1024)
 
 
-@pytest.mark.parametrize("S,topk,T", [(12000, 3000, 700), (12000, 5000, 400), (9500, 9000, 600)])
+@pytest.mark.parametrize("S,topk,T", [(40000, 2048, 300), (40000, 4096, 200), (12000, 3000, 700),
+                                      (12000, 5000, 400), (9500, 9000, 600)])
 def test_topk_above_the_register_and_candidate_slots(gpu_device, S, topk, T):
-    # No step bounds the top-k: above the register slots (3,072 candidates) most rows take
-    # the LDS selection, above the 8,192 candidate slots every row the brute-force path (the
-    # first 512 scored on the matrix cores). Every row against the oracle, then the backward
-    # (the CSR path at these k) against the oracle on the GPU's indices.
+    # No step bounds the top-k: at S = 40,000, k = 2,048 and 4,096 expect ≈ 3,000 and 5,400
+    # candidates, which the 64- and 96-slot register selects hold; past those slots rows take
+    # the LDS selection, and where the lists would overflow every row is scored over every
+    # key on the matrix cores. Every row against the oracle, then the backward (the CSR path above k = 2,048)
+    # against the oracle on the GPU's indices.
     from geoweave_amd.custom_indexer._backward import indexer_topk_backward
     g = torch.Generator().manual_seed(topk)
     q = torch.randn(1, T, 4, 64, generator=g).bfloat16()
