@@ -771,8 +771,8 @@ __global__ __launch_bounds__(256) void indexer_tau_kernel(const float* samp, int
 //
 // The row's lists (one per key split) are read as one sequence: entry e of the sequence
 // goes to register slot e / 64 of lane e % 64, for up to 64 * KS entries (about 1.7 x topk
-// are expected; KS is the smallest of kSelRegsTiers whose slots hold the expected count plus
-// five of its Poisson deviations, e.g. 48 for topk = 1024 and 64 for 2048 at S = 32). A row
+// are expected; KS is the smallest of kSelRegsTiers whose slots hold 1.25 x the expected
+// count plus five Poisson deviations, e.g. 48 for topk = 1024 and 64 for 2048 at S = 32). A row
 // with an overflowed list or fewer than topk candidates goes to the exact fallback; one with
 // more candidates than the registers hold goes to the LDS selection. No barriers:
 // reductions are wave-wide.
@@ -1511,10 +1511,13 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   fs.rows = rows;
   fs.force_wide = base.force_wide;
   const dim3 sgrid2((unsigned)((rows + 3) / 4));
-  // Register slots: the fewest that hold the expected candidates per query plus five Poisson
-  // deviations (the largest tier when none does: rows beyond it take the LDS selection).
+  // Register slots: the fewest that hold 1.25 x the expected candidates per query plus five
+  // Poisson deviations (the largest tier when none does: rows beyond it take the LDS
+  // selection). Real rows spread wider than Poisson: for topk = 1024 at S = 32 (1,880
+  // candidates on average) 32 slots sent so many rows to the LDS selection that the call
+  // took 2.87 instead of 2.12 ms.
   const double expect = pl.sample ? (double)pl.rank * (double)base.S / (double)pl.Ms : (double)base.S;
-  const double need = expect + 5.0 * std::sqrt(expect);
+  const double need = 1.25 * expect + 5.0 * std::sqrt(expect);
   if (need <= 64.0 * kSelRegsTiers[0])
     hipLaunchKernelGGL((indexer_select_kernel<E, kSelRegsTiers[0]>), sgrid2, dim3(256), 0, st, fs);
   else if (need <= 64.0 * kSelRegsTiers[1])
