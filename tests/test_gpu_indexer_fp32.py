@@ -121,6 +121,17 @@ def test_other_head_counts_fp32(gpu_device, heads):
     _check_all_rows(q, k, w, idx, sc, 300)
 
 
+def test_full_rows_path_fp32(gpu_device):
+    # k = 9,000 of 9,500 keys: every row scored over every key on the matrix cores (fp32
+    # products) and selected exactly, in two rounds of rows.
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn(1, 600, 4, 64, generator=g)
+    k = torch.randn(1, 9500, 4, 64, generator=g)
+    w = 1 + 0.3 * torch.randn(1, 9500, 4, generator=g)
+    idx, sc = _gpu_topk(q, k, w, 9000)
+    _check_all_rows(q, k, w, idx, sc, 9000)
+
+
 def test_eight_heads_fp32_not_built(gpu_device):
     q = torch.zeros(1, 8, 8, 64, device="cuda")
     w = torch.zeros(1, 8, 8, device="cuda")
