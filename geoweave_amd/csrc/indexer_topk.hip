@@ -36,8 +36,8 @@
 // topk candidates and goes to the brute force). Ties at the k-th value are broken
 // deterministically (candidate order: split, then position in the list). No step bounds
 // topk: one whose expected candidates exceed 3/4 of the candidate slots (kSubTotal) sends
-// every row through K3's full scoring and row select, in rounds of kFullRows rows per batch
-// element (no threshold, filter or list select), and one above the register slots (at most
+// every row through K3's full scoring and row select, in rounds of up to 4 x kFullRows rows
+// per batch element (no threshold, filter or list select), and one above the register slots (at most
 // 96 per lane) sends most queries to K2b.
 //
 // MFMA layout (v_mfma_f32_32x32x16_{bf16,f16}), transposed: per tile of 32 keys a wave
@@ -1301,6 +1301,7 @@ struct Plan {
   int Kk = 0;
   bool sample = false;
   bool full_all = false;  // every row through the full scoring and the row select
+  int full_rows = 0;      // rows per batch element scored per round on the full path
   int Ms = 0, rank = 0;
   int nsplit = 1, cap = 0;
   size_t off_tau = 0, off_samp = 0, off_counts = 0, off_cand = 0, off_fb = 0, off_fblist = 0,
@@ -1322,6 +1323,14 @@ Plan make_layout(int64_t B, int64_t T, int64_t S, int64_t topk) {
     // full path instead.
     pl.full_all = (double)pl.rank * (double)S / (double)pl.Ms > 0.75 * kSubTotal;
   }
+  // Full-path rounds: kFullRows rows per batch element for the queued rows of the usual
+  // path; when every row takes it, up to 4 x as many (fewer, fuller rounds) while their
+  // scores stay within 512 MiB.
+  pl.full_rows = kFullRows;
+  if (pl.full_all) {
+    const int64_t fit = ((int64_t)512 << 20) / ((int64_t)B * S * 4);
+    pl.full_rows = (int)std::max<int64_t>(kFullRows, std::min<int64_t>(4 * kFullRows, fit / kFullRows * kFullRows));
+  }
   const size_t rows = (size_t)B * (size_t)T;
   size_t off = 0;
   pl.off_tau = off;      off = align_up(off + rows * 4, 256);
@@ -1332,7 +1341,7 @@ Plan make_layout(int64_t B, int64_t T, int64_t S, int64_t topk) {
   pl.off_fblist = off;   off = align_up(off + rows * 4, 256);
   pl.off_widelist = off; off = align_up(off + rows * 4, 256);
   pl.off_scratch = off;  off = align_up(off + (size_t)kFallbackBlocks * (size_t)S * 4, 256);
-  pl.off_full = off;     off = align_up(off + (size_t)B * kFullRows * (size_t)S * 4, 256);
+  pl.off_full = off;     off = align_up(off + (size_t)B * pl.full_rows * (size_t)S * 4, 256);
   pl.total = off;
   return pl;
 }
@@ -1382,15 +1391,15 @@ int choose_nsplit(int64_t tiles, int64_t S, int slots, bool sample, int bn) {
   return best;
 }
 
-// Launch configuration of indexer_score_kernel<SAMPLE> over every key for up to kFullRows
+// Launch configuration of indexer_score_kernel<SAMPLE> over every key for up to rows_cap
 // queued rows per batch element (rows and their count set by the caller).
 template <typename E, int HI, int BIAS>
-ScoreParams full_rows_params(const ScoreParams& base, float* full) {
+ScoreParams full_rows_params(const ScoreParams& base, float* full, int rows_cap) {
   using Shape = ScoreShape<row_bytes<E, HI>()>;
   ScoreParams fp2 = base;
   fp2.samp = full;
   fp2.Ms = base.S;
-  fp2.rows_cap = kFullRows;
+  fp2.rows_cap = rows_cap;
   fp2.tau = nullptr;
   fp2.tau_mode = kTauArray;
   fp2.nstages = (base.S + Shape::BN - 1) / Shape::BN;
@@ -1399,8 +1408,9 @@ ScoreParams full_rows_params(const ScoreParams& base, float* full) {
 
 // A top-k whose expected candidates would overflow the lists (Plan::full_all): every row is
 // scored over every key on the matrix cores and selected exactly by
-// indexer_full_select_kernel, in rounds of kFullRows rows per batch element (round r0 takes
-// rows r0 .. r0 + kFullRows - 1 of each batch element through a queue that lists every row).
+// indexer_full_select_kernel, in rounds of Plan::full_rows rows per batch element (round r0
+// takes rows r0 .. r0 + full_rows - 1 of each batch element through a queue that lists
+// every row).
 template <typename E, int HI, int BIAS>
 int run_full_rows(const ScoreParams& base, const Plan& pl, int64_t B, int32_t* out_idx, void* out_scores,
                   uint8_t* ws, hipStream_t st) {
@@ -1414,16 +1424,17 @@ int run_full_rows(const ScoreParams& base, const Plan& pl, int64_t B, int32_t* o
   hipLaunchKernelGGL(iota_kernel, dim3((unsigned)std::min<int64_t>((rows + 255) / 256, 4096)), dim3(256), 0, st,
                      list, rows);
   GW_HIP_LAUNCH_CHECK("iota_kernel");
-  ScoreParams fp2 = full_rows_params<E, HI, BIAS>(base, full);
+  const int nr = pl.full_rows;
+  ScoreParams fp2 = full_rows_params<E, HI, BIAS>(base, full, nr);
   fp2.nrows = counts;
-  const int ftiles = (kFullRows + BM - 1) / BM;
+  const int ftiles = (nr + BM - 1) / BM;
   const int fslots = filter_slots((const void*)indexer_score_kernel<E, HI, true, BIAS>, THREADS);
   const int64_t want = (2 * (int64_t)fslots + (int64_t)ftiles * B - 1) / ((int64_t)ftiles * B);
   fp2.nsplit = (int)std::max<int64_t>(1, std::min<int64_t>(want, std::max(1, fp2.nstages / 2)));
   FallbackParams bp{};
   bp.fb_count = counts;
   bp.full = full;
-  bp.rows_cap = kFullRows;
+  bp.rows_cap = nr;
   bp.B = (int)B;
   bp.out_idx = out_idx;
   bp.out_scores = out_scores;
@@ -1431,7 +1442,7 @@ int run_full_rows(const ScoreParams& base, const Plan& pl, int64_t B, int32_t* o
   bp.S = base.S;
   bp.Kk = pl.Kk;
   bp.scale = base.scale;
-  for (int r0 = 0; r0 < base.T; r0 += kFullRows) {
+  for (int r0 = 0; r0 < base.T; r0 += nr) {
     hipLaunchKernelGGL(set_ints_kernel, dim3(1), dim3(256), 0, st, counts, (int)B, base.T - r0);
     GW_HIP_LAUNCH_CHECK("set_ints_kernel");
     fp2.rows = list + r0;
@@ -1533,7 +1544,7 @@ int run_typed(const ScoreParams& base, Plan pl, int64_t B, int32_t* out_idx, voi
   // fewer queued rows return at once).
   float* full = reinterpret_cast<float*>(ws + pl.off_full);
   {
-    ScoreParams fp2 = full_rows_params<E, HI, BIAS>(base, full);
+    ScoreParams fp2 = full_rows_params<E, HI, BIAS>(base, full, kFullRows);
     fp2.rows = fs.fb_list;
     fp2.nrows = fs.fb_count;
     const int ftiles = (kFullRows + BM - 1) / BM;

@@ -106,7 +106,7 @@ int gw_sparse_attn_fwd(int dtype,
  * (bf16, fp16 or fp32). Supported: Di = 64, Hi in {1,2,4,8} ({1,2,4} for fp32),
  * any topk >= 1 (K = min(topk, S); a K whose expected candidates exceed 3/4 of the 8192
  * candidate slots per query scores every row over every key on the matrix cores and selects
- * it exactly, in rounds of 512 rows per batch element), softmax_scale > 0.
+ * it exactly, in rounds of up to 2,048 rows per batch element), softmax_scale > 0.
  * workspace: gw_indexer_topk_workspace_size(B, T, S, topk) bytes, 16-byte aligned.
  * flags: 0 normally. Test hooks that force the exact fallback paths:
  *   GW_TOPK_FLAG_TAU_PLUS_INF  - no key passes the candidate filter (every query falls
